@@ -1,0 +1,245 @@
+#!/usr/bin/env python3
+"""MLA decode benchmark on one MI355X.
+
+Headline (one JSON line on stdout): absorbed-MLA decode, batch 1, 128 heads,
+kv_lora 512 + rope 64 (576-wide bf16 latent rows), context 32768, fp32
+softmax/accumulation, bf16 output -- microseconds per layer, with the
+achieved HBM fraction of the dominant (split) kernel, and the sparse top-2048
+decode (batch 4, 128 heads, 128K context) as a second figure.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W]
+
+A step is one decode layer (split kernel + combine kernel) over inputs
+already resident in HBM.  Caches rotate over enough copies that the 256 MB
+Infinity Cache cannot hold them, so the traffic is HBM traffic.  Inputs are
+synthetic (torch RNG with a fixed seed, the workload's distributions).
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import platform
+import subprocess
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "minirun-app_amd"))
+
+HBM_PEAK_GBS = 8000.0
+H, N, R, DR = 128, 32768, 512, 64
+SCALE = 192 ** -0.5
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def cache_bytes_per_layer():
+    # algorithmic bytes of one decode layer: cache rows + q + bf16 out
+    return N * (R + DR) * 2 + H * (R + DR) * 2 + H * R * 2
+
+
+def split_kernel_bytes():
+    # the split kernel reads the cache rows and q; the combine writes out
+    return N * (R + DR) * 2 + H * (R + DR) * 2
+
+
+def sparse_bytes(B=4, K=2048):
+    return B * K * (R + DR) * 2 + B * K * 4 + B * H * (R + DR) * 2 + B * H * R * 2
+
+
+def make_decode_inputs(torch, nbuf):
+    g = torch.Generator(device="cuda")
+    g.manual_seed(0x4D4C410001)
+    q_lat = torch.randn(1, H, R, generator=g, device="cuda").to(torch.bfloat16)
+    q_rope = torch.randn(1, H, DR, generator=g, device="cuda").to(torch.bfloat16)
+    caches = [(0.5 * torch.randn(N, R + DR, generator=g, device="cuda")).to(torch.bfloat16) for _ in range(nbuf)]
+    return q_lat, q_rope, caches
+
+
+def make_sparse_inputs(torch, ncache, nidx, B=4, NC=131072, K=2048, window=128):
+    g = torch.Generator(device="cuda")
+    g.manual_seed(0x4D4C410004)
+    q_lat = torch.randn(B, H, R, generator=g, device="cuda").to(torch.bfloat16)
+    q_rope = torch.randn(B, H, DR, generator=g, device="cuda").to(torch.bfloat16)
+    caches = [(0.5 * torch.randn(B, NC, R + DR, generator=g, device="cuda")).to(torch.bfloat16)
+              for _ in range(ncache)]
+    gc = torch.Generator()
+    gc.manual_seed(4)
+    sets = []
+    for _ in range(nidx):
+        rows = []
+        for _b in range(B):
+            drawn = torch.randperm(NC - window, generator=gc)[: K - window]
+            rows.append(torch.sort(torch.cat([drawn, torch.arange(NC - window, NC)])).values)
+        sets.append(torch.stack(rows).to(torch.int32).cuda())
+    return q_lat, q_rope, caches, sets
+
+
+def time_decode(torch, M, steps, warmup):
+    nbuf = 10  # 10 x 37.7 MB > 256 MB Infinity Cache
+    q_lat, q_rope, caches = make_decode_inputs(torch, nbuf)
+    out = torch.empty(1, H, R, dtype=torch.bfloat16, device="cuda")
+    args = []
+    ws = None
+    for c in caches:
+        a, _, ws = M.decode_args(q_lat, q_rope, c[:, :R], c[:, R:], scale=SCALE, out=out, workspace=ws)
+        args.append(a)
+    lib = M.load()
+    stream = torch.cuda.current_stream()
+    sp = M._stream(stream)
+    import ctypes as C
+
+    for i in range(warmup):
+        M._check(lib.mr_mla_decode(C.byref(args[i % nbuf]), sp))
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(steps):
+        M._check(lib.mr_mla_decode(C.byref(args[i % nbuf]), sp))
+    torch.cuda.synchronize()
+    wall = (time.perf_counter() - t0) / steps
+
+    # per-kernel breakdown with the phase-accounting events
+    n_ev = min(steps, 200)
+    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(n_ev)]
+    handles = [(C.c_void_p * 3)(*[e.cuda_event for e in ev]) for ev in evs]
+    for i in range(n_ev):
+        a = args[i % nbuf]
+        a.phase_events = C.cast(handles[i], C.c_void_p)
+        M._check(lib.mr_mla_decode(C.byref(a), sp))
+        a.phase_events = None
+    torch.cuda.synchronize()
+    split_ms = sum(ev[0].elapsed_time(ev[1]) for ev in evs) / n_ev
+    layer_ms = sum(ev[0].elapsed_time(ev[2]) for ev in evs) / n_ev
+    return {"wall_ms": wall * 1e3, "split_ms": split_ms, "layer_ms": layer_ms, "splits": None}
+
+
+def time_sparse(torch, M, steps, warmup):
+    q_lat, q_rope, caches, sets = make_sparse_inputs(torch, 2, 16)
+    out = torch.empty(4, H, R, dtype=torch.bfloat16, device="cuda")
+    import ctypes as C
+
+    lib = M.load()
+    sp = M._stream(torch.cuda.current_stream())
+    args, ws = [], None
+    for i in range(32):
+        c = caches[i % 2]
+        a, _, ws = M.decode_args(q_lat, q_rope, c[..., :R], c[..., R:], scale=SCALE, indices=sets[i % 16], out=out,
+                                 workspace=ws)
+        args.append(a)
+    for i in range(warmup):
+        M._check(lib.mr_mla_decode(C.byref(args[i % 32]), sp))
+    torch.cuda.synchronize()
+    n_ev = min(steps, 200)
+    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(n_ev)]
+    handles = [(C.c_void_p * 3)(*[e.cuda_event for e in ev]) for ev in evs]
+    t0 = time.perf_counter()
+    for i in range(n_ev):
+        a = args[i % 32]
+        a.phase_events = C.cast(handles[i], C.c_void_p)
+        M._check(lib.mr_mla_decode(C.byref(a), sp))
+        a.phase_events = None
+    torch.cuda.synchronize()
+    wall = (time.perf_counter() - t0) / n_ev
+    split_ms = sum(ev[0].elapsed_time(ev[1]) for ev in evs) / n_ev
+    layer_ms = sum(ev[0].elapsed_time(ev[2]) for ev in evs) / n_ev
+    return {"wall_ms": wall * 1e3, "split_ms": split_ms, "layer_ms": layer_ms}
+
+
+def cpu_baseline(budget_s=12.0):
+    """The oracle (scalar C, OpenMP over heads) on the same workload, timed on
+    this host's cores; a bounded sample: whole config-2 decode calls until the
+    time budget is used (at least 2)."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import numpy as np
+
+    import oracle as O
+
+    threads = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()
+    threads = max(1, min(threads, 16))
+    ql = O.normal_bf16("c2.q_lat", (H, R), threads=threads)
+    qr = O.normal_bf16("c2.q_rope", (H, DR), threads=threads)
+    cache = O.normal_bf16("c2.cache", (N, R + DR), std=0.5, threads=threads)
+    O.mla_decode(ql, qr, cache, acc=0, threads=threads)  # warm
+    times = []
+    t_start = time.perf_counter()
+    while len(times) < 2 or time.perf_counter() - t_start < budget_s:
+        t0 = time.perf_counter()
+        O.mla_decode(ql, qr, cache, acc=0, threads=threads)
+        times.append(time.perf_counter() - t0)
+        if len(times) >= 50:
+            break
+    times.sort()
+    med = times[len(times) // 2]
+    try:
+        model = [l.split(":", 1)[1].strip() for l in open("/proc/cpuinfo") if l.startswith("model name")][0]
+    except Exception:
+        model = platform.processor()
+    return {"value": round(med * 1e6, 1), "unit": "us/layer", "cores": threads, "kind": "port",
+            "sample": f"{len(times)} full decode layers (H=128, N=32768) in fp32, oracle C port, "
+                      f"median; host: {model}"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=400)
+    ap.add_argument("--warmup", type=int, default=50)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported "
+              "(the decode path is single-GPU; context sharding is described in DESIGN.md)", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    import minirun_hip as M
+
+    M.load()
+    log(f"bench: decode H={H} N={N} steps={args.steps} warmup={args.warmup}")
+    d = time_decode(torch, M, args.steps, args.warmup)
+    log(f"bench: decode {d}")
+    log("bench: sparse B=4 H=128 N=131072 K=2048")
+    s = time_sparse(torch, M, args.steps, args.warmup)
+    log(f"bench: sparse {s}")
+
+    layer_us = d["wall_ms"] * 1e3
+    split_s = d["split_ms"] * 1e-3
+    achieved = split_kernel_bytes() / split_s / 1e9
+    result = {
+        "metric": "MLA decode us/layer + % HBM peak (128 heads, 32K ctx); sparse top-2048 us",
+        "value": round(layer_us, 3),
+        "unit": "us/layer",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(d["wall_ms"], 5),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (torch RNG, fixed seed; q~N(0,1), cache~N(0,0.5) bf16)",
+        "config": {"workload": "mla_absorbed_decode", "batch": 1, "heads": H, "context": N,
+                   "kv_lora_rank": R, "rope_dim": DR, "softmax": "fp32", "out": "bf16",
+                   "cache_rotation": 10},
+        "hbm_fraction_layer": round(cache_bytes_per_layer() / (d["layer_ms"] * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+        "layer_us_events": round(d["layer_ms"] * 1e3, 3),
+        "split_kernel_us": round(d["split_ms"] * 1e3, 3),
+        "sparse_top2048_us": round(s["layer_ms"] * 1e3, 3),
+        "sparse_split_kernel_us": round(s["split_ms"] * 1e3, 3),
+        "sparse_hbm_fraction": round(sparse_bytes() / (s["layer_ms"] * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "mla_decode_split", "algorithmic_bytes": split_kernel_bytes()},
+    }
+    if not args.no_cpu_baseline:
+        log("bench: cpu baseline (oracle port)")
+        result["cpu_baseline"] = cpu_baseline()
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

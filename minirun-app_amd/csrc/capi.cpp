@@ -1,0 +1,244 @@
+// C-ABI layer: argument validation with named errors, workspace layout,
+// launch-shape choice.  No device memory is allocated here.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <atomic>
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <string>
+#include <vector>
+
+#include "../../include/minirun_hip.h"
+#include "mr_kernels.hpp"
+
+namespace {
+
+thread_local std::string g_last_error;
+
+mr_status fail(mr_status st, const char* fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    g_last_error = buf;
+    return st;
+}
+
+mr_status hip_fail(hipError_t e, const char* what) {
+    return fail(MR_HIP_ERROR, "%s: %s", what, hipGetErrorString(e));
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+constexpr int kMaxDevices = 64;
+std::atomic<int> g_cu_count[kMaxDevices];
+
+int cu_count() {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return 256;
+    int v = g_cu_count[dev].load(std::memory_order_relaxed);
+    if (v > 0) return v;
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    g_cu_count[dev].store(n, std::memory_order_relaxed);
+    return n;
+}
+
+size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
+
+struct DecodePlan {
+    int n_rows, head_groups, h_pad, splits, rows_per_split;
+    size_t o_bytes, ml_bytes, total;
+};
+
+DecodePlan plan_decode(const mr_mla_decode_args* a) {
+    DecodePlan pl{};
+    pl.n_rows = a->indices ? a->n_idx : a->n_ctx;
+    pl.head_groups = mr::decode_head_groups(a->heads);
+    pl.h_pad = pl.head_groups * 32;
+    const int rows = std::max(pl.n_rows, 0);
+    int splits;
+    if (a->num_splits > 0) {
+        splits = a->num_splits;
+    } else {
+        const double per = double(cu_count()) / double(std::max(1, a->batch * pl.head_groups));
+        splits = std::max(1, int(std::lround(per)));
+    }
+    const int max_splits = std::max(1, (rows + 63) / 64);
+    splits = std::min(splits, max_splits);
+    int rps = (rows + splits - 1) / splits;
+    rps = std::max(64, (rps + 63) / 64 * 64);
+    if (a->indices && rps > mr::MAX_GATHER_ROWS) rps = mr::MAX_GATHER_ROWS;
+    splits = std::max(1, (rows + rps - 1) / rps);
+    pl.splits = splits;
+    pl.rows_per_split = rps;
+    const size_t recs = size_t(std::max(a->batch, 0)) * size_t(splits) * size_t(pl.h_pad);
+    pl.o_bytes = align256(recs * 512 * sizeof(float));
+    pl.ml_bytes = align256(recs * 2 * sizeof(float));
+    pl.total = pl.o_bytes + pl.ml_bytes;
+    return pl;
+}
+
+mr_status check_decode(const mr_mla_decode_args* a) {
+    if (!a) return fail(MR_INVALID_ARGUMENT, "mr_mla_decode: args is NULL");
+    if (a->batch <= 0 || a->heads <= 0)
+        return fail(MR_INVALID_SHAPE, "mla decode: batch %d and heads %d must be positive", a->batch, a->heads);
+    if (a->kv_rank != 512)
+        return fail(MR_INVALID_SHAPE, "mla decode: kv_rank must be 512, got %d", a->kv_rank);
+    if (a->rope_dim != 64 && a->rope_dim != 0)
+        return fail(MR_INVALID_SHAPE, "mla decode: rope_dim must be 64 or 0, got %d", a->rope_dim);
+    if (!(std::isfinite(a->scale) && a->scale > 0))
+        return fail(MR_INVALID_SHAPE, "sparse attention queries, shared KV, sinks, indices, or scale are invalid: "
+                                      "scale %g must be finite and positive", double(a->scale));
+    if (a->indices) {
+        if (a->n_idx < 0) return fail(MR_INVALID_SHAPE, "mla decode: n_idx %d is negative", a->n_idx);
+        if (a->n_ctx <= 0) return fail(MR_INVALID_SHAPE, "mla decode: the cache has no rows (n_ctx %d)", a->n_ctx);
+    } else if (a->n_ctx <= 0) {
+        return fail(MR_INVALID_SHAPE, "mla decode: n_ctx %d must be positive", a->n_ctx);
+    }
+    if (!a->q_lat || !a->latent || !a->out)
+        return fail(MR_INVALID_ARGUMENT, "mla decode: q_lat, latent and out must be non-NULL");
+    if (a->rope_dim && (!a->q_rope || !a->rope_keys))
+        return fail(MR_INVALID_ARGUMENT, "mla decode: rope_dim %d needs q_rope and rope_keys", a->rope_dim);
+    if (!aligned16(a->q_lat) || !aligned16(a->latent) || (a->rope_dim && (!aligned16(a->q_rope) || !aligned16(a->rope_keys))))
+        return fail(MR_INVALID_ARGUMENT, "mla decode: q and cache base pointers must be 16-byte aligned");
+    const int64_t strides[] = {a->q_lat_head_stride, a->q_lat_batch_stride, a->latent_row_stride, a->latent_batch_stride};
+    for (int64_t s : strides)
+        if (s < 0 || s % 8) return fail(MR_INVALID_ARGUMENT, "mla decode: q/latent strides must be non-negative multiples of 8 elements");
+    if (a->latent_row_stride < 512 || a->q_lat_head_stride < 512)
+        return fail(MR_INVALID_ARGUMENT, "mla decode: latent_row_stride and q_lat_head_stride must be >= 512");
+    if (a->rope_dim) {
+        const int64_t rs[] = {a->q_rope_head_stride, a->q_rope_batch_stride, a->rope_row_stride, a->rope_batch_stride};
+        for (int64_t s : rs)
+            if (s < 0 || s % 8) return fail(MR_INVALID_ARGUMENT, "mla decode: rope strides must be non-negative multiples of 8 elements");
+        if (a->rope_row_stride < 64 || a->q_rope_head_stride < 64)
+            return fail(MR_INVALID_ARGUMENT, "mla decode: rope strides must be >= 64");
+    }
+    if (a->out_dtype != MR_BF16 && a->out_dtype != MR_F32)
+        return fail(MR_INVALID_DTYPE, "mla decode: out_dtype must be MR_BF16 or MR_F32");
+    if (a->out_head_stride < 512 || a->out_batch_stride < 0)
+        return fail(MR_INVALID_ARGUMENT, "mla decode: out strides too small");
+    if (a->num_splits < 0) return fail(MR_INVALID_ARGUMENT, "mla decode: num_splits must be >= 0");
+    return MR_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* mr_version(void) { return "minirun-hip 0.1.0 gfx950"; }
+
+const char* mr_get_last_error(void) { return g_last_error.c_str(); }
+
+size_t mr_mla_decode_workspace_size(const mr_mla_decode_args* args) {
+    if (!args) return 0;
+    return plan_decode(args).total;
+}
+
+size_t mr_validate_indices_workspace_size(int32_t batch, int32_t n_idx) {
+    (void)n_idx;
+    return align256(size_t(std::max(batch, 0)) * 2 * sizeof(int32_t));
+}
+
+mr_status mr_validate_indices(const int32_t* indices, int32_t batch, int32_t n_idx, int32_t n_rows,
+                              void* workspace, size_t workspace_bytes, int32_t* bad_token,
+                              int32_t* bad_position, void* stream) {
+    if (bad_token) *bad_token = -1;
+    if (bad_position) *bad_position = -1;
+    if (batch <= 0 || n_idx < 0 || n_rows < 0)
+        return fail(MR_INVALID_SHAPE, "index validation: batch %d, n_idx %d, n_rows %d", batch, n_idx, n_rows);
+    if (n_idx == 0) return MR_OK;
+    if (n_idx > 4096) return fail(MR_INVALID_SHAPE, "index validation: n_idx %d exceeds 4096", n_idx);
+    if (!indices || !workspace) return fail(MR_INVALID_ARGUMENT, "index validation: NULL indices or workspace");
+    if (workspace_bytes < mr_validate_indices_workspace_size(batch, n_idx))
+        return fail(MR_WORKSPACE_TOO_SMALL, "index validation: workspace %zu bytes < %zu", workspace_bytes,
+                    mr_validate_indices_workspace_size(batch, n_idx));
+    hipStream_t st = (hipStream_t)stream;
+    int32_t* res = (int32_t*)workspace;
+    hipError_t e = mr::launch_validate_indices(indices, batch, n_idx, n_rows, res, st);
+    if (e != hipSuccess) return hip_fail(e, "index validation launch");
+    std::vector<int32_t> host(size_t(batch) * 2);
+    e = hipMemcpyAsync(host.data(), res, host.size() * sizeof(int32_t), hipMemcpyDeviceToHost, st);
+    if (e == hipSuccess) e = hipStreamSynchronize(st);
+    if (e != hipSuccess) return hip_fail(e, "index validation readback");
+    std::vector<int32_t> idx_host(1);
+    for (int32_t b = 0; b < batch; ++b) {
+        const int32_t rp = host[2 * b], dp = host[2 * b + 1];
+        if (rp == 0x7fffffff && dp == 0x7fffffff) continue;
+        const int32_t pos = std::min(rp, dp);
+        if (bad_token) *bad_token = b;
+        if (bad_position) *bad_position = pos;
+        e = hipMemcpy(idx_host.data(), indices + int64_t(b) * n_idx + pos, sizeof(int32_t), hipMemcpyDeviceToHost);
+        const int32_t v = e == hipSuccess ? idx_host[0] : -1;
+        if (rp <= dp)
+            return fail(MR_INDEX_OUT_OF_RANGE, "token %d names KV row %d, outside the cache", b, v);
+        return fail(MR_DUPLICATE_INDEX, "token %d names KV row %d more than once", b, v);
+    }
+    return MR_OK;
+}
+
+mr_status mr_mla_decode(const mr_mla_decode_args* a, void* stream) {
+    mr_status st = check_decode(a);
+    if (st != MR_OK) return st;
+    const DecodePlan pl = plan_decode(a);
+    if (!a->workspace || a->workspace_bytes < pl.total)
+        return fail(MR_WORKSPACE_TOO_SMALL, "mla decode: workspace %zu bytes < %zu required", a->workspace_bytes, pl.total);
+    if (!aligned16(a->workspace)) return fail(MR_INVALID_ARGUMENT, "mla decode: workspace must be 16-byte aligned");
+    if (a->indices && (a->flags & MR_DECODE_VALIDATE_INDICES) && a->n_idx > 0) {
+        st = mr_validate_indices(a->indices, a->batch, a->n_idx, a->n_ctx, a->workspace, a->workspace_bytes, nullptr,
+                                 nullptr, stream);
+        if (st != MR_OK) return st;
+    }
+    mr::DecodeParams p{};
+    p.q_lat = (const uint16_t*)a->q_lat;
+    p.q_lat_bs = a->q_lat_batch_stride;
+    p.q_lat_hs = a->q_lat_head_stride;
+    p.q_rope = (const uint16_t*)a->q_rope;
+    p.q_rope_bs = a->q_rope_batch_stride;
+    p.q_rope_hs = a->q_rope_head_stride;
+    p.latent = (const uint16_t*)a->latent;
+    p.lat_rs = a->latent_row_stride;
+    p.lat_bs = a->latent_batch_stride;
+    p.rope = (const uint16_t*)a->rope_keys;
+    p.rope_rs = a->rope_row_stride;
+    p.rope_bs = a->rope_batch_stride;
+    p.indices = a->indices;
+    p.n_idx = a->n_idx;
+    p.batch = a->batch;
+    p.heads = a->heads;
+    p.n_ctx = a->n_ctx;
+    p.rope_dim = a->rope_dim;
+    p.n_rows = pl.n_rows;
+    p.splits = pl.splits;
+    p.rows_per_split = pl.rows_per_split;
+    p.head_groups = pl.head_groups;
+    p.h_pad = pl.h_pad;
+    p.scale_log2 = a->scale * 1.4426950408889634f;
+    p.ws_o = (float*)a->workspace;
+    p.ws_ml = (float*)((char*)a->workspace + pl.o_bytes);
+    p.err_flag = nullptr;
+
+    mr::CombineParams cp{};
+    cp.ws_o = p.ws_o;
+    cp.ws_ml = p.ws_ml;
+    cp.sinks = a->sinks;
+    cp.out = a->out;
+    cp.out_bs = a->out_batch_stride;
+    cp.out_hs = a->out_head_stride;
+    cp.batch = a->batch;
+    cp.heads = a->heads;
+    cp.splits = pl.splits;
+    cp.h_pad = pl.h_pad;
+    cp.out_f32 = a->out_dtype == MR_F32;
+
+    const hipError_t e =
+        mr::launch_mla_decode(p, cp, (a->flags & MR_DECODE_NO_TRANSPOSE_READ) == 0,
+                              (hipEvent_t const*)a->phase_events, (hipStream_t)stream);
+    if (e != hipSuccess) return hip_fail(e, "mla decode launch");
+    return MR_OK;
+}
+
+}  // extern "C"

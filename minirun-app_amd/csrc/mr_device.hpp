@@ -1,0 +1,83 @@
+// Shared device-side helpers for the gfx950 kernels of the MLA path.
+//
+// Operand layouts used throughout (pinned on hardware by selftest.hip and
+// tests/test_gpu_selftest.py):
+//
+//   v_mfma_f32_16x16x32_bf16   A[16][32]: lane l holds row l%16, k = 8*(l/16)+0..7
+//                              B[32][16]: lane l holds col l%16, k = 8*(l/16)+0..7
+//                              D[16][16]: lane l holds col l%16, rows 4*(l/16)+0..3
+//   v_mfma_f32_32x32x16_bf16   A[32][16]: lane l holds row l%32, k = 8*(l/32)+0..7
+//                              B[16][32]: lane l holds col l%32, k = 8*(l/32)+0..7
+//                              D[32][32]: lane l holds col l%32,
+//                                         acc i -> row 8*(i/4) + 4*(l/32) + i%4
+//   ds_read_b64_tr_b16         within each 16-lane group, lane j supplies the
+//                              address of 4 consecutive b16 of "row" j/4,
+//                              "cols" 4*(j%4)..+3 of a 4x16 block; lane i gets
+//                              column i of that block (rows 0..3).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace mr {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+#define MR_LDS __attribute__((address_space(3)))
+
+__device__ __forceinline__ f32x4 mfma16(const bf16x8& a, const bf16x8& b, const f32x4& c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ f32x16 mfma32(const bf16x8& a, const bf16x8& b, const f32x16& c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+
+// LDS transpose read: 4 x b16 (see the layout note above).
+// `p` must point into __shared__ memory (8-byte aligned).
+__device__ __forceinline__ bf16x4 ds_read_tr16(const void* p) {
+    typedef MR_LDS bf16x4 lds_bf16x4;
+    return __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)(p));
+}
+
+__device__ __forceinline__ float bf16_bits_to_f32(uint16_t h) {
+    return __uint_as_float(((uint32_t)h) << 16);
+}
+
+// Round-to-nearest-even float -> bf16 bits (NaN kept quiet).
+__device__ __forceinline__ uint16_t f32_to_bf16_bits(float x) {
+    uint32_t u = __float_as_uint(x);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return (uint16_t)(u >> 16);
+}
+
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+    return (uint32_t)f32_to_bf16_bits(lo) | ((uint32_t)f32_to_bf16_bits(hi) << 16);
+}
+
+__device__ __forceinline__ float f16_bits_to_f32(uint16_t h) {
+    return (float)__builtin_bit_cast(_Float16, h);
+}
+
+template <int N>
+__device__ __forceinline__ bf16x8 as_bf16x8(const u32x4& v) {
+    return __builtin_bit_cast(bf16x8, v);
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+    for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
+    return v;
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+    for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o);
+    return v;
+}
+
+}  // namespace mr

@@ -1,0 +1,66 @@
+"""CPU checks of the C-ABI library: it loads, exports every function that
+include/minirun_hip.h declares, and rejects bad arguments with named errors
+without touching a GPU (argument checks run before any HIP call)."""
+import ctypes as C
+import os
+import re
+
+import pytest
+
+import minirun_hip as M
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def declared_functions():
+    names = []
+    for fn in os.listdir(os.path.join(ROOT, "include")):
+        if fn.endswith(".h"):
+            text = open(os.path.join(ROOT, "include", fn)).read()
+            text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+            names += re.findall(r"\b(mr_[a-z0-9_]+)\s*\(", text)
+    return sorted(set(names))
+
+
+def test_library_exports_every_declared_symbol():
+    lib = M.load()
+    names = declared_functions()
+    assert "mr_mla_decode" in names
+    missing = [n for n in names if not hasattr(lib, n)]
+    assert not missing, f"declared but not exported: {missing}"
+    assert set(names) <= set(M.SIGNATURES), "binding lacks a signature for a declared function"
+
+
+def test_version_and_error_string():
+    assert M.version().startswith("minirun-hip")
+    assert isinstance(M.last_error(), str)
+
+
+def test_decode_rejects_bad_arguments_before_any_gpu_call():
+    lib = M.load()
+    a = M.DecodeArgs()
+    a.batch, a.heads, a.n_ctx, a.kv_rank, a.rope_dim, a.scale = 1, 16, 512, 256, 64, 0.07
+    assert lib.mr_mla_decode(C.byref(a), None) == M.INVALID_SHAPE
+    assert "kv_rank" in M.last_error()
+    a.kv_rank = 512
+    a.scale = -1.0
+    assert lib.mr_mla_decode(C.byref(a), None) == M.INVALID_SHAPE
+    a.scale = 0.07
+    assert lib.mr_mla_decode(C.byref(a), None) == M.INVALID_ARGUMENT  # NULL pointers
+    assert lib.mr_mla_decode(None, None) == M.INVALID_ARGUMENT
+
+
+def test_workspace_size_is_deterministic_and_covers_partials():
+    lib = M.load()
+    a = M.DecodeArgs()
+    a.batch, a.heads, a.n_ctx, a.kv_rank, a.rope_dim, a.scale = 1, 128, 32768, 512, 64, 0.07
+    a.num_splits = 64
+    n = lib.mr_mla_decode_workspace_size(C.byref(a))
+    assert n >= 64 * 128 * 514 * 4
+    assert n == lib.mr_mla_decode_workspace_size(C.byref(a))
+
+
+def test_validate_indices_rejects_oversize_without_gpu():
+    lib = M.load()
+    st = lib.mr_validate_indices(None, 1, 5000, 10, None, 0, None, None, None)
+    assert st == M.INVALID_SHAPE

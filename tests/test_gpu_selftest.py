@@ -1,0 +1,81 @@
+"""Pins, on the GPU, the operand layouts the decode kernel is written for:
+16x16x32 and 32x32x16 bf16 MFMA and the ds_read_b64_tr_b16 lane mapping.
+Inputs are small integers, exact in bf16 and in fp32 accumulation."""
+import ctypes as C
+import sys
+
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def st():
+    import minirun_hip as M
+
+    lib = C.CDLL(M.SELFTEST_PATH)
+    for n in ("mr_selftest_mfma16", "mr_selftest_mfma32"):
+        getattr(lib, n).argtypes = [C.c_void_p] * 4
+    lib.mr_selftest_tr16.argtypes = [C.c_void_p] * 4
+    return lib
+
+
+def _bf16(torch, a):
+    return torch.tensor(a.astype(np.float32)).to(torch.bfloat16).cuda()
+
+
+def test_mfma16_layout(st):
+    import torch
+
+    print("selftest mfma16", flush=True)
+    rng = np.random.default_rng(0)
+    A = rng.integers(-4, 5, (16, 32))
+    B = rng.integers(-4, 5, (32, 16))
+    D = torch.zeros(16, 16, dtype=torch.float32, device="cuda")
+    assert st.mr_selftest_mfma16(_bf16(torch, A).data_ptr(), _bf16(torch, B).data_ptr(), D.data_ptr(), None) == 0
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(D.cpu().numpy(), (A @ B).astype(np.float32))
+
+
+def test_mfma32_layout(st):
+    import torch
+
+    print("selftest mfma32", flush=True)
+    rng = np.random.default_rng(1)
+    A = rng.integers(-4, 5, (32, 16))
+    B = rng.integers(-4, 5, (16, 32))
+    D = torch.zeros(32, 32, dtype=torch.float32, device="cuda")
+    assert st.mr_selftest_mfma32(_bf16(torch, A).data_ptr(), _bf16(torch, B).data_ptr(), D.data_ptr(), None) == 0
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(D.cpu().numpy(), (A @ B).astype(np.float32))
+
+
+def test_ds_read_tr16_mapping(st):
+    """A 16x64 b16 matrix M[r][c] = 64r + c sits in LDS (row stride 128 B).
+    Each 16-lane group g reads the 4x16 block at rows 4g.., cols 16g..: lane j
+    addresses row 4g + j/4, cols 16g + 4(j%4).  Expected: lane i of the group
+    receives column 16g + i of rows 4g..4g+3."""
+    import torch
+
+    print("selftest tr16", flush=True)
+    offs = np.zeros(64, np.int32)
+    for lane in range(64):
+        g, j = lane // 16, lane % 16
+        row, col = 4 * g + j // 4, 16 * g + 4 * (j % 4)
+        offs[lane] = (row * 64 + col) * 2
+    d_offs = torch.tensor(offs, device="cuda")
+    out = torch.zeros(64 * 4, dtype=torch.int16, device="cuda")
+    assert st.mr_selftest_tr16(offs.ctypes.data, d_offs.data_ptr(), out.data_ptr(), None) == 0
+    torch.cuda.synchronize()
+    got = out.cpu().numpy().view(np.uint16).reshape(64, 4)
+    exp = np.zeros((64, 4), np.uint16)
+    for lane in range(64):
+        g, i = lane // 16, lane % 16
+        for e in range(4):
+            exp[lane, e] = (4 * g + e) * 64 + 16 * g + i
+    if not np.array_equal(got, exp):
+        print("tr16 raw result (lane: 4 values):", file=sys.stderr)
+        for lane in range(64):
+            print(lane, got[lane].tolist(), file=sys.stderr)
+    np.testing.assert_array_equal(got, exp)
