@@ -356,41 +356,44 @@ void mro_mla_decode(const uint16_t *q_lat, const uint16_t *q_rope, const uint16_
     free(sel);
 }
 
-/* DeepSeekV4Attention.swift:884-895: -1 skips, out of range and duplicates
- * are errors.  bad_position receives the offending column. */
+/* DeepSeekV4Attention.swift:884-895: one in-order scan; -1 skips, an entry
+ * outside [0, n_rows) stops the scan with a range error, an entry equal to
+ * an earlier (in-range) entry stops it with a duplicate error.  bad_position
+ * receives the column where the scan stopped. */
+static int cmp_i64(const void *a, const void *b) {
+    int64_t x = *(const int64_t *)a, y = *(const int64_t *)b;
+    return (x > y) - (x < y);
+}
+
 int mro_validate_indices(const int32_t *indices, int32_t n_idx, int32_t n_rows,
                          int32_t *bad_position) {
-    int32_t *copy = (int32_t *)malloc(sizeof(int32_t) * (size_t)(n_idx > 0 ? n_idx : 1));
+    /* (value, position) keys of the in-range entries, sorted: the first key
+     * of a value holds the position where that value is first seen */
+    int64_t *keys = (int64_t *)malloc(sizeof(int64_t) * (size_t)(n_idx > 0 ? n_idx : 1));
     int32_t n = 0;
     for (int32_t i = 0; i < n_idx; ++i) {
         int32_t v = indices[i];
+        if (v >= 0 && v < n_rows) keys[n++] = ((int64_t)v << 32) | (int64_t)i;
+    }
+    qsort(keys, (size_t)n, sizeof(int64_t), cmp_i64);
+    int status = MRO_OK;
+    for (int32_t i = 0; i < n_idx && status == MRO_OK; ++i) {
+        int32_t v = indices[i];
         if (v == -1) continue;
         if (v < 0 || v >= n_rows) {
-            if (bad_position) *bad_position = i;
-            free(copy);
-            return MRO_INDEX_OUT_OF_RANGE;
+            status = MRO_INDEX_OUT_OF_RANGE;
+        } else {
+            int32_t lo = 0, hi = n; /* first key with value v */
+            while (lo < hi) {
+                int32_t mid = (lo + hi) / 2;
+                if ((keys[mid] >> 32) < v) lo = mid + 1; else hi = mid;
+            }
+            if ((int32_t)(keys[lo] & 0xffffffff) < i) status = MRO_DUPLICATE_INDEX;
         }
-        copy[n++] = v;
+        if (status != MRO_OK && bad_position) *bad_position = i;
     }
-    /* duplicates: the reference reports the first repeated occurrence in
-     * index order; find it with a sorted copy, then scan. */
-    qsort(copy, (size_t)n, sizeof(int32_t), cmp_i32);
-    int dup = 0;
-    for (int32_t i = 1; i < n; ++i)
-        if (copy[i] == copy[i - 1]) dup = 1;
-    free(copy);
-    if (dup) {
-        for (int32_t i = 0; i < n_idx && bad_position; ++i) {
-            if (indices[i] == -1) continue;
-            for (int32_t j = 0; j < i; ++j)
-                if (indices[j] == indices[i]) {
-                    *bad_position = i;
-                    return MRO_DUPLICATE_INDEX;
-                }
-        }
-        return MRO_DUPLICATE_INDEX;
-    }
-    return MRO_OK;
+    free(keys);
+    return status;
 }
 
 int mro_sparse_attention(const uint16_t *q_lat, const uint16_t *q_rope, const uint16_t *cache,

@@ -162,7 +162,13 @@ def test_sparse_all_indices_equals_dense(M):
     perm = np.random.default_rng(2).permutation(1024).astype(np.int32)
     a = run_sparse(M, ql[None], qr[None], cache[None], perm[None], out_dtype=torch.float32)
     b = run_decode(M, ql, qr, cache, out_dtype=torch.float32)
-    np.testing.assert_allclose(host_f32(a), host_f32(b), rtol=2e-5, atol=2e-6)
+    ref = O.mla_decode(ql, qr, cache)[0]
+    check(host_f32(a)[0], ref, "sparse-all", scale_bar=2e-3)
+    check(host_f32(b)[0], ref, "dense", scale_bar=2e-3)
+    # P is rounded to bf16 against the running max, which depends on the row
+    # order, so the two orders agree to bf16-P precision, not bitwise
+    d = np.abs(host_f32(a) - host_f32(b)).max() / np.abs(ref).max()
+    assert d < 2e-3, d
 
 
 def test_sparse_v4_form_no_rope(M):

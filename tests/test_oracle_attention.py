@@ -158,6 +158,11 @@ def test_sparse_errors_and_empty():
     assert st == O.DUPLICATE_INDEX
     assert O.validate_indices(np.array([4, 9, -1, 4]), 64) == (O.DUPLICATE_INDEX, 3)
     assert O.validate_indices(np.array([4, 99]), 64) == (O.INDEX_OUT_OF_RANGE, 1)
+    # in-order scan: the repeat at 1 stops it before the out-of-range entry at 2
+    assert O.validate_indices(np.array([7, 7, 99]), 64) == (O.DUPLICATE_INDEX, 1)
+    assert O.validate_indices(np.array([7, 99, 7]), 64) == (O.INDEX_OUT_OF_RANGE, 1)
+    assert O.validate_indices(np.array([-1, 3, -1, 3]), 64) == (O.DUPLICATE_INDEX, 3)
+    assert O.validate_indices(np.array([-1, -1]), 64) == (O.OK, -1)
     st, got = O.sparse_attention(ql, qr, cache, np.array([-1, -1], np.int32), kv_rank=32, rope_dim=8)
     assert st == O.OK and (got == 0).all()
 
