@@ -78,6 +78,17 @@ def make_sparse_inputs(torch, ncache, nidx, B=4, NC=131072, K=2048, window=128):
     return q_lat, q_rope, caches, sets
 
 
+def make_events(torch, n):
+    # torch creates the underlying hipEvent lazily: record each once so the
+    # handle exists before the library records it
+    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(n)]
+    for ev in evs:
+        for e in ev:
+            e.record()
+    torch.cuda.synchronize()
+    return evs
+
+
 def time_decode(torch, M, steps, warmup):
     nbuf = 10  # 10 x 37.7 MB > 256 MB Infinity Cache
     q_lat, q_rope, caches = make_decode_inputs(torch, nbuf)
@@ -103,7 +114,7 @@ def time_decode(torch, M, steps, warmup):
 
     # per-kernel breakdown with the phase-accounting events
     n_ev = min(steps, 200)
-    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(n_ev)]
+    evs = make_events(torch, n_ev)
     handles = [(C.c_void_p * 3)(*[e.cuda_event for e in ev]) for ev in evs]
     for i in range(n_ev):
         a = args[i % nbuf]
@@ -133,7 +144,7 @@ def time_sparse(torch, M, steps, warmup):
         M._check(lib.mr_mla_decode(C.byref(args[i % 32]), sp))
     torch.cuda.synchronize()
     n_ev = min(steps, 200)
-    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(n_ev)]
+    evs = make_events(torch, n_ev)
     handles = [(C.c_void_p * 3)(*[e.cuda_event for e in ev]) for ev in evs]
     t0 = time.perf_counter()
     for i in range(n_ev):

@@ -73,6 +73,10 @@ DecodePlan plan_decode(const mr_mla_decode_args* a) {
     rps = std::max(64, (rps + 63) / 64 * 64);
     if (a->indices && rps > mr::MAX_GATHER_ROWS) rps = mr::MAX_GATHER_ROWS;
     splits = std::max(1, (rows + rps - 1) / rps);
+    if (splits > mr::MAX_COMBINE_SPLITS) {  // very long contexts: fewer, longer splits
+        rps = ((rows + mr::MAX_COMBINE_SPLITS - 1) / mr::MAX_COMBINE_SPLITS + 63) / 64 * 64;
+        splits = std::max(1, (rows + rps - 1) / rps);
+    }
     pl.splits = splits;
     pl.rows_per_split = rps;
     const size_t recs = size_t(std::max(a->batch, 0)) * size_t(splits) * size_t(pl.h_pad);
@@ -119,8 +123,9 @@ mr_status check_decode(const mr_mla_decode_args* a) {
     }
     if (a->out_dtype != MR_BF16 && a->out_dtype != MR_F32)
         return fail(MR_INVALID_DTYPE, "mla decode: out_dtype must be MR_BF16 or MR_F32");
-    if (a->out_head_stride < 512 || a->out_batch_stride < 0)
-        return fail(MR_INVALID_ARGUMENT, "mla decode: out strides too small");
+    if (a->out_head_stride < 512 || a->out_batch_stride < 0 || a->out_head_stride % 4 || a->out_batch_stride % 4)
+        return fail(MR_INVALID_ARGUMENT, "mla decode: out strides must be multiples of 4, head stride >= 512");
+    if (!aligned16(a->out)) return fail(MR_INVALID_ARGUMENT, "mla decode: out must be 16-byte aligned");
     if (a->num_splits < 0) return fail(MR_INVALID_ARGUMENT, "mla decode: num_splits must be >= 0");
     return MR_OK;
 }

@@ -11,10 +11,13 @@
 //   grid unit   = (batch, context split) x head group of 32 heads
 //   blockIdx    -> XCD-aware: the head groups of one unit share blockIdx % 8,
 //                  so they run on one XCD and read the same rows through its L2
-//   sub-chunk   = 64 cache rows, staged global -> VGPR -> LDS, double buffered,
-//                 LDS rows padded to DK*2+16 bytes (conflict-free MFMA reads)
+//   sub-chunk   = 32 cache rows, global -> LDS by DMA (global_load_lds_dwordx4),
+//                 4 buffers so 3 sub-chunks are in flight while one is used;
+//                 rows unpadded, 16-byte chunks XOR-swizzled (bank-conflict
+//                 free MFMA and transposed reads); LDS-only barriers keep the
+//                 DMA in flight across them
 //   QK          = 16x16x32 bf16 MFMA, A = cache rows (LDS), B = Q (VGPRs);
-//                 wave w scores 16 rows x 32 heads
+//                 wave w scores one 16-row x 16-head tile
 //   softmax     = online, base-2, the running max shared by the 4 waves
 //   PV          = 16x16x32 bf16 MFMA, A = P (LDS, bf16), B = cache rows read
 //                 transposed with ds_read_b64_tr_b16; wave w owns 128 of the
@@ -29,39 +32,68 @@ namespace mr {
 namespace {
 
 constexpr int R = 512;
-constexpr int ROWS = 64;      // rows per sub-chunk
+constexpr int ROWS = 32;      // rows per sub-chunk
+constexpr int NBUF = 4;       // LDS sub-chunk buffers (3 in flight while one is consumed)
 constexpr int HG = 32;        // heads per workgroup
 constexpr int THREADS = 256;  // 4 waves
-constexpr int PSTR = 144;     // bytes per head row of P (64 bf16 + 16 pad)
+constexpr int PSTR = 80;      // bytes per head row of P (32 bf16 + 16 pad)
 constexpr float NEG_INF = -__builtin_huge_valf();
 constexpr float LOG2E = 1.4426950408889634f;
 
 template <int DR>
 struct Geo {
     static constexpr int DK = R + DR;
-    static constexpr int KS = DK / 32;             // MFMA k-steps for QK
-    static constexpr int CPR = DK / 8;             // 16-byte chunks per row
-    static constexpr int LROW = DK * 2 + 16;       // padded LDS row, bytes
-    static constexpr int BUF = ROWS * LROW;        // one sub-chunk buffer
-    static constexpr int NCH = ROWS * CPR / THREADS;  // chunks per thread
-    static_assert(ROWS * CPR % THREADS == 0, "chunking");
+    static constexpr int KS = DK / 32;        // MFMA k-steps of QK
+    static constexpr int CPR = DK / 8;        // 16-byte chunks per row
+    static constexpr int ROWB = DK * 2;       // bytes per LDS row (unpadded, swizzled)
+    static constexpr int BUF = ROWS * ROWB;   // one sub-chunk
+    static constexpr int NLD = BUF / 1024 / 4;  // 1 KB DMA loads per wave per sub-chunk
+    static_assert(BUF % 4096 == 0, "sub-chunk must split into 4 waves x 1 KB loads");
 };
 
-// row of the 64-row sub-chunk that MFMA A-row `a` (0..15) of wave w scores:
-// rows 16w + {0,2,4,6}, {1,3,5,7}, {8,..14}, {9,..15} for a/4 = 0..3.  The
-// order makes the P write contiguous and the transposed PV reads
-// bank-conflict free (see rho() below).
-__device__ __forceinline__ int sigma_row(int w, int a) {
-    int g = a >> 2;
-    return 16 * w + 8 * (g >> 1) + (g & 1) + 2 * (a & 3);
+// Physical 16-byte slot of logical chunk c in LDS row r.  The XOR keeps the
+// QK A-operand reads (16 rows, one chunk column) and the transposed PV reads
+// (8 rows of one parity, one chunk pair) on distinct banks.  The rope chunks
+// (c >= 64) swizzle inside their own 8-chunk group.  The map is an involution.
+__device__ __forceinline__ int swz(int c, int r) {
+    return c < 64 ? (c ^ (r & 15)) : (64 + ((c - 64) ^ (r & 7)));
+}
+
+// Row of the 32-row sub-chunk that MFMA A-row `a` of row tile `rt` scores:
+// rows 16rt + {0,2,4,6}, {1,3,5,7}, {8..14 even}, {9..15 odd} for a/4 = 0..3.
+// This makes each lane's four P values contiguous in the PV k order below.
+__device__ __forceinline__ int sigma_row(int rt, int a) {
+    const int g = a >> 2;
+    return 16 * rt + 8 * (g >> 1) + (g & 1) + 2 * (a & 3);
+}
+
+// LDS-only barrier: waits for this wave's LDS traffic, not for its global
+// (DMA) loads, so prefetches stay in flight across it.
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
+// All global -> LDS traffic of the split kernel is issued with this
+// instruction from inline asm, so the compiler neither knows of it nor
+// inserts its conservative vmcnt(0) before LDS reads; the kernel waits for
+// it explicitly with wait_vmcnt.  The kernel issues no other vector-memory
+// load after the first DMA, which keeps those counts exact.  (Extra loads
+// the compiler does not see can only make its own waits stricter.)
+__device__ __forceinline__ void dma16(const void* src, const void* lds_dst_wave_base) {
+    const uint32_t m0 = (uint32_t)(uintptr_t)lds_dst_wave_base;  // LDS offset (low 32 bits)
+    asm volatile("global_load_lds_dwordx4 %0, off" ::"v"(src), "{m0}"(m0) : "memory");
+}
+
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
 
 template <int DR, bool GATHER, bool TR>
 __global__ void __launch_bounds__(THREADS, 1) mla_decode_split(DecodeParams p) {
     using G = Geo<DR>;
-    __shared__ __attribute__((aligned(16))) char cbuf[2 * G::BUF];
+    __shared__ __attribute__((aligned(1024))) char cbuf[NBUF * G::BUF];
     __shared__ __attribute__((aligned(16))) char pbuf[HG * PSTR];
-    __shared__ float red[4][HG];
+    __shared__ float red[4][16];
     __shared__ __attribute__((aligned(16))) float alpha_s[HG];
     __shared__ int32_t idx_s[GATHER ? MAX_GATHER_ROWS : 1];
 
@@ -83,6 +115,8 @@ __global__ void __launch_bounds__(THREADS, 1) mla_decode_split(DecodeParams p) {
     const int l = tid & 63;
     const int lg = l >> 4;
     const int lc = l & 15;
+    const int rt = w >> 1;  // QK row tile of this wave
+    const int ht = w & 1;   // QK head tile of this wave
 
     const uint16_t* lat = p.latent + (int64_t)b * p.lat_bs;
     const uint16_t* rop = DR ? p.rope + (int64_t)b * p.rope_bs : nullptr;
@@ -90,66 +124,37 @@ __global__ void __launch_bounds__(THREADS, 1) mla_decode_split(DecodeParams p) {
     if (GATHER) {
         const int32_t* ind = p.indices + (int64_t)b * p.n_idx;
         for (int i = tid; i < nrows; i += THREADS) {
-            int32_t v = ind[row_begin + i];
-            bool ok = v >= 0 && v < p.n_ctx;
-            if (!ok && v != -1 && p.err_flag) atomicOr(p.err_flag, 1);
-            idx_s[i] = ok ? v : -1;
+            const int32_t v = ind[row_begin + i];
+            idx_s[i] = (v >= 0 && v < p.n_ctx) ? v : -1;
         }
         __syncthreads();
     }
 
-    // ---- Q for this head group, B-operand layout: head 16T+lc, k = 32ks+8lg..+7
-    bf16x8 qreg[G::KS][2];
-#pragma unroll
-    for (int T = 0; T < 2; ++T) {
-        const int h = hg * HG + 16 * T + lc;
-        const bool hv = h < p.heads;
-#pragma unroll
-        for (int ks = 0; ks < G::KS; ++ks) {
-            const int d = 32 * ks + 8 * lg;
-            u32x4 v = {0u, 0u, 0u, 0u};
-            if (hv) {
-                const uint16_t* src = d < R ? p.q_lat + (int64_t)b * p.q_lat_bs + (int64_t)h * p.q_lat_hs + d
-                                            : p.q_rope + (int64_t)b * p.q_rope_bs + (int64_t)h * p.q_rope_hs + (d - R);
-                v = *(const u32x4*)src;
-            }
-            qreg[ks][T] = __builtin_bit_cast(bf16x8, v);
-        }
-    }
-
-    // ---- staging of one sub-chunk: global -> registers
-    u32x4 stage[G::NCH];
-    auto load_sub = [&](int s) {
+    // ---- DMA of sub-chunk s into buffer s % NBUF: wave w issues the 1 KB
+    // blocks w, w+4, ...; lane l fills slot 64j + l of the buffer.  Every lane
+    // always loads (a row past the split or a -1 index reads a valid dummy row
+    // and is masked to P = 0 later), so each wave issues exactly NLD loads
+    // per sub-chunk and the vmcnt waits below are exact.
+    const int dummy_row = GATHER ? 0 : row_begin;
+    auto issue = [&](int s) {
+        char* base = cbuf + (s & (NBUF - 1)) * G::BUF;
         const int rbase = row_begin + s * ROWS;
 #pragma unroll
-        for (int k = 0; k < G::NCH; ++k) {
-            const int c = tid + THREADS * k;
-            const int row = c / G::CPR;
-            const int cc = c - row * G::CPR;
+        for (int k = 0; k < G::NLD; ++k) {
+            const int j = w + 4 * k;
+            const int slot = 64 * j + l;
+            const int row = slot / G::CPR;
+            const int pos = slot - row * G::CPR;
+            const int c = swz(pos, row);
             const int r = rbase + row;
-            int src_row = r;
-            bool ok = r < row_end;
+            int src_row = r < row_end ? r : dummy_row;
             if (GATHER) {
-                src_row = ok ? idx_s[r - row_begin] : -1;
-                ok = src_row >= 0;
+                const int v = r < row_end ? idx_s[r - row_begin] : -1;
+                src_row = v >= 0 ? v : dummy_row;
             }
-            u32x4 v = {0u, 0u, 0u, 0u};
-            if (ok) {
-                const uint16_t* src = cc < R / 8 ? lat + (int64_t)src_row * p.lat_rs + cc * 8
-                                                 : rop + (int64_t)src_row * p.rope_rs + (cc - R / 8) * 8;
-                v = __builtin_nontemporal_load((const u32x4*)src);
-            }
-            stage[k] = v;
-        }
-    };
-    auto store_sub = [&](int buf) {
-        char* base = cbuf + buf * G::BUF;
-#pragma unroll
-        for (int k = 0; k < G::NCH; ++k) {
-            const int c = tid + THREADS * k;
-            const int row = c / G::CPR;
-            const int cc = c - row * G::CPR;
-            *(u32x4*)(base + row * G::LROW + cc * 16) = stage[k];
+            const uint16_t* src = c < R / 8 ? lat + (int64_t)src_row * p.lat_rs + c * 8
+                                            : rop + (int64_t)src_row * p.rope_rs + (c - R / 8) * 8;
+            dma16(src, base + 1024 * j);
         }
     };
     auto row_valid = [&](int s, int r_local) -> bool {
@@ -159,147 +164,158 @@ __global__ void __launch_bounds__(THREADS, 1) mla_decode_split(DecodeParams p) {
         return true;
     };
 
+    // ---- Q of the head group, staged through the last buffer: "row" h of the
+    // buffer is head hg*32+h (q_lat ++ q_rope, the same 576/512-wide shape and
+    // swizzle as a cache row).  Heads past p.heads read head 0 (discarded).
+    {
+        char* base = cbuf + (NBUF - 1) * G::BUF;
+#pragma unroll
+        for (int k = 0; k < G::NLD; ++k) {
+            const int j = w + 4 * k;
+            const int slot = 64 * j + l;
+            const int row = slot / G::CPR;
+            const int pos = slot - row * G::CPR;
+            const int c = swz(pos, row);
+            const int h0 = hg * HG + row;
+            const int h = h0 < p.heads ? h0 : 0;
+            const uint16_t* src = c < R / 8 ? p.q_lat + (int64_t)b * p.q_lat_bs + (int64_t)h * p.q_lat_hs + c * 8
+                                            : p.q_rope + (int64_t)b * p.q_rope_bs + (int64_t)h * p.q_rope_hs + (c - R / 8) * 8;
+            dma16(src, base + 1024 * j);
+        }
+    }
+    for (int s = 0; s < NBUF - 1 && s < nsub; ++s) issue(s);
+    const int pro = min(nsub, NBUF - 1);  // sub-chunks issued after Q
+    if (pro >= 3)
+        wait_vmcnt<3 * G::NLD>();
+    else if (pro == 2)
+        wait_vmcnt<2 * G::NLD>();
+    else if (pro == 1)
+        wait_vmcnt<G::NLD>();
+    else
+        wait_vmcnt<0>();
+    lds_barrier();
+    // B-operand layout: head 16ht+lc, k = 32ks+8lg..+7
+    bf16x8 qreg[G::KS];
+    {
+        const int qrow = 16 * ht + lc;
+        const char* qp = cbuf + (NBUF - 1) * G::BUF + qrow * G::ROWB;
+#pragma unroll
+        for (int ks = 0; ks < G::KS; ++ks) qreg[ks] = *(const bf16x8*)(qp + 16 * swz(4 * ks + lg, qrow));
+    }
+    // the loop's first barrier orders these reads before buffer NBUF-1 is refilled
+
     f32x4 oacc[2][8];
 #pragma unroll
     for (int T = 0; T < 2; ++T)
 #pragma unroll
         for (int J = 0; J < 8; ++J) oacc[T][J] = f32x4{0.f, 0.f, 0.f, 0.f};
-    float m_run[2] = {NEG_INF, NEG_INF};
-    float l_run[2] = {0.f, 0.f};
+    float m_run = NEG_INF;  // running max (base 2) of head 16ht+lc
+    float l_run = 0.f;      // this lane's share of that head's running sum
 
-    if (nsub > 0) {
-        load_sub(0);
-        store_sub(0);
-        if (nsub > 1) load_sub(1);
-    }
-
-    const int arow = sigma_row(w, lc);
-    const int lbase = 8 * (lg >> 1) + (lg & 1);  // sigma base of this lane group
+    const int arow = sigma_row(rt, lc);
+    const int lbase = 8 * (lg >> 1) + (lg & 1);
+    const int kap = 8 * (2 * rt + (lg >> 1)) + 4 * (lg & 1);  // P k-slot of this lane's 4 rows
 
     for (int s = 0; s < nsub; ++s) {
-        const int cb = s & 1;
-        const char* cur = cbuf + cb * G::BUF;
-        __syncthreads();  // sub-chunk s in LDS; every wave is done with s-1
+        const char* cur = cbuf + (s & (NBUF - 1)) * G::BUF;
+        const int later = min(nsub - 1 - s, NBUF - 2);  // sub-chunks issued after s
+        if (later >= 2)
+            wait_vmcnt<2 * G::NLD>();
+        else if (later == 1)
+            wait_vmcnt<G::NLD>();
+        else
+            wait_vmcnt<0>();
+        lds_barrier();  // sub-chunk s landed for every wave; PV(s-1) done everywhere
+        if (s + NBUF - 1 < nsub) issue(s + NBUF - 1);
 
-        // ---- QK: S[16 rows][32 heads]
-        f32x4 sacc[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
-        const char* arow_p = cur + arow * G::LROW + 16 * lg;
+        // ---- QK: S[16 rows][16 heads]
+        f32x4 sacc = {0.f, 0.f, 0.f, 0.f};
+        const char* arow_p = cur + arow * G::ROWB;
 #pragma unroll
         for (int ks = 0; ks < G::KS; ++ks) {
-            const bf16x8 a = *(const bf16x8*)(arow_p + 64 * ks);
-            sacc[0] = mfma16(a, qreg[ks][0], sacc[0]);
-            sacc[1] = mfma16(a, qreg[ks][1], sacc[1]);
+            const bf16x8 a = *(const bf16x8*)(arow_p + 16 * swz(4 * ks + lg, arow));
+            sacc = mfma16(a, qreg[ks], sacc);
         }
+        float sv[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) sv[i] = row_valid(s, 16 * rt + lbase + 2 * i) ? sacc[i] * p.scale_log2 : NEG_INF;
+        float mx = fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3]));
+        mx = fmaxf(mx, __shfl_xor(mx, 16));
+        mx = fmaxf(mx, __shfl_xor(mx, 32));
+        if (lg == 0) red[w][lc] = mx;
+        lds_barrier();
 
-        float sv[2][4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const bool ok = row_valid(s, 16 * w + lbase + 2 * i);
-#pragma unroll
-            for (int T = 0; T < 2; ++T) sv[T][i] = ok ? sacc[T][i] * p.scale_log2 : NEG_INF;
-        }
-#pragma unroll
-        for (int T = 0; T < 2; ++T) {
-            float mx = fmaxf(fmaxf(sv[T][0], sv[T][1]), fmaxf(sv[T][2], sv[T][3]));
-            mx = fmaxf(mx, __shfl_xor(mx, 16));
-            mx = fmaxf(mx, __shfl_xor(mx, 32));
-            if (lg == 0) red[w][16 * T + lc] = mx;
-        }
-        __syncthreads();
-
-        // ---- running max, P, l
-        const int kso = w >> 1;  // k-step of the PV product this wave's rows fall in
-        const int kap = 8 * (2 * (w & 1) + (lg >> 1)) + 4 * (lg & 1);
-#pragma unroll
-        for (int T = 0; T < 2; ++T) {
-            const int hh = 16 * T + lc;
-            const float cm = fmaxf(fmaxf(red[0][hh], red[1][hh]), fmaxf(red[2][hh], red[3][hh]));
-            const float m_new = fmaxf(m_run[T], cm);
-            const float alpha = (m_run[T] == NEG_INF) ? 0.f : exp2f(m_run[T] - m_new);
-            m_run[T] = m_new;
+        // ---- running max, P (bf16, into LDS in PV k order), l
+        {
+            const float cm = fmaxf(red[w][lc], red[w ^ 2][lc]);
+            const float m_new = fmaxf(m_run, cm);
+            const float alpha = (m_run == NEG_INF) ? 0.f : exp2f(m_run - m_new);
+            m_run = m_new;
             float pv[4];
-            float psum = 0.f;
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                pv[i] = (m_new == NEG_INF) ? 0.f : exp2f(sv[T][i] - m_new);
-                psum += pv[i];
-            }
-            l_run[T] = l_run[T] * alpha + psum;
-            u32x2 pk = {pack_bf16x2(pv[0], pv[1]), pack_bf16x2(pv[2], pv[3])};
-            *(u32x2*)(pbuf + hh * PSTR + (32 * kso + kap) * 2) = pk;
-            if (w == 0 && lg == 0) alpha_s[hh] = alpha;
+            for (int i = 0; i < 4; ++i) pv[i] = (m_new == NEG_INF) ? 0.f : exp2f(sv[i] - m_new);
+            l_run = l_run * alpha + ((pv[0] + pv[1]) + (pv[2] + pv[3]));
+            const int hh = 16 * ht + lc;
+            *(u32x2*)(pbuf + hh * PSTR + kap * 2) = u32x2{pack_bf16x2(pv[0], pv[1]), pack_bf16x2(pv[2], pv[3])};
+            if (rt == 0 && lg == 0) alpha_s[hh] = alpha;
         }
-        __syncthreads();
+        lds_barrier();
 
-        // ---- PV: O[32 heads][128w .. 128w+127] += P[32][64] . C[64][...]
+        // ---- PV: O[32 heads][128w .. 128w+127] += P[32][32] . C[32][...]
+        bf16x8 pa[2];
 #pragma unroll
         for (int T = 0; T < 2; ++T) {
             const f32x4 a4 = *(const f32x4*)(alpha_s + 16 * T + 4 * lg);
 #pragma unroll
             for (int J = 0; J < 8; ++J) oacc[T][J] *= a4;
+            pa[T] = *(const bf16x8*)(pbuf + (16 * T + lc) * PSTR + 16 * lg);
         }
+        // k index 8lg + 4t + e of the product <-> row 16(lg/2) + 8(lg%2) + 2e + t
+        const int r0 = 16 * (lg >> 1) + 8 * (lg & 1) + 2 * (lc >> 2);
 #pragma unroll
-        for (int ks = 0; ks < 2; ++ks) {
-            bf16x8 pa[2];
+        for (int J = 0; J < 8; ++J) {
+            const int v0 = 128 * w + 16 * J;
+            bf16x8 bb;
+            if (TR) {
+                const int c = (v0 >> 3) + ((lc & 3) >> 1);
+                const int sub = 8 * (lc & 1);
+                const bf16x4 b0 = ds_read_tr16(cur + r0 * G::ROWB + 16 * swz(c, r0) + sub);
+                const bf16x4 b1 = ds_read_tr16(cur + (r0 + 1) * G::ROWB + 16 * swz(c, r0 + 1) + sub);
+                bb = __builtin_shufflevector(b0, b1, 0, 1, 2, 3, 4, 5, 6, 7);
+            } else {
+                uint16_t e[8];
+                const int c = (v0 + lc) >> 3;
+                const int sub = 2 * ((v0 + lc) & 7);
+                const int rr = 16 * (lg >> 1) + 8 * (lg & 1);
 #pragma unroll
-            for (int T = 0; T < 2; ++T)
-                pa[T] = *(const bf16x8*)(pbuf + (16 * T + lc) * PSTR + (32 * ks + 8 * lg) * 2);
-            // rho(g, t, e) = 16(g/2) + 8(g%2) + 2e + t  (row inside the k-step)
-            const int rrow = 32 * ks + 16 * (lg >> 1) + 8 * (lg & 1);
+                for (int t = 0; t < 2; ++t)
 #pragma unroll
-            for (int J = 0; J < 8; ++J) {
-                const int v0 = 128 * w + 16 * J;
-                bf16x8 bb;
-                if (TR) {
-                    const char* bp = cur + (rrow + 2 * (lc >> 2)) * G::LROW + (v0 + 4 * (lc & 3)) * 2;
-                    const bf16x4 b0 = ds_read_tr16(bp);
-                    const bf16x4 b1 = ds_read_tr16(bp + G::LROW);
-                    bb = __builtin_shufflevector(b0, b1, 0, 1, 2, 3, 4, 5, 6, 7);
-                } else {
-                    uint16_t e[8];
+                    for (int q = 0; q < 4; ++q) {
+                        const int row = rr + 2 * q + t;
+                        e[4 * t + q] = *(const uint16_t*)(cur + row * G::ROWB + 16 * swz(c, row) + sub);
+                    }
+                u32x4 u;
 #pragma unroll
-                    for (int t = 0; t < 2; ++t)
-#pragma unroll
-                        for (int q = 0; q < 4; ++q)
-                            e[4 * t + q] = *(const uint16_t*)(cur + (rrow + 2 * q + t) * G::LROW + (v0 + lc) * 2);
-                    u32x4 u;
-#pragma unroll
-                    for (int j = 0; j < 4; ++j) u[j] = e[2 * j] | ((uint32_t)e[2 * j + 1] << 16);
-                    bb = __builtin_bit_cast(bf16x8, u);
-                }
-#pragma unroll
-                for (int T = 0; T < 2; ++T) oacc[T][J] = mfma16(pa[T], bb, oacc[T][J]);
+                for (int j = 0; j < 4; ++j) u[j] = e[2 * j] | ((uint32_t)e[2 * j + 1] << 16);
+                bb = __builtin_bit_cast(bf16x8, u);
             }
-        }
-
-        // ---- next sub-chunk into the other buffer, prefetch the one after
-        if (s + 1 < nsub) {
-            store_sub(cb ^ 1);
-            if (s + 2 < nsub) load_sub(s + 2);
+#pragma unroll
+            for (int T = 0; T < 2; ++T) oacc[T][J] = mfma16(pa[T], bb, oacc[T][J]);
         }
     }
 
-    // ---- epilogue: l over lane groups and waves, then the partial record
-#pragma unroll
-    for (int T = 0; T < 2; ++T) {
-        l_run[T] += __shfl_xor(l_run[T], 16);
-        l_run[T] += __shfl_xor(l_run[T], 32);
-    }
-    __syncthreads();
-#pragma unroll
-    for (int T = 0; T < 2; ++T)
-        if (lg == 0) red[w][16 * T + lc] = l_run[T];
-    __syncthreads();
+    // ---- epilogue: l over lane groups and the two row tiles, then the record
+    l_run += __shfl_xor(l_run, 16);
+    l_run += __shfl_xor(l_run, 32);
+    lds_barrier();
+    if (lg == 0) red[w][lc] = l_run;
+    lds_barrier();
 
     const int64_t rec = (int64_t)unit * p.h_pad + hg * HG;
-    if (w == 0 && lg == 0) {
-#pragma unroll
-        for (int T = 0; T < 2; ++T) {
-            const int hh = 16 * T + lc;
-            const float lt = red[0][hh] + red[1][hh] + red[2][hh] + red[3][hh];
-            p.ws_ml[(rec + hh) * 2 + 0] = m_run[T];
-            p.ws_ml[(rec + hh) * 2 + 1] = lt;
-        }
+    if (rt == 0 && lg == 0) {
+        const int hh = 16 * ht + lc;
+        p.ws_ml[(rec + hh) * 2 + 0] = m_run;
+        p.ws_ml[(rec + hh) * 2 + 1] = red[w][lc] + red[w ^ 2][lc];
     }
 #pragma unroll
     for (int T = 0; T < 2; ++T)
@@ -311,37 +327,68 @@ __global__ void __launch_bounds__(THREADS, 1) mla_decode_split(DecodeParams p) {
         }
 }
 
-// Merge the split partials of one (batch, head): 256 threads, 2 blocks per
-// head cover the 512 output columns.
-__global__ void __launch_bounds__(256) mla_combine(CombineParams p) {
+// Merge the split partials: one wave per (batch, head, 256-column half).
+// The split weights are computed once into LDS; each lane then streams four
+// columns of every split with independent 16-byte loads.
+__global__ void __launch_bounds__(64) mla_combine(CombineParams p) {
+    __shared__ float wgt[MAX_COMBINE_SPLITS];
+    __shared__ float tot;
     const int bh = blockIdx.x;
     const int b = bh / p.heads;
     const int h = bh % p.heads;
-    const int v = blockIdx.y * 256 + threadIdx.x;
+    const int l = threadIdx.x;
+    const int64_t rec0 = (int64_t)b * p.splits * p.h_pad + h;
     float M = NEG_INF;
-    for (int s = 0; s < p.splits; ++s) M = fmaxf(M, p.ws_ml[(((int64_t)(b * p.splits + s)) * p.h_pad + h) * 2]);
+    for (int s = l; s < p.splits; s += 64) M = fmaxf(M, p.ws_ml[(rec0 + (int64_t)s * p.h_pad) * 2]);
+    M = wave_max(M);
     const bool any = M != NEG_INF;
-    float sink2 = NEG_INF;
-    if (p.sinks) {
-        sink2 = p.sinks[h] * LOG2E;
-        M = fmaxf(M, sink2);
-    }
-    float L = 0.f, acc = 0.f;
-    for (int s = 0; s < p.splits; ++s) {
-        const int64_t rec = ((int64_t)(b * p.splits + s)) * p.h_pad + h;
+    const float sink2 = p.sinks ? p.sinks[h] * LOG2E : NEG_INF;
+    M = fmaxf(M, sink2);
+    float L = 0.f;
+    for (int s = l; s < p.splits; s += 64) {
+        const int64_t rec = rec0 + (int64_t)s * p.h_pad;
         const float ms = p.ws_ml[rec * 2];
-        if (ms == NEG_INF) continue;
-        const float wgt = exp2f(ms - M);
-        L += p.ws_ml[rec * 2 + 1] * wgt;
-        acc += wgt * p.ws_o[rec * R + v];
+        const float wv = ms == NEG_INF ? 0.f : exp2f(ms - M);
+        wgt[s] = wv;
+        L += wv * p.ws_ml[rec * 2 + 1];
     }
+    L = wave_sum(L);
     if (p.sinks) L += exp2f(sink2 - M);
-    const float r = any ? acc / L : 0.f;
+    if (l == 0) tot = L;
+    __syncthreads();
+    const float inv = any ? 1.f / tot : 0.f;
+    const int v = blockIdx.y * 256 + 4 * l;
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+    const float* src = p.ws_o + rec0 * R + v;
+    const int64_t step = (int64_t)p.h_pad * R;
+    int s = 0;
+    for (; s + 4 <= p.splits; s += 4) {
+        const f32x4 x0 = *(const f32x4*)(src + (s + 0) * step);
+        const f32x4 x1 = *(const f32x4*)(src + (s + 1) * step);
+        const f32x4 x2 = *(const f32x4*)(src + (s + 2) * step);
+        const f32x4 x3 = *(const f32x4*)(src + (s + 3) * step);
+        // a split with no valid row has weight 0 and may hold non-finite
+        // scratch: select, never multiply it in
+        acc += wgt[s] != 0.f ? wgt[s] * x0 : f32x4{0.f, 0.f, 0.f, 0.f};
+        acc += wgt[s + 1] != 0.f ? wgt[s + 1] * x1 : f32x4{0.f, 0.f, 0.f, 0.f};
+        acc += wgt[s + 2] != 0.f ? wgt[s + 2] * x2 : f32x4{0.f, 0.f, 0.f, 0.f};
+        acc += wgt[s + 3] != 0.f ? wgt[s + 3] * x3 : f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+    for (; s < p.splits; ++s) {
+        const f32x4 x = *(const f32x4*)(src + s * step);
+        acc += wgt[s] != 0.f ? wgt[s] * x : f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+    acc *= inv;
     const int64_t o = (int64_t)b * p.out_bs + (int64_t)h * p.out_hs + v;
-    if (p.out_f32)
-        ((float*)p.out)[o] = r;
-    else
-        ((uint16_t*)p.out)[o] = f32_to_bf16_bits(r);
+    if (p.out_f32) {
+        float* out = (float*)p.out + o;
+        out[0] = acc[0];
+        out[1] = acc[1];
+        out[2] = acc[2];
+        out[3] = acc[3];
+    } else {
+        *(u32x2*)((uint16_t*)p.out + o) = u32x2{pack_bf16x2(acc[0], acc[1]), pack_bf16x2(acc[2], acc[3])};
+    }
 }
 
 template <int DR, bool GATHER, bool TR>
@@ -440,7 +487,7 @@ hipError_t launch_mla_decode(const DecodeParams& p, const CombineParams& cp, boo
     }
     if (e != hipSuccess) return e;
     if (events && (e = hipEventRecord(events[1], st)) != hipSuccess) return e;
-    hipLaunchKernelGGL(mla_combine, dim3(p.batch * p.heads, R / 256), dim3(256), 0, st, cp);
+    hipLaunchKernelGGL(mla_combine, dim3(p.batch * p.heads, R / 256), dim3(64), 0, st, cp);
     if ((e = hipGetLastError()) != hipSuccess) return e;
     if (events && (e = hipEventRecord(events[2], st)) != hipSuccess) return e;
     return hipSuccess;

@@ -9,7 +9,8 @@
 
 namespace mr {
 
-constexpr int MAX_GATHER_ROWS = 1024;  // index rows one decode workgroup stages in LDS
+constexpr int MAX_GATHER_ROWS = 1024;     // index rows one decode workgroup stages in LDS
+constexpr int MAX_COMBINE_SPLITS = 1024;  // context splits the combine kernel merges
 
 // ---------------------------------------------------------------- decode
 struct DecodeParams {
