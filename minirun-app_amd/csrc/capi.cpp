@@ -127,6 +127,9 @@ mr_status check_decode(const mr_mla_decode_args* a) {
         return fail(MR_INVALID_ARGUMENT, "mla decode: out strides must be multiples of 4, head stride >= 512");
     if (!aligned16(a->out)) return fail(MR_INVALID_ARGUMENT, "mla decode: out must be 16-byte aligned");
     if (a->num_splits < 0) return fail(MR_INVALID_ARGUMENT, "mla decode: num_splits must be >= 0");
+    // row offsets inside one batch element's cache are formed in 32 bits
+    if (double(a->n_ctx) * double(a->latent_row_stride) * 2.0 >= 4294967296.0)
+        return fail(MR_INVALID_SHAPE, "mla decode: n_ctx * latent_row_stride * 2 bytes must be < 4 GiB per batch element");
     return MR_OK;
 }
 

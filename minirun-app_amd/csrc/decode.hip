@@ -82,13 +82,20 @@ __device__ __forceinline__ void dma16(const void* src, const void* lds_dst_wave_
     asm volatile("global_load_lds_dwordx4 %0, off" ::"v"(src), "{m0}"(m0) : "memory");
 }
 
+// Same DMA with a wave-uniform 64-bit base in SGPRs and a 32-bit per-lane
+// byte offset: one VGPR per load instead of two.
+__device__ __forceinline__ void dma16_off(const void* sbase, uint32_t voff, const void* lds_dst_wave_base) {
+    const uint32_t m0 = (uint32_t)(uintptr_t)lds_dst_wave_base;
+    asm volatile("global_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase), "{m0}"(m0) : "memory");
+}
+
 template <int N>
 __device__ __forceinline__ void wait_vmcnt() {
     static_assert(N >= 0 && N < 64, "vmcnt range");
     asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
 
-template <int DR, bool GATHER, bool TR>
+template <int DR, bool GATHER, bool TR, bool PACKED>
 __global__ void __launch_bounds__(THREADS, 1) mla_decode_split(DecodeParams p) {
     using G = Geo<DR>;
     __shared__ __attribute__((aligned(1024))) char cbuf[NBUF * G::BUF];
@@ -135,10 +142,16 @@ __global__ void __launch_bounds__(THREADS, 1) mla_decode_split(DecodeParams p) {
     // always loads (a row past the split or a -1 index reads a valid dummy row
     // and is masked to P = 0 later), so each wave issues exactly NLD loads
     // per sub-chunk and the vmcnt waits below are exact.
-    const int dummy_row = GATHER ? 0 : row_begin;
+    // rows past the split read the split's last row (dense) or row 0
+    // (gather); both are valid memory and are masked to P = 0
+    const int dummy_row = GATHER ? 0 : row_end - 1;
+    // PACKED: rope key = latent + 512 with one row stride (the [P, 576] row),
+    // so every chunk of a row is (row base + 16 c) from one SGPR base.
+    const uint32_t rs_b = (uint32_t)(p.lat_rs * 2);
     auto issue = [&](int s) {
         char* base = cbuf + (s & (NBUF - 1)) * G::BUF;
         const int rbase = row_begin + s * ROWS;
+        const char* sb = (const char*)lat + (GATHER ? 0 : (int64_t)rbase * p.lat_rs * 2);
 #pragma unroll
         for (int k = 0; k < G::NLD; ++k) {
             const int j = w + 4 * k;
@@ -147,14 +160,19 @@ __global__ void __launch_bounds__(THREADS, 1) mla_decode_split(DecodeParams p) {
             const int pos = slot - row * G::CPR;
             const int c = swz(pos, row);
             const int r = rbase + row;
-            int src_row = r < row_end ? r : dummy_row;
+            int src_row = r < row_end ? r : dummy_row;  // >= rbase for a dense sub-chunk
             if (GATHER) {
                 const int v = r < row_end ? idx_s[r - row_begin] : -1;
                 src_row = v >= 0 ? v : dummy_row;
             }
-            const uint16_t* src = c < R / 8 ? lat + (int64_t)src_row * p.lat_rs + c * 8
-                                            : rop + (int64_t)src_row * p.rope_rs + (c - R / 8) * 8;
-            dma16(src, base + 1024 * j);
+            if (PACKED) {
+                const uint32_t off = (uint32_t)(GATHER ? src_row : src_row - rbase) * rs_b + 16u * (uint32_t)c;
+                dma16_off(sb, off, base + 1024 * j);
+            } else {
+                const uint16_t* src = c < R / 8 ? lat + (int64_t)src_row * p.lat_rs + c * 8
+                                                : rop + (int64_t)src_row * p.rope_rs + (c - R / 8) * 8;
+                dma16(src, base + 1024 * j);
+            }
         }
     };
     auto row_valid = [&](int s, int r_local) -> bool {
@@ -214,6 +232,21 @@ __global__ void __launch_bounds__(THREADS, 1) mla_decode_split(DecodeParams p) {
 
     const int arow = sigma_row(rt, lc);
     const int lbase = 8 * (lg >> 1) + (lg & 1);
+    int qk_off[4], qk_rope[2];
+    {
+        const int x = arow & 15, y = x >> 2, z0 = (lg ^ x) & 3;
+#pragma unroll
+        for (int u = 0; u < 4; ++u) qk_off[u] = 16 * z0 + 64 * (u ^ y);
+#pragma unroll
+        for (int u = 0; u < 2; ++u) qk_rope[u] = 1024 + 16 * z0 + 64 * (u ^ (y & 1));
+    }
+    // PV transposed reads: chunk (16w + 2J + h) of rows r0 / r0+1 (r0 even)
+    // sits at 256w + 32(J ^ z) + 16h (+16 flip on the odd row)
+    const int pv_r0 = 16 * (lg >> 1) + 8 * (lg & 1) + 2 * (lc >> 2);
+    const int pv_z32 = 32 * ((pv_r0 & 15) >> 1);
+    const int pv_h = (lc & 3) >> 1;
+    const int pv_b0 = pv_r0 * G::ROWB + 256 * w + 16 * pv_h + 8 * (lc & 1);
+    const int pv_b1 = (pv_r0 + 1) * G::ROWB + 256 * w + 16 * (pv_h ^ 1) + 8 * (lc & 1);
     const int kap = 8 * (2 * rt + (lg >> 1)) + 4 * (lg & 1);  // P k-slot of this lane's 4 rows
 
     for (int s = 0; s < nsub; ++s) {
@@ -228,13 +261,19 @@ __global__ void __launch_bounds__(THREADS, 1) mla_decode_split(DecodeParams p) {
         lds_barrier();  // sub-chunk s landed for every wave; PV(s-1) done everywhere
         if (s + NBUF - 1 < nsub) issue(s + NBUF - 1);
 
-        // ---- QK: S[16 rows][16 heads]
+        // ---- QK: S[16 rows][16 heads].  Chunk 4ks+lg of row `arow` sits at
+        // 16*((4ks+lg) ^ (arow&15)) = qk_off[ks%4] + 256*(ks/4) (latent) and
+        // qk_rope[ks-16] (rope): immediates after four base registers.
         f32x4 sacc = {0.f, 0.f, 0.f, 0.f};
-        const char* arow_p = cur + arow * G::ROWB;
+        {
+            const char* rp = cur + arow * G::ROWB;
+            bf16x8 a[G::KS];
 #pragma unroll
-        for (int ks = 0; ks < G::KS; ++ks) {
-            const bf16x8 a = *(const bf16x8*)(arow_p + 16 * swz(4 * ks + lg, arow));
-            sacc = mfma16(a, qreg[ks], sacc);
+            for (int ks = 0; ks < 16; ++ks) a[ks] = *(const bf16x8*)(rp + qk_off[ks & 3] + 256 * (ks >> 2));
+#pragma unroll
+            for (int ks = 16; ks < G::KS; ++ks) a[ks] = *(const bf16x8*)(rp + qk_rope[ks - 16]);
+#pragma unroll
+            for (int ks = 0; ks < G::KS; ++ks) sacc = mfma16(a[ks], qreg[ks], sacc);
         }
         float sv[4];
 #pragma unroll
@@ -271,18 +310,24 @@ __global__ void __launch_bounds__(THREADS, 1) mla_decode_split(DecodeParams p) {
             pa[T] = *(const bf16x8*)(pbuf + (16 * T + lc) * PSTR + 16 * lg);
         }
         // k index 8lg + 4t + e of the product <-> row 16(lg/2) + 8(lg%2) + 2e + t
-        const int r0 = 16 * (lg >> 1) + 8 * (lg & 1) + 2 * (lc >> 2);
+        if (TR) {
+            bf16x4 b0[8], b1[8];
 #pragma unroll
-        for (int J = 0; J < 8; ++J) {
-            const int v0 = 128 * w + 16 * J;
-            bf16x8 bb;
-            if (TR) {
-                const int c = (v0 >> 3) + ((lc & 3) >> 1);
-                const int sub = 8 * (lc & 1);
-                const bf16x4 b0 = ds_read_tr16(cur + r0 * G::ROWB + 16 * swz(c, r0) + sub);
-                const bf16x4 b1 = ds_read_tr16(cur + (r0 + 1) * G::ROWB + 16 * swz(c, r0 + 1) + sub);
-                bb = __builtin_shufflevector(b0, b1, 0, 1, 2, 3, 4, 5, 6, 7);
-            } else {
+            for (int J = 0; J < 8; ++J) {
+                const int o = (32 * J) ^ pv_z32;
+                b0[J] = ds_read_tr16(cur + pv_b0 + o);
+                b1[J] = ds_read_tr16(cur + pv_b1 + o);
+            }
+#pragma unroll
+            for (int J = 0; J < 8; ++J) {
+                const bf16x8 bb = __builtin_shufflevector(b0[J], b1[J], 0, 1, 2, 3, 4, 5, 6, 7);
+#pragma unroll
+                for (int T = 0; T < 2; ++T) oacc[T][J] = mfma16(pa[T], bb, oacc[T][J]);
+            }
+        } else {
+#pragma unroll
+            for (int J = 0; J < 8; ++J) {
+                const int v0 = 128 * w + 16 * J;
                 uint16_t e[8];
                 const int c = (v0 + lc) >> 3;
                 const int sub = 2 * ((v0 + lc) & 7);
@@ -297,10 +342,10 @@ __global__ void __launch_bounds__(THREADS, 1) mla_decode_split(DecodeParams p) {
                 u32x4 u;
 #pragma unroll
                 for (int j = 0; j < 4; ++j) u[j] = e[2 * j] | ((uint32_t)e[2 * j + 1] << 16);
-                bb = __builtin_bit_cast(bf16x8, u);
-            }
+                const bf16x8 bb = __builtin_bit_cast(bf16x8, u);
 #pragma unroll
-            for (int T = 0; T < 2; ++T) oacc[T][J] = mfma16(pa[T], bb, oacc[T][J]);
+                for (int T = 0; T < 2; ++T) oacc[T][J] = mfma16(pa[T], bb, oacc[T][J]);
+            }
         }
     }
 
@@ -327,25 +372,32 @@ __global__ void __launch_bounds__(THREADS, 1) mla_decode_split(DecodeParams p) {
         }
 }
 
-// Merge the split partials: one wave per (batch, head, 256-column half).
-// The split weights are computed once into LDS; each lane then streams four
-// columns of every split with independent 16-byte loads.
-__global__ void __launch_bounds__(64) mla_combine(CombineParams p) {
+// Merge the split partials: one 256-thread block per (batch, head, 256-column
+// half).  Split weights are computed once into LDS; wave q then streams the
+// splits q, q+4, ... with independent 16-byte loads (four columns per lane)
+// and the four waves' sums are added through LDS.
+__global__ void __launch_bounds__(256) mla_combine(CombineParams p) {
     __shared__ float wgt[MAX_COMBINE_SPLITS];
-    __shared__ float tot;
+    __shared__ float red_w[4];
+    __shared__ f32x4 part[3][64];
     const int bh = blockIdx.x;
     const int b = bh / p.heads;
     const int h = bh % p.heads;
-    const int l = threadIdx.x;
+    const int tid = threadIdx.x;
+    const int q = tid >> 6;
+    const int l = tid & 63;
     const int64_t rec0 = (int64_t)b * p.splits * p.h_pad + h;
     float M = NEG_INF;
-    for (int s = l; s < p.splits; s += 64) M = fmaxf(M, p.ws_ml[(rec0 + (int64_t)s * p.h_pad) * 2]);
+    for (int s = tid; s < p.splits; s += 256) M = fmaxf(M, p.ws_ml[(rec0 + (int64_t)s * p.h_pad) * 2]);
     M = wave_max(M);
+    if (l == 0) red_w[q] = M;
+    __syncthreads();
+    M = fmaxf(fmaxf(red_w[0], red_w[1]), fmaxf(red_w[2], red_w[3]));
     const bool any = M != NEG_INF;
     const float sink2 = p.sinks ? p.sinks[h] * LOG2E : NEG_INF;
     M = fmaxf(M, sink2);
     float L = 0.f;
-    for (int s = l; s < p.splits; s += 64) {
+    for (int s = tid; s < p.splits; s += 256) {
         const int64_t rec = rec0 + (int64_t)s * p.h_pad;
         const float ms = p.ws_ml[rec * 2];
         const float wv = ms == NEG_INF ? 0.f : exp2f(ms - M);
@@ -353,39 +405,43 @@ __global__ void __launch_bounds__(64) mla_combine(CombineParams p) {
         L += wv * p.ws_ml[rec * 2 + 1];
     }
     L = wave_sum(L);
-    if (p.sinks) L += exp2f(sink2 - M);
-    if (l == 0) tot = L;
     __syncthreads();
-    const float inv = any ? 1.f / tot : 0.f;
+    if (l == 0) red_w[q] = L;
+    __syncthreads();
+    L = (red_w[0] + red_w[1]) + (red_w[2] + red_w[3]);
+    if (p.sinks) L += exp2f(sink2 - M);
     const int v = blockIdx.y * 256 + 4 * l;
-    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
     const float* src = p.ws_o + rec0 * R + v;
     const int64_t step = (int64_t)p.h_pad * R;
-    int s = 0;
-    for (; s + 4 <= p.splits; s += 4) {
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+    const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
+    int s = q;
+    // a split with no valid row has weight 0 and may hold non-finite
+    // scratch: select, never multiply it in
+    for (; s + 12 < p.splits; s += 16) {
         const f32x4 x0 = *(const f32x4*)(src + (s + 0) * step);
-        const f32x4 x1 = *(const f32x4*)(src + (s + 1) * step);
-        const f32x4 x2 = *(const f32x4*)(src + (s + 2) * step);
-        const f32x4 x3 = *(const f32x4*)(src + (s + 3) * step);
-        // a split with no valid row has weight 0 and may hold non-finite
-        // scratch: select, never multiply it in
-        acc += wgt[s] != 0.f ? wgt[s] * x0 : f32x4{0.f, 0.f, 0.f, 0.f};
-        acc += wgt[s + 1] != 0.f ? wgt[s + 1] * x1 : f32x4{0.f, 0.f, 0.f, 0.f};
-        acc += wgt[s + 2] != 0.f ? wgt[s + 2] * x2 : f32x4{0.f, 0.f, 0.f, 0.f};
-        acc += wgt[s + 3] != 0.f ? wgt[s + 3] * x3 : f32x4{0.f, 0.f, 0.f, 0.f};
+        const f32x4 x1 = *(const f32x4*)(src + (s + 4) * step);
+        const f32x4 x2 = *(const f32x4*)(src + (s + 8) * step);
+        const f32x4 x3 = *(const f32x4*)(src + (s + 12) * step);
+        acc += wgt[s] != 0.f ? wgt[s] * x0 : zero;
+        acc += wgt[s + 4] != 0.f ? wgt[s + 4] * x1 : zero;
+        acc += wgt[s + 8] != 0.f ? wgt[s + 8] * x2 : zero;
+        acc += wgt[s + 12] != 0.f ? wgt[s + 12] * x3 : zero;
     }
-    for (; s < p.splits; ++s) {
+    for (; s < p.splits; s += 4) {
         const f32x4 x = *(const f32x4*)(src + s * step);
-        acc += wgt[s] != 0.f ? wgt[s] * x : f32x4{0.f, 0.f, 0.f, 0.f};
+        acc += wgt[s] != 0.f ? wgt[s] * x : zero;
     }
-    acc *= inv;
+    if (q > 0) part[q - 1][l] = acc;
+    __syncthreads();
+    if (q != 0) return;
+    acc += part[0][l];
+    acc += part[1][l];
+    acc += part[2][l];
+    acc *= any ? 1.f / L : 0.f;
     const int64_t o = (int64_t)b * p.out_bs + (int64_t)h * p.out_hs + v;
     if (p.out_f32) {
-        float* out = (float*)p.out + o;
-        out[0] = acc[0];
-        out[1] = acc[1];
-        out[2] = acc[2];
-        out[3] = acc[3];
+        *(f32x4*)((float*)p.out + o) = acc;
     } else {
         *(u32x2*)((uint16_t*)p.out + o) = u32x2{pack_bf16x2(acc[0], acc[1]), pack_bf16x2(acc[2], acc[3])};
     }
@@ -393,7 +449,11 @@ __global__ void __launch_bounds__(64) mla_combine(CombineParams p) {
 
 template <int DR, bool GATHER, bool TR>
 hipError_t launch_split(const DecodeParams& p, int grid, hipStream_t st) {
-    hipLaunchKernelGGL((mla_decode_split<DR, GATHER, TR>), dim3(grid), dim3(THREADS), 0, st, p);
+    const bool packed = DR == 0 || (p.rope == p.latent + R && p.rope_rs == p.lat_rs && p.rope_bs == p.lat_bs);
+    if (packed)
+        hipLaunchKernelGGL((mla_decode_split<DR, GATHER, TR, true>), dim3(grid), dim3(THREADS), 0, st, p);
+    else
+        hipLaunchKernelGGL((mla_decode_split<DR, GATHER, TR, false>), dim3(grid), dim3(THREADS), 0, st, p);
     return hipGetLastError();
 }
 
@@ -487,7 +547,7 @@ hipError_t launch_mla_decode(const DecodeParams& p, const CombineParams& cp, boo
     }
     if (e != hipSuccess) return e;
     if (events && (e = hipEventRecord(events[1], st)) != hipSuccess) return e;
-    hipLaunchKernelGGL(mla_combine, dim3(p.batch * p.heads, R / 256), dim3(64), 0, st, cp);
+    hipLaunchKernelGGL(mla_combine, dim3(p.batch * p.heads, R / 256), dim3(256), 0, st, cp);
     if ((e = hipGetLastError()) != hipSuccess) return e;
     if (events && (e = hipEventRecord(events[2], st)) != hipSuccess) return e;
     return hipSuccess;
