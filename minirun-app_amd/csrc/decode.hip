@@ -95,6 +95,8 @@ __device__ __forceinline__ void wait_vmcnt() {
     asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
 
+constexpr float TAU = 8.f;  // log2 headroom before the running max is raised
+
 template <int DR, bool GATHER, bool TR, bool PACKED>
 __global__ void __launch_bounds__(THREADS, 1) mla_decode_split(DecodeParams p) {
     using G = Geo<DR>;
@@ -102,6 +104,7 @@ __global__ void __launch_bounds__(THREADS, 1) mla_decode_split(DecodeParams p) {
     __shared__ __attribute__((aligned(16))) char pbuf[HG * PSTR];
     __shared__ float red[4][16];
     __shared__ __attribute__((aligned(16))) float alpha_s[HG];
+    __shared__ int flag_s[2];
     __shared__ int32_t idx_s[GATHER ? MAX_GATHER_ROWS : 1];
 
     const int bid = blockIdx.x;
@@ -137,71 +140,65 @@ __global__ void __launch_bounds__(THREADS, 1) mla_decode_split(DecodeParams p) {
         __syncthreads();
     }
 
-    // ---- DMA of sub-chunk s into buffer s % NBUF: wave w issues the 1 KB
-    // blocks w, w+4, ...; lane l fills slot 64j + l of the buffer.  Every lane
-    // always loads (a row past the split or a -1 index reads a valid dummy row
-    // and is masked to P = 0 later), so each wave issues exactly NLD loads
-    // per sub-chunk and the vmcnt waits below are exact.
-    // rows past the split read the split's last row (dense) or row 0
-    // (gather); both are valid memory and are masked to P = 0
-    const int dummy_row = GATHER ? 0 : row_end - 1;
-    // PACKED: rope key = latent + 512 with one row stride (the [P, 576] row),
-    // so every chunk of a row is (row base + 16 c) from one SGPR base.
+    // ---- DMA geometry, loop invariant: load k of this lane fills slot
+    // 64(w+4k)+l, i.e. chunk dma_c[k] of row dma_row[k] of a sub-chunk.
+    int dma_row[G::NLD], dma_c16[G::NLD];
+#pragma unroll
+    for (int k = 0; k < G::NLD; ++k) {
+        const int slot = 64 * (w + 4 * k) + l;
+        dma_row[k] = slot / G::CPR;
+        dma_c16[k] = 16 * swz(slot - dma_row[k] * G::CPR, dma_row[k]);
+    }
     const uint32_t rs_b = (uint32_t)(p.lat_rs * 2);
-    auto issue = [&](int s) {
-        char* base = cbuf + (s & (NBUF - 1)) * G::BUF;
+    // Every lane always loads: a row past the split reads the split's last
+    // row (dense) or row 0 (gather) and is masked to P = 0, so each wave issues
+    // exactly NLD loads per sub-chunk and the vmcnt waits are exact.
+    auto issue = [&](int s, char* base) {
         const int rbase = row_begin + s * ROWS;
-        const char* sb = (const char*)lat + (GATHER ? 0 : (int64_t)rbase * p.lat_rs * 2);
+        const bool tail = rbase + ROWS > row_end;
 #pragma unroll
         for (int k = 0; k < G::NLD; ++k) {
-            const int j = w + 4 * k;
-            const int slot = 64 * j + l;
-            const int row = slot / G::CPR;
-            const int pos = slot - row * G::CPR;
-            const int c = swz(pos, row);
-            const int r = rbase + row;
-            int src_row = r < row_end ? r : dummy_row;  // >= rbase for a dense sub-chunk
+            int rr = dma_row[k];  // row relative to rbase
+            int src_row;
             if (GATHER) {
-                const int v = r < row_end ? idx_s[r - row_begin] : -1;
-                src_row = v >= 0 ? v : dummy_row;
+                const int v = (rbase + rr < row_end) ? idx_s[rbase + rr - row_begin] : -1;
+                src_row = v >= 0 ? v : 0;
+            } else {
+                if (tail) rr = min(rr, row_end - 1 - rbase);
+                src_row = rbase + rr;
             }
             if (PACKED) {
-                const uint32_t off = (uint32_t)(GATHER ? src_row : src_row - rbase) * rs_b + 16u * (uint32_t)c;
-                dma16_off(sb, off, base + 1024 * j);
+                if (GATHER)
+                    dma16_off(lat, (uint32_t)src_row * rs_b + (uint32_t)dma_c16[k], base + 1024 * (w + 4 * k));
+                else
+                    dma16_off((const char*)lat + (int64_t)rbase * rs_b, (uint32_t)rr * rs_b + (uint32_t)dma_c16[k],
+                              base + 1024 * (w + 4 * k));
             } else {
+                const int c = dma_c16[k] >> 4;
                 const uint16_t* src = c < R / 8 ? lat + (int64_t)src_row * p.lat_rs + c * 8
                                                 : rop + (int64_t)src_row * p.rope_rs + (c - R / 8) * 8;
-                dma16(src, base + 1024 * j);
+                dma16(src, base + 1024 * (w + 4 * k));
             }
         }
     };
-    auto row_valid = [&](int s, int r_local) -> bool {
-        const int r = row_begin + s * ROWS + r_local;
-        if (r >= row_end) return false;
-        if (GATHER) return idx_s[r - row_begin] >= 0;
-        return true;
-    };
 
     // ---- Q of the head group, staged through the last buffer: "row" h of the
-    // buffer is head hg*32+h (q_lat ++ q_rope, the same 576/512-wide shape and
-    // swizzle as a cache row).  Heads past p.heads read head 0 (discarded).
+    // buffer is head hg*32+h (q_lat ++ q_rope, the shape and swizzle of a cache
+    // row).  Heads past p.heads read head 0 (their outputs are discarded).
     {
         char* base = cbuf + (NBUF - 1) * G::BUF;
 #pragma unroll
         for (int k = 0; k < G::NLD; ++k) {
-            const int j = w + 4 * k;
-            const int slot = 64 * j + l;
-            const int row = slot / G::CPR;
-            const int pos = slot - row * G::CPR;
-            const int c = swz(pos, row);
+            const int row = dma_row[k];
+            const int c = dma_c16[k] >> 4;
             const int h0 = hg * HG + row;
             const int h = h0 < p.heads ? h0 : 0;
             const uint16_t* src = c < R / 8 ? p.q_lat + (int64_t)b * p.q_lat_bs + (int64_t)h * p.q_lat_hs + c * 8
                                             : p.q_rope + (int64_t)b * p.q_rope_bs + (int64_t)h * p.q_rope_hs + (c - R / 8) * 8;
-            dma16(src, base + 1024 * j);
+            dma16(src, base + 1024 * (w + 4 * k));
         }
     }
-    for (int s = 0; s < NBUF - 1 && s < nsub; ++s) issue(s);
+    for (int s = 0; s < NBUF - 1 && s < nsub; ++s) issue(s, cbuf + s * G::BUF);
     const int pro = min(nsub, NBUF - 1);  // sub-chunks issued after Q
     if (pro >= 3)
         wait_vmcnt<3 * G::NLD>();
@@ -212,45 +209,55 @@ __global__ void __launch_bounds__(THREADS, 1) mla_decode_split(DecodeParams p) {
     else
         wait_vmcnt<0>();
     lds_barrier();
-    // B-operand layout: head 16ht+lc, k = 32ks+8lg..+7
-    bf16x8 qreg[G::KS];
+    bf16x8 qreg[G::KS];  // B operand: head 16ht+lc, k = 32ks+8lg..+7
     {
         const int qrow = 16 * ht + lc;
         const char* qp = cbuf + (NBUF - 1) * G::BUF + qrow * G::ROWB;
 #pragma unroll
         for (int ks = 0; ks < G::KS; ++ks) qreg[ks] = *(const bf16x8*)(qp + 16 * swz(4 * ks + lg, qrow));
     }
-    // the loop's first barrier orders these reads before buffer NBUF-1 is refilled
+    // (the first loop barrier orders these reads before buffer NBUF-1 refills)
 
     f32x4 oacc[2][8];
 #pragma unroll
     for (int T = 0; T < 2; ++T)
 #pragma unroll
         for (int J = 0; J < 8; ++J) oacc[T][J] = f32x4{0.f, 0.f, 0.f, 0.f};
-    float m_run = NEG_INF;  // running max (base 2) of head 16ht+lc
-    float l_run = 0.f;      // this lane's share of that head's running sum
+    float m_run = NEG_INF;  // reference max (base 2) of head 16ht+lc; scores may exceed it by < TAU
+    float l_run = 0.f;      // this lane's share of that head's sum
 
+    // QK A operand: chunk 4ks+lg of row `arow` is at
+    // 16*((4ks+lg) ^ (arow&15)) = qk_off[ks%4] + 256*(ks/4) (latent) and qk_rope[ks-16].
     const int arow = sigma_row(rt, lc);
     const int lbase = 8 * (lg >> 1) + (lg & 1);
     int qk_off[4], qk_rope[2];
     {
         const int x = arow & 15, y = x >> 2, z0 = (lg ^ x) & 3;
 #pragma unroll
-        for (int u = 0; u < 4; ++u) qk_off[u] = 16 * z0 + 64 * (u ^ y);
+        for (int u = 0; u < 4; ++u) qk_off[u] = arow * G::ROWB + 16 * z0 + 64 * (u ^ y);
 #pragma unroll
-        for (int u = 0; u < 2; ++u) qk_rope[u] = 1024 + 16 * z0 + 64 * (u ^ (y & 1));
+        for (int u = 0; u < 2; ++u) qk_rope[u] = arow * G::ROWB + 1024 + 16 * z0 + 64 * (u ^ (y & 1));
     }
-    // PV transposed reads: chunk (16w + 2J + h) of rows r0 / r0+1 (r0 even)
-    // sits at 256w + 32(J ^ z) + 16h (+16 flip on the odd row)
-    const int pv_r0 = 16 * (lg >> 1) + 8 * (lg & 1) + 2 * (lc >> 2);
-    const int pv_z32 = 32 * ((pv_r0 & 15) >> 1);
-    const int pv_h = (lc & 3) >> 1;
-    const int pv_b0 = pv_r0 * G::ROWB + 256 * w + 16 * pv_h + 8 * (lc & 1);
-    const int pv_b1 = (pv_r0 + 1) * G::ROWB + 256 * w + 16 * (pv_h ^ 1) + 8 * (lc & 1);
+    // PV transposed reads: chunk (16w + 2J + h) of rows r0 / r0+1 (r0 even) is
+    // at 256w + 32(J ^ z) + 16h (+16 flipped on the odd row)
+    int tr0[8], tr1[8];
+    {
+        const int r0 = 16 * (lg >> 1) + 8 * (lg & 1) + 2 * (lc >> 2);
+        const int z32 = 32 * ((r0 & 15) >> 1);
+        const int h = (lc & 3) >> 1;
+        const int b0 = r0 * G::ROWB + 256 * w + 16 * h + 8 * (lc & 1);
+        const int b1 = (r0 + 1) * G::ROWB + 256 * w + 16 * (h ^ 1) + 8 * (lc & 1);
+#pragma unroll
+        for (int J = 0; J < 8; ++J) {
+            tr0[J] = b0 + ((32 * J) ^ z32);
+            tr1[J] = b1 + ((32 * J) ^ z32);
+        }
+    }
     const int kap = 8 * (2 * rt + (lg >> 1)) + 4 * (lg & 1);  // P k-slot of this lane's 4 rows
+    const float scale2 = p.scale_log2;
 
-    for (int s = 0; s < nsub; ++s) {
-        const char* cur = cbuf + (s & (NBUF - 1)) * G::BUF;
+    auto step = [&](int s, const char* cur) {
+        // ---- wait for sub-chunk s, then refill the buffer freed by s-1
         const int later = min(nsub - 1 - s, NBUF - 2);  // sub-chunks issued after s
         if (later >= 2)
             wait_vmcnt<2 * G::NLD>();
@@ -258,65 +265,87 @@ __global__ void __launch_bounds__(THREADS, 1) mla_decode_split(DecodeParams p) {
             wait_vmcnt<G::NLD>();
         else
             wait_vmcnt<0>();
-        lds_barrier();  // sub-chunk s landed for every wave; PV(s-1) done everywhere
-        if (s + NBUF - 1 < nsub) issue(s + NBUF - 1);
+        lds_barrier();  // s landed for every wave; PV(s-1) done everywhere
+        if (s + NBUF - 1 < nsub) {
+            const int sn = s + NBUF - 1;
+            issue(sn, cbuf + (sn & (NBUF - 1)) * G::BUF);
+        }
 
-        // ---- QK: S[16 rows][16 heads].  Chunk 4ks+lg of row `arow` sits at
-        // 16*((4ks+lg) ^ (arow&15)) = qk_off[ks%4] + 256*(ks/4) (latent) and
-        // qk_rope[ks-16] (rope): immediates after four base registers.
+        // ---- QK: S[16 rows][16 heads]
         f32x4 sacc = {0.f, 0.f, 0.f, 0.f};
         {
-            const char* rp = cur + arow * G::ROWB;
             bf16x8 a[G::KS];
 #pragma unroll
-            for (int ks = 0; ks < 16; ++ks) a[ks] = *(const bf16x8*)(rp + qk_off[ks & 3] + 256 * (ks >> 2));
+            for (int ks = 0; ks < 16; ++ks) a[ks] = *(const bf16x8*)(cur + qk_off[ks & 3] + 256 * (ks >> 2));
 #pragma unroll
-            for (int ks = 16; ks < G::KS; ++ks) a[ks] = *(const bf16x8*)(rp + qk_rope[ks - 16]);
+            for (int ks = 16; ks < G::KS; ++ks) a[ks] = *(const bf16x8*)(cur + qk_rope[ks - 16]);
 #pragma unroll
             for (int ks = 0; ks < G::KS; ++ks) sacc = mfma16(a[ks], qreg[ks], sacc);
         }
         float sv[4];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) sv[i] = row_valid(s, 16 * rt + lbase + 2 * i) ? sacc[i] * p.scale_log2 : NEG_INF;
+        for (int i = 0; i < 4; ++i) sv[i] = sacc[i] * scale2;
+        const int rbase = row_begin + s * ROWS;
+        if (GATHER || rbase + ROWS > row_end) {  // mask rows past the split / -1 entries
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int r = rbase + 16 * rt + lbase + 2 * i;
+                bool ok = r < row_end;
+                if (GATHER) ok = ok && idx_s[r - row_begin] >= 0;
+                if (!ok) sv[i] = NEG_INF;
+            }
+        }
         float mx = fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3]));
         mx = fmaxf(mx, __shfl_xor(mx, 16));
         mx = fmaxf(mx, __shfl_xor(mx, 32));
         if (lg == 0) red[w][lc] = mx;
         lds_barrier();
 
-        // ---- running max, P (bf16, into LDS in PV k order), l
-        {
-            const float cm = fmaxf(red[w][lc], red[w ^ 2][lc]);
-            const float m_new = fmaxf(m_run, cm);
-            const float alpha = (m_run == NEG_INF) ? 0.f : exp2f(m_run - m_new);
-            m_run = m_new;
-            float pv[4];
+        // ---- reference max: raised only when a score passes it by TAU (or
+        // on the first valid rows), so O is rarely rescaled; P <= 2^TAU.
+        const float cm = fmaxf(red[w][lc], red[w ^ 2][lc]);
+        const bool raise = cm > m_run + TAU;  // false while cm is -inf
+        const float m_new = raise ? cm : m_run;
+        const float alpha = raise ? exp2f(m_run - m_new) : 1.f;  // 0 when m_run was -inf
+        m_run = m_new;
+        float pv[4];
 #pragma unroll
-            for (int i = 0; i < 4; ++i) pv[i] = (m_new == NEG_INF) ? 0.f : exp2f(sv[i] - m_new);
-            l_run = l_run * alpha + ((pv[0] + pv[1]) + (pv[2] + pv[3]));
+        for (int i = 0; i < 4; ++i) pv[i] = (m_new == NEG_INF) ? 0.f : __builtin_amdgcn_exp2f(sv[i] - m_new);
+        l_run = l_run * alpha + ((pv[0] + pv[1]) + (pv[2] + pv[3]));
+        {
+            typedef __bf16 bf16x2v __attribute__((ext_vector_type(2)));
+            const bf16x2v lo = {(__bf16)pv[0], (__bf16)pv[1]};
+            const bf16x2v hi = {(__bf16)pv[2], (__bf16)pv[3]};
             const int hh = 16 * ht + lc;
-            *(u32x2*)(pbuf + hh * PSTR + kap * 2) = u32x2{pack_bf16x2(pv[0], pv[1]), pack_bf16x2(pv[2], pv[3])};
-            if (rt == 0 && lg == 0) alpha_s[hh] = alpha;
+            *(u32x2*)(pbuf + hh * PSTR + kap * 2) =
+                u32x2{__builtin_bit_cast(uint32_t, lo), __builtin_bit_cast(uint32_t, hi)};
+            if (rt == 0) {
+                if (lg == 0) alpha_s[hh] = alpha;
+                const bool any = __builtin_amdgcn_ballot_w64(raise) != 0;
+                if (l == 0) flag_s[ht] = any;
+            }
         }
         lds_barrier();
 
         // ---- PV: O[32 heads][128w .. 128w+127] += P[32][32] . C[32][...]
+        if (flag_s[0] | flag_s[1]) {  // some head's reference max moved: rescale
+#pragma unroll
+            for (int T = 0; T < 2; ++T) {
+                const f32x4 a4 = *(const f32x4*)(alpha_s + 16 * T + 4 * lg);
+#pragma unroll
+                for (int J = 0; J < 8; ++J) oacc[T][J] *= a4;
+            }
+        }
         bf16x8 pa[2];
 #pragma unroll
-        for (int T = 0; T < 2; ++T) {
-            const f32x4 a4 = *(const f32x4*)(alpha_s + 16 * T + 4 * lg);
-#pragma unroll
-            for (int J = 0; J < 8; ++J) oacc[T][J] *= a4;
-            pa[T] = *(const bf16x8*)(pbuf + (16 * T + lc) * PSTR + 16 * lg);
-        }
+        for (int T = 0; T < 2; ++T) pa[T] = *(const bf16x8*)(pbuf + (16 * T + lc) * PSTR + 16 * lg);
         // k index 8lg + 4t + e of the product <-> row 16(lg/2) + 8(lg%2) + 2e + t
         if (TR) {
             bf16x4 b0[8], b1[8];
 #pragma unroll
             for (int J = 0; J < 8; ++J) {
-                const int o = (32 * J) ^ pv_z32;
-                b0[J] = ds_read_tr16(cur + pv_b0 + o);
-                b1[J] = ds_read_tr16(cur + pv_b1 + o);
+                b0[J] = ds_read_tr16(cur + tr0[J]);
+                b1[J] = ds_read_tr16(cur + tr1[J]);
             }
 #pragma unroll
             for (int J = 0; J < 8; ++J) {
@@ -347,13 +376,30 @@ __global__ void __launch_bounds__(THREADS, 1) mla_decode_split(DecodeParams p) {
                 for (int T = 0; T < 2; ++T) oacc[T][J] = mfma16(pa[T], bb, oacc[T][J]);
             }
         }
+    };
+
+    // four copies of the step, one per buffer, so buffer offsets are constants
+    for (int s0 = 0; s0 < nsub; s0 += NBUF) {
+        step(s0, cbuf);
+        if (s0 + 1 < nsub) step(s0 + 1, cbuf + G::BUF);
+        if (s0 + 2 < nsub) step(s0 + 2, cbuf + 2 * G::BUF);
+        if (s0 + 3 < nsub) step(s0 + 3, cbuf + 3 * G::BUF);
     }
 
-    // ---- epilogue: l over lane groups and the two row tiles, then the record
+    // ---- epilogue: l over lane groups and the two row tiles
     l_run += __shfl_xor(l_run, 16);
     l_run += __shfl_xor(l_run, 32);
-    lds_barrier();
+    lds_barrier();  // every wave is past its last LDS read of the buffers
     if (lg == 0) red[w][lc] = l_run;
+    // O through LDS (the sub-chunk buffers are free): [32 heads][512] fp32,
+    // then 16-byte coalesced stores of the partial record
+    float* ostage = (float*)cbuf;
+#pragma unroll
+    for (int T = 0; T < 2; ++T)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int J = 0; J < 8; ++J) ostage[(16 * T + 4 * lg + i) * R + 128 * w + 16 * J + lc] = oacc[T][J][i];
     lds_barrier();
 
     const int64_t rec = (int64_t)unit * p.h_pad + hg * HG;
@@ -362,14 +408,12 @@ __global__ void __launch_bounds__(THREADS, 1) mla_decode_split(DecodeParams p) {
         p.ws_ml[(rec + hh) * 2 + 0] = m_run;
         p.ws_ml[(rec + hh) * 2 + 1] = red[w][lc] + red[w ^ 2][lc];
     }
+    float* dst = p.ws_o + rec * R;
 #pragma unroll
-    for (int T = 0; T < 2; ++T)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            float* dst = p.ws_o + (rec + 16 * T + 4 * lg + i) * R + 128 * w + lc;
-#pragma unroll
-            for (int J = 0; J < 8; ++J) dst[16 * J] = oacc[T][J][i];
-        }
+    for (int k = 0; k < HG * R / 4 / THREADS; ++k) {
+        const int e4 = tid + THREADS * k;
+        *(f32x4*)(dst + 4 * e4) = *(const f32x4*)(ostage + 4 * e4);
+    }
 }
 
 // Merge the split partials: one 256-thread block per (batch, head, 256-column

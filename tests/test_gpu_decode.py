@@ -71,6 +71,20 @@ def test_config2_decode_128_heads_32k(M):
     check(host_f32(out32)[0], ref, "config2-f32", scale_bar=2e-3)
 
 
+def test_bf16_output_is_rne_of_f32_output(M):
+    # the split kernel is shared; only the combine's final conversion differs,
+    # so the bf16 output must be the round-to-nearest-even of the f32 output
+    print("decode bf16 == RNE(f32)", flush=True)
+    import torch
+
+    ql, qr, cache = MI.decode_inputs(128, 8192, tag="rne")
+    a = run_decode(M, ql, qr, cache, out_dtype=torch.float32)
+    b = run_decode(M, ql, qr, cache)
+    exp = O.f32_to_bf16(host_f32(a))
+    got = b.cpu().view(torch.int16).numpy().view(np.uint16)
+    np.testing.assert_array_equal(got, exp)
+
+
 @pytest.mark.parametrize("splits", [1, 2, 7, 64])
 def test_split_count_invariance(M, splits):
     print(f"decode split invariance splits={splits}", flush=True)
