@@ -32,12 +32,16 @@ FLAGS = [
 ]
 
 LIB_SOURCES = ["capi.cpp", "decode.hip"]
+# Per-source flags.  The decode kernel keeps its MFMA accumulators in VGPRs
+# (VGPR-form MFMA): with the AGPR form the compiler shuttles all 64 of them
+# through v_accvgpr moves on every 32-row step.
+EXTRA = {"decode.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
 SELFTEST_SOURCES = ["selftest.hip"]
 
 
 def _compile(src: str) -> str:
     out = os.path.join(OBJ, os.path.splitext(src)[0] + ".o")
-    cmd = [HIPCC, *FLAGS, "-c", os.path.join(CSRC, src), "-o", out]
+    cmd = [HIPCC, *FLAGS, *EXTRA.get(src, []), "-c", os.path.join(CSRC, src), "-o", out]
     if src.endswith(".cpp"):
         cmd.insert(1, "-x")
         cmd.insert(2, "hip")
