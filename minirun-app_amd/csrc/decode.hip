@@ -103,6 +103,7 @@ __global__ void __launch_bounds__(THREADS, 1) mla_decode_split(DecodeParams p) {
     __shared__ __attribute__((aligned(1024))) char cbuf[NBUF * G::BUF];
     __shared__ __attribute__((aligned(16))) char pbuf[HG * PSTR];
     __shared__ float red[4][16];
+    __shared__ __attribute__((aligned(16))) float red4[4][16][4];  // [wave][head col][lane group] partial maxes
     __shared__ __attribute__((aligned(16))) float alpha_s[HG];
     __shared__ int flag_s[2];
     __shared__ int32_t idx_s[GATHER ? MAX_GATHER_ROWS : 1];
@@ -153,33 +154,33 @@ __global__ void __launch_bounds__(THREADS, 1) mla_decode_split(DecodeParams p) {
     // Every lane always loads: a row past the split reads the split's last
     // row (dense) or row 0 (gather) and is masked to P = 0, so each wave issues
     // exactly NLD loads per sub-chunk and the vmcnt waits are exact.
-    auto issue = [&](int s, char* base) {
+    auto issue_one = [&](int s, char* base, int k) {
         const int rbase = row_begin + s * ROWS;
-        const bool tail = rbase + ROWS > row_end;
-#pragma unroll
-        for (int k = 0; k < G::NLD; ++k) {
-            int rr = dma_row[k];  // row relative to rbase
-            int src_row;
-            if (GATHER) {
-                const int v = (rbase + rr < row_end) ? idx_s[rbase + rr - row_begin] : -1;
-                src_row = v >= 0 ? v : 0;
-            } else {
-                if (tail) rr = min(rr, row_end - 1 - rbase);
-                src_row = rbase + rr;
-            }
-            if (PACKED) {
-                if (GATHER)
-                    dma16_off(lat, (uint32_t)src_row * rs_b + (uint32_t)dma_c16[k], base + 1024 * (w + 4 * k));
-                else
-                    dma16_off((const char*)lat + (int64_t)rbase * rs_b, (uint32_t)rr * rs_b + (uint32_t)dma_c16[k],
-                              base + 1024 * (w + 4 * k));
-            } else {
-                const int c = dma_c16[k] >> 4;
-                const uint16_t* src = c < R / 8 ? lat + (int64_t)src_row * p.lat_rs + c * 8
-                                                : rop + (int64_t)src_row * p.rope_rs + (c - R / 8) * 8;
-                dma16(src, base + 1024 * (w + 4 * k));
-            }
+        int rr = dma_row[k];  // row relative to rbase
+        int src_row;
+        if (GATHER) {
+            const int v = (rbase + rr < row_end) ? idx_s[rbase + rr - row_begin] : -1;
+            src_row = v >= 0 ? v : 0;
+        } else {
+            if (rbase + ROWS > row_end) rr = min(rr, row_end - 1 - rbase);
+            src_row = rbase + rr;
         }
+        if (PACKED) {
+            if (GATHER)
+                dma16_off(lat, (uint32_t)src_row * rs_b + (uint32_t)dma_c16[k], base + 1024 * (w + 4 * k));
+            else
+                dma16_off((const char*)lat + (int64_t)rbase * rs_b, (uint32_t)rr * rs_b + (uint32_t)dma_c16[k],
+                          base + 1024 * (w + 4 * k));
+        } else {
+            const int c = dma_c16[k] >> 4;
+            const uint16_t* src = c < R / 8 ? lat + (int64_t)src_row * p.lat_rs + c * 8
+                                            : rop + (int64_t)src_row * p.rope_rs + (c - R / 8) * 8;
+            dma16(src, base + 1024 * (w + 4 * k));
+        }
+    };
+    auto issue = [&](int s, char* base) {
+#pragma unroll
+        for (int k = 0; k < G::NLD; ++k) issue_one(s, base, k);
     };
 
     // ---- Q of the head group, staged through the last buffer: "row" h of the
@@ -266,10 +267,11 @@ __global__ void __launch_bounds__(THREADS, 1) mla_decode_split(DecodeParams p) {
         else
             wait_vmcnt<0>();
         lds_barrier();  // s landed for every wave; PV(s-1) done everywhere
-        if (s + NBUF - 1 < nsub) {
-            const int sn = s + NBUF - 1;
-            issue(sn, cbuf + (sn & (NBUF - 1)) * G::BUF);
-        }
+        // refill the buffer freed by s-1 with sub-chunk s+3; the DMA is issued
+        // between the QK MFMAs so the address unit drains while they run
+        const bool refill = s + NBUF - 1 < nsub;
+        const int sn = s + NBUF - 1;
+        char* nbuf = cbuf + (sn & (NBUF - 1)) * G::BUF;
 
         // ---- QK: S[16 rows][16 heads]
         f32x4 sacc = {0.f, 0.f, 0.f, 0.f};
@@ -280,7 +282,14 @@ __global__ void __launch_bounds__(THREADS, 1) mla_decode_split(DecodeParams p) {
 #pragma unroll
             for (int ks = 16; ks < G::KS; ++ks) a[ks] = *(const bf16x8*)(cur + qk_rope[ks - 16]);
 #pragma unroll
-            for (int ks = 0; ks < G::KS; ++ks) sacc = mfma16(a[ks], qreg[ks], sacc);
+            for (int ks = 0; ks < G::KS; ++ks) {
+                sacc = mfma16(a[ks], qreg[ks], sacc);
+                if ((ks & 1) && (ks >> 1) < G::NLD) {
+                    __builtin_amdgcn_sched_barrier(0);
+                    if (refill) issue_one(sn, nbuf, ks >> 1);
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+            }
         }
         float sv[4];
 #pragma unroll
@@ -295,15 +304,17 @@ __global__ void __launch_bounds__(THREADS, 1) mla_decode_split(DecodeParams p) {
                 if (!ok) sv[i] = NEG_INF;
             }
         }
-        float mx = fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3]));
-        mx = fmaxf(mx, __shfl_xor(mx, 16));
-        mx = fmaxf(mx, __shfl_xor(mx, 32));
-        if (lg == 0) red[w][lc] = mx;
+        // partial max over this lane's 4 rows; the 8 partials of a head (4 lane
+        // groups x 2 row tiles) are combined after the barrier, no shuffles
+        red4[w][lc][lg] = fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3]));
         lds_barrier();
 
         // ---- reference max: raised only when a score passes it by TAU (or
         // on the first valid rows), so O is rarely rescaled; P <= 2^TAU.
-        const float cm = fmaxf(red[w][lc], red[w ^ 2][lc]);
+        const f32x4 pm0 = *(const f32x4*)red4[w][lc];
+        const f32x4 pm1 = *(const f32x4*)red4[w ^ 2][lc];
+        const float cm = fmaxf(fmaxf(fmaxf(pm0[0], pm0[1]), fmaxf(pm0[2], pm0[3])),
+                               fmaxf(fmaxf(pm1[0], pm1[1]), fmaxf(pm1[2], pm1[3])));
         const bool raise = cm > m_run + TAU;  // false while cm is -inf
         const float m_new = raise ? cm : m_run;
         const float alpha = raise ? exp2f(m_run - m_new) : 1.f;  // 0 when m_run was -inf
