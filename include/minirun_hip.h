@@ -123,6 +123,142 @@ mr_status mr_validate_indices(const int32_t *indices, int32_t batch, int32_t n_i
                               int32_t n_rows, void *workspace, size_t workspace_bytes,
                               int32_t *bad_token, int32_t *bad_position, void *stream);
 
+
+/* ------------------------------------------------------------------------
+ * MLX affine quantized weights (Sources/MLXBridge/AffineWeights.swift).
+ *
+ * packed: uint32 [experts?, out_features, in_features * bits / 32], element j
+ * of a word at bit offset bits*j (element 0 in the low bits: the word's
+ * little-endian byte image is the checkpoint stream, MXFP4Weights.swift:42-48);
+ * scales, biases: [experts?, out_features, in_features / group] in one of
+ * bf16 / f16 / f32; w = scale * q + bias.
+ * ------------------------------------------------------------------------ */
+typedef struct mr_affine_weight {
+    const uint32_t *packed;
+    const void *scales;
+    const void *biases;
+    mr_dtype scale_dtype;
+    int64_t out_features, in_features;
+    int32_t group, bits;
+} mr_affine_weight;
+
+/* AffineWeights.init validation (AffineWeights.swift:84-157), in the
+ * reference's order and with its messages: packed dtype, scale dtype,
+ * scale/bias dtype agreement, scale/bias shape agreement, rank 2 or 3,
+ * bits dividing 32, positive group, expert count, row count, in_features a
+ * multiple of the group, group count.  Shapes are given as rank + dims.
+ * On success fills the geometry (experts = 0 for a single matrix). */
+mr_status mr_affine_validate(mr_dtype packed_dtype, int32_t packed_rank, const int64_t *packed_shape,
+                             mr_dtype scales_dtype, int32_t scales_rank, const int64_t *scales_shape,
+                             mr_dtype biases_dtype, int32_t biases_rank, const int64_t *biases_shape,
+                             int32_t group, int32_t bits, int64_t *experts, int64_t *out_features,
+                             int64_t *in_features);
+
+/* affineDequantize (AffineWeights.swift:328-342): dense [out, in] in f32
+ * (default, bit-exact: the bf16/f16-scale product is exact in fp32) or
+ * bf16 (round-to-nearest-even of the f32 value). */
+mr_status mr_affine_dequantize(const mr_affine_weight *w, void *out, mr_dtype out_dtype, void *stream);
+
+/* affineMM (AffineWeights.swift:239-254): y[t, :] = x[t, :] . dequant(W)^T,
+ * transpose fixed (W is [out, in]).  x: [tokens, in] bf16 or f32 with row
+ * stride x_stride; y: [tokens, out] bf16 or f32 with row stride y_stride;
+ * fp32 accumulation.  4-bit / group-64 / bf16 x / one token runs the fused
+ * dequant-GEMV; other shapes run a generic kernel. */
+mr_status mr_affine_matmul(const void *x, mr_dtype x_dtype, int32_t tokens, int64_t x_stride,
+                           const mr_affine_weight *w, void *y, mr_dtype y_dtype, int64_t y_stride,
+                           void *stream);
+
+/* K3Norm.rms (Sources/ModelAdapters/Operators/Normalization.swift:15-19):
+ * out = weight * (x * rsqrt(mean(x^2) + eps)) per row, fp32 arithmetic. */
+mr_status mr_rmsnorm(const void *x, mr_dtype x_dtype, int64_t rows, int32_t dim, int64_t x_stride,
+                     const void *weight, mr_dtype w_dtype, float eps, void *out, mr_dtype out_dtype,
+                     int64_t out_stride, void *stream);
+
+/* DeepSeekV4RotaryParameters (DeepSeekV4Attention.swift:28-99), host side:
+ * pair frequencies base^(-2i/dim) with the YaRN ramp when original_len > 0.
+ * freqs_out has dim/2 doubles. */
+mr_status mr_rope_frequencies(int32_t dim, int32_t original_len, double base, double factor,
+                              double beta_fast, double beta_slow, double *freqs_out);
+/* Host cos/sin tables [n_pos, half] (DeepSeekV4Attention.swift:126-149):
+ * angle = (inverse ? -1 : 1) * position * freq in double, rounded to float. */
+mr_status mr_rope_table(const int64_t *positions, int64_t n_pos, const double *freqs, int32_t half,
+                        int32_t inverse, float *cos_out, float *sin_out);
+/* DeepSeekV4Rotary.apply (DeepSeekV4Attention.swift:108-165), device, in
+ * place: x [n_pos, inner, row_stride] (bf16 or f32), columns
+ * [col0, col0 + dim) rotated as adjacent pairs with the device tables
+ * cos_t / sin_t [n_pos, dim/2]. */
+mr_status mr_rope_apply(void *x, mr_dtype dtype, int64_t n_pos, int64_t inner, int64_t row_stride,
+                        int64_t col0, int32_t dim, const float *cos_t, const float *sin_t, void *stream);
+
+/* Latent-cache append (K3MLA.forward, MLA.swift:142-157): for each of
+ * `tokens` kv_a rows [kv_rank ++ rope_dim] (bf16 or f32), write
+ * RMSNorm(latent) * norm_w as bf16 to latent[start_row + t] and the rope
+ * key, rotated with cos_t/sin_t [tokens, rope_dim/2], to rope[start_row + t]. */
+mr_status mr_mla_cache_append(const void *kv, mr_dtype kv_dtype, int64_t kv_stride, int64_t tokens,
+                              const void *norm_w, mr_dtype w_dtype, float eps, int32_t kv_rank,
+                              int32_t rope_dim, const float *cos_t, const float *sin_t, void *latent,
+                              int64_t latent_row_stride, void *rope, int64_t rope_row_stride,
+                              int64_t start_row, void *stream);
+
+/* Query absorption (MLA.swift:180-188): q_lat[h] = q_nope[h] . W_UK[h] with
+ * W_UK the rows h*(nope+v) .. +nope of the affine kv_b_proj
+ * [heads*(nope+v), kv_rank] (4-bit, group 64, kv_rank 512).  q: bf16 heads
+ * of q_head_stride elements, nope part first; q_lat: bf16 [heads, kv_rank]. */
+mr_status mr_mla_absorb_query(const void *q, int64_t q_head_stride, int32_t heads, int32_t nope_dim,
+                              int32_t v_dim, const mr_affine_weight *kv_b, void *q_lat,
+                              int64_t q_lat_head_stride, void *stream);
+
+/* Value un-absorption (MLA.swift:196-197): out[h] = ctx[h] . W_UV[h]^T with
+ * W_UV the rows h*(nope+v)+nope .. +v of kv_b; ctx bf16 [heads, kv_rank],
+ * out [heads, v_dim] bf16 or f32 (contiguous). */
+mr_status mr_mla_unabsorb_values(const void *ctx, int64_t ctx_head_stride, int32_t heads, int32_t nope_dim,
+                                 int32_t v_dim, const mr_affine_weight *kv_b, void *out, mr_dtype out_dtype,
+                                 void *stream);
+
+/* ------------------------------------------------------------------------
+ * One decode token through the whole MLA block with affine projections
+ * (K3MLA.forwardWithoutTrace, MLA.swift:91-98 -> :124-229, absorbed branch):
+ *   h = RMSNorm(x) (input norm; skipped when input_norm_w is NULL)
+ *   q = q_b(RMSNorm(q_a(h)))  [heads, nope + rope]; rope part rotated
+ *   kv = kv_a(h) -> cache row `position` (mr_mla_cache_append)
+ *   q_lat = absorb(q_nope, kv_b)
+ *   ctx = mr_mla_decode over rows [0, position]   (append, then attend)
+ *   out = o_proj(unabsorb(ctx, kv_b))
+ * The output gate is not part of this block.  All activations between the
+ * projections are bf16 (the affine matmul output dtype for bf16 input).
+ * ------------------------------------------------------------------------ */
+typedef struct mr_mla_block_args {
+    int32_t hidden, q_lora_rank, heads, qk_nope_dim, qk_rope_dim, v_head_dim, kv_rank;
+    float eps, scale;
+    const void *x; /* bf16 [hidden], one token */
+    const void *input_norm_w, *q_a_norm_w, *kv_a_norm_w;
+    mr_dtype norm_w_dtype; /* bf16 or f32, all three */
+    mr_affine_weight q_a, q_b, kv_a, kv_b, o_proj;
+    void *cache_latent; /* bf16 rows, kv_rank wide */
+    int64_t latent_row_stride;
+    void *cache_rope; /* bf16 rows, qk_rope_dim wide */
+    int64_t rope_row_stride;
+    int32_t position, capacity; /* rows cached before this token; rows available */
+    const float *rope_cos, *rope_sin; /* device [qk_rope_dim/2]: angle table at `position` */
+    void *out; /* bf16 [hidden] */
+    void *workspace;
+    size_t workspace_bytes;
+} mr_mla_block_args;
+
+size_t mr_mla_decode_block_workspace_size(const mr_mla_block_args *args);
+mr_status mr_mla_decode_block(const mr_mla_block_args *args, void *stream);
+
+/* ------------------------------------------------------------------------
+ * Index tables of DeepSeek V4 attention (DeepSeekV4Attention.swift:169-237),
+ * host side, -1 = invalid entry.  `out` must hold rows*cols entries:
+ * window: seq_len*min(seq_len, window) (or window when start_pos > 0);
+ * compressed: seq_len*(seq_len/ratio) (or (start_pos+1)/ratio).
+ * ------------------------------------------------------------------------ */
+mr_status mr_attention_indices_window(int32_t window, int32_t seq_len, int32_t start_pos, int32_t *out,
+                                      int32_t *rows, int32_t *cols);
+mr_status mr_attention_indices_compressed(int32_t ratio, int32_t seq_len, int32_t start_pos, int32_t offset,
+                                          int32_t *out, int32_t *rows, int32_t *cols);
+
 #ifdef __cplusplus
 }
 #endif

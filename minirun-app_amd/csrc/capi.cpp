@@ -11,11 +11,14 @@
 #include <vector>
 
 #include "../../include/minirun_hip.h"
+#include "capi_util.hpp"
 #include "mr_kernels.hpp"
 
 namespace {
-
 thread_local std::string g_last_error;
+}  // namespace
+
+namespace mrc {
 
 mr_status fail(mr_status st, const char* fmt, ...) {
     char buf[512];
@@ -31,7 +34,24 @@ mr_status hip_fail(hipError_t e, const char* what) {
     return fail(MR_HIP_ERROR, "%s: %s", what, hipGetErrorString(e));
 }
 
-bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+const char* dtype_name(mr_dtype d) {
+    switch (d) {
+        case MR_BF16: return "bfloat16";
+        case MR_F16: return "float16";
+        case MR_F32: return "float32";
+        case MR_U32: return "uint32";
+        case MR_I32: return "int32";
+    }
+    return "unknown";
+}
+
+}  // namespace mrc
+
+namespace {
+using mrc::aligned16;
+using mrc::align256;
+using mrc::fail;
+using mrc::hip_fail;
 
 constexpr int kMaxDevices = 64;
 std::atomic<int> g_cu_count[kMaxDevices];
@@ -46,8 +66,6 @@ int cu_count() {
     g_cu_count[dev].store(n, std::memory_order_relaxed);
     return n;
 }
-
-size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 
 struct DecodePlan {
     int n_rows, head_groups, h_pad, splits, rows_per_split;

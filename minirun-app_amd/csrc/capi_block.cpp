@@ -1,0 +1,538 @@
+// C-ABI: affine weights, RMSNorm, rotary, cache append, absorption, the
+// composed decode block, and the V4 index tables.  Validation first, with
+// the reference's messages where it has them; no device allocation.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstdio>
+#include <string>
+
+#include "../../include/minirun_hip.h"
+#include "capi_util.hpp"
+#include "mr_kernels.hpp"
+
+using mrc::aligned16;
+using mrc::align256;
+using mrc::dtype_name;
+using mrc::fail;
+using mrc::hip_fail;
+
+namespace {
+
+std::string shape_str(int32_t rank, const int64_t* dims) {
+    std::string s = "[";
+    for (int32_t i = 0; i < rank; ++i) {
+        if (i) s += ", ";
+        s += std::to_string(dims[i]);
+    }
+    return s + "]";
+}
+
+bool is_float_dtype(mr_dtype d) { return d == MR_BF16 || d == MR_F16 || d == MR_F32; }
+int scale_code(mr_dtype d) { return d == MR_BF16 ? 0 : (d == MR_F16 ? 1 : 2); }
+
+mr_status check_weight(const mr_affine_weight* w, const char* what) {
+    if (!w) return fail(MR_INVALID_ARGUMENT, "%s: weight descriptor is NULL", what);
+    if (!w->packed || !w->scales || !w->biases)
+        return fail(MR_INVALID_ARGUMENT, "%s: packed, scales and biases must be non-NULL", what);
+    if (!is_float_dtype(w->scale_dtype))
+        return fail(MR_INVALID_DTYPE,
+                    "affine scales must be a floating-point type — .bfloat16 for this checkpoint, .float16 or "
+                    ".float32 for others — got %s", dtype_name(w->scale_dtype));
+    if (w->bits <= 0 || 32 % w->bits != 0)
+        return fail(MR_INVALID_SHAPE, "bits %d must divide 32 for the uint32 packing", w->bits);
+    if (w->group <= 0) return fail(MR_INVALID_SHAPE, "group size must be positive");
+    if (w->out_features <= 0 || w->in_features <= 0)
+        return fail(MR_INVALID_SHAPE, "%s: out_features %lld and in_features %lld must be positive", what,
+                    (long long)w->out_features, (long long)w->in_features);
+    if (w->in_features % w->group != 0)
+        return fail(MR_INVALID_SHAPE,
+                    "inFeatures %lld is not a multiple of the group size %d; partial final groups are not supported",
+                    (long long)w->in_features, w->group);
+    if (w->in_features % (32 / w->bits) != 0)
+        return fail(MR_INVALID_SHAPE, "%s: in_features %lld does not fill whole uint32 words", what,
+                    (long long)w->in_features);
+    if (!mrc::aligned4(w->packed) || !mrc::aligned4(w->scales) || !mrc::aligned4(w->biases))
+        return fail(MR_INVALID_ARGUMENT, "%s: packed, scales and biases must be 4-byte aligned", what);
+    return MR_OK;
+}
+
+bool act_dtype_ok(mr_dtype d) { return d == MR_BF16 || d == MR_F32; }
+
+mr::AffineGemvParams gemv_params(const mr_affine_weight* w) {
+    mr::AffineGemvParams g{};
+    g.packed = w->packed;
+    g.scales = w->scales;
+    g.biases = w->biases;
+    g.scale_dtype = scale_code(w->scale_dtype);
+    g.out_rows = (int)w->out_features;
+    g.in_features = (int)w->in_features;
+    g.group = w->group;
+    g.bits = w->bits;
+    g.map_a = (int)w->out_features;
+    g.map_b = 0;
+    g.map_c = 0;
+    return g;
+}
+
+}  // namespace
+
+extern "C" {
+
+mr_status mr_affine_validate(mr_dtype packed_dtype, int32_t packed_rank, const int64_t* ps, mr_dtype scales_dtype,
+                             int32_t scales_rank, const int64_t* ss, mr_dtype biases_dtype, int32_t biases_rank,
+                             const int64_t* bs, int32_t group, int32_t bits, int64_t* experts, int64_t* out_features,
+                             int64_t* in_features) {
+    // AffineWeights.swift:84-157, same order
+    if (packed_dtype != MR_U32)
+        return fail(MR_INVALID_DTYPE,
+                    "packed affine weights must be .uint32 (the little-endian reinterpretation of the checkpoint's "
+                    "stream), got %s", dtype_name(packed_dtype));
+    if (!is_float_dtype(scales_dtype))
+        return fail(MR_INVALID_DTYPE,
+                    "affine scales must be a floating-point type — .bfloat16 for this checkpoint, .float16 or "
+                    ".float32 for others — got %s", dtype_name(scales_dtype));
+    if (scales_dtype != biases_dtype)
+        return fail(MR_INVALID_DTYPE, "scales are %s but biases are %s; MLX emits both in one dtype",
+                    dtype_name(scales_dtype), dtype_name(biases_dtype));
+    if (packed_rank < 0 || scales_rank < 0 || biases_rank < 0 || packed_rank > 8 || scales_rank > 8 || biases_rank > 8 ||
+        (packed_rank && !ps) || (scales_rank && !ss) || (biases_rank && !bs))
+        return fail(MR_INVALID_ARGUMENT, "affine validation: bad shape arrays");
+    bool same = scales_rank == biases_rank;
+    for (int32_t i = 0; same && i < scales_rank; ++i) same = ss[i] == bs[i];
+    if (!same)
+        return fail(MR_INVALID_SHAPE, "scales %s and biases %s must have one shape", shape_str(scales_rank, ss).c_str(),
+                    shape_str(biases_rank, bs).c_str());
+    if (!(packed_rank == scales_rank && (packed_rank == 2 || packed_rank == 3)))
+        return fail(MR_INVALID_SHAPE,
+                    "packed %s and scales %s must both be rank 2 (one matrix) or rank 3 (an expert stack), and must agree",
+                    shape_str(packed_rank, ps).c_str(), shape_str(scales_rank, ss).c_str());
+    if (bits <= 0 || 32 % bits != 0) return fail(MR_INVALID_SHAPE, "bits %d must divide 32 for the uint32 packing", bits);
+    if (group <= 0) return fail(MR_INVALID_SHAPE, "group size must be positive");
+    const int64_t ex = packed_rank == 3 ? ps[0] : 0;
+    if (packed_rank == 3 && ss[0] != ex)
+        return fail(MR_INVALID_SHAPE, "expert count differs: packed has %lld, scales has %lld", (long long)ex,
+                    (long long)ss[0]);
+    const int64_t out = ps[packed_rank - 2];
+    if (ss[scales_rank - 2] != out)
+        return fail(MR_INVALID_SHAPE, "row count differs: packed has %lld, scales has %lld", (long long)out,
+                    (long long)ss[scales_rank - 2]);
+    const int64_t in = ps[packed_rank - 1] * (32 / bits);
+    if (in % group != 0)
+        return fail(MR_INVALID_SHAPE,
+                    "inFeatures %lld is not a multiple of the group size %d; partial final groups are not supported",
+                    (long long)in, group);
+    const int64_t expected = in / group;
+    if (ss[scales_rank - 1] != expected)
+        return fail(MR_INVALID_SHAPE,
+                    "group count differs: %lld input features at group size %d need %lld scales per row, got %lld",
+                    (long long)in, group, (long long)expected, (long long)ss[scales_rank - 1]);
+    if (experts) *experts = ex;
+    if (out_features) *out_features = out;
+    if (in_features) *in_features = in;
+    return MR_OK;
+}
+
+mr_status mr_affine_dequantize(const mr_affine_weight* w, void* out, mr_dtype out_dtype, void* stream) {
+    mr_status st = check_weight(w, "affine dequantize");
+    if (st != MR_OK) return st;
+    if (!out) return fail(MR_INVALID_ARGUMENT, "affine dequantize: out is NULL");
+    if (!act_dtype_ok(out_dtype)) return fail(MR_INVALID_DTYPE, "affine dequantize: out dtype must be bf16 or f32");
+    mr::AffineDequantParams p{};
+    p.packed = w->packed;
+    p.scales = w->scales;
+    p.biases = w->biases;
+    p.scale_dtype = scale_code(w->scale_dtype);
+    p.out_features = w->out_features;
+    p.in_features = w->in_features;
+    p.group = w->group;
+    p.bits = w->bits;
+    p.out = out;
+    p.out_f32 = out_dtype == MR_F32;
+    const hipError_t e = mr::launch_affine_dequant(p, (hipStream_t)stream);
+    return e == hipSuccess ? MR_OK : hip_fail(e, "affine dequantize launch");
+}
+
+mr_status mr_affine_matmul(const void* x, mr_dtype x_dtype, int32_t tokens, int64_t x_stride, const mr_affine_weight* w,
+                           void* y, mr_dtype y_dtype, int64_t y_stride, void* stream) {
+    mr_status st = check_weight(w, "affine matmul");
+    if (st != MR_OK) return st;
+    if (!x || !y) return fail(MR_INVALID_ARGUMENT, "affine matmul: x and y must be non-NULL");
+    if (!act_dtype_ok(x_dtype) || !act_dtype_ok(y_dtype))
+        return fail(MR_INVALID_DTYPE, "affine matmul: x and y must be bf16 or f32");
+    if (tokens <= 0) return fail(MR_INVALID_SHAPE, "affine matmul: tokens %d must be positive", tokens);
+    if (x_stride < w->in_features || y_stride < w->out_features)
+        return fail(MR_INVALID_SHAPE, "affine matmul: x rows need %lld features, y rows %lld",
+                    (long long)w->in_features, (long long)w->out_features);
+    if (w->in_features > INT32_MAX || w->out_features > INT32_MAX)
+        return fail(MR_INVALID_SHAPE, "affine matmul: dimensions exceed int32");
+    mr::AffineGemvParams g = gemv_params(w);
+    g.x = x;
+    g.x_f32 = x_dtype == MR_F32;
+    g.x_stride = x_stride;
+    g.m = tokens;
+    g.y = y;
+    g.y_f32 = y_dtype == MR_F32;
+    g.y_stride_row = 1;
+    g.y_stride_token = y_stride;
+    g.force_generic = !aligned16(w->packed);  // the fused kernel loads 16-byte row chunks
+    const hipError_t e = mr::launch_affine_gemv(g, (hipStream_t)stream);
+    return e == hipSuccess ? MR_OK : hip_fail(e, "affine matmul launch");
+}
+
+mr_status mr_rmsnorm(const void* x, mr_dtype x_dtype, int64_t rows, int32_t dim, int64_t x_stride, const void* weight,
+                     mr_dtype w_dtype, float eps, void* out, mr_dtype out_dtype, int64_t out_stride, void* stream) {
+    if (!x || !weight || !out) return fail(MR_INVALID_ARGUMENT, "rmsnorm: NULL pointer");
+    if (!act_dtype_ok(x_dtype) || !act_dtype_ok(w_dtype) || !act_dtype_ok(out_dtype))
+        return fail(MR_INVALID_DTYPE, "rmsnorm: dtypes must be bf16 or f32");
+    if (rows <= 0 || dim <= 0 || x_stride < dim || out_stride < dim || rows > INT32_MAX)
+        return fail(MR_INVALID_SHAPE, "rmsnorm: rows %lld, dim %d, strides %lld/%lld", (long long)rows, dim,
+                    (long long)x_stride, (long long)out_stride);
+    if (!(eps >= 0) || !std::isfinite(eps)) return fail(MR_INVALID_ARGUMENT, "rmsnorm: eps must be finite, >= 0");
+    mr::RmsNormParams p{x, x_dtype == MR_F32, x_stride, weight, w_dtype == MR_F32, out, out_dtype == MR_F32,
+                        out_stride, rows, dim, eps};
+    const hipError_t e = mr::launch_rmsnorm(p, (hipStream_t)stream);
+    return e == hipSuccess ? MR_OK : hip_fail(e, "rmsnorm launch");
+}
+
+mr_status mr_rope_frequencies(int32_t dim, int32_t original_len, double base, double factor, double beta_fast,
+                              double beta_slow, double* freqs) {
+    // DeepSeekV4Attention.swift:36-99
+    if (!(dim > 0 && dim % 2 == 0))
+        return fail(MR_INVALID_SHAPE, "rotary dimension must be positive and even, got %d", dim);
+    if (original_len < 0) return fail(MR_INVALID_SHAPE, "original rotary sequence length cannot be negative");
+    if (!(std::isfinite(base) && base > 1 && std::isfinite(factor) && factor > 0 && std::isfinite(beta_fast) &&
+          beta_fast > 0 && std::isfinite(beta_slow) && beta_slow > 0))
+        return fail(MR_INVALID_SHAPE, "rotary base, factor, and correction rotations must be finite and positive");
+    if (!freqs) return fail(MR_INVALID_ARGUMENT, "rotary frequencies: output is NULL");
+    const int half = dim / 2;
+    for (int i = 0; i < half; ++i) freqs[i] = 1.0 / std::pow(base, double(i * 2) / double(dim));
+    if (original_len > 0) {
+        auto corr = [&](double rot) {
+            return double(dim) * std::log(double(original_len) / (rot * 2.0 * M_PI)) / (2.0 * std::log(base));
+        };
+        const int64_t low = std::max<int64_t>(int64_t(std::floor(corr(beta_fast))), 0);
+        const int64_t high = std::min<int64_t>(int64_t(std::ceil(corr(beta_slow))), dim - 1);
+        const double den = low == high ? 0.001 : double(high - low);
+        for (int i = 0; i < half; ++i) {
+            const double ramp = std::min(std::max((double(i) - double(low)) / den, 0.0), 1.0);
+            const double smooth = 1.0 - ramp;
+            freqs[i] = freqs[i] / factor * (1.0 - smooth) + freqs[i] * smooth;
+        }
+    }
+    for (int i = 0; i < half; ++i)
+        if (!(std::isfinite(freqs[i]) && freqs[i] > 0))
+            return fail(MR_NONFINITE, "rotary frequency table is not finite and positive");
+    return MR_OK;
+}
+
+mr_status mr_rope_table(const int64_t* positions, int64_t n_pos, const double* freqs, int32_t half, int32_t inverse,
+                        float* cos_out, float* sin_out) {
+    // DeepSeekV4Attention.swift:126-149
+    if (n_pos < 0 || half <= 0 || (n_pos && (!positions || !freqs || !cos_out || !sin_out)))
+        return fail(MR_INVALID_ARGUMENT, "rotary table: bad arguments");
+    for (int64_t i = 0; i < n_pos; ++i)
+        if (positions[i] < 0) return fail(MR_INVALID_SHAPE, "rotary positions cannot be negative");
+    const double dir = inverse ? -1.0 : 1.0;
+    for (int64_t i = 0; i < n_pos; ++i)
+        for (int32_t k = 0; k < half; ++k) {
+            const double a = dir * double(positions[i]) * freqs[k];
+            if (!std::isfinite(a)) return fail(MR_NONFINITE, "rotary angle is not finite");
+            cos_out[i * half + k] = float(std::cos(a));
+            sin_out[i * half + k] = float(std::sin(a));
+        }
+    return MR_OK;
+}
+
+mr_status mr_rope_apply(void* x, mr_dtype dtype, int64_t n_pos, int64_t inner, int64_t row_stride, int64_t col0,
+                        int32_t dim, const float* cos_t, const float* sin_t, void* stream) {
+    if (!x || !cos_t || !sin_t) return fail(MR_INVALID_ARGUMENT, "rotary apply: NULL pointer");
+    if (!act_dtype_ok(dtype))
+        return fail(MR_INVALID_DTYPE, "rotary input must have a real floating-point dtype (bf16 or f32 here)");
+    if (!(dim > 0 && dim % 2 == 0) || n_pos < 0 || inner <= 0 || col0 < 0 || col0 + dim > row_stride)
+        return fail(MR_INVALID_SHAPE, "rotary input must be [sequence, ..., %d] with one position per sequence row", dim);
+    if (n_pos == 0) return MR_OK;
+    mr::RopeParams p{x, dtype == MR_F32, n_pos, inner, row_stride, col0, dim, cos_t, sin_t};
+    const hipError_t e = mr::launch_rope(p, (hipStream_t)stream);
+    return e == hipSuccess ? MR_OK : hip_fail(e, "rotary launch");
+}
+
+mr_status mr_mla_cache_append(const void* kv, mr_dtype kv_dtype, int64_t kv_stride, int64_t tokens, const void* norm_w,
+                              mr_dtype w_dtype, float eps, int32_t kv_rank, int32_t rope_dim, const float* cos_t,
+                              const float* sin_t, void* latent, int64_t latent_row_stride, void* rope,
+                              int64_t rope_row_stride, int64_t start_row, void* stream) {
+    if (!kv || !norm_w || !latent || (rope_dim && (!rope || !cos_t || !sin_t)))
+        return fail(MR_INVALID_ARGUMENT, "cache append: NULL pointer");
+    if (!act_dtype_ok(kv_dtype) || !act_dtype_ok(w_dtype)) return fail(MR_INVALID_DTYPE, "cache append: dtypes");
+    if (tokens <= 0 || kv_rank <= 0 || rope_dim < 0 || rope_dim % 2 || kv_stride < kv_rank + rope_dim ||
+        latent_row_stride < kv_rank || (rope_dim && rope_row_stride < rope_dim) || start_row < 0 || tokens > INT32_MAX)
+        return fail(MR_INVALID_SHAPE, "cache append: bad geometry");
+    mr::CacheAppendParams p{kv, kv_dtype == MR_F32, kv_stride, norm_w, w_dtype == MR_F32, eps, kv_rank, rope_dim,
+                            cos_t, sin_t, (uint16_t*)latent, latent_row_stride, (uint16_t*)rope, rope_row_stride,
+                            start_row, tokens};
+    const hipError_t e = mr::launch_cache_append(p, (hipStream_t)stream);
+    return e == hipSuccess ? MR_OK : hip_fail(e, "cache append launch");
+}
+
+static mr_status check_kv_b(const mr_affine_weight* kv_b, int32_t heads, int32_t nope_dim, int32_t v_dim) {
+    mr_status st = check_weight(kv_b, "kv_b_proj");
+    if (st != MR_OK) return st;
+    if (kv_b->bits != 4 || kv_b->group != 64 || kv_b->in_features != 512)
+        return fail(MR_INVALID_SHAPE, "kv_b_proj: the absorbed path needs 4-bit, group 64, kv_rank 512 (got %d/%d/%lld)",
+                    kv_b->bits, kv_b->group, (long long)kv_b->in_features);
+    if (heads <= 0 || nope_dim <= 0 || v_dim <= 0 || kv_b->out_features != int64_t(heads) * (nope_dim + v_dim))
+        return fail(MR_INVALID_SHAPE, "kv_b_proj has %lld rows; heads %d x (nope %d + v %d) expected",
+                    (long long)kv_b->out_features, heads, nope_dim, v_dim);
+    return MR_OK;
+}
+
+mr_status mr_mla_absorb_query(const void* q, int64_t q_head_stride, int32_t heads, int32_t nope_dim, int32_t v_dim,
+                              const mr_affine_weight* kv_b, void* q_lat, int64_t q_lat_head_stride, void* stream) {
+    mr_status st = check_kv_b(kv_b, heads, nope_dim, v_dim);
+    if (st != MR_OK) return st;
+    if (!q || !q_lat || q_head_stride < nope_dim || q_lat_head_stride < 512)
+        return fail(MR_INVALID_ARGUMENT, "absorb query: bad q / q_lat");
+    mr::AbsorbParams p{(const uint16_t*)q, q_head_stride, kv_b->packed, kv_b->scales, kv_b->biases,
+                       scale_code(kv_b->scale_dtype), heads, nope_dim, v_dim, 512, (uint16_t*)q_lat, q_lat_head_stride};
+    const hipError_t e = mr::launch_absorb_q(p, (hipStream_t)stream);
+    return e == hipSuccess ? MR_OK : hip_fail(e, "absorb launch");
+}
+
+mr_status mr_mla_unabsorb_values(const void* ctx, int64_t ctx_head_stride, int32_t heads, int32_t nope_dim,
+                                 int32_t v_dim, const mr_affine_weight* kv_b, void* out, mr_dtype out_dtype,
+                                 void* stream) {
+    mr_status st = check_kv_b(kv_b, heads, nope_dim, v_dim);
+    if (st != MR_OK) return st;
+    if (!ctx || !out || ctx_head_stride < 512) return fail(MR_INVALID_ARGUMENT, "unabsorb values: bad ctx / out");
+    if (!act_dtype_ok(out_dtype)) return fail(MR_INVALID_DTYPE, "unabsorb values: out must be bf16 or f32");
+    mr::AffineGemvParams g = gemv_params(kv_b);
+    g.out_rows = heads * v_dim;
+    g.map_a = v_dim;
+    g.map_b = nope_dim + v_dim;
+    g.map_c = nope_dim;
+    g.x = ctx;
+    g.x_f32 = 0;
+    g.x_stride = ctx_head_stride;
+    g.m = 1;
+    g.y = out;
+    g.y_f32 = out_dtype == MR_F32;
+    g.y_stride_row = 1;
+    g.y_stride_token = int64_t(heads) * v_dim;
+    const hipError_t e = mr::launch_affine_gemv(g, (hipStream_t)stream);
+    return e == hipSuccess ? MR_OK : hip_fail(e, "unabsorb launch");
+}
+
+// ---------------------------------------------------------------- decode block
+namespace {
+
+struct BlockLayout {
+    size_t h, q_lora, q_lora_n, q, q_lat, kv, ctx, attn, dec, total;
+    mr_mla_decode_args dec_args;
+};
+
+bool block_layout(const mr_mla_block_args* a, BlockLayout* L) {
+    size_t off = 0;
+    auto take = [&](size_t bytes) {
+        const size_t at = off;
+        off += align256(bytes);
+        return at;
+    };
+    const int dq = a->qk_nope_dim + a->qk_rope_dim;
+    L->h = take(size_t(a->hidden) * 2);
+    L->q_lora = take(size_t(a->q_lora_rank) * 2);
+    L->q_lora_n = take(size_t(a->q_lora_rank) * 2);
+    L->q = take(size_t(a->heads) * dq * 2);
+    L->q_lat = take(size_t(a->heads) * a->kv_rank * 2);
+    L->kv = take(size_t(a->kv_rank + a->qk_rope_dim) * 2);
+    L->ctx = take(size_t(a->heads) * a->kv_rank * 2);
+    L->attn = take(size_t(a->heads) * a->v_head_dim * 2);
+    mr_mla_decode_args& d = L->dec_args;
+    d = mr_mla_decode_args{};
+    d.batch = 1;
+    d.heads = a->heads;
+    d.n_ctx = a->position + 1;
+    d.kv_rank = a->kv_rank;
+    d.rope_dim = a->qk_rope_dim;
+    d.scale = a->scale;
+    d.q_lat_head_stride = a->kv_rank;
+    d.q_rope_head_stride = dq;
+    d.latent_row_stride = a->latent_row_stride;
+    d.rope_row_stride = a->rope_row_stride;
+    d.out_dtype = MR_BF16;
+    d.out_head_stride = a->kv_rank;
+    L->dec = off;
+    const size_t dec_bytes = mr_mla_decode_workspace_size(&d);
+    take(dec_bytes);
+    L->total = off;
+    return true;
+}
+
+}  // namespace
+
+size_t mr_mla_decode_block_workspace_size(const mr_mla_block_args* a) {
+    if (!a || a->heads <= 0 || a->position < 0) return 0;
+    BlockLayout L;
+    block_layout(a, &L);
+    return L.total;
+}
+
+mr_status mr_mla_decode_block(const mr_mla_block_args* a, void* stream) {
+    if (!a) return fail(MR_INVALID_ARGUMENT, "mla block: args is NULL");
+    if (a->kv_rank != 512 || a->qk_rope_dim != 64 || a->heads <= 0 || a->qk_nope_dim <= 0 || a->v_head_dim <= 0 ||
+        a->hidden <= 0 || a->q_lora_rank <= 0)
+        return fail(MR_INVALID_SHAPE, "mla block: kv_rank 512, rope 64 and positive dims required");
+    if (a->position < 0 || a->position >= a->capacity)
+        return fail(MR_INVALID_SHAPE, "mla block: position %d outside the cache capacity %d", a->position, a->capacity);
+    if (!a->x || !a->q_a_norm_w || !a->kv_a_norm_w || !a->cache_latent || !a->cache_rope || !a->rope_cos ||
+        !a->rope_sin || !a->out || !a->workspace)
+        return fail(MR_INVALID_ARGUMENT, "mla block: NULL pointer");
+    if (!act_dtype_ok(a->norm_w_dtype)) return fail(MR_INVALID_DTYPE, "mla block: norm weights must be bf16 or f32");
+    const int dq = a->qk_nope_dim + a->qk_rope_dim;
+    struct {
+        const mr_affine_weight* w;
+        int64_t out, in;
+        const char* name;
+    } ws[] = {{&a->q_a, a->q_lora_rank, a->hidden, "q_a_proj"},
+              {&a->q_b, int64_t(a->heads) * dq, a->q_lora_rank, "q_b_proj"},
+              {&a->kv_a, a->kv_rank + a->qk_rope_dim, a->hidden, "kv_a_proj_with_mqa"},
+              {&a->o_proj, a->hidden, int64_t(a->heads) * a->v_head_dim, "o_proj"}};
+    for (auto& e : ws) {
+        mr_status st = check_weight(e.w, e.name);
+        if (st != MR_OK) return st;
+        if (e.w->out_features != e.out || e.w->in_features != e.in)
+            return fail(MR_INVALID_SHAPE, "mla block: %s is [%lld, %lld], expected [%lld, %lld]", e.name,
+                        (long long)e.w->out_features, (long long)e.w->in_features, (long long)e.out, (long long)e.in);
+    }
+    mr_status st = check_kv_b(&a->kv_b, a->heads, a->qk_nope_dim, a->v_head_dim);
+    if (st != MR_OK) return st;
+    BlockLayout L;
+    block_layout(a, &L);
+    if (a->workspace_bytes < L.total)
+        return fail(MR_WORKSPACE_TOO_SMALL, "mla block: workspace %zu bytes < %zu", a->workspace_bytes, L.total);
+    if (!aligned16(a->workspace)) return fail(MR_INVALID_ARGUMENT, "mla block: workspace must be 16-byte aligned");
+    char* W = (char*)a->workspace;
+    void* h = W + L.h;
+    void* q_lora = W + L.q_lora;
+    void* q_lora_n = W + L.q_lora_n;
+    uint16_t* q = (uint16_t*)(W + L.q);
+    void* q_lat = W + L.q_lat;
+    void* kv = W + L.kv;
+    void* ctx = W + L.ctx;
+    void* attn = W + L.attn;
+    const mr_dtype nd = a->norm_w_dtype;
+
+    // h = input norm (or x)
+    const void* hin = a->x;
+    if (a->input_norm_w) {
+        st = mr_rmsnorm(a->x, MR_BF16, 1, a->hidden, a->hidden, a->input_norm_w, nd, a->eps, h, MR_BF16, a->hidden, stream);
+        if (st != MR_OK) return st;
+        hin = h;
+    }
+    // query path: q_a -> RMSNorm -> q_b -> rotate the rope part -> absorb W_UK
+    if ((st = mr_affine_matmul(hin, MR_BF16, 1, a->hidden, &a->q_a, q_lora, MR_BF16, a->q_lora_rank, stream)) != MR_OK)
+        return st;
+    if ((st = mr_rmsnorm(q_lora, MR_BF16, 1, a->q_lora_rank, a->q_lora_rank, a->q_a_norm_w, nd, a->eps, q_lora_n,
+                         MR_BF16, a->q_lora_rank, stream)) != MR_OK)
+        return st;
+    if ((st = mr_affine_matmul(q_lora_n, MR_BF16, 1, a->q_lora_rank, &a->q_b, q, MR_BF16, int64_t(a->heads) * dq,
+                               stream)) != MR_OK)
+        return st;
+    if ((st = mr_rope_apply(q, MR_BF16, 1, a->heads, dq, a->qk_nope_dim, a->qk_rope_dim, a->rope_cos, a->rope_sin,
+                            stream)) != MR_OK)
+        return st;
+    if ((st = mr_mla_absorb_query(q, dq, a->heads, a->qk_nope_dim, a->v_head_dim, &a->kv_b, q_lat, a->kv_rank,
+                                  stream)) != MR_OK)
+        return st;
+    // key path: kv_a -> cache row `position` (norm + rope), then attend
+    if ((st = mr_affine_matmul(hin, MR_BF16, 1, a->hidden, &a->kv_a, kv, MR_BF16, a->kv_rank + a->qk_rope_dim,
+                               stream)) != MR_OK)
+        return st;
+    if ((st = mr_mla_cache_append(kv, MR_BF16, a->kv_rank + a->qk_rope_dim, 1, a->kv_a_norm_w, nd, a->eps, a->kv_rank,
+                                  a->qk_rope_dim, a->rope_cos, a->rope_sin, a->cache_latent, a->latent_row_stride,
+                                  a->cache_rope, a->rope_row_stride, a->position, stream)) != MR_OK)
+        return st;
+    mr_mla_decode_args d = L.dec_args;
+    d.q_lat = q_lat;
+    d.q_rope = q + a->qk_nope_dim;
+    d.latent = a->cache_latent;
+    d.rope_keys = a->cache_rope;
+    d.out = ctx;
+    d.workspace = W + L.dec;
+    d.workspace_bytes = L.total - L.dec;
+    if ((st = mr_mla_decode(&d, stream)) != MR_OK) return st;
+    // values: un-absorb W_UV per head, then o_proj
+    if ((st = mr_mla_unabsorb_values(ctx, a->kv_rank, a->heads, a->qk_nope_dim, a->v_head_dim, &a->kv_b, attn, MR_BF16,
+                                     stream)) != MR_OK)
+        return st;
+    return mr_affine_matmul(attn, MR_BF16, 1, int64_t(a->heads) * a->v_head_dim, &a->o_proj, a->out, MR_BF16,
+                            a->hidden, stream);
+}
+
+// ---------------------------------------------------------------- V4 index tables (host)
+mr_status mr_attention_indices_window(int32_t window, int32_t seq_len, int32_t start_pos, int32_t* out, int32_t* rows,
+                                      int32_t* cols) {
+    // DeepSeekV4Attention.swift:170-198
+    if (!(window > 0 && seq_len > 0 && start_pos >= 0))
+        return fail(MR_INVALID_SHAPE, "window size and sequence length must be positive and start position nonnegative");
+    if (!out || !rows || !cols) return fail(MR_INVALID_ARGUMENT, "window indices: NULL output");
+    if (start_pos > 0) {
+        if (seq_len != 1) return fail(MR_INVALID_SHAPE, "incremental window indexing accepts exactly one token");
+        *rows = 1;
+        *cols = window;
+        int n = 0;
+        if (start_pos >= window - 1) {
+            const int32_t cursor = start_pos % window;
+            for (int32_t k = cursor + 1; k < window; ++k) out[n++] = k;
+            for (int32_t k = 0; k <= cursor; ++k) out[n++] = k;
+        } else {
+            for (int32_t k = 0; k <= start_pos; ++k) out[n++] = k;
+            for (int32_t k = 0; k < window - start_pos - 1; ++k) out[n++] = -1;
+        }
+        return MR_OK;
+    }
+    const int32_t width = std::min(seq_len, window);
+    *rows = seq_len;
+    *cols = width;
+    for (int32_t pos = 0; pos < seq_len; ++pos) {
+        const int32_t first = std::max(0, pos - window + 1);
+        for (int32_t c = 0; c < width; ++c) {
+            const int32_t cand = first + c;
+            out[int64_t(pos) * width + c] = cand <= pos ? cand : -1;
+        }
+    }
+    return MR_OK;
+}
+
+mr_status mr_attention_indices_compressed(int32_t ratio, int32_t seq_len, int32_t start_pos, int32_t offset,
+                                          int32_t* out, int32_t* rows, int32_t* cols) {
+    // DeepSeekV4Attention.swift:200-236
+    if (!(ratio > 0 && seq_len > 0 && start_pos >= 0 && offset >= 0))
+        return fail(MR_INVALID_SHAPE,
+                    "compression ratio and sequence length must be positive; position and offset must be nonnegative");
+    if (!out || !rows || !cols) return fail(MR_INVALID_ARGUMENT, "compressed indices: NULL output");
+    if (start_pos > 0) {
+        if (seq_len != 1) return fail(MR_INVALID_SHAPE, "incremental compressed indexing accepts exactly one token");
+        const int64_t count = (int64_t(start_pos) + 1) / ratio;
+        *rows = 1;
+        *cols = int32_t(count);
+        for (int64_t k = 0; k < count; ++k) {
+            if (int64_t(offset) + k > INT32_MAX) return fail(MR_INVALID_SHAPE, "cache index overflows Int");
+            out[k] = int32_t(offset + k);
+        }
+        return MR_OK;
+    }
+    const int32_t width = seq_len / ratio;
+    *rows = seq_len;
+    *cols = width;
+    for (int32_t pos = 0; pos < seq_len; ++pos) {
+        const int32_t visible = (pos + 1) / ratio;
+        for (int32_t k = 0; k < width; ++k) {
+            if (k < visible && int64_t(offset) + k > INT32_MAX) return fail(MR_INVALID_SHAPE, "cache index overflows Int");
+            out[int64_t(pos) * width + k] = k < visible ? offset + k : -1;
+        }
+    }
+    return MR_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,19 @@
+// Internal helpers of the C-ABI layer: thread-local error text and checks.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+#include "../../include/minirun_hip.h"
+
+namespace mrc {
+
+mr_status fail(mr_status st, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+mr_status hip_fail(hipError_t e, const char* what);
+inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+inline bool aligned4(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 3u) == 0; }
+inline size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
+const char* dtype_name(mr_dtype d);
+
+}  // namespace mrc

@@ -49,4 +49,100 @@ hipError_t launch_validate_indices(const int32_t* indices, int32_t batch, int32_
 hipError_t launch_mla_decode(const DecodeParams& p, const CombineParams& cp, bool transpose_reads,
                              hipEvent_t const* events, hipStream_t st);
 
+// ---------------------------------------------------------------- affine
+struct AffineDequantParams {
+    const uint32_t* packed;
+    const void* scales;
+    const void* biases;
+    int scale_dtype;  // 0 bf16, 1 f16, 2 f32
+    int64_t out_features, in_features;
+    int group, bits;
+    void* out;
+    int out_f32;
+};
+
+// y[token m][row j] = sum_i x[m, xvec(j)][i] * W[wrow(j)][i]
+//   wrow(j) = (j / map_a) * map_b + map_c + (j % map_a),  xvec(j) = j / map_a
+struct AffineGemvParams {
+    const void* x;
+    int x_f32;
+    int64_t x_stride;  // elements between activation vectors
+    int m;             // tokens
+    const uint32_t* packed;
+    const void* scales;
+    const void* biases;
+    int scale_dtype;
+    int out_rows;
+    int in_features;
+    int group, bits;
+    int map_a;
+    int64_t map_b, map_c;
+    void* y;
+    int y_f32;
+    int64_t y_stride_row, y_stride_token;
+    int force_generic;
+};
+
+hipError_t launch_affine_dequant(const AffineDequantParams& p, hipStream_t st);
+bool affine_gemv_fast_ok(const AffineGemvParams& p);
+hipError_t launch_affine_gemv(const AffineGemvParams& p, hipStream_t st);
+
+// ---------------------------------------------------------------- block pieces
+struct RmsNormParams {
+    const void* x;
+    int x_f32;
+    int64_t x_stride;
+    const void* weight;
+    int w_f32;
+    void* out;
+    int out_f32;
+    int64_t out_stride;
+    int64_t rows;
+    int dim;
+    float eps;
+};
+
+struct RopeParams {
+    void* x;
+    int x_f32;
+    int64_t n_pos, inner, row_stride, col0;
+    int dim;
+    const float* cos_t;  // [n_pos, dim/2]
+    const float* sin_t;
+};
+
+struct CacheAppendParams {
+    const void* kv;  // [tokens, kv_rank + rope_dim]
+    int kv_f32;
+    int64_t kv_stride;
+    const void* norm_w;
+    int w_f32;
+    float eps;
+    int kv_rank, rope_dim;
+    const float* cos_t;  // [tokens, rope_dim/2]
+    const float* sin_t;
+    uint16_t* latent;
+    int64_t latent_stride;
+    uint16_t* rope;
+    int64_t rope_stride;
+    int64_t start_row, tokens;
+};
+
+struct AbsorbParams {
+    const uint16_t* q;  // [heads, q_head_stride], nope part first
+    int64_t q_head_stride;
+    const uint32_t* packed;  // kv_b [heads*(nope+v), kv_rank], 4-bit group 64
+    const void* scales;
+    const void* biases;
+    int scale_dtype;
+    int heads, nope_dim, v_dim, kv_rank;
+    uint16_t* q_lat;
+    int64_t q_lat_head_stride;
+};
+
+hipError_t launch_rmsnorm(const RmsNormParams& p, hipStream_t st);
+hipError_t launch_rope(const RopeParams& p, hipStream_t st);
+hipError_t launch_cache_append(const CacheAppendParams& p, hipStream_t st);
+hipError_t launch_absorb_q(const AbsorbParams& p, hipStream_t st);
+
 }  // namespace mr

@@ -52,6 +52,35 @@ class DecodeArgs(C.Structure):
     ]
 
 
+class AffineWeightDesc(C.Structure):
+    _fields_ = [
+        ("packed", C.c_void_p), ("scales", C.c_void_p), ("biases", C.c_void_p), ("scale_dtype", C.c_int),
+        ("out_features", C.c_int64), ("in_features", C.c_int64), ("group", C.c_int32), ("bits", C.c_int32),
+    ]
+
+
+class BlockArgs(C.Structure):
+    _fields_ = [
+        ("hidden", C.c_int32), ("q_lora_rank", C.c_int32), ("heads", C.c_int32), ("qk_nope_dim", C.c_int32),
+        ("qk_rope_dim", C.c_int32), ("v_head_dim", C.c_int32), ("kv_rank", C.c_int32),
+        ("eps", C.c_float), ("scale", C.c_float),
+        ("x", C.c_void_p), ("input_norm_w", C.c_void_p), ("q_a_norm_w", C.c_void_p), ("kv_a_norm_w", C.c_void_p),
+        ("norm_w_dtype", C.c_int),
+        ("q_a", AffineWeightDesc), ("q_b", AffineWeightDesc), ("kv_a", AffineWeightDesc), ("kv_b", AffineWeightDesc),
+        ("o_proj", AffineWeightDesc),
+        ("cache_latent", C.c_void_p), ("latent_row_stride", C.c_int64),
+        ("cache_rope", C.c_void_p), ("rope_row_stride", C.c_int64),
+        ("position", C.c_int32), ("capacity", C.c_int32),
+        ("rope_cos", C.c_void_p), ("rope_sin", C.c_void_p),
+        ("out", C.c_void_p),
+        ("workspace", C.c_void_p), ("workspace_bytes", C.c_size_t),
+    ]
+
+
+_P = C.c_void_p
+_I32P = C.POINTER(C.c_int32)
+_I64P = C.POINTER(C.c_int64)
+
 # Every symbol include/minirun_hip.h declares, with its ctypes signature.
 SIGNATURES = {
     "mr_version": (C.c_char_p, []),
@@ -61,6 +90,26 @@ SIGNATURES = {
     "mr_validate_indices_workspace_size": (C.c_size_t, [C.c_int32, C.c_int32]),
     "mr_validate_indices": (C.c_int, [C.c_void_p, C.c_int32, C.c_int32, C.c_int32, C.c_void_p, C.c_size_t,
                                       C.POINTER(C.c_int32), C.POINTER(C.c_int32), C.c_void_p]),
+    "mr_affine_validate": (C.c_int, [C.c_int, C.c_int32, _I64P, C.c_int, C.c_int32, _I64P, C.c_int, C.c_int32, _I64P,
+                                     C.c_int32, C.c_int32, _I64P, _I64P, _I64P]),
+    "mr_affine_dequantize": (C.c_int, [C.POINTER(AffineWeightDesc), _P, C.c_int, _P]),
+    "mr_affine_matmul": (C.c_int, [_P, C.c_int, C.c_int32, C.c_int64, C.POINTER(AffineWeightDesc), _P, C.c_int,
+                                   C.c_int64, _P]),
+    "mr_rmsnorm": (C.c_int, [_P, C.c_int, C.c_int64, C.c_int32, C.c_int64, _P, C.c_int, C.c_float, _P, C.c_int,
+                             C.c_int64, _P]),
+    "mr_rope_frequencies": (C.c_int, [C.c_int32, C.c_int32, C.c_double, C.c_double, C.c_double, C.c_double, _P]),
+    "mr_rope_table": (C.c_int, [_P, C.c_int64, _P, C.c_int32, C.c_int32, _P, _P]),
+    "mr_rope_apply": (C.c_int, [_P, C.c_int, C.c_int64, C.c_int64, C.c_int64, C.c_int64, C.c_int32, _P, _P, _P]),
+    "mr_mla_cache_append": (C.c_int, [_P, C.c_int, C.c_int64, C.c_int64, _P, C.c_int, C.c_float, C.c_int32, C.c_int32,
+                                      _P, _P, _P, C.c_int64, _P, C.c_int64, C.c_int64, _P]),
+    "mr_mla_absorb_query": (C.c_int, [_P, C.c_int64, C.c_int32, C.c_int32, C.c_int32, C.POINTER(AffineWeightDesc), _P,
+                                      C.c_int64, _P]),
+    "mr_mla_unabsorb_values": (C.c_int, [_P, C.c_int64, C.c_int32, C.c_int32, C.c_int32, C.POINTER(AffineWeightDesc),
+                                         _P, C.c_int, _P]),
+    "mr_mla_decode_block_workspace_size": (C.c_size_t, [C.POINTER(BlockArgs)]),
+    "mr_mla_decode_block": (C.c_int, [C.POINTER(BlockArgs), _P]),
+    "mr_attention_indices_window": (C.c_int, [C.c_int32, C.c_int32, C.c_int32, _P, _I32P, _I32P]),
+    "mr_attention_indices_compressed": (C.c_int, [C.c_int32, C.c_int32, C.c_int32, C.c_int32, _P, _I32P, _I32P]),
 }
 
 _lib = None
@@ -221,3 +270,190 @@ def validate_indices(indices, n_rows, stream=None):
     st = load().mr_validate_indices(_ptr(idx), B, K, int(n_rows), _ptr(ws), ws.numel(), C.byref(bt), C.byref(bp),
                                     _stream(stream))
     return st, bt.value, bp.value, (last_error() if st != OK else "")
+
+
+# ------------------------------------------------------------------ affine weights
+class AffineWeights:
+    """MLXBridge.AffineWeights (AffineWeights.swift:65-157) over device tensors.
+
+    packed: uint32 (torch.int32 storage) [out, in*bits/32]; scales, biases:
+    [out, in/group] bf16 / f16 / f32.  Construction validates through
+    mr_affine_validate, so the errors are the reference's.
+    """
+
+    def __init__(self, packed, scales, biases, group_size=64, bits=4):
+        torch = _torch()
+        dt = {torch.bfloat16: BF16, torch.float16: F16, torch.float32: F32}
+        sdt = dt.get(scales.dtype, 99)
+        bdt = dt.get(biases.dtype, 99)
+        pdt = U32 if packed.dtype in (torch.int32, torch.uint32) else (F32 if packed.dtype == torch.float32 else 99)
+        ps = (C.c_int64 * packed.dim())(*packed.shape)
+        ss = (C.c_int64 * scales.dim())(*scales.shape)
+        bs = (C.c_int64 * biases.dim())(*biases.shape)
+        ex, of, inf = C.c_int64(), C.c_int64(), C.c_int64()
+        _check(load().mr_affine_validate(pdt, packed.dim(), ps, sdt, scales.dim(), ss, bdt, biases.dim(), bs,
+                                         group_size, bits, C.byref(ex), C.byref(of), C.byref(inf)))
+        for t, n in ((packed, "packed"), (scales, "scales"), (biases, "biases")):
+            _need(t, n)
+            if not t.is_contiguous():
+                raise ValueError(f"{n} must be contiguous")
+        self.packed, self.scales, self.biases = packed, scales, biases
+        self.group_size, self.bits = group_size, bits
+        self.experts = ex.value or None
+        self.out_features, self.in_features = of.value, inf.value
+        self.scale_dtype = sdt
+
+    def desc(self):
+        return AffineWeightDesc(self.packed.data_ptr(), self.scales.data_ptr(), self.biases.data_ptr(),
+                                self.scale_dtype, self.out_features, self.in_features, self.group_size, self.bits)
+
+
+def affine_dequantize(w: AffineWeights, dtype=None, stream=None):
+    """affineDequantize (AffineWeights.swift:328-342): dense [out, in], f32 by default."""
+    torch = _torch()
+    out = torch.empty(w.out_features, w.in_features, dtype=dtype or torch.float32, device=w.packed.device)
+    _check(load().mr_affine_dequantize(C.byref(w.desc()), _ptr(out), _dtype_code(out.dtype), _stream(stream)))
+    return out
+
+
+def affine_mm(x, w: AffineWeights, out_dtype=None, stream=None):
+    """affineMM (AffineWeights.swift:239-254): x [tokens, in] -> [tokens, out]."""
+    torch = _torch()
+    _need(x, "x")
+    x2 = x if x.dim() == 2 else x.reshape(1, -1)
+    y = torch.empty(x2.shape[0], w.out_features, dtype=out_dtype or x.dtype, device=x.device)
+    _check(load().mr_affine_matmul(_ptr(x2), _dtype_code(x2.dtype), x2.shape[0], x2.stride(0), C.byref(w.desc()),
+                                   _ptr(y), _dtype_code(y.dtype), y.stride(0), _stream(stream)))
+    return y if x.dim() == 2 else y.reshape(w.out_features)
+
+
+def rms_norm(x, weight, eps=1e-6, out_dtype=None, stream=None):
+    """K3Norm.rms (Normalization.swift:15-19) over the last axis."""
+    torch = _torch()
+    _need(x, "x")
+    _need(weight, "weight")
+    x2 = x.reshape(-1, x.shape[-1])
+    out = torch.empty(x2.shape, dtype=out_dtype or x.dtype, device=x.device)
+    _check(load().mr_rmsnorm(_ptr(x2), _dtype_code(x2.dtype), x2.shape[0], x2.shape[1], x2.stride(0), _ptr(weight),
+                             _dtype_code(weight.dtype), eps, _ptr(out), _dtype_code(out.dtype), out.stride(0),
+                             _stream(stream)))
+    return out.reshape(x.shape)
+
+
+def rope_frequencies(dim, base=10000.0, original_len=0, factor=1.0, beta_fast=32.0, beta_slow=1.0):
+    import numpy as np
+
+    out = np.empty(dim // 2, np.float64)
+    _check(load().mr_rope_frequencies(dim, original_len, base, factor, beta_fast, beta_slow,
+                                      out.ctypes.data_as(C.c_void_p)))
+    return out
+
+
+def rope_table(positions, freqs, inverse=False):
+    import numpy as np
+
+    pos = np.ascontiguousarray(positions, np.int64)
+    half = len(freqs)
+    cos = np.empty((pos.size, half), np.float32)
+    sin = np.empty((pos.size, half), np.float32)
+    _check(load().mr_rope_table(pos.ctypes.data_as(C.c_void_p), pos.size,
+                                np.ascontiguousarray(freqs, np.float64).ctypes.data_as(C.c_void_p), half, int(inverse),
+                                cos.ctypes.data_as(C.c_void_p), sin.ctypes.data_as(C.c_void_p)))
+    return cos, sin
+
+
+def rope_apply_(x, cos_t, sin_t, col0, dim, stream=None):
+    """DeepSeekV4Rotary.apply in place on x [n_pos, inner..., row] (device tables)."""
+    _need(x, "x")
+    n_pos = x.shape[0]
+    inner = 1
+    for d in x.shape[1:-1]:
+        inner *= d
+    _check(load().mr_rope_apply(_ptr(x), _dtype_code(x.dtype), n_pos, inner, x.shape[-1], col0, dim, _ptr(cos_t),
+                                _ptr(sin_t), _stream(stream)))
+    return x
+
+
+def mla_cache_append(kv, norm_w, eps, cos_t, sin_t, latent, rope, start_row, kv_rank=512, rope_dim=64, stream=None):
+    _need(kv, "kv")
+    kv2 = kv.reshape(-1, kv.shape[-1])
+    _check(load().mr_mla_cache_append(_ptr(kv2), _dtype_code(kv2.dtype), kv2.stride(0), kv2.shape[0], _ptr(norm_w),
+                                      _dtype_code(norm_w.dtype), eps, kv_rank, rope_dim, _ptr(cos_t), _ptr(sin_t),
+                                      _ptr(latent), latent.stride(0), _ptr(rope), rope.stride(0), start_row,
+                                      _stream(stream)))
+
+
+def mla_absorb_query(q, heads, nope_dim, v_dim, kv_b: AffineWeights, stream=None):
+    torch = _torch()
+    q_lat = torch.empty(heads, 512, dtype=torch.bfloat16, device=q.device)
+    _check(load().mr_mla_absorb_query(_ptr(q), q.stride(0), heads, nope_dim, v_dim, C.byref(kv_b.desc()), _ptr(q_lat),
+                                      512, _stream(stream)))
+    return q_lat
+
+
+def mla_unabsorb_values(ctx, heads, nope_dim, v_dim, kv_b: AffineWeights, out_dtype=None, stream=None):
+    torch = _torch()
+    out = torch.empty(heads, v_dim, dtype=out_dtype or torch.bfloat16, device=ctx.device)
+    _check(load().mr_mla_unabsorb_values(_ptr(ctx), ctx.stride(0), heads, nope_dim, v_dim, C.byref(kv_b.desc()),
+                                         _ptr(out), _dtype_code(out.dtype), _stream(stream)))
+    return out
+
+
+def block_args(x, weights, cache, position, rope_cos, rope_sin, out, *, hidden=7168, q_lora_rank=1536, heads=128,
+               nope=128, rope=64, v=128, kv_rank=512, eps=1e-6, scale=None, workspace=None):
+    """Fill BlockArgs; `weights` is a dict with input_norm, q_a_norm, kv_a_norm
+    (tensors) and q_a, q_b, kv_a, kv_b, o_proj (AffineWeights)."""
+    torch = _torch()
+    a = BlockArgs()
+    a.hidden, a.q_lora_rank, a.heads, a.qk_nope_dim, a.qk_rope_dim, a.v_head_dim, a.kv_rank = \
+        hidden, q_lora_rank, heads, nope, rope, v, kv_rank
+    a.eps = eps
+    a.scale = scale if scale is not None else (nope + rope) ** -0.5
+    a.x = x.data_ptr()
+    a.input_norm_w = weights["input_norm"].data_ptr() if weights.get("input_norm") is not None else None
+    a.q_a_norm_w = weights["q_a_norm"].data_ptr()
+    a.kv_a_norm_w = weights["kv_a_norm"].data_ptr()
+    a.norm_w_dtype = _dtype_code(weights["q_a_norm"].dtype)
+    for n in ("q_a", "q_b", "kv_a", "kv_b", "o_proj"):
+        setattr(a, n, weights[n].desc())
+    a.cache_latent, a.latent_row_stride = cache.data_ptr(), cache.stride(0)
+    a.cache_rope, a.rope_row_stride = cache[:, kv_rank:].data_ptr(), cache.stride(0)
+    a.position, a.capacity = position, cache.shape[0]
+    a.rope_cos, a.rope_sin = rope_cos.data_ptr(), rope_sin.data_ptr()
+    a.out = out.data_ptr()
+    need = load().mr_mla_decode_block_workspace_size(C.byref(a))
+    if workspace is None:
+        workspace = torch.empty(need, dtype=torch.uint8, device=x.device)
+    a.workspace, a.workspace_bytes = workspace.data_ptr(), workspace.numel()
+    return a, workspace
+
+
+def mla_decode_block(x, weights, cache, position, rope_cos, rope_sin, stream=None, **kw):
+    """K3MLA.forwardWithoutTrace for one decode token with affine projections."""
+    torch = _torch()
+    out = torch.empty(kw.get("hidden", 7168), dtype=torch.bfloat16, device=x.device)
+    a, ws = block_args(x, weights, cache, position, rope_cos, rope_sin, out, **kw)
+    _check(load().mr_mla_decode_block(C.byref(a), _stream(stream)))
+    return out
+
+
+def attention_indices_window(window, seq_len, start_pos):
+    import numpy as np
+
+    n = max(seq_len * min(seq_len, window), window, 1)
+    out = np.empty(n, np.int32)
+    r, c = C.c_int32(), C.c_int32()
+    _check(load().mr_attention_indices_window(window, seq_len, start_pos, out.ctypes.data_as(C.c_void_p), C.byref(r),
+                                              C.byref(c)))
+    return out[: r.value * c.value].reshape(r.value, c.value)
+
+
+def attention_indices_compressed(ratio, seq_len, start_pos, offset):
+    import numpy as np
+
+    width = max(seq_len // max(ratio, 1), (start_pos + 1) // max(ratio, 1), 1)
+    out = np.empty(max(seq_len, 1) * width, np.int32)
+    r, c = C.c_int32(), C.c_int32()
+    _check(load().mr_attention_indices_compressed(ratio, seq_len, start_pos, offset, out.ctypes.data_as(C.c_void_p),
+                                                  C.byref(r), C.byref(c)))
+    return out[: r.value * c.value].reshape(r.value, c.value)

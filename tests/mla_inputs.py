@@ -51,3 +51,77 @@ def within_tolerance(got, ref, atol=1e-2, rtol=2e-2):
     ok = err <= atol + rtol * np.abs(ref)
     scale_err = err.max() / max(np.abs(ref).max(), 1e-30)
     return bool(ok.all()), float(err.max()), float(scale_err)
+
+
+# ---------------------------------------------------------------- config 5: the block
+def affine_weight(tag, out, inp, group=64):
+    """MLX affine 4-bit operand: nibbles U{0..15}, scales |N(0,0.01)|, biases N(0,0.01), bf16."""
+    packed = O.u32(f"{tag}.packed", (out, inp // 8))
+    scales = O.abs_normal_bf16(f"{tag}.scales", (out, inp // group), std=0.01)
+    biases = O.normal_bf16(f"{tag}.biases", (out, inp // group), std=0.01)
+    return packed, scales, biases
+
+
+BLOCK_DIMS = dict(hidden=7168, q_lora_rank=1536, heads=128, nope=128, rope=64, v=128, kv_rank=512)
+
+
+def block_inputs(ctx=32768, tag="c5", hidden=7168, q_lora_rank=1536, heads=128, nope=128, rope=64, v=128,
+                 kv_rank=512):
+    """One decode token at position ctx-1 over a cache whose rows 0..ctx-2
+    are written (roped at their positions); row ctx-1 is written by the block."""
+    norm = lambda name, n: O.f32_to_bf16(1 + 0.02 * O.bf16_to_f32(O.normal_bf16(f"{tag}.{name}", (n,))))
+    d = {
+        "x": O.normal_bf16(f"{tag}.x", (hidden,)),
+        "input_norm": norm("input_norm", hidden),
+        "q_a_norm": norm("q_a_norm", q_lora_rank),
+        "kv_a_norm": norm("kv_a_norm", kv_rank),
+        "q_a": affine_weight(f"{tag}.q_a", q_lora_rank, hidden),
+        "q_b": affine_weight(f"{tag}.q_b", heads * (nope + rope), q_lora_rank),
+        "kv_a": affine_weight(f"{tag}.kv_a", kv_rank + rope, hidden),
+        "kv_b": affine_weight(f"{tag}.kv_b", heads * (nope + v), kv_rank),
+        "o_proj": affine_weight(f"{tag}.o_proj", hidden, heads * v),
+    }
+    cache = O.normal_bf16(f"{tag}.cache", (ctx, kv_rank + rope), std=0.5)
+    cache = rope_rows(cache.reshape(ctx, 1, kv_rank + rope), np.arange(ctx)).reshape(ctx, kv_rank + rope)
+    cache[ctx - 1] = 0
+    d["cache"] = cache
+    d["position"] = ctx - 1
+    return d
+
+
+def _bf(a):
+    return O.bf16_to_f32(O.f32_to_bf16(np.asarray(a, np.float32)))
+
+
+def _mm(x, w):
+    packed, s, b = w
+    return O.affine_matmul(np.asarray(x, np.float32)[None], packed, s, b, acc=1)[0]
+
+
+def block_reference(d, hidden=7168, q_lora_rank=1536, heads=128, nope=128, rope=64, v=128, kv_rank=512, eps=1e-6):
+    """The block on the oracle, rounding to bf16 where the HIP path stores
+    bf16 (every projection output, the normed activations, the cache row).
+    Returns (out [hidden] f32 of bf16 values, the written cache row)."""
+    f = O.bf16_to_f32
+    pos = d["position"]
+    freqs = O.rope_frequencies(rope)
+    cos, sin = O.rope_table([pos], freqs)
+    h = _bf(O.rmsnorm(f(d["x"])[None], f(d["input_norm"]), eps)[0])
+    q_lora = _bf(_mm(h, d["q_a"]))
+    q_lora_n = _bf(O.rmsnorm(q_lora[None], f(d["q_a_norm"]), eps)[0])
+    q = O.f32_to_bf16(_mm(q_lora_n, d["q_b"])).reshape(heads, nope + rope)
+    q = O.rope_apply_bf16(q.reshape(1, heads, nope + rope), cos, sin, nope, rope).reshape(heads, nope + rope)
+    kvb = O.affine_dequantize(*d["kv_b"]).reshape(heads, nope + v, kv_rank).astype(np.float64)
+    q_lat = O.f32_to_bf16(np.einsum("hd,hdr->hr", f(q[:, :nope]).astype(np.float64), kvb[:, :nope]).astype(np.float32))
+    kv = O.f32_to_bf16(_mm(h, d["kv_a"]))
+    row = np.empty(kv_rank + rope, np.uint16)
+    row[:kv_rank] = O.f32_to_bf16(O.rmsnorm(f(kv[:kv_rank])[None], f(d["kv_a_norm"]), eps)[0])
+    row[kv_rank:] = O.rope_apply_bf16(kv[kv_rank:].reshape(1, 1, rope), cos, sin, 0, rope).reshape(rope)
+    cache = d["cache"].copy()
+    cache[pos] = row
+    ctx = O.mla_decode(q_lat, q[:, nope:], cache[: pos + 1], kv_rank=kv_rank, rope_dim=rope,
+                       scale=(nope + rope) ** -0.5)[0]
+    ctx = _bf(ctx).astype(np.float64)
+    attn = _bf(np.einsum("hr,hvr->hv", ctx, kvb[:, nope:]).astype(np.float32))
+    out = _bf(_mm(attn.reshape(-1), d["o_proj"]))
+    return out, row

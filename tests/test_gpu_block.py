@@ -1,0 +1,231 @@
+"""Parity of the HIP projection path against the oracle: affine dequantize
+(bit-exact in f32), the fused dequant-GEMV (tolerance), RMSNorm, RoPE,
+the latent-cache append, query absorption / value un-absorption and the
+whole decode block of the fifth workload (hidden 7168, 128 heads, 32K
+context, 4-bit group-64 affine projections).
+
+Bars: bit-exact where the arithmetic is exact or identical by construction
+(dequantized weights, rotary on bf16 inputs); otherwise the workload bar
+|hip - oracle| <= 1e-2 + 2e-2 |oracle| plus an output-scale error bound.
+"""
+import numpy as np
+import pytest
+
+import mla_inputs as MI
+import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def M():
+    import minirun_hip as M
+
+    M.load()
+    return M
+
+
+def dev(a):
+    import torch
+
+    t = torch.from_numpy(np.ascontiguousarray(a))
+    if a.dtype == np.uint16:
+        t = t.view(torch.bfloat16)
+    elif a.dtype == np.uint32:
+        t = t.view(torch.int32)
+    return t.cuda()
+
+
+def f32(t):
+    return t.float().cpu().numpy()
+
+
+def bits16(t):
+    import torch
+
+    return t.cpu().view(torch.int16).numpy().view(np.uint16)
+
+
+def sync():
+    import torch
+
+    torch.cuda.synchronize()
+
+
+def check(got, ref, tag, scale_bar=1e-2):
+    ok, maxerr, scale_err = MI.within_tolerance(got, ref)
+    print(f"{tag}: max|d|={maxerr:.3e} scale_err={scale_err:.3e}", flush=True)
+    assert ok, f"{tag}: elementwise tolerance violated (max |d| {maxerr})"
+    assert scale_err < scale_bar, f"{tag}: output-scale error {scale_err}"
+
+
+def weights(M, w):
+    return M.AffineWeights(dev(w[0]), dev(w[1]), dev(w[2]))
+
+
+# ---------------------------------------------------------------- dequantize
+@pytest.mark.parametrize("bits,group,sdt", [(4, 64, O.BF16), (4, 32, O.F16), (8, 64, O.BF16), (2, 64, O.F32)])
+def test_dequantize_bit_exact(M, bits, group, sdt):
+    print(f"dequant bits={bits} group={group} sdt={sdt}", flush=True)
+    import torch
+
+    out_f, in_f = 96, 512
+    packed = O.u32(f"dq{bits}.p", (out_f, in_f * bits // 32))
+    if sdt == O.F32:
+        s = O.bf16_to_f32(O.abs_normal_bf16("dq.s", (out_f, in_f // group), std=0.01)) * 1.37
+        b = O.bf16_to_f32(O.normal_bf16("dq.b", (out_f, in_f // group), std=0.01)) * 0.71
+        s, b = s.astype(np.float32), b.astype(np.float32)
+        ts, tb = torch.from_numpy(s).cuda(), torch.from_numpy(b).cuda()
+    else:
+        s = O.abs_normal_bf16("dq.s", (out_f, in_f // group), std=0.01)
+        b = O.normal_bf16("dq.b", (out_f, in_f // group), std=0.01)
+        if sdt == O.F16:
+            s = np.float16(O.bf16_to_f32(s)).view(np.uint16)
+            b = np.float16(O.bf16_to_f32(b)).view(np.uint16)
+            ts, tb = torch.from_numpy(s).view(torch.float16).cuda(), torch.from_numpy(b).view(torch.float16).cuda()
+        else:
+            ts, tb = dev(s), dev(b)
+    w = M.AffineWeights(dev(packed), ts, tb, group_size=group, bits=bits)
+    got = M.affine_dequantize(w)
+    got_bf = M.affine_dequantize(w, dtype=torch.bfloat16)
+    sync()
+    ref = O.affine_dequantize(packed, s, b, group=group, bits=bits, scale_dtype=sdt)
+    np.testing.assert_array_equal(got.cpu().numpy().view(np.uint32), ref.view(np.uint32))
+    np.testing.assert_array_equal(bits16(got_bf), O.f32_to_bf16(ref))
+
+
+# ---------------------------------------------------------------- GEMV
+@pytest.mark.parametrize("name,out_f,in_f", [("q_a", 1536, 7168), ("q_b", 24576, 1536), ("kv_a", 576, 7168),
+                                             ("o_proj", 7168, 16384), ("kv_b", 32768, 512)])
+def test_affine_gemv_config5_shapes(M, name, out_f, in_f):
+    print(f"gemv {name} {out_f}x{in_f}", flush=True)
+    import torch
+
+    w = MI.affine_weight(f"gv.{name}", out_f, in_f)
+    x = O.normal_bf16(f"gv.{name}.x", (in_f,))
+    ref = O.affine_matmul(O.bf16_to_f32(x)[None], *w, acc=1)[0]
+    y = M.affine_mm(dev(x), weights(M, w), out_dtype=torch.float32)
+    sync()
+    check(f32(y), ref, f"gemv-{name}", scale_bar=1e-4)
+
+
+def test_affine_matmul_generic_paths(M):
+    print("gemv generic: 3 tokens, f32 x, 8-bit, f16 scales", flush=True)
+    import torch
+
+    out_f, in_f = 200, 384
+    packed = O.u32("gg.p", (out_f, in_f * 8 // 32))
+    s = np.float16(O.bf16_to_f32(O.abs_normal_bf16("gg.s", (out_f, in_f // 64), std=0.001))).view(np.uint16)
+    b = np.float16(O.bf16_to_f32(O.normal_bf16("gg.b", (out_f, in_f // 64), std=0.01))).view(np.uint16)
+    w = M.AffineWeights(dev(packed), torch.from_numpy(s).view(torch.float16).cuda(),
+                        torch.from_numpy(b).view(torch.float16).cuda(), group_size=64, bits=8)
+    x = O.bf16_to_f32(O.normal_bf16("gg.x", (3, in_f)))
+    y = M.affine_mm(torch.from_numpy(x).cuda(), w, out_dtype=torch.float32)
+    sync()
+    ref = O.affine_matmul(x, packed, s, b, group=64, bits=8, scale_dtype=O.F16, acc=1)
+    check(f32(y), ref, "gemv-generic", scale_bar=1e-5)
+
+
+# ---------------------------------------------------------------- norm / rope / append
+def test_rmsnorm(M):
+    print("rmsnorm", flush=True)
+    import torch
+
+    x = O.normal_bf16("rn.x", (5, 7168))
+    w = O.f32_to_bf16(1 + 0.02 * O.bf16_to_f32(O.normal_bf16("rn.w", (7168,))))
+    got = M.rms_norm(dev(x), dev(w), 1e-6, out_dtype=torch.float32)
+    sync()
+    ref = O.rmsnorm(O.bf16_to_f32(x), O.bf16_to_f32(w), 1e-6)
+    np.testing.assert_allclose(f32(got), ref, rtol=2e-6, atol=1e-6)
+
+
+def test_rope_apply_bit_exact(M):
+    print("rope apply", flush=True)
+    import torch
+
+    q = O.normal_bf16("ra.q", (3, 128, 192))
+    pos = np.array([0, 4095, 32767])
+    f = M.rope_frequencies(64)
+    c, s = M.rope_table(pos, f)
+    t = dev(q)
+    M.rope_apply_(t, torch.from_numpy(c).cuda(), torch.from_numpy(s).cuda(), 128, 64)
+    sync()
+    exp = O.rope_apply_bf16(q, c, s, 128, 64)
+    np.testing.assert_array_equal(bits16(t), exp)
+
+
+def test_cache_append(M):
+    print("cache append", flush=True)
+    import torch
+
+    T = 3
+    kv = O.normal_bf16("ca.kv", (T, 576))
+    w = O.f32_to_bf16(1 + 0.02 * O.bf16_to_f32(O.normal_bf16("ca.w", (512,))))
+    pos = np.array([10, 11, 12])
+    c, s = M.rope_table(pos, M.rope_frequencies(64))
+    cache = dev(np.zeros((20, 576), np.uint16))
+    M.mla_cache_append(dev(kv), dev(w), 1e-6, torch.from_numpy(c).cuda(), torch.from_numpy(s).cuda(), cache[:, :512],
+                       cache[:, 512:], start_row=10)
+    sync()
+    got = bits16(cache)
+    lat = O.f32_to_bf16(O.rmsnorm(O.bf16_to_f32(kv[:, :512]), O.bf16_to_f32(w), 1e-6))
+    rk = O.rope_apply_bf16(kv[:, 512:].reshape(T, 1, 64), c, s, 0, 64).reshape(T, 64)
+    assert (got[:10] == 0).all() and (got[13:] == 0).all()
+    np.testing.assert_array_equal(got[10:13, 512:], rk)
+    # latent: fp32 sum order differs -> at most one bf16 ulp
+    d = np.abs(got[10:13, :512].astype(np.int32) - lat.astype(np.int32))
+    assert d.max() <= 1, d.max()
+
+
+def test_absorb_and_unabsorb(M):
+    print("absorb / unabsorb", flush=True)
+    import torch
+
+    H, dn, dv = 128, 128, 128
+    kvb = MI.affine_weight("ab.kvb", H * (dn + dv), 512)
+    q = O.normal_bf16("ab.q", (H, 192))
+    w = weights(M, kvb)
+    q_lat = M.mla_absorb_query(dev(q), H, dn, dv, w)
+    ctx = O.normal_bf16("ab.ctx", (H, 512), std=0.05)
+    out = M.mla_unabsorb_values(dev(ctx), H, dn, dv, w, out_dtype=torch.float32)
+    sync()
+    W = O.affine_dequantize(*kvb).reshape(H, dn + dv, 512).astype(np.float64)
+    ref_lat = np.einsum("hd,hdr->hr", O.bf16_to_f32(q[:, :dn]).astype(np.float64), W[:, :dn])
+    check(f32(q_lat), ref_lat, "absorb", scale_bar=1e-2)
+    ref_out = np.einsum("hr,hvr->hv", O.bf16_to_f32(ctx).astype(np.float64), W[:, dn:])
+    check(f32(out), ref_out, "unabsorb", scale_bar=1e-4)
+
+
+# ---------------------------------------------------------------- the block
+def run_block(M, d, **dims):
+    import torch
+
+    w = {k: dev(d[k]) for k in ("input_norm", "q_a_norm", "kv_a_norm")}
+    for k in ("q_a", "q_b", "kv_a", "kv_b", "o_proj"):
+        w[k] = weights(M, d[k])
+    cache = dev(d["cache"])
+    c, s = M.rope_table([d["position"]], M.rope_frequencies(dims.get("rope", 64)))
+    out = M.mla_decode_block(dev(d["x"]), w, cache, d["position"], torch.from_numpy(c).cuda(),
+                             torch.from_numpy(s).cuda(), **dims)
+    sync()
+    return out, cache
+
+
+def test_block_config5_full(M):
+    print("block config5 hidden=7168 H=128 ctx=32768", flush=True)
+    d = MI.block_inputs()
+    out, cache = run_block(M, d)
+    ref, row = MI.block_reference(d)
+    got_row = bits16(cache)[d["position"]]
+    np.testing.assert_array_equal(got_row[512:], row[512:])   # rotary key: bit-exact
+    assert np.abs(got_row[:512].astype(np.int32) - row[:512].astype(np.int32)).max() <= 1
+    check(f32(out), ref, "block-config5", scale_bar=1e-2)
+
+
+def test_block_small_context_and_first_token(M):
+    print("block small: position 0 and 70", flush=True)
+    for ctx in (1, 71):
+        d = MI.block_inputs(ctx=ctx, tag=f"b{ctx}")
+        out, _ = run_block(M, d)
+        ref, _ = MI.block_reference(d)
+        check(f32(out), ref, f"block-ctx{ctx}", scale_bar=1e-2)

@@ -1,0 +1,110 @@
+"""Host-side entry points of the C-ABI, checked on the CPU against the oracle
+and the reference's stated rules: AffineWeights validation (order and
+messages, AffineWeights.swift:84-157), rotary frequencies and tables
+(DeepSeekV4Attention.swift:28-149, bit-exact) and the V4 index tables
+(DeepSeekV4Attention.swift:169-237, bit-exact)."""
+import ctypes as C
+
+import numpy as np
+import pytest
+
+import minirun_hip as M
+import oracle as O
+
+
+def validate(pdt=M.U32, ps=(1536, 896), sdt=M.BF16, ss=(1536, 112), bdt=None, bs=None, group=64, bits=4):
+    bdt = sdt if bdt is None else bdt
+    bs = ss if bs is None else bs
+    arr = lambda s: (C.c_int64 * len(s))(*s)
+    ex, of, inf = C.c_int64(), C.c_int64(), C.c_int64()
+    st = M.load().mr_affine_validate(pdt, len(ps), arr(ps), sdt, len(ss), arr(ss), bdt, len(bs), arr(bs), group, bits,
+                                     C.byref(ex), C.byref(of), C.byref(inf))
+    return st, M.last_error() if st else "", (ex.value, of.value, inf.value)
+
+
+def test_affine_validate_accepts_config_shapes():
+    for out, inp in [(1536, 7168), (24576, 1536), (576, 7168), (7168, 16384), (32768, 512)]:
+        st, _, geo = validate(ps=(out, inp // 8), ss=(out, inp // 64))
+        assert st == M.OK and geo == (0, out, inp)
+    st, _, geo = validate(ps=(8, 64, 32), ss=(8, 64, 4))
+    assert st == M.OK and geo == (8, 64, 256)
+
+
+@pytest.mark.parametrize(
+    "kw,status,needle",
+    [
+        (dict(pdt=M.F32), M.INVALID_DTYPE, "must be .uint32"),
+        (dict(sdt=M.I32), M.INVALID_DTYPE, "must be a floating-point type"),
+        (dict(sdt=M.BF16, bdt=M.F16), M.INVALID_DTYPE, "scales are bfloat16 but biases are float16"),
+        (dict(bs=(1536, 111)), M.INVALID_SHAPE, "must have one shape"),
+        (dict(ps=(1536,), ss=(1536,)), M.INVALID_SHAPE, "rank 2 (one matrix) or rank 3"),
+        (dict(bits=3), M.INVALID_SHAPE, "bits 3 must divide 32"),
+        (dict(group=0), M.INVALID_SHAPE, "group size must be positive"),
+        (dict(ps=(4, 1536, 896), ss=(5, 1536, 112)), M.INVALID_SHAPE, "expert count differs: packed has 4, scales has 5"),
+        (dict(ss=(1535, 112)), M.INVALID_SHAPE, "row count differs: packed has 1536, scales has 1535"),
+        (dict(ps=(1536, 895)), M.INVALID_SHAPE, "inFeatures 7160 is not a multiple of the group size 64"),
+        (dict(ss=(1536, 111)), M.INVALID_SHAPE, "group count differs: 7168 input features at group size 64 need 112"),
+    ],
+)
+def test_affine_validate_errors_in_reference_order(kw, status, needle):
+    st, msg, _ = validate(**kw)
+    assert st == status and needle in msg, (st, msg)
+    # the oracle's shape rules agree where they overlap
+    if status == M.INVALID_SHAPE and set(kw) == {"ss"} and kw["ss"][0] == 1536:
+        ost, _ = O.affine_validate(1536, 896, kw["ss"][1], kw.get("group", 64), kw.get("bits", 4))
+        assert ost == O.INVALID_SHAPE
+
+
+def test_validation_order_dtype_before_shape():
+    # both the dtype and the shape are wrong: the dtype error is reported
+    st, msg, _ = validate(sdt=M.BF16, bdt=M.F32, bs=(3, 3))
+    assert st == M.INVALID_DTYPE
+
+
+@pytest.mark.parametrize("dim,orig,base,factor", [(64, 0, 10000.0, 1.0), (64, 4096, 10000.0, 40.0),
+                                                   (128, 65536, 50000.0, 16.0), (16, 0, 1e6, 1.0)])
+def test_rope_frequencies_bit_exact(dim, orig, base, factor):
+    a = M.rope_frequencies(dim, base=base, original_len=orig, factor=factor)
+    b = O.rope_frequencies(dim, base=base, original_len=orig, factor=factor)
+    np.testing.assert_array_equal(a, b)
+
+
+def test_rope_table_bit_exact_and_errors():
+    f = M.rope_frequencies(64)
+    pos = np.array([0, 1, 2, 511, 32767, 131071, 1 << 20])
+    for inv in (False, True):
+        c1, s1 = M.rope_table(pos, f, inverse=inv)
+        c2, s2 = O.rope_table(pos, f, inverse=inv)
+        np.testing.assert_array_equal(c1, c2)
+        np.testing.assert_array_equal(s1, s2)
+    with pytest.raises(M.MRError) as e:
+        M.rope_table([3, -1], f)
+    assert "cannot be negative" in e.value.message
+    with pytest.raises(M.MRError) as e:
+        M.rope_frequencies(63)
+    assert "positive and even" in e.value.message
+
+
+@pytest.mark.parametrize("window,seq,start", [(4, 1, 5), (4, 1, 3), (4, 1, 2), (3, 5, 0), (128, 1, 130000),
+                                              (128, 300, 0), (7, 1, 6), (1, 3, 0)])
+def test_window_indices_bit_exact(window, seq, start):
+    st, exp = O.window_indices(window, seq, start)
+    assert st == O.OK
+    np.testing.assert_array_equal(M.attention_indices_window(window, seq, start), exp)
+
+
+@pytest.mark.parametrize("ratio,seq,start,off", [(4, 1, 9, 100), (4, 1, 2, 100), (2, 5, 0, 7), (128, 1, 131071, 128),
+                                                 (4, 333, 0, 128), (1, 4, 0, 0)])
+def test_compressed_indices_bit_exact(ratio, seq, start, off):
+    st, exp = O.compressed_indices(ratio, seq, start, off)
+    assert st == O.OK
+    np.testing.assert_array_equal(M.attention_indices_compressed(ratio, seq, start, off), exp)
+
+
+def test_index_table_errors():
+    with pytest.raises(M.MRError) as e:
+        M.attention_indices_window(4, 2, 1)
+    assert "exactly one token" in e.value.message
+    with pytest.raises(M.MRError) as e:
+        M.attention_indices_compressed(0, 2, 0, 0)
+    assert e.value.status == M.INVALID_SHAPE
