@@ -16,6 +16,11 @@
 
 #include "mr_kernels.hpp"
 
+// Products and sums below round exactly as written: hipcc contracts a*b+c
+// into one FMA by default, which changes dequantized weights whenever the
+// product is inexact (f32 scales).  FMAs are spelled fmaf where intended.
+#pragma clang fp contract(off)
+
 namespace mr {
 
 namespace {
@@ -50,7 +55,7 @@ __global__ void __launch_bounds__(256) affine_dequant_kernel(AffineDequantParams
             const float s = load_scale<SDT>(p.scales, gi);
             const float b = load_scale<SDT>(p.biases, gi);
             const float q = (float)((word >> (p.bits * j)) & mask);
-            const float v = __fadd_rn(__fmul_rn(s, q), b);
+            const float v = add_rn(mul_rn(s, q), b);
             const int64_t oi = o * p.in_features + i;
             if (p.out_f32)
                 ((float*)p.out)[oi] = v;
@@ -132,12 +137,13 @@ __global__ void __launch_bounds__(GEMV_THREADS) affine_gemv4_kernel(AffineGemvPa
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
                     const uint32_t pr = ((word >> (4 * j)) & 0x000F000Fu) | 0x43004300u;
-                    d = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2v, pr),
-                                                       __builtin_bit_cast(bf16x2v, xv[k][j]), d, false);
+                    const uint32_t xw = xv[k][j];  // bit_cast of a vector-element lvalue reads element 0
+                    d = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2v, pr), __builtin_bit_cast(bf16x2v, xw),
+                                                       d, false);
                 }
             }
             // sum x (128 + q) = d  ->  sum x q = d - 128 sum x
-            acc[r] += s * d + (bb - 128.f * s) * xsum;
+            acc[r] = fmaf(s, d, fmaf(bb - 128.f * s, xsum, acc[r]));
         }
     }
 #pragma unroll
@@ -176,7 +182,7 @@ __global__ void __launch_bounds__(256) affine_gemv_generic_kernel(AffineGemvPara
         const float q = (float)((word >> (p.bits * (i % per))) & mask);
         const float s = load_scale<SDT>(p.scales, wr * groups + i / p.group);
         const float b = load_scale<SDT>(p.biases, wr * groups + i / p.group);
-        const float wv = __fadd_rn(__fmul_rn(s, q), b);
+        const float wv = add_rn(mul_rn(s, q), b);
         acc = fmaf(load_act(p.x, p.x_f32, (int64_t)xrow * p.x_stride + i), wv, acc);
     }
     acc = wave_sum(acc);

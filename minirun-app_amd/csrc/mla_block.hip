@@ -5,6 +5,10 @@
 
 #include "mr_kernels.hpp"
 
+// Arithmetic rounds as written (no a*b+c contraction): the rotary and the
+// normalisation follow the reference's separate fp32 operations.
+#pragma clang fp contract(off)
+
 namespace mr {
 
 namespace {
@@ -64,8 +68,8 @@ __global__ void __launch_bounds__(256) rope_kernel(RopeParams p) {
         const float o = ld(p.x, p.x_f32, base + 1);
         const float c = p.cos_t[pos * half + i];
         const float s = p.sin_t[pos * half + i];
-        const float re = __fsub_rn(__fmul_rn(e, c), __fmul_rn(o, s));
-        const float im = __fadd_rn(__fmul_rn(e, s), __fmul_rn(o, c));
+        const float re = sub_rn(mul_rn(e, c), mul_rn(o, s));
+        const float im = add_rn(mul_rn(e, s), mul_rn(o, c));
         st(p.x, p.x_f32, base, re);
         st(p.x, p.x_f32, base + 1, im);
     }
@@ -98,8 +102,8 @@ __global__ void __launch_bounds__(256) cache_append_kernel(CacheAppendParams p) 
         const float o = ld(p.kv, p.kv_f32, t * p.kv_stride + p.kv_rank + 2 * i + 1);
         const float c = p.cos_t[t * half + i];
         const float s = p.sin_t[t * half + i];
-        rk[2 * i] = f32_to_bf16_bits(__fsub_rn(__fmul_rn(e, c), __fmul_rn(o, s)));
-        rk[2 * i + 1] = f32_to_bf16_bits(__fadd_rn(__fmul_rn(e, s), __fmul_rn(o, c)));
+        rk[2 * i] = f32_to_bf16_bits(sub_rn(mul_rn(e, c), mul_rn(o, s)));
+        rk[2 * i + 1] = f32_to_bf16_bits(add_rn(mul_rn(e, s), mul_rn(o, c)));
     }
 }
 
@@ -130,7 +134,7 @@ __global__ void __launch_bounds__(256) absorb_q_kernel(AbsorbParams p) {
         const float qn = bf16_bits_to_f32(p.q[(int64_t)h * p.q_head_stride + d]);
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
-            const float wv = __fadd_rn(__fmul_rn(s, (float)((word >> (4 * j)) & 15u)), b);
+            const float wv = add_rn(mul_rn(s, (float)((word >> (4 * j)) & 15u)), b);
             acc[j] = fmaf(qn, wv, acc[j]);
         }
     }

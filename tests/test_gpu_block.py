@@ -6,7 +6,11 @@ context, 4-bit group-64 affine projections).
 
 Bars: bit-exact where the arithmetic is exact or identical by construction
 (dequantized weights, rotary on bf16 inputs); otherwise the workload bar
-|hip - oracle| <= 1e-2 + 2e-2 |oracle| plus an output-scale error bound.
+|hip - oracle| <= 1e-2 + 2e-2 |oracle| plus an output-scale error bound per
+kernel, and for the composed block (five bf16-rounded stages) the chain bar
+of mla_inputs.within_block_tolerance.  Affine weights come in two kinds: the
+block workload's own (biases N(0,0.01), a large common-mode term) and
+centred ones, which leave the attention visible in the block's output.
 """
 import numpy as np
 import pytest
@@ -95,18 +99,19 @@ def test_dequantize_bit_exact(M, bits, group, sdt):
 
 
 # ---------------------------------------------------------------- GEMV
+@pytest.mark.parametrize("centred", [False, True])
 @pytest.mark.parametrize("name,out_f,in_f", [("q_a", 1536, 7168), ("q_b", 24576, 1536), ("kv_a", 576, 7168),
                                              ("o_proj", 7168, 16384), ("kv_b", 32768, 512)])
-def test_affine_gemv_config5_shapes(M, name, out_f, in_f):
-    print(f"gemv {name} {out_f}x{in_f}", flush=True)
+def test_affine_gemv_config5_shapes(M, name, out_f, in_f, centred):
+    print(f"gemv {name} {out_f}x{in_f} centred={centred}", flush=True)
     import torch
 
-    w = MI.affine_weight(f"gv.{name}", out_f, in_f)
+    w = MI.affine_weight(f"gv.{name}", out_f, in_f, centred=centred)
     x = O.normal_bf16(f"gv.{name}.x", (in_f,))
     ref = O.affine_matmul(O.bf16_to_f32(x)[None], *w, acc=1)[0]
     y = M.affine_mm(dev(x), weights(M, w), out_dtype=torch.float32)
     sync()
-    check(f32(y), ref, f"gemv-{name}", scale_bar=1e-4)
+    check(f32(y), ref, f"gemv-{name}{'-centred' if centred else ''}", scale_bar=1e-4)
 
 
 def test_affine_matmul_generic_paths(M):
@@ -182,7 +187,7 @@ def test_absorb_and_unabsorb(M):
     import torch
 
     H, dn, dv = 128, 128, 128
-    kvb = MI.affine_weight("ab.kvb", H * (dn + dv), 512)
+    kvb = MI.affine_weight("ab.kvb", H * (dn + dv), 512, centred=True)
     q = O.normal_bf16("ab.q", (H, 192))
     w = weights(M, kvb)
     q_lat = M.mla_absorb_query(dev(q), H, dn, dv, w)
@@ -211,21 +216,28 @@ def run_block(M, d, **dims):
     return out, cache
 
 
-def test_block_config5_full(M):
-    print("block config5 hidden=7168 H=128 ctx=32768", flush=True)
-    d = MI.block_inputs()
+def check_block(got, ref, tag):
+    ok, maxerr, scale_err = MI.within_block_tolerance(got, ref)
+    print(f"{tag}: max|d|={maxerr:.3e} scale_err={scale_err:.3e}", flush=True)
+    assert ok, f"{tag}: block bar violated (max |d| {maxerr}, output-scale {scale_err})"
+
+
+@pytest.mark.parametrize("centred", [False, True])
+def test_block_config5_full(M, centred):
+    print(f"block config5 hidden=7168 H=128 ctx=32768 centred={centred}", flush=True)
+    d = MI.block_inputs(centred=centred)
     out, cache = run_block(M, d)
     ref, row = MI.block_reference(d)
     got_row = bits16(cache)[d["position"]]
     np.testing.assert_array_equal(got_row[512:], row[512:])   # rotary key: bit-exact
     assert np.abs(got_row[:512].astype(np.int32) - row[:512].astype(np.int32)).max() <= 1
-    check(f32(out), ref, "block-config5", scale_bar=1e-2)
+    check_block(f32(out), ref, f"block-config5{'-centred' if centred else ''}")
 
 
 def test_block_small_context_and_first_token(M):
-    print("block small: position 0 and 70", flush=True)
+    print("block small: position 0 and 70, centred weights", flush=True)
     for ctx in (1, 71):
-        d = MI.block_inputs(ctx=ctx, tag=f"b{ctx}")
+        d = MI.block_inputs(ctx=ctx, tag=f"b{ctx}", centred=True)
         out, _ = run_block(M, d)
         ref, _ = MI.block_reference(d)
-        check(f32(out), ref, f"block-ctx{ctx}", scale_bar=1e-2)
+        check_block(f32(out), ref, f"block-ctx{ctx}")
