@@ -46,6 +46,13 @@ def split_kernel_bytes():
     return N * (R + DR) * 2 + H * (R + DR) * 2
 
 
+# HBM bytes one launch of the dense split kernel moves (H=128, N=32768):
+# FETCH_SIZE x 2.0 + WRITE_SIZE x 1.0 (factors from a streaming kernel of
+# known size), measured with rocprofv3 --pmc; profiles/mla_decode_hbm_counters.md
+# holds the passes.  Of it, 16,842,752 B are the fp32 split partials written.
+SPLIT_TRAFFIC_BYTES = 56059184
+
+
 def sparse_bytes(B=4, K=2048):
     return B * K * (R + DR) * 2 + B * K * 4 + B * H * (R + DR) * 2 + B * H * R * 2
 
@@ -76,6 +83,66 @@ def make_sparse_inputs(torch, ncache, nidx, B=4, NC=131072, K=2048, window=128):
             rows.append(torch.sort(torch.cat([drawn, torch.arange(NC - window, NC)])).values)
         sets.append(torch.stack(rows).to(torch.int32).cuda())
     return q_lat, q_rope, caches, sets
+
+
+BLOCK = dict(hidden=7168, q_lora_rank=1536, heads=128, nope=128, rope=64, v=128, kv_rank=512)
+BLOCK_SHAPES = {"q_a": (1536, 7168), "q_b": (128 * 192, 1536), "kv_a": (576, 7168), "kv_b": (128 * 256, 512),
+                "o_proj": (7168, 128 * 128)}
+
+
+def block_bytes():
+    """Algorithmic HBM bytes of one decode block: every affine operand once
+    (packed nibbles + bf16 scales and biases, kv_b included), the cache rows
+    read by the attention, and 264,320 bytes of activations."""
+    w = sum(o * i // 2 + 2 * 2 * o * (i // 64) for o, i in BLOCK_SHAPES.values())
+    return w + N * (R + DR) * 2 + 264320
+
+
+def make_block_inputs(torch, M, nset):
+    g = torch.Generator(device="cuda")
+    g.manual_seed(0x4D4C410005)
+    sets = []
+    for _ in range(nset):
+        w = {}
+        for name, (o, i) in BLOCK_SHAPES.items():
+            packed = torch.randint(-2 ** 31, 2 ** 31 - 1, (o, i // 8), generator=g, device="cuda", dtype=torch.int32)
+            sc = (0.01 * torch.randn(o, i // 64, generator=g, device="cuda")).abs().to(torch.bfloat16)
+            bi = (0.01 * torch.randn(o, i // 64, generator=g, device="cuda")).to(torch.bfloat16)
+            w[name] = M.AffineWeights(packed, sc, bi)
+        for name, n in (("input_norm", 7168), ("q_a_norm", 1536), ("kv_a_norm", 512)):
+            w[name] = (1 + 0.02 * torch.randn(n, generator=g, device="cuda")).to(torch.bfloat16)
+        cache = (0.5 * torch.randn(N, R + DR, generator=g, device="cuda")).to(torch.bfloat16)
+        sets.append((w, cache))
+    x = torch.randn(7168, generator=g, device="cuda").to(torch.bfloat16)
+    return x, sets
+
+
+def time_block(torch, M, steps, warmup):
+    """The decode block (affine 4-bit projections + absorbed attention over a
+    32768-row cache) for one token at position 32767; two weight/cache sets
+    (2 x 143 MB) rotate so the Infinity Cache cannot hold the operands."""
+    import ctypes as C
+    import numpy as np
+
+    x, sets = make_block_inputs(torch, M, 2)
+    pos = N - 1
+    c, s = M.rope_table(np.array([pos]), M.rope_frequencies(DR))
+    cos_t, sin_t = torch.from_numpy(c).cuda(), torch.from_numpy(s).cuda()
+    out = torch.empty(7168, dtype=torch.bfloat16, device="cuda")
+    args, ws = [], None
+    for w, cache in sets:
+        a, ws = M.block_args(x, w, cache, pos, cos_t, sin_t, out, workspace=ws, **BLOCK)
+        args.append(a)
+    lib = M.load()
+    sp = M._stream(torch.cuda.current_stream())
+    for i in range(warmup):
+        M._check(lib.mr_mla_decode_block(C.byref(args[i % 2]), sp))
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(steps):
+        M._check(lib.mr_mla_decode_block(C.byref(args[i % 2]), sp))
+    torch.cuda.synchronize()
+    return {"wall_ms": (time.perf_counter() - t0) / steps * 1e3}
 
 
 def make_events(torch, n):
@@ -199,6 +266,9 @@ def main():
     ap.add_argument("--steps", type=int, default=400)
     ap.add_argument("--warmup", type=int, default=50)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="also run a plain streaming kernel of known size (torch.neg over 64M fp32, 256 MiB read + "
+                         "256 MiB written, 3 launches) so HBM counters can be scaled to bytes")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported "
@@ -216,6 +286,9 @@ def main():
     log("bench: sparse B=4 H=128 N=131072 K=2048")
     s = time_sparse(torch, M, args.steps, args.warmup)
     log(f"bench: sparse {s}")
+    log("bench: decode block, hidden 7168, affine 4-bit g64, ctx 32768")
+    blk = time_block(torch, M, max(args.steps // 4, 10), max(args.warmup // 4, 5))
+    log(f"bench: block {blk}")
 
     layer_us = d["wall_ms"] * 1e3
     split_s = d["split_ms"] * 1e-3
@@ -242,10 +315,19 @@ def main():
         "sparse_top2048_us": round(s["layer_ms"] * 1e3, 3),
         "sparse_split_kernel_us": round(s["split_ms"] * 1e3, 3),
         "sparse_hbm_fraction": round(sparse_bytes() / (s["layer_ms"] * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+        "block_us": round(blk["wall_ms"] * 1e3, 3),
+        "block_hbm_fraction": round(block_bytes() / (blk["wall_ms"] * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": SPLIT_TRAFFIC_BYTES,
                      "kernel": "mla_decode_split", "algorithmic_bytes": split_kernel_bytes()},
     }
+    if args.copy_calibration:
+        src = torch.randn(64 << 20, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            torch.neg(src, out=dst)
+        torch.cuda.synchronize()
+        log("bench: copy calibration: 3 x neg over 268435456 B read + 268435456 B written")
     if not args.no_cpu_baseline:
         log("bench: cpu baseline (oracle port)")
         result["cpu_baseline"] = cpu_baseline()
