@@ -249,6 +249,47 @@ size_t mr_mla_decode_block_workspace_size(const mr_mla_block_args *args);
 mr_status mr_mla_decode_block(const mr_mla_block_args *args, void *stream);
 
 /* ------------------------------------------------------------------------
+ * Causal MLA prefill, eager (expanded) form (K3MLA.forward,
+ * Sources/ModelAdapters/Operators/MLA.swift:159-168,198-206; expand :231-245;
+ * causalMask :257-275).  For each head h the keys are
+ *   K[p] = [latent[p] . W_UK[h]^T  ++  rope_keys[p]]   (rope key shared)
+ * and the values V[p] = latent[p] . W_UV[h]^T, with W_UK / W_UV the rows
+ * h*(nope+v) + d and h*(nope+v) + nope + d of kv_b_proj [H*(nope+v),
+ * kv_rank] (output-major, the layout k3Linear consumes, MLA.swift:180-186).
+ * Query i of `tokens` sits at cache position n_ctx - tokens + i and sees
+ * keys 0 .. n_ctx - tokens + i (the reference adds -FLT_MAX to the rest);
+ * fp32 softmax.  out[i][h] = softmax(q . K^T * scale) . V.
+ * Fixed widths: qk_nope 128, qk_rope 64, v_head 128, kv_rank 512.
+ * Workspace: the up-projected keys/values, n_ctx * heads * 512 bytes.
+ * phase_events: NULL or 3 hipEvents recorded before the up-projection,
+ * between the two kernels and after the attention.
+ * ------------------------------------------------------------------------ */
+typedef struct mr_mla_prefill_args {
+    int32_t tokens; /* T >= 1 */
+    int32_t n_ctx;  /* P >= T cached rows, the last T of which are the queries' */
+    int32_t heads;
+    int32_t qk_nope_dim, qk_rope_dim, v_head_dim, kv_rank;
+    float scale; /* (qk_nope + qk_rope)^-1/2, MLA.swift:170 */
+    const void *q; /* bf16 [T][H][nope + rope] */
+    int64_t q_token_stride, q_head_stride;
+    const void *latent; /* bf16 [P][kv_rank] (normed latent) */
+    int64_t latent_row_stride;
+    const void *rope_keys; /* bf16 [P][qk_rope] (rotated) */
+    int64_t rope_row_stride;
+    const void *kv_b; /* bf16 [H*(nope+v)][kv_rank] */
+    int64_t kv_b_row_stride;
+    void *out; /* [T][H][v_head] */
+    mr_dtype out_dtype; /* MR_BF16 or MR_F32 */
+    int64_t out_token_stride, out_head_stride;
+    void *workspace;
+    size_t workspace_bytes;
+    void *const *phase_events;
+} mr_mla_prefill_args;
+
+size_t mr_mla_prefill_workspace_size(const mr_mla_prefill_args *args);
+mr_status mr_mla_prefill(const mr_mla_prefill_args *args, void *stream);
+
+/* ------------------------------------------------------------------------
  * Index tables of DeepSeek V4 attention (DeepSeekV4Attention.swift:169-237),
  * host side, -1 = invalid entry.  `out` must hold rows*cols entries:
  * window: seq_len*min(seq_len, window) (or window when start_pos > 0);

@@ -1,0 +1,114 @@
+// C-ABI of the causal MLA prefill: validation, workspace layout, launches.
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+
+#include "../../include/minirun_hip.h"
+#include "capi_util.hpp"
+#include "mr_kernels.hpp"
+
+namespace {
+using mrc::aligned16;
+using mrc::align256;
+using mrc::fail;
+using mrc::hip_fail;
+
+size_t kv_bytes(const mr_mla_prefill_args* a) {
+    return align256(size_t(a->n_ctx) * size_t(a->heads) * 256 * 2);
+}
+
+mr_status check_prefill(const mr_mla_prefill_args* a) {
+    if (!a) return fail(MR_INVALID_ARGUMENT, "mr_mla_prefill: args is NULL");
+    if (a->qk_nope_dim != 128 || a->qk_rope_dim != 64 || a->v_head_dim != 128 || a->kv_rank != 512)
+        return fail(MR_INVALID_SHAPE,
+                    "mla prefill: widths must be qk_nope 128, qk_rope 64, v_head 128, kv_rank 512 (got %d, %d, %d, %d)",
+                    a->qk_nope_dim, a->qk_rope_dim, a->v_head_dim, a->kv_rank);
+    if (a->tokens <= 0 || a->heads <= 0)
+        return fail(MR_INVALID_SHAPE, "mla prefill: tokens %d and heads %d must be positive", a->tokens, a->heads);
+    if (a->n_ctx < a->tokens)
+        return fail(MR_INVALID_SHAPE, "mla prefill: n_ctx %d must cover the %d query tokens", a->n_ctx, a->tokens);
+    if (double(a->heads) * 256.0 * double(a->n_ctx) >= 2147483648.0 || a->heads > 65536)
+        return fail(MR_INVALID_SHAPE, "mla prefill: n_ctx * heads * 256 must stay below 2^31");
+    if (!(std::isfinite(a->scale) && a->scale > 0))
+        return fail(MR_INVALID_SHAPE, "mla prefill: scale %g must be finite and positive", double(a->scale));
+    if (!a->q || !a->latent || !a->rope_keys || !a->kv_b || !a->out)
+        return fail(MR_INVALID_ARGUMENT, "mla prefill: q, latent, rope_keys, kv_b and out must be non-NULL");
+    if (!aligned16(a->q) || !aligned16(a->latent) || !aligned16(a->rope_keys) || !aligned16(a->kv_b) ||
+        !aligned16(a->out))
+        return fail(MR_INVALID_ARGUMENT, "mla prefill: q, latent, rope_keys, kv_b and out must be 16-byte aligned");
+    const int64_t st[] = {a->q_token_stride, a->q_head_stride, a->latent_row_stride, a->rope_row_stride,
+                          a->kv_b_row_stride};
+    for (int64_t s : st)
+        if (s < 0 || s % 8)
+            return fail(MR_INVALID_ARGUMENT, "mla prefill: input strides must be non-negative multiples of 8 elements");
+    if (a->q_head_stride < 192 || a->q_token_stride < 192 || a->latent_row_stride < 512 || a->rope_row_stride < 64 ||
+        a->kv_b_row_stride < 512)
+        return fail(MR_INVALID_ARGUMENT, "mla prefill: strides are smaller than the rows they step over");
+    if (a->out_dtype != MR_BF16 && a->out_dtype != MR_F32)
+        return fail(MR_INVALID_DTYPE, "mla prefill: out_dtype must be MR_BF16 or MR_F32");
+    const int64_t vec = a->out_dtype == MR_F32 ? 4 : 8;  // 16-byte output pieces
+    if (a->out_head_stride < 128 || a->out_token_stride < 128 || a->out_head_stride % vec || a->out_token_stride % vec)
+        return fail(MR_INVALID_ARGUMENT, "mla prefill: out strides must be >= 128 and multiples of %lld elements",
+                    (long long)vec);
+    return MR_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+size_t mr_mla_prefill_workspace_size(const mr_mla_prefill_args* a) {
+    if (!a || a->n_ctx <= 0 || a->heads <= 0) return 0;
+    return kv_bytes(a);
+}
+
+mr_status mr_mla_prefill(const mr_mla_prefill_args* a, void* stream) {
+    mr_status st = check_prefill(a);
+    if (st != MR_OK) return st;
+    const size_t need = kv_bytes(a);
+    if (!a->workspace || a->workspace_bytes < need)
+        return fail(MR_WORKSPACE_TOO_SMALL, "mla prefill: workspace %zu bytes < %zu required", a->workspace_bytes, need);
+    if (!aligned16(a->workspace)) return fail(MR_INVALID_ARGUMENT, "mla prefill: workspace must be 16-byte aligned");
+    hipStream_t s = (hipStream_t)stream;
+    hipEvent_t const* ev = (hipEvent_t const*)a->phase_events;
+    uint16_t* kv = (uint16_t*)a->workspace;
+    const int64_t kv_rs = int64_t(a->heads) * 256;
+
+    mr::UpProjParams u{};
+    u.a = (const uint16_t*)a->latent;
+    u.lda = a->latent_row_stride;
+    u.b = (const uint16_t*)a->kv_b;
+    u.ldb = a->kv_b_row_stride;
+    u.c = kv;
+    u.ldc = kv_rs;
+    u.M = a->n_ctx;
+    u.N = a->heads * 256;
+    u.K = 512;
+
+    mr::PrefillAttnParams p{};
+    p.q = (const uint16_t*)a->q;
+    p.q_ts = a->q_token_stride;
+    p.q_hs = a->q_head_stride;
+    p.kv = kv;
+    p.kv_rs = kv_rs;
+    p.rope = (const uint16_t*)a->rope_keys;
+    p.rope_rs = a->rope_row_stride;
+    p.out = a->out;
+    p.out_ts = a->out_token_stride;
+    p.out_hs = a->out_head_stride;
+    p.out_f32 = a->out_dtype == MR_F32;
+    p.T = a->tokens;
+    p.P = a->n_ctx;
+    p.H = a->heads;
+    p.scale_log2 = float(double(a->scale) * 1.4426950408889634);
+
+    hipError_t e = hipSuccess;
+    if (ev) e = hipEventRecord(ev[0], s);
+    if (e == hipSuccess) e = mr::launch_upproj(u, s);
+    if (e == hipSuccess && ev) e = hipEventRecord(ev[1], s);
+    if (e == hipSuccess) e = mr::launch_prefill_attn(p, s);
+    if (e == hipSuccess && ev) e = hipEventRecord(ev[2], s);
+    return e == hipSuccess ? MR_OK : hip_fail(e, "mla prefill launch");
+}
+
+}  // extern "C"

@@ -49,6 +49,40 @@ hipError_t launch_validate_indices(const int32_t* indices, int32_t batch, int32_
 hipError_t launch_mla_decode(const DecodeParams& p, const CombineParams& cp, bool transpose_reads,
                              hipEvent_t const* events, hipStream_t st);
 
+// ---------------------------------------------------------------- prefill
+// Up-projection (NT GEMM): kv[p][n] = sum_r latent[p][r] * kv_b[n][r], bf16
+// in, fp32 accumulation, bf16 out.  M = rows, N = output features (a
+// multiple of 128), K = 512.
+struct UpProjParams {
+    const uint16_t* a;  // latent rows [M][K], row stride lda
+    int64_t lda;
+    const uint16_t* b;  // kv_b [N][K], row stride ldb
+    int64_t ldb;
+    uint16_t* c;        // [M][N], row stride ldc
+    int64_t ldc;
+    int32_t M, N, K;
+};
+
+// Causal attention over the up-projected keys/values.  Head h of key p:
+// K = [kv[p][h*256 + 0..127] ++ rope[p][0..63]], V = kv[p][h*256 + 128..255].
+// Query i (of T, at cache position P - T + i) attends keys 0 .. P - T + i.
+struct PrefillAttnParams {
+    const uint16_t* q;  // [T][H][192] bf16 (nope 128 ++ rope 64)
+    int64_t q_ts, q_hs;
+    const uint16_t* kv;  // [P][H*256]
+    int64_t kv_rs;
+    const uint16_t* rope;  // [P][64] rows, stride rope_rs
+    int64_t rope_rs;
+    void* out;  // [T][H][128]
+    int64_t out_ts, out_hs;
+    int32_t out_f32;
+    int32_t T, P, H;
+    float scale_log2;  // softmax scale * log2(e)
+};
+
+hipError_t launch_upproj(const UpProjParams& p, hipStream_t st);
+hipError_t launch_prefill_attn(const PrefillAttnParams& p, hipStream_t st);
+
 // ---------------------------------------------------------------- affine
 struct AffineDequantParams {
     const uint32_t* packed;

@@ -1,0 +1,340 @@
+// Causal MLA prefill on gfx950 (K3MLA.forward eager branch, MLA.swift:159-168,
+// 198-206; expand :231-245; causal mask :257-275).
+//
+// Two kernels:
+//   upproj_kernel       kv[p][h*256 + e] = latent[p] . kv_b[h*256 + e]: the
+//                       per-head keys (e < 128, W_UK rows) and values (e >= 128,
+//                       W_UV rows) of every cached position, one NT GEMM on
+//                       32x32x16 bf16 MFMA, fp32 accumulation, bf16 out.
+//   prefill_attn_kernel flash attention over those keys/values plus the
+//                       shared rotary key, fp32 online softmax, bf16 P.
+//
+// The attention computes S^T = K . Q^T and O^T = V^T . P^T, so a lane owns
+// one query: its row max, row sum and rescale never leave the lane except
+// for one exchange between the two 32-lane halves that hold different keys.
+// P goes from the S^T accumulators into the B operand of the PV product
+// without a shuffle; V^T comes from row-major V tiles through
+// ds_read_b64_tr_b16.
+#include <algorithm>
+#include <math.h>
+
+#include "mr_kernels.hpp"
+
+namespace mr {
+
+namespace {
+
+// ---------------------------------------------------------------- up-projection
+constexpr int UG_TILE = 128;  // M and N tile
+constexpr int UG_BK = 32;     // K per stage
+
+// 64-byte LDS rows of 4 x 16-byte chunks; chunk c of row r sits at
+// c ^ ((r >> 2) & 3): 16 consecutive rows read at one chunk hit 16
+// distinct bank groups.
+__device__ __forceinline__ int ug_off(int r, int c) { return r * UG_BK + ((c ^ ((r >> 2) & 3)) << 3); }
+
+__global__ void __launch_bounds__(256, 2) upproj_kernel(UpProjParams p) {
+    __shared__ __attribute__((aligned(16))) uint16_t lds[4 * UG_TILE * UG_BK];  // 2 stages x (A, B): 32 KB
+    const int tid = threadIdx.x, w = tid >> 6, l = tid & 63;
+    const int m_tiles = (p.M + UG_TILE - 1) / UG_TILE;
+    const int total = m_tiles * (p.N / UG_TILE);
+    // XCD-aware order: the workgroups one XCD runs are consecutive tiles,
+    // which share an N tile (kv_b rows) across all M tiles
+    int bid = blockIdx.x;
+    if ((total & 7) == 0) bid = (bid & 7) * (total >> 3) + (bid >> 3);
+    const int mt = bid % m_tiles, nt = bid / m_tiles;
+    const int m0 = mt * UG_TILE, n0 = nt * UG_TILE;
+
+    // stage s: A tile at lds + 2s * 4096, B tile right after it
+    auto sa = [&](int s) { return lds + (2 * s) * UG_TILE * UG_BK; };
+    auto sb = [&](int s) { return lds + (2 * s + 1) * UG_TILE * UG_BK; };
+    u32x4 ra[2], rb[2];
+    auto gload = [&](int k0) {
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const int q = tid + 256 * i, row = q >> 2, ch = q & 3;
+            const int am = min(m0 + row, p.M - 1);
+            ra[i] = *(const u32x4*)(p.a + (int64_t)am * p.lda + k0 + ch * 8);
+            rb[i] = *(const u32x4*)(p.b + (int64_t)(n0 + row) * p.ldb + k0 + ch * 8);
+        }
+    };
+    auto sstore = [&](int buf) {
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const int q = tid + 256 * i, row = q >> 2, ch = q & 3;
+            *(u32x4*)(sa(buf) + ug_off(row, ch)) = ra[i];
+            *(u32x4*)(sb(buf) + ug_off(row, ch)) = rb[i];
+        }
+    };
+
+    const int wm = w >> 1, wn = w & 1;  // this wave's 64 x 64 sub-tile
+    f32x16 acc[2][2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) acc[i][j] = f32x16{};
+
+    const int ksteps = p.K / UG_BK;
+    gload(0);
+    sstore(0);
+    __syncthreads();
+    for (int kt = 0; kt < ksteps; ++kt) {
+        const int buf = kt & 1;
+        if (kt + 1 < ksteps) gload((kt + 1) * UG_BK);
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) {
+            bf16x8 av[2], bv[2];
+            const int ch = 2 * ks + (l >> 5);
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+                av[i] = *(const bf16x8*)(sa(buf) + ug_off(wm * 64 + i * 32 + (l & 31), ch));
+                bv[i] = *(const bf16x8*)(sb(buf) + ug_off(wn * 64 + i * 32 + (l & 31), ch));
+            }
+#pragma unroll
+            for (int i = 0; i < 2; ++i)
+#pragma unroll
+                for (int j = 0; j < 2; ++j) acc[i][j] = mfma32(av[i], bv[j], acc[i][j]);
+        }
+        if (kt + 1 < ksteps) sstore(buf ^ 1);
+        __syncthreads();
+    }
+
+    // epilogue: the 128 x 128 bf16 tile through LDS (32 KB), then 16-byte
+    // row-contiguous stores
+    uint16_t* tile = lds;  // [128][128]
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int row = wm * 64 + i * 32 + 8 * (r >> 2) + 4 * (l >> 5) + (r & 3);
+                const int col = wn * 64 + j * 32 + (l & 31);
+                tile[row * UG_TILE + col] = f32_to_bf16_bits(acc[i][j][r]);
+            }
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const int q = tid + 256 * i, row = q >> 4, ch = q & 15;
+        if (m0 + row < p.M)
+            *(u32x4*)(p.c + (int64_t)(m0 + row) * p.ldc + n0 + ch * 8) = *(const u32x4*)(tile + row * UG_TILE + ch * 8);
+    }
+}
+
+// ---------------------------------------------------------------- attention
+constexpr int AT_Q = 128;   // queries per workgroup (32 per wave)
+constexpr int AT_K = 64;    // keys per tile
+constexpr int AT_DK = 192;  // key width: 128 nope + 64 rope
+constexpr int AT_DV = 128;
+
+// K tile [64][192] bf16 (384-byte rows, 24 chunks): chunk c of row r at
+// c ^ ((r >> 1) & 7).  V tile [64][128] (256-byte rows): chunk c of row r at
+// c ^ ((r & 3) << 1).  Both conflict-free for the reads below.
+__device__ __forceinline__ int k_off(int r, int c) { return r * AT_DK + ((c ^ ((r >> 1) & 7)) << 3); }
+__device__ __forceinline__ int v_off(int r, int d) { return r * AT_DV + ((((d >> 3) ^ ((r & 3) << 1))) << 3) + (d & 7); }
+
+__global__ void __launch_bounds__(256, 1) prefill_attn_kernel(PrefillAttnParams p) {
+    __shared__ __attribute__((aligned(16))) uint16_t lds[AT_K * AT_DK + AT_K * AT_DV];  // 40 KB
+    uint16_t* ks_lds = lds;
+    uint16_t* vs_lds = lds + AT_K * AT_DK;
+    const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, lq = l & 31, hh = l >> 5;
+
+    // work item: (head, query tile); one XCD takes all query tiles of a head
+    // (heaviest first) so that head's keys and values stay in its L2
+    const int qtiles = (p.T + AT_Q - 1) / AT_Q;
+    const int total = qtiles * p.H;
+    int head, qt;
+    if ((p.H & 7) == 0) {
+        const int xcd = blockIdx.x & 7, slot = blockIdx.x >> 3;
+        head = (slot / qtiles) * 8 + xcd;
+        qt = qtiles - 1 - slot % qtiles;
+    } else {
+        head = blockIdx.x / qtiles;
+        qt = qtiles - 1 - blockIdx.x % qtiles;
+    }
+    if (head >= p.H || blockIdx.x >= total) return;
+    const int q0 = qt * AT_Q;
+    const int off = p.P - p.T;  // query i sits at position off + i
+
+    // this lane's query as a column of S^T; its 192 features as the B operand
+    const int qi = q0 + 32 * w + lq;
+    const uint16_t* qp = p.q + (int64_t)min(qi, p.T - 1) * p.q_ts + (int64_t)head * p.q_hs;
+    bf16x8 qf[12];
+#pragma unroll
+    for (int ks = 0; ks < 12; ++ks) qf[ks] = *(const bf16x8*)(qp + 16 * ks + 8 * hh);
+    const int q_limit = off + qi;  // keys <= q_limit are visible
+
+    const int wg_kend = off + min(q0 + AT_Q, p.T);  // keys [0, wg_kend) for the workgroup
+    const int ntiles = (wg_kend + AT_K - 1) / AT_K;
+    const int wave_first = off + q0 + 32 * w;              // smallest visible limit in this wave
+    // keys this wave can see (none when all its queries lie past T)
+    const int wave_kend = q0 + 32 * w < p.T ? off + min(q0 + 32 * w + 32, p.T) : 0;
+
+    const uint16_t* kv_h = p.kv + (int64_t)head * 256;
+    u32x4 rk[6], rv[4];
+    auto gload = [&](int kt) {
+#pragma unroll
+        for (int i = 0; i < 6; ++i) {
+            const int q = tid + 256 * i, row = q / 24, ch = q % 24;
+            const int key = min(kt * AT_K + row, p.P - 1);
+            rk[i] = ch < 16 ? *(const u32x4*)(kv_h + (int64_t)key * p.kv_rs + ch * 8)
+                            : *(const u32x4*)(p.rope + (int64_t)key * p.rope_rs + (ch - 16) * 8);
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int q = tid + 256 * i, row = q >> 4, ch = q & 15;
+            const int key = min(kt * AT_K + row, p.P - 1);
+            rv[i] = *(const u32x4*)(kv_h + (int64_t)key * p.kv_rs + 128 + ch * 8);
+        }
+    };
+    auto sstore = [&]() {
+#pragma unroll
+        for (int i = 0; i < 6; ++i) {
+            const int q = tid + 256 * i, row = q / 24, ch = q % 24;
+            *(u32x4*)(ks_lds + k_off(row, ch)) = rk[i];
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int q = tid + 256 * i, row = q >> 4, ch = q & 15;
+            *(u32x4*)(vs_lds + v_off(row, ch * 8)) = rv[i];
+        }
+    };
+
+    float m_run = -INFINITY, l_part = 0.f;
+    f32x16 o[4];
+#pragma unroll
+    for (int d = 0; d < 4; ++d) o[d] = f32x16{};
+
+    // tr-read addressing for the V^T operand (fixed per lane)
+    const int g = l >> 4, j = l & 15;
+    const int tr_key = 4 * (g >> 1) + (j >> 2);
+    const int tr_d = 16 * (g & 1) + 4 * (j & 3);
+
+    gload(0);
+    for (int kt = 0; kt < ntiles; ++kt) {
+        if (kt > 0) __syncthreads();
+        sstore();
+        __syncthreads();
+        if (kt + 1 < ntiles) gload(kt + 1);
+        const int k0 = kt * AT_K;
+        if (k0 >= wave_kend) continue;  // every query of this wave is past this tile
+
+        // S^T = K . Q^T: two 32-key blocks, 12 k-steps of 16 features
+        f32x16 s[2] = {f32x16{}, f32x16{}};
+#pragma unroll
+        for (int ks = 0; ks < 12; ++ks) {
+#pragma unroll
+            for (int kb = 0; kb < 2; ++kb) {
+                const bf16x8 a = *(const bf16x8*)(ks_lds + k_off(kb * 32 + lq, 2 * ks + hh));
+                s[kb] = mfma32(a, qf[ks], s[kb]);
+            }
+        }
+        // scale, causal mask, running max (lane = query, 32 of its keys)
+        const bool diag = k0 + AT_K - 1 > wave_first;
+        float mx = -INFINITY;
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                float v = s[kb][i] * p.scale_log2;
+                if (diag) {
+                    const int key = k0 + kb * 32 + 8 * (i >> 2) + 4 * hh + (i & 3);
+                    if (key > q_limit) v = -INFINITY;
+                }
+                s[kb][i] = v;
+                mx = fmaxf(mx, v);
+            }
+        mx = fmaxf(mx, __shfl_xor(mx, 32));
+        const float m_new = fmaxf(m_run, mx);
+        const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
+        m_run = m_new;
+        float ls = 0.f;
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const float e = __builtin_amdgcn_exp2f(s[kb][i] - m_new);
+                s[kb][i] = e;
+                ls += e;
+            }
+        l_part = l_part * alpha + ls;
+#pragma unroll
+        for (int d = 0; d < 4; ++d) o[d] *= alpha;
+
+        // O^T += V^T . P^T: k-step t covers tile keys 16t .. 16t+15
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            const int kb = t >> 1, base = 8 * (t & 1);
+            bf16x8 pb;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) pb[e] = (__bf16)s[kb][base + e];
+#pragma unroll
+            for (int db = 0; db < 4; ++db) {
+                const int d = 32 * db + tr_d;
+                const bf16x4 lo = ds_read_tr16(vs_lds + v_off(16 * t + tr_key, d));
+                const bf16x4 hi = ds_read_tr16(vs_lds + v_off(16 * t + 8 + tr_key, d));
+                const bf16x8 a = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+                o[db] = mfma32(a, pb, o[db]);
+            }
+        }
+    }
+
+    // normalise: the two halves of the wave hold partial sums of one query
+    const float l_tot = l_part + __shfl_xor(l_part, 32);
+    const float inv = 1.f / l_tot;
+    const bool q_ok = qi < p.T;
+    if (p.out_f32) {
+        float* op = (float*)p.out + (int64_t)qi * p.out_ts + (int64_t)head * p.out_hs;
+        if (q_ok) {
+#pragma unroll
+            for (int db = 0; db < 4; ++db)
+#pragma unroll
+                for (int r4 = 0; r4 < 4; ++r4) {
+                    const int d = 32 * db + 8 * r4 + 4 * hh;
+                    *(f32x4*)(op + d) = f32x4{o[db][4 * r4] * inv, o[db][4 * r4 + 1] * inv, o[db][4 * r4 + 2] * inv,
+                                              o[db][4 * r4 + 3] * inv};
+                }
+        }
+        return;
+    }
+    // bf16: stage this wave's [32 queries][128] tile in LDS, then store rows
+    __syncthreads();
+    uint16_t* st = lds + w * 32 * AT_DV;
+#pragma unroll
+    for (int db = 0; db < 4; ++db)
+#pragma unroll
+        for (int r4 = 0; r4 < 4; ++r4) {
+            const int d = 32 * db + 8 * r4 + 4 * hh;
+            u32x2 v;
+            v[0] = pack_bf16x2(o[db][4 * r4] * inv, o[db][4 * r4 + 1] * inv);
+            v[1] = pack_bf16x2(o[db][4 * r4 + 2] * inv, o[db][4 * r4 + 3] * inv);
+            *(u32x2*)(st + lq * AT_DV + d) = v;
+        }
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const int q = l + 64 * i, row = q >> 4, ch = q & 15;  // 32 rows x 16 chunks
+        const int qq = q0 + 32 * w + row;
+        if (qq < p.T)
+            *(u32x4*)((uint16_t*)p.out + (int64_t)qq * p.out_ts + (int64_t)head * p.out_hs + ch * 8) =
+                *(const u32x4*)(st + row * AT_DV + ch * 8);
+    }
+}
+
+}  // namespace
+
+hipError_t launch_upproj(const UpProjParams& p, hipStream_t st) {
+    const int m_tiles = (p.M + UG_TILE - 1) / UG_TILE;
+    const unsigned grid = (unsigned)(m_tiles * (p.N / UG_TILE));
+    hipLaunchKernelGGL(upproj_kernel, dim3(grid), dim3(256), 0, st, p);
+    return hipGetLastError();
+}
+
+hipError_t launch_prefill_attn(const PrefillAttnParams& p, hipStream_t st) {
+    const int qtiles = (p.T + AT_Q - 1) / AT_Q;
+    const unsigned grid = (unsigned)(qtiles * p.H);
+    hipLaunchKernelGGL(prefill_attn_kernel, dim3(grid), dim3(256), 0, st, p);
+    return hipGetLastError();
+}
+
+}  // namespace mr

@@ -77,6 +77,21 @@ class BlockArgs(C.Structure):
     ]
 
 
+class PrefillArgs(C.Structure):
+    _fields_ = [
+        ("tokens", C.c_int32), ("n_ctx", C.c_int32), ("heads", C.c_int32),
+        ("qk_nope_dim", C.c_int32), ("qk_rope_dim", C.c_int32), ("v_head_dim", C.c_int32), ("kv_rank", C.c_int32),
+        ("scale", C.c_float),
+        ("q", C.c_void_p), ("q_token_stride", C.c_int64), ("q_head_stride", C.c_int64),
+        ("latent", C.c_void_p), ("latent_row_stride", C.c_int64),
+        ("rope_keys", C.c_void_p), ("rope_row_stride", C.c_int64),
+        ("kv_b", C.c_void_p), ("kv_b_row_stride", C.c_int64),
+        ("out", C.c_void_p), ("out_dtype", C.c_int), ("out_token_stride", C.c_int64), ("out_head_stride", C.c_int64),
+        ("workspace", C.c_void_p), ("workspace_bytes", C.c_size_t),
+        ("phase_events", C.c_void_p),
+    ]
+
+
 _P = C.c_void_p
 _I32P = C.POINTER(C.c_int32)
 _I64P = C.POINTER(C.c_int64)
@@ -108,6 +123,8 @@ SIGNATURES = {
                                          _P, C.c_int, _P]),
     "mr_mla_decode_block_workspace_size": (C.c_size_t, [C.POINTER(BlockArgs)]),
     "mr_mla_decode_block": (C.c_int, [C.POINTER(BlockArgs), _P]),
+    "mr_mla_prefill_workspace_size": (C.c_size_t, [C.POINTER(PrefillArgs)]),
+    "mr_mla_prefill": (C.c_int, [C.POINTER(PrefillArgs), _P]),
     "mr_attention_indices_window": (C.c_int, [C.c_int32, C.c_int32, C.c_int32, _P, _I32P, _I32P]),
     "mr_attention_indices_compressed": (C.c_int, [C.c_int32, C.c_int32, C.c_int32, C.c_int32, _P, _I32P, _I32P]),
 }
@@ -434,6 +451,45 @@ def mla_decode_block(x, weights, cache, position, rope_cos, rope_sin, stream=Non
     out = torch.empty(kw.get("hidden", 7168), dtype=torch.bfloat16, device=x.device)
     a, ws = block_args(x, weights, cache, position, rope_cos, rope_sin, out, **kw)
     _check(load().mr_mla_decode_block(C.byref(a), _stream(stream)))
+    return out
+
+
+def prefill_args(q, latent, rope_keys, kv_b, *, scale=None, out=None, out_dtype=None, workspace=None):
+    """Fill PrefillArgs: q [T,H,192] bf16; latent [P,>=512] and rope_keys
+    [P,>=64] bf16 row views (both may be views of one [P,576] cache);
+    kv_b [H*256, 512] bf16 (kv_b_proj, output-major)."""
+    torch = _torch()
+    for t, n in ((q, "q"), (latent, "latent"), (rope_keys, "rope_keys"), (kv_b, "kv_b")):
+        _need(t, n, torch.bfloat16)
+    T, H, D = q.shape
+    P = latent.shape[0]
+    a = PrefillArgs()
+    a.tokens, a.n_ctx, a.heads = T, P, H
+    a.qk_nope_dim, a.qk_rope_dim, a.v_head_dim, a.kv_rank = D - rope_keys.shape[1], rope_keys.shape[1], 128, 512
+    a.scale = scale if scale is not None else D ** -0.5
+    a.q, a.q_token_stride, a.q_head_stride = q.data_ptr(), q.stride(0), q.stride(1)
+    a.latent, a.latent_row_stride = latent.data_ptr(), latent.stride(0)
+    a.rope_keys, a.rope_row_stride = rope_keys.data_ptr(), rope_keys.stride(0)
+    a.kv_b, a.kv_b_row_stride = kv_b.data_ptr(), kv_b.stride(0)
+    if out is None:
+        out = torch.empty(T, H, 128, dtype=out_dtype or torch.bfloat16, device=q.device)
+    a.out, a.out_dtype = out.data_ptr(), _dtype_code(out.dtype)
+    a.out_token_stride, a.out_head_stride = out.stride(0), out.stride(1)
+    need = load().mr_mla_prefill_workspace_size(C.byref(a))
+    if workspace is None:
+        workspace = torch.empty(need, dtype=torch.uint8, device=q.device)
+    a.workspace, a.workspace_bytes = workspace.data_ptr(), workspace.numel()
+    a._keep = (q, latent, rope_keys, kv_b, out, workspace)
+    return a, out, workspace
+
+
+def mla_prefill(q, latent, rope_keys, kv_b, *, scale=None, out=None, out_dtype=None, workspace=None, stream=None):
+    """K3MLA.forward eager prefill (MLA.swift:159-168,198-206): causal
+    attention of the T queries over the P cached rows, per-head keys/values
+    up-projected through kv_b."""
+    a, out, _ = prefill_args(q, latent, rope_keys, kv_b, scale=scale, out=out, out_dtype=out_dtype,
+                             workspace=workspace)
+    _check(load().mr_mla_prefill(C.byref(a), _stream(stream)))
     return out
 
 

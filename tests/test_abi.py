@@ -64,3 +64,21 @@ def test_validate_indices_rejects_oversize_without_gpu():
     lib = M.load()
     st = lib.mr_validate_indices(None, 1, 5000, 10, None, 0, None, None, None)
     assert st == M.INVALID_SHAPE
+
+
+def test_prefill_rejects_bad_arguments_before_any_gpu_call():
+    lib = M.load()
+    a = M.PrefillArgs()
+    a.tokens, a.n_ctx, a.heads = 4096, 4096, 128
+    a.qk_nope_dim, a.qk_rope_dim, a.v_head_dim, a.kv_rank = 128, 64, 128, 256
+    a.scale = 192 ** -0.5
+    assert lib.mr_mla_prefill(C.byref(a), None) == M.INVALID_SHAPE
+    assert "kv_rank 512" in M.last_error()
+    a.kv_rank = 512
+    a.n_ctx = 100
+    assert lib.mr_mla_prefill(C.byref(a), None) == M.INVALID_SHAPE
+    assert "cover" in M.last_error()
+    a.n_ctx = 4096
+    assert lib.mr_mla_prefill(C.byref(a), None) == M.INVALID_ARGUMENT  # NULL pointers
+    assert lib.mr_mla_prefill(None, None) == M.INVALID_ARGUMENT
+    assert lib.mr_mla_prefill_workspace_size(C.byref(a)) == 4096 * 128 * 512

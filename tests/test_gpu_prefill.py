@@ -1,0 +1,124 @@
+"""Parity of the HIP causal MLA prefill (K3MLA.forward eager branch,
+MLA.swift:159-168,198-206,231-275) against the oracle.
+
+Bars: the workload bar |hip - oracle| <= 1e-2 + 2e-2 |oracle| elementwise on
+bf16 outputs; since late queries average over thousands of keys (outputs of
+a few 1e-3), also a per-(token, head) relative L2 error <= 1e-2.  The oracle
+forms keys/values in fp64 and rounds them to bf16 once (round_kv), as the
+HIP path stores them; the unrounded oracle is checked at the same bar.
+Prefix consistency (causality) is bit-exact: a query's result does not
+depend on how many queries follow it.
+"""
+import numpy as np
+import pytest
+
+import mla_inputs as MI
+import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def M():
+    import minirun_hip as M
+
+    M.load()
+    return M
+
+
+def prefill_inputs(T, P, H, tag, q_std=1.0):
+    """q [T,H,192] ~N(0,q_std), cache [P,576] ~N(0,0.5) (latent ++ rope key),
+    W_UK / W_UV [512, H*128] ~N(0,0.02) (input-major) and kv_b_proj
+    [H*256, 512] holding the same values output-major."""
+    q = O.normal_bf16(f"{tag}.q", (T, H, 192), std=q_std)
+    cache = O.normal_bf16(f"{tag}.cache", (P, 576), std=0.5)
+    w_uk = O.normal_bf16(f"{tag}.w_uk", (512, H * 128), std=0.02)
+    w_uv = O.normal_bf16(f"{tag}.w_uv", (512, H * 128), std=0.02)
+    kv_b = np.empty((H, 256, 512), np.uint16)
+    kv_b[:, :128, :] = w_uk.reshape(512, H, 128).transpose(1, 2, 0)
+    kv_b[:, 128:, :] = w_uv.reshape(512, H, 128).transpose(1, 2, 0)
+    return q, cache, w_uk, w_uv, kv_b.reshape(H * 256, 512)
+
+
+def run(M, q, cache, kv_b, out_dtype=None):
+    import torch
+
+    qd = torch.from_numpy(q).view(torch.bfloat16).cuda()
+    cd = torch.from_numpy(cache).view(torch.bfloat16).cuda()
+    kd = torch.from_numpy(kv_b).view(torch.bfloat16).cuda()
+    out = M.mla_prefill(qd, cd[:, :512], cd[:, 512:], kd, out_dtype=out_dtype or torch.bfloat16)
+    torch.cuda.synchronize()
+    return out.float().cpu().numpy()
+
+
+def check_rows(got, ref, tag):
+    ok, maxerr, scale_err = MI.within_tolerance(got, ref)
+    rel = np.linalg.norm(got - ref, axis=-1) / np.maximum(np.linalg.norm(ref, axis=-1), 1e-30)
+    print(f"{tag}: max|d|={maxerr:.3e} scale_err={scale_err:.3e} worst row rel-L2={rel.max():.3e}", flush=True)
+    assert ok, f"{tag}: elementwise bar violated (max |d| {maxerr})"
+    assert rel.max() <= 1e-2, f"{tag}: row relative error {rel.max()}"
+
+
+def all_pairs(T, H):
+    t, h = np.meshgrid(np.arange(T), np.arange(H), indexing="ij")
+    return t.ravel().astype(np.int32), h.ravel().astype(np.int32)
+
+
+@pytest.mark.parametrize("T,P,H,q_std", [(64, 64, 8, 1.0), (37, 100, 8, 1.0), (300, 300, 8, 4.0), (1, 257, 16, 1.0),
+                                         (129, 129, 8, 4.0)])
+def test_prefill_small_all_rows(M, T, P, H, q_std):
+    print(f"prefill T={T} P={P} H={H} q_std={q_std}", flush=True)
+    q, cache, w_uk, w_uv, kv_b = prefill_inputs(T, P, H, f"pf{T}.{P}", q_std)
+    got = run(M, q, cache, kv_b)
+    st, sh = all_pairs(T, H)
+    ref = O.mla_prefill_rows(q, cache, w_uk, w_uv, st, sh, round_kv=True).reshape(T, H, 128)
+    check_rows(got, ref, f"prefill-{T}-{P}-{H}")
+    ref_exact = O.mla_prefill_rows(q, cache, w_uk, w_uv, st, sh, round_kv=False).reshape(T, H, 128)
+    check_rows(got, ref_exact, f"prefill-{T}-{P}-{H}-unrounded-kv")
+
+
+def test_prefill_f32_output(M):
+    import torch
+
+    print("prefill f32 out T=96 P=160 H=8", flush=True)
+    q, cache, w_uk, w_uv, kv_b = prefill_inputs(96, 160, 8, "pf32", 2.0)
+    got = run(M, q, cache, kv_b, out_dtype=torch.float32)
+    got_bf = run(M, q, cache, kv_b)
+    st, sh = all_pairs(96, 8)
+    ref = O.mla_prefill_rows(q, cache, w_uk, w_uv, st, sh, round_kv=True).reshape(96, 8, 128)
+    check_rows(got, ref, "prefill-f32")
+    # the bf16 output is the f32 one rounded to nearest-even
+    np.testing.assert_array_equal(O.f32_to_bf16(got), O.f32_to_bf16(got_bf))
+
+
+def test_prefill_prefix_consistency_bit_exact(M):
+    print("prefill prefix consistency T=P=300 vs T=P=200", flush=True)
+    q, cache, _, _, kv_b = prefill_inputs(300, 300, 8, "pfx", 4.0)
+    full = run(M, q, cache, kv_b)
+    pre = run(M, q[:200], cache[:200], kv_b)
+    np.testing.assert_array_equal(full[:200], pre)
+
+
+def test_prefill_first_query_is_first_value(M):
+    # query 0 (P == T) sees only key 0: softmax weight 1, output = V[0]
+    print("prefill first query", flush=True)
+    q, cache, w_uk, w_uv, kv_b = prefill_inputs(8, 8, 8, "pf0", 8.0)
+    got = run(M, q, cache, kv_b)
+    c0 = O.bf16_to_f32(cache[0, :512]).astype(np.float64)
+    v0 = O.bf16_to_f32(O.f32_to_bf16((c0 @ O.bf16_to_f32(w_uv).astype(np.float64)).astype(np.float32)))
+    np.testing.assert_allclose(got[0], v0.reshape(8, 128), rtol=8e-3, atol=1e-6)
+
+
+def test_prefill_config3_sampled(M):
+    T = P = 4096
+    H = 128
+    print(f"prefill config3 T={T} H={H}", flush=True)
+    q, cache, w_uk, w_uv, kv_b = prefill_inputs(T, P, H, "c3")
+    got = run(M, q, cache, kv_b)
+    assert np.isfinite(got).all()
+    rows = np.array([0, 1, 2, 63, 64, 127, 128, 129, 1000, 2047, 2048, 3001, 4094, 4095])
+    heads = np.array([0, 7, 64, 127])
+    t, h = np.meshgrid(rows, heads, indexing="ij")
+    st, sh = t.ravel().astype(np.int32), h.ravel().astype(np.int32)
+    ref = O.mla_prefill_rows(q, cache, w_uk, w_uv, st, sh, round_kv=True)
+    check_rows(got[st, sh], ref, "prefill-config3")
