@@ -145,6 +145,45 @@ def time_block(torch, M, steps, warmup):
     return {"wall_ms": (time.perf_counter() - t0) / steps * 1e3}
 
 
+MFMA_PEAK_TFLOPS = 2500.0  # dense bf16
+PREFILL_T = 4096
+# algorithmic work of the causal prefill (T = P = 4096, 128 heads): the
+# up-projection 2*T*512*(128*256), QK 2*192 and PV 2*128 flops per visible
+# (query, key) pair per head, T(T+1)/2 pairs
+UPPROJ_FLOP = 2 * PREFILL_T * 512 * 128 * 256
+ATTN_FLOP = (2 * 192 + 2 * 128) * 128 * PREFILL_T * (PREFILL_T + 1) // 2
+
+
+def time_prefill(torch, M, steps, warmup):
+    """Causal prefill, 4096 tokens over a 4096-row latent cache, 128 heads:
+    q [4096,128,192] ~N(0,1), latent ~N(0,0.5), kv_b_proj [32768,512] ~N(0,0.02)."""
+    import ctypes as C
+
+    g = torch.Generator(device="cuda")
+    g.manual_seed(0x4D4C410003)
+    T = PREFILL_T
+    q = torch.randn(T, H, 192, generator=g, device="cuda").to(torch.bfloat16)
+    cache = (0.5 * torch.randn(T, R + DR, generator=g, device="cuda")).to(torch.bfloat16)
+    kv_b = (0.02 * torch.randn(H * 256, R, generator=g, device="cuda")).to(torch.bfloat16)
+    a, out, ws = M.prefill_args(q, cache[:, :R], cache[:, R:], kv_b)
+    lib = M.load()
+    sp = M._stream(torch.cuda.current_stream())
+    for _ in range(warmup):
+        M._check(lib.mr_mla_prefill(C.byref(a), sp))
+    torch.cuda.synchronize()
+    evs = make_events(torch, steps)
+    handles = [(C.c_void_p * 3)(*[e.cuda_event for e in ev]) for ev in evs]
+    t0 = time.perf_counter()
+    for i in range(steps):
+        a.phase_events = C.cast(handles[i], C.c_void_p)
+        M._check(lib.mr_mla_prefill(C.byref(a), sp))
+    torch.cuda.synchronize()
+    wall = (time.perf_counter() - t0) / steps
+    up_ms = sum(ev[0].elapsed_time(ev[1]) for ev in evs) / steps
+    at_ms = sum(ev[1].elapsed_time(ev[2]) for ev in evs) / steps
+    return {"wall_ms": wall * 1e3, "upproj_ms": up_ms, "attn_ms": at_ms}
+
+
 def make_events(torch, n):
     # torch creates the underlying hipEvent lazily: record each once so the
     # handle exists before the library records it
@@ -289,6 +328,9 @@ def main():
     log("bench: decode block, hidden 7168, affine 4-bit g64, ctx 32768")
     blk = time_block(torch, M, max(args.steps // 4, 10), max(args.warmup // 4, 5))
     log(f"bench: block {blk}")
+    log("bench: causal prefill T=4096 H=128")
+    pf = time_prefill(torch, M, max(args.steps // 20, 5), 3)
+    log(f"bench: prefill {pf}")
 
     layer_us = d["wall_ms"] * 1e3
     split_s = d["split_ms"] * 1e-3
@@ -317,6 +359,11 @@ def main():
         "sparse_hbm_fraction": round(sparse_bytes() / (s["layer_ms"] * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
         "block_us": round(blk["wall_ms"] * 1e3, 3),
         "block_hbm_fraction": round(block_bytes() / (blk["wall_ms"] * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+        "prefill_us": round(pf["wall_ms"] * 1e3, 2),
+        "prefill_mfma_fraction": round((UPPROJ_FLOP + ATTN_FLOP) / (pf["wall_ms"] * 1e-3) / 1e12 / MFMA_PEAK_TFLOPS, 4),
+        "prefill_upproj_us": round(pf["upproj_ms"] * 1e3, 2),
+        "prefill_attn_us": round(pf["attn_ms"] * 1e3, 2),
+        "prefill_attn_mfma_fraction": round(ATTN_FLOP / (pf["attn_ms"] * 1e-3) / 1e12 / MFMA_PEAK_TFLOPS, 4),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": SPLIT_TRAFFIC_BYTES,
                      "kernel": "mla_decode_split", "algorithmic_bytes": split_kernel_bytes()},
