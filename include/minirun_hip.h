@@ -300,6 +300,43 @@ mr_status mr_attention_indices_window(int32_t window, int32_t seq_len, int32_t s
 mr_status mr_attention_indices_compressed(int32_t ratio, int32_t seq_len, int32_t start_pos, int32_t offset,
                                           int32_t *out, int32_t *rows, int32_t *cols);
 
+/* ------------------------------------------------------------------------
+ * Lightning-indexer top-k selection (DeepSeekV4LightningIndexer.selecting,
+ * DeepSeekV4Attention.swift:582-645), on the device, bit-exact.
+ * scores [rows][cols] f32.  available = (start_pos + rows) / ratio keys are
+ * ranked per row by descending score, ties by ascending key id; in row r
+ * keys >= visible (visible = (r + 1) / ratio when start_pos == 0, else
+ * available) compare as -infinity.  The first selected = min(top_k,
+ * available) keys are written as offset + key, or -1 for a key >= visible.
+ * Geometry errors are the reference's (:590-612), checked on the host; a
+ * NaN score (anywhere in the matrix, :622-624) is reported through `status`
+ * (device int32: 0 or MR_NONFINITE) and, with MR_TOPK_CHECK, by a
+ * synchronising read that returns MR_NONFINITE.  Limits: top_k selected
+ * <= 4096, available <= 65535, offset + available - 1 <= INT32_MAX.
+ * Workspace: 4 * rows bytes (per-row NaN flags).
+ * ------------------------------------------------------------------------ */
+enum { MR_TOPK_CHECK = 1 };
+
+typedef struct mr_topk_args {
+    const float *scores;
+    int64_t score_row_stride;
+    int32_t rows, cols;
+    int32_t top_k, ratio, start_pos, offset;
+    int32_t *out; /* device [rows][out_row_stride], selected entries per row */
+    int64_t out_row_stride;
+    int32_t *status; /* NULL or device int32 */
+    int32_t flags;
+    void *workspace;
+    size_t workspace_bytes;
+} mr_topk_args;
+
+/* Host-only geometry check: the reference's errors, and the number of keys
+ * each row receives. */
+mr_status mr_topk_geometry(int32_t rows, int32_t cols, int32_t top_k, int32_t ratio, int32_t start_pos,
+                           int32_t offset, int32_t *selected);
+size_t mr_topk_workspace_size(int32_t rows);
+mr_status mr_topk_select(const mr_topk_args *args, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,0 +1,85 @@
+// C-ABI of the lightning-indexer top-k selection: the reference's geometry
+// checks (DeepSeekV4Attention.swift:590-612) on the host, the selection on
+// the device.
+#include <hip/hip_runtime.h>
+
+#include <vector>
+
+#include "../../include/minirun_hip.h"
+#include "capi_util.hpp"
+#include "mr_kernels.hpp"
+
+namespace {
+using mrc::fail;
+using mrc::hip_fail;
+}  // namespace
+
+extern "C" {
+
+mr_status mr_topk_geometry(int32_t rows, int32_t cols, int32_t top_k, int32_t ratio, int32_t start_pos,
+                           int32_t offset, int32_t* selected) {
+    if (!(rows > 0 && cols >= 0 && top_k > 0 && ratio > 0 && start_pos >= 0 && offset >= 0))
+        return fail(MR_INVALID_SHAPE, "invalid lightning-index selection geometry");
+    if (start_pos > 0 && rows != 1)
+        return fail(MR_INVALID_SHAPE, "incremental lightning indexing accepts exactly one token");
+    const int64_t end = int64_t(start_pos) + rows;
+    if (end > INT32_MAX) return fail(MR_INVALID_SHAPE, "lightning-index end position overflows Int");
+    const int32_t available = int32_t(end / ratio);
+    if (available > cols)
+        return fail(MR_INVALID_SHAPE, "score matrix has fewer compressed keys than the sequence position requires");
+    const int32_t sel = top_k < available ? top_k : available;
+    if (sel > mr::TOPK_MAX)
+        return fail(MR_INVALID_SHAPE, "top-k selection: %d keys per row exceed the limit of %d", sel, mr::TOPK_MAX);
+    if (available > mr::TOPK_MAX_KEYS)
+        return fail(MR_INVALID_SHAPE, "top-k selection: %d available keys exceed the limit of %d", available,
+                    mr::TOPK_MAX_KEYS);
+    if (available > 0 && int64_t(offset) + available - 1 > INT32_MAX)
+        return fail(MR_INVALID_SHAPE, "lightning cache index overflows Int");
+    if (selected) *selected = sel;
+    return MR_OK;
+}
+
+size_t mr_topk_workspace_size(int32_t rows) { return rows > 0 ? mrc::align256(size_t(rows) * 4) : 0; }
+
+mr_status mr_topk_select(const mr_topk_args* a, void* stream) {
+    if (!a) return fail(MR_INVALID_ARGUMENT, "mr_topk_select: args is NULL");
+    int32_t selected = 0;
+    mr_status st = mr_topk_geometry(a->rows, a->cols, a->top_k, a->ratio, a->start_pos, a->offset, &selected);
+    if (st != MR_OK) return st;
+    if (!a->scores || (selected > 0 && !a->out))
+        return fail(MR_INVALID_ARGUMENT, "top-k selection: scores and out must be non-NULL");
+    if (a->score_row_stride < a->cols || (selected > 0 && a->out_row_stride < selected))
+        return fail(MR_INVALID_ARGUMENT, "top-k selection: row strides are smaller than the rows");
+    const size_t need = mr_topk_workspace_size(a->rows);
+    if (!a->workspace || a->workspace_bytes < need)
+        return fail(MR_WORKSPACE_TOO_SMALL, "top-k selection: workspace %zu bytes < %zu required", a->workspace_bytes,
+                    need);
+    if (selected == 0) return MR_OK;  // every row is empty (:613-616)
+    hipStream_t s = (hipStream_t)stream;
+    mr::TopkParams p{};
+    p.scores = a->scores;
+    p.row_stride = a->score_row_stride;
+    p.rows = a->rows;
+    p.cols = a->cols;
+    p.available = int32_t((int64_t(a->start_pos) + a->rows) / a->ratio);
+    p.selected = selected;
+    p.ratio = a->ratio;
+    p.start_pos = a->start_pos;
+    p.offset = a->offset;
+    p.out = a->out;
+    p.out_stride = a->out_row_stride;
+    p.nan_flags = (int32_t*)a->workspace;
+    hipError_t e = mr::launch_topk_select(p, a->status, s);
+    if (e != hipSuccess) return hip_fail(e, "top-k selection launch");
+    if (a->flags & MR_TOPK_CHECK) {
+        std::vector<int32_t> flags(size_t(a->rows));
+        e = hipMemcpyAsync(flags.data(), p.nan_flags, size_t(a->rows) * 4, hipMemcpyDeviceToHost, s);
+        if (e == hipSuccess) e = hipStreamSynchronize(s);
+        if (e != hipSuccess) return hip_fail(e, "top-k selection check");
+        for (int32_t f : flags)
+            if (f) return fail(MR_NONFINITE, "lightning-index score contains NaN");
+    }
+    return MR_OK;
+}
+
+}  // extern "C"

@@ -83,6 +83,23 @@ struct PrefillAttnParams {
 hipError_t launch_upproj(const UpProjParams& p, hipStream_t st);
 hipError_t launch_prefill_attn(const PrefillAttnParams& p, hipStream_t st);
 
+// ---------------------------------------------------------------- top-k
+constexpr int TOPK_MAX = 4096;          // selected keys per row
+constexpr int TOPK_MAX_KEYS = 65535;    // available keys per row
+
+struct TopkParams {
+    const float* scores;  // [rows][cols], row stride row_stride
+    int64_t row_stride;
+    int32_t rows, cols;
+    int32_t available, selected;  // keys ranked per row, keys emitted per row
+    int32_t ratio, start_pos, offset;
+    int32_t* out;  // [rows][selected], row stride out_stride
+    int64_t out_stride;
+    int32_t* nan_flags;  // [rows]: 1 when the row holds a NaN
+};
+
+hipError_t launch_topk_select(const TopkParams& p, int32_t* status, hipStream_t st);
+
 // ---------------------------------------------------------------- affine
 struct AffineDequantParams {
     const uint32_t* packed;

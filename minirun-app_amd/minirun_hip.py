@@ -92,6 +92,17 @@ class PrefillArgs(C.Structure):
     ]
 
 
+class TopkArgs(C.Structure):
+    _fields_ = [
+        ("scores", C.c_void_p), ("score_row_stride", C.c_int64), ("rows", C.c_int32), ("cols", C.c_int32),
+        ("top_k", C.c_int32), ("ratio", C.c_int32), ("start_pos", C.c_int32), ("offset", C.c_int32),
+        ("out", C.c_void_p), ("out_row_stride", C.c_int64), ("status", C.c_void_p), ("flags", C.c_int32),
+        ("workspace", C.c_void_p), ("workspace_bytes", C.c_size_t),
+    ]
+
+
+TOPK_CHECK = 1
+
 _P = C.c_void_p
 _I32P = C.POINTER(C.c_int32)
 _I64P = C.POINTER(C.c_int64)
@@ -125,6 +136,9 @@ SIGNATURES = {
     "mr_mla_decode_block": (C.c_int, [C.POINTER(BlockArgs), _P]),
     "mr_mla_prefill_workspace_size": (C.c_size_t, [C.POINTER(PrefillArgs)]),
     "mr_mla_prefill": (C.c_int, [C.POINTER(PrefillArgs), _P]),
+    "mr_topk_geometry": (C.c_int, [C.c_int32, C.c_int32, C.c_int32, C.c_int32, C.c_int32, C.c_int32, _I32P]),
+    "mr_topk_workspace_size": (C.c_size_t, [C.c_int32]),
+    "mr_topk_select": (C.c_int, [C.POINTER(TopkArgs), _P]),
     "mr_attention_indices_window": (C.c_int, [C.c_int32, C.c_int32, C.c_int32, _P, _I32P, _I32P]),
     "mr_attention_indices_compressed": (C.c_int, [C.c_int32, C.c_int32, C.c_int32, C.c_int32, _P, _I32P, _I32P]),
 }
@@ -491,6 +505,36 @@ def mla_prefill(q, latent, rope_keys, kv_b, *, scale=None, out=None, out_dtype=N
                              workspace=workspace)
     _check(load().mr_mla_prefill(C.byref(a), _stream(stream)))
     return out
+
+
+def topk_geometry(rows, cols, top_k, ratio, start_pos, offset):
+    """The reference's selection-geometry checks (DeepSeekV4Attention.swift:
+    590-612); returns the number of keys each row receives."""
+    sel = C.c_int32()
+    _check(load().mr_topk_geometry(rows, cols, top_k, ratio, start_pos, offset, C.byref(sel)))
+    return sel.value
+
+
+def lightning_select(scores, top_k, ratio, start_pos, offset, *, check=True, status=None, stream=None):
+    """DeepSeekV4LightningIndexer.select on the device: scores [rows, cols]
+    f32 -> int32 [rows, selected] (offset + key, -1 past the visible keys).
+    check=True synchronises and raises MRError (NONFINITE) on a NaN score,
+    as the reference throws."""
+    torch = _torch()
+    _need(scores, "scores", torch.float32)
+    rows, cols = scores.shape
+    sel = topk_geometry(rows, cols, top_k, ratio, start_pos, offset)
+    out = torch.empty(rows, max(sel, 1), dtype=torch.int32, device=scores.device)
+    ws = torch.empty(max(load().mr_topk_workspace_size(rows), 1), dtype=torch.uint8, device=scores.device)
+    a = TopkArgs()
+    a.scores, a.score_row_stride, a.rows, a.cols = scores.data_ptr(), scores.stride(0), rows, cols
+    a.top_k, a.ratio, a.start_pos, a.offset = top_k, ratio, start_pos, offset
+    a.out, a.out_row_stride = out.data_ptr(), out.stride(0)
+    a.status = status.data_ptr() if status is not None else None
+    a.flags = TOPK_CHECK if check else 0
+    a.workspace, a.workspace_bytes = ws.data_ptr(), ws.numel()
+    _check(load().mr_topk_select(C.byref(a), _stream(stream)))
+    return out[:, :sel]
 
 
 def attention_indices_window(window, seq_len, start_pos):

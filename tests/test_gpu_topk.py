@@ -1,0 +1,89 @@
+"""Parity of the device lightning-indexer selection
+(DeepSeekV4LightningIndexer.selecting, DeepSeekV4Attention.swift:582-645)
+with the oracle: bit-exact indices, including ties (ascending key id),
+masked keys (-1), -0 == +0, infinities, NaN reporting and the edge sizes."""
+import numpy as np
+import pytest
+
+import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def M():
+    import minirun_hip as M
+
+    M.load()
+    return M
+
+
+def dev(a):
+    import torch
+
+    return torch.from_numpy(np.ascontiguousarray(a, np.float32)).cuda()
+
+
+def compare(M, scores, top_k, ratio, start_pos, offset, tag):
+    print(f"topk {tag}: rows={scores.shape[0]} cols={scores.shape[1]} k={top_k} ratio={ratio} start={start_pos}",
+          flush=True)
+    st, exp = O.topk_select(scores, top_k, ratio, start_pos, offset)
+    assert st == O.OK
+    got = M.lightning_select(dev(scores), top_k, ratio, start_pos, offset).cpu().numpy()
+    assert got.shape == exp.shape
+    np.testing.assert_array_equal(got, exp)
+
+
+def normal(tag, shape):
+    return O.bf16_to_f32(O.normal_bf16(tag, shape)) * np.float32(1.37)
+
+
+def test_decode_row_top2048_of_32768(M):
+    # one decode token at position 131071, ratio 4: 32768 compressed keys
+    compare(M, normal("tk.dec", (1, 32768)), 2048, 4, 131071, 0, "decode")
+
+
+def test_ties_break_by_ascending_key(M):
+    s = np.floor(normal("tk.ties", (1, 5000)) * 2).astype(np.float32)  # ~10 distinct values
+    compare(M, s, 1000, 1, 4999, 7, "ties")
+    s2 = np.zeros((1, 3000), np.float32)  # one value everywhere
+    compare(M, s2, 512, 1, 2999, 0, "all-equal")
+
+
+def test_signed_zero_and_infinities(M):
+    s = normal("tk.inf", (1, 4096))
+    s[0, ::7] = 0.0
+    s[0, 3::7] = -0.0
+    s[0, 5::97] = np.inf
+    s[0, 6::89] = -np.inf
+    compare(M, s, 1024, 1, 4095, 0, "zeros-infs")
+    s2 = np.full((1, 600), -np.inf, np.float32)  # visible -inf ties masked keys by key id
+    compare(M, s2, 100, 1, 599, 0, "all-minus-inf")
+
+
+@pytest.mark.parametrize("rows,cols,top_k,ratio,offset", [(300, 75, 16, 4, 128), (64, 64, 64, 1, 0),
+                                                          (17, 40, 100, 2, 3), (4096, 1024, 512, 4, 0)])
+def test_prefill_rows_with_masking(M, rows, cols, top_k, ratio, offset):
+    compare(M, normal(f"tk.pf{rows}", (rows, cols)), top_k, ratio, 0, offset, "prefill")
+
+
+def test_limits(M):
+    compare(M, normal("tk.max", (1, 65535)), 4096, 1, 65534, 0, "max-keys")
+    compare(M, normal("tk.one", (1, 1)), 1, 1, 0, 0, "one-key")
+
+
+def test_nan_is_reported(M):
+    import torch
+
+    import minirun_hip as MH
+
+    s = normal("tk.nan", (3, 64))
+    s[2, 63] = np.nan  # outside the visible keys of every row: still an error
+    with pytest.raises(MH.MRError) as e:
+        M.lightning_select(dev(s), 8, 1, 0, 0)
+    assert e.value.status == MH.NONFINITE and "NaN" in e.value.message
+    status = torch.full((1,), -1, dtype=torch.int32, device="cuda")
+    M.lightning_select(dev(s), 8, 1, 0, 0, check=False, status=status)
+    assert int(status.item()) == MH.NONFINITE
+    M.lightning_select(dev(normal("tk.ok", (3, 64))), 8, 1, 0, 0, check=False, status=status)
+    assert int(status.item()) == 0

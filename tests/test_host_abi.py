@@ -108,3 +108,31 @@ def test_index_table_errors():
     with pytest.raises(M.MRError) as e:
         M.attention_indices_compressed(0, 2, 0, 0)
     assert e.value.status == M.INVALID_SHAPE
+
+
+@pytest.mark.parametrize("rows,cols,top_k,ratio,start,offset,needle", [
+    (0, 4, 2, 1, 0, 0, "invalid lightning-index selection geometry"),
+    (2, 4, 2, 0, 0, 0, "invalid lightning-index selection geometry"),
+    (2, 4, 2, 1, 3, 0, "exactly one token"),
+    (1, 2, 2, 1, 3, 0, "fewer compressed keys"),
+    (1, 70000, 8, 1, 69999, 0, "exceed the limit"),
+    (1, 8, 5000, 1, 7, 0, None),
+    (1, 8, 4, 1, 7, 2147483645, "overflows"),
+])
+def test_topk_geometry_errors(rows, cols, top_k, ratio, start, offset, needle):
+    if needle is None:
+        assert M.topk_geometry(rows, cols, top_k, ratio, start, offset) == 8
+        return
+    with pytest.raises(M.MRError) as e:
+        M.topk_geometry(rows, cols, top_k, ratio, start, offset)
+    assert needle in e.value.message, e.value.message
+    # the oracle rejects the reference's own geometry errors alike
+    if rows > 0 and "limit" not in needle and "overflows" not in needle:
+        st, _ = O.topk_select(np.zeros((rows, cols), np.float32), top_k, ratio, start, offset)
+        assert st == O.INVALID_SHAPE
+
+
+def test_topk_geometry_counts():
+    assert M.topk_geometry(1, 32768, 2048, 4, 131071, 0) == 2048
+    assert M.topk_geometry(300, 75, 16, 4, 0, 128) == 16
+    assert M.topk_geometry(3, 4, 16, 4, 0, 0) == 0   # fewer than ratio tokens: empty rows

@@ -269,6 +269,11 @@ def test_topk_select_brute_force_ties_and_masking():
     st, got = O.topk_select(s1, top_k=8, ratio=4, start_pos=200, offset=0)
     assert got.tolist() == _brute_topk(s1, 8, 4, 200, 0)
     assert got[0, 0] == 5 and got[0, 1] == 9  # tie -> ascending key id
+    # a visible -inf score ties with masked keys (both compare as -inf): key order
+    s2 = np.array([[1.0, -np.inf, 2.0, 5.0, 5.0, 5.0]], np.float32)
+    st, got = O.topk_select(np.repeat(s2, 6, axis=0), top_k=6, ratio=1, start_pos=0, offset=0)
+    assert got.tolist() == _brute_topk(np.repeat(s2, 6, axis=0), 6, 1, 0, 0)
+    assert got[2].tolist() == [2, 0, -1, -1, -1, -1] and got[1].tolist() == [0, 1, -1, -1, -1, -1]
 
 
 def test_topk_select_errors_and_empty():
