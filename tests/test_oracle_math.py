@@ -273,7 +273,7 @@ def test_topk_select_brute_force_ties_and_masking():
     s2 = np.array([[1.0, -np.inf, 2.0, 5.0, 5.0, 5.0]], np.float32)
     st, got = O.topk_select(np.repeat(s2, 6, axis=0), top_k=6, ratio=1, start_pos=0, offset=0)
     assert got.tolist() == _brute_topk(np.repeat(s2, 6, axis=0), 6, 1, 0, 0)
-    assert got[2].tolist() == [2, 0, -1, -1, -1, -1] and got[1].tolist() == [0, 1, -1, -1, -1, -1]
+    assert got[2].tolist() == [2, 0, 1, -1, -1, -1] and got[1].tolist() == [0, 1, -1, -1, -1, -1]
 
 
 def test_topk_select_errors_and_empty():
