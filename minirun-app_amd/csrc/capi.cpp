@@ -68,15 +68,16 @@ int cu_count() {
 }
 
 struct DecodePlan {
-    int n_rows, head_groups, h_pad, splits, rows_per_split;
+    int n_rows, hg_size, head_groups, h_pad, splits, rows_per_split;
     size_t o_bytes, ml_bytes, total;
 };
 
 DecodePlan plan_decode(const mr_mla_decode_args* a) {
     DecodePlan pl{};
     pl.n_rows = a->indices ? a->n_idx : a->n_ctx;
-    pl.head_groups = mr::decode_head_groups(a->heads);
-    pl.h_pad = pl.head_groups * 32;
+    pl.hg_size = mr::decode_head_group_size(a->heads, (a->flags & MR_DECODE_NO_TRANSPOSE_READ) == 0);
+    pl.head_groups = (a->heads + pl.hg_size - 1) / pl.hg_size;
+    pl.h_pad = pl.head_groups * pl.hg_size;
     const int rows = std::max(pl.n_rows, 0);
     int splits;
     if (a->num_splits > 0) {
@@ -98,7 +99,8 @@ DecodePlan plan_decode(const mr_mla_decode_args* a) {
     pl.splits = splits;
     pl.rows_per_split = rps;
     const size_t recs = size_t(std::max(a->batch, 0)) * size_t(splits) * size_t(pl.h_pad);
-    pl.o_bytes = align256(recs * 512 * sizeof(float));
+    // split partials in the output's precision: bf16 for bf16 output, f32 for f32
+    pl.o_bytes = align256(recs * 512 * (a->out_dtype == MR_F32 ? sizeof(float) : sizeof(uint16_t)));
     pl.ml_bytes = align256(recs * 2 * sizeof(float));
     pl.total = pl.o_bytes + pl.ml_bytes;
     return pl;
@@ -141,8 +143,11 @@ mr_status check_decode(const mr_mla_decode_args* a) {
     }
     if (a->out_dtype != MR_BF16 && a->out_dtype != MR_F32)
         return fail(MR_INVALID_DTYPE, "mla decode: out_dtype must be MR_BF16 or MR_F32");
-    if (a->out_head_stride < 512 || a->out_batch_stride < 0 || a->out_head_stride % 4 || a->out_batch_stride % 4)
-        return fail(MR_INVALID_ARGUMENT, "mla decode: out strides must be multiples of 4, head stride >= 512");
+    // the combine stores 16 bytes per lane: 8 bf16 or 4 f32 elements
+    const int64_t ovec = a->out_dtype == MR_F32 ? 4 : 8;
+    if (a->out_head_stride < 512 || a->out_batch_stride < 0 || a->out_head_stride % ovec || a->out_batch_stride % ovec)
+        return fail(MR_INVALID_ARGUMENT, "mla decode: out strides must be multiples of %lld elements, head stride >= 512",
+                    (long long)ovec);
     if (!aligned16(a->out)) return fail(MR_INVALID_ARGUMENT, "mla decode: out must be 16-byte aligned");
     if (a->num_splits < 0) return fail(MR_INVALID_ARGUMENT, "mla decode: num_splits must be >= 0");
     // row offsets inside one batch element's cache are formed in 32 bits
@@ -242,13 +247,16 @@ mr_status mr_mla_decode(const mr_mla_decode_args* a, void* stream) {
     p.rows_per_split = pl.rows_per_split;
     p.head_groups = pl.head_groups;
     p.h_pad = pl.h_pad;
+    p.hg_size = pl.hg_size;
     p.scale_log2 = a->scale * 1.4426950408889634f;
-    p.ws_o = (float*)a->workspace;
+    p.ws_o = a->workspace;
+    p.ws_f32 = a->out_dtype == MR_F32;
     p.ws_ml = (float*)((char*)a->workspace + pl.o_bytes);
     p.err_flag = nullptr;
 
     mr::CombineParams cp{};
     cp.ws_o = p.ws_o;
+    cp.ws_f32 = p.ws_f32;
     cp.ws_ml = p.ws_ml;
     cp.sinks = a->sinks;
     cp.out = a->out;

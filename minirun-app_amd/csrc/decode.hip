@@ -97,6 +97,12 @@ __device__ __forceinline__ void wait_vmcnt() {
 
 constexpr float TAU = 8.f;  // log2 headroom before the running max is raised
 
+// Partial record of (batch b, head, split): [batch][h_pad][splits] order, so
+// the splits of one head are contiguous for the combine.
+__device__ __forceinline__ int64_t part_rec(const DecodeParams& p, int b, int head, int split) {
+    return ((int64_t)b * p.h_pad + head) * p.splits + split;
+}
+
 template <int DR, bool GATHER, bool TR, bool PACKED>
 __global__ void __launch_bounds__(THREADS, 1) mla_decode_split(DecodeParams p) {
     using G = Geo<DR>;
@@ -402,113 +408,545 @@ __global__ void __launch_bounds__(THREADS, 1) mla_decode_split(DecodeParams p) {
     l_run += __shfl_xor(l_run, 32);
     lds_barrier();  // every wave is past its last LDS read of the buffers
     if (lg == 0) red[w][lc] = l_run;
-    // O through LDS (the sub-chunk buffers are free): [32 heads][512] fp32,
-    // then 16-byte coalesced stores of the partial record
-    float* ostage = (float*)cbuf;
+    lds_barrier();
+    // O / l through LDS (the sub-chunk buffers are free): [32 heads][512] in
+    // the partial precision, then 16-byte coalesced stores of the record.
+    // Head 16T + j sums the row tiles of waves T and T + 2.
+    float inv[2][4];
+#pragma unroll
+    for (int T = 0; T < 2; ++T)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const float lt = red[T][4 * lg + i] + red[T + 2][4 * lg + i];
+            inv[T][i] = lt > 0.f ? 1.f / lt : 0.f;
+        }
 #pragma unroll
     for (int T = 0; T < 2; ++T)
 #pragma unroll
         for (int i = 0; i < 4; ++i)
 #pragma unroll
-            for (int J = 0; J < 8; ++J) ostage[(16 * T + 4 * lg + i) * R + 128 * w + 16 * J + lc] = oacc[T][J][i];
+            for (int J = 0; J < 8; ++J) {
+                const int e = (16 * T + 4 * lg + i) * R + 128 * w + 16 * J + lc;
+                const float v = oacc[T][J][i] * inv[T][i];
+                if (p.ws_f32)
+                    ((float*)cbuf)[e] = v;
+                else
+                    ((__bf16*)cbuf)[e] = (__bf16)v;
+            }
     lds_barrier();
 
-    const int64_t rec = (int64_t)unit * p.h_pad + hg * HG;
     if (rt == 0 && lg == 0) {
         const int hh = 16 * ht + lc;
-        p.ws_ml[(rec + hh) * 2 + 0] = m_run;
-        p.ws_ml[(rec + hh) * 2 + 1] = red[w][lc] + red[w ^ 2][lc];
+        const int64_t r = part_rec(p, b, hg * HG + hh, split);
+        p.ws_ml[r * 2 + 0] = m_run;
+        p.ws_ml[r * 2 + 1] = red[w][lc] + red[w ^ 2][lc];
     }
-    float* dst = p.ws_o + rec * R;
-#pragma unroll
-    for (int k = 0; k < HG * R / 4 / THREADS; ++k) {
-        const int e4 = tid + THREADS * k;
-        *(f32x4*)(dst + 4 * e4) = *(const f32x4*)(ostage + 4 * e4);
+    const int esz = p.ws_f32 ? 4 : 2;
+    const int cpr = R * esz / 16;  // 16-byte chunks per head row
+    for (int e = tid; e < HG * cpr; e += THREADS) {
+        const int r = e / cpr, c = e - r * cpr;
+        *(u32x4*)((char*)p.ws_o + part_rec(p, b, hg * HG + r, split) * R * esz + 16 * c) =
+            *(const u32x4*)(cbuf + r * R * esz + 16 * c);
     }
 }
 
-// Merge the split partials: one 256-thread block per (batch, head, 256-column
-// half).  Split weights are computed once into LDS; wave q then streams the
-// splits q, q+4, ... with independent 16-byte loads (four columns per lane)
-// and the four waves' sums are added through LDS.
-__global__ void __launch_bounds__(256) mla_combine(CombineParams p) {
+// ---------------------------------------------------------------------------
+// Role-split variant for head groups of HGS heads (32 or 64).  HGS/32 QK
+// waves score 32 heads each over all 32 rows of a sub-chunk as
+// S^T = K . Q^T on 32x32x16 MFMA: a lane owns one head, so its running max
+// and sum stay in the lane (one exchange between the wave halves), and each
+// cache row is read from LDS once per 32 heads; P goes to LDS as
+// [head][key].  Four PV waves own 128 output columns each, run one
+// sub-chunk behind the QK waves and issue all the DMA.  One barrier per phase: in phase j the QK
+// waves turn sub-chunk j into P buffer j&1 while the PV waves consume P
+// buffer (j-1)&1 with the rows of j-1 and refill the buffer of j-2 with
+// j+2.  Each role runs its own loop, so neither carries the other's
+// registers.
+template <int HGS>
+struct WsShape {
+    static constexpr int QKW = HGS / 32;           // QK waves
+    static constexpr int THREADS = 64 * (QKW + 4);  // + 4 PV waves
+};
+
+template <int DR, bool GATHER, bool PACKED, int HGS>
+__global__ void __launch_bounds__(WsShape<HGS>::THREADS, 1) mla_decode_ws(DecodeParams p) {
+    using G = Geo<DR>;
+    constexpr int QKW = WsShape<HGS>::QKW;
+    constexpr int NT = WsShape<HGS>::THREADS;
+    constexpr int HT = HGS / 16;  // 16-head tiles of a PV wave
+    __shared__ __attribute__((aligned(1024))) char cbuf[NBUF * G::BUF];
+    __shared__ __attribute__((aligned(16))) char pbuf[2][HGS * PSTR];
+    __shared__ __attribute__((aligned(16))) float alpha_s[2][HGS];
+    __shared__ __attribute__((aligned(16))) float l_s[HGS];
+    __shared__ int flag_s[2][QKW];
+    __shared__ int32_t idx_s[GATHER ? MAX_GATHER_ROWS : 1];
+
+    const int bid = blockIdx.x;
+    const int xcd = bid & 7;
+    const int qb = bid >> 3;
+    const int hg = qb % p.head_groups;
+    const int unit = (qb / p.head_groups) * 8 + xcd;
+    if (unit >= p.batch * p.splits) return;
+    const int b = unit / p.splits;
+    const int split = unit % p.splits;
+    const int row_begin = split * p.rows_per_split;
+    const int row_end = min(row_begin + p.rows_per_split, p.n_rows);
+    const int nrows = max(row_end - row_begin, 0);
+    const int nsub = (nrows + ROWS - 1) / ROWS;
+
+    const int tid = threadIdx.x;
+    const int l = tid & 63;
+    const int lg = l >> 4;
+    const int lc = l & 15;
+    const int wu = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform role choice
+    const bool is_qk = wu < QKW;
+    const int qw = wu;        // QK wave: 32-head tile
+    const int pw = wu - QKW;  // PV wave: 128-column quarter
+
+    const uint16_t* lat = p.latent + (int64_t)b * p.lat_bs;
+    const uint16_t* rop = DR ? p.rope + (int64_t)b * p.rope_bs : nullptr;
+
+    if (GATHER) {
+        const int32_t* ind = p.indices + (int64_t)b * p.n_idx;
+        for (int i = tid; i < nrows; i += NT) {
+            const int32_t v = ind[row_begin + i];
+            idx_s[i] = (v >= 0 && v < p.n_ctx) ? v : -1;
+        }
+        __syncthreads();
+    }
+
+    const float scale2 = p.scale_log2;
+    // staging of the partial record after the last phase: rows of 512 values
+    // padded by 16 bytes, so the four lane groups' rows fall on distinct banks
+    const int esz = p.ws_f32 ? 4 : 2;
+    const int srow = R * esz + 16;
+
+    if (is_qk) {
+        // ---------------------------------------------------------- QK role
+        // B operand of 32x32x16: head 32qw + l%32, k = 16ks + 8(l/32)..+7
+        const int hq = 32 * qw + (l & 31);  // this lane's head within the group
+        const int kh = l >> 5;              // k half / key half
+        bf16x8 qreg[2 * G::KS];
+        {
+            const int h0 = hg * HGS + hq;
+            const int h = h0 < p.heads ? h0 : 0;
+            const uint16_t* ql = p.q_lat + (int64_t)b * p.q_lat_bs + (int64_t)h * p.q_lat_hs;
+            const uint16_t* qr = DR ? p.q_rope + (int64_t)b * p.q_rope_bs + (int64_t)h * p.q_rope_hs : nullptr;
+#pragma unroll
+            for (int ks = 0; ks < 2 * G::KS; ++ks) {
+                const int d = 16 * ks + 8 * kh;
+                qreg[ks] = d < R ? *(const bf16x8*)(ql + d) : *(const bf16x8*)(qr + (d - R));
+            }
+        }
+        // A operand: row (key) l%32 of the sub-chunk, chunk 2ks + kh; with the
+        // row swizzle, chunk 16v + u2 sits at 256v + qo[u2/2 ...]: latent
+        // k-steps ks -> qo[ks%8] + 256 (ks/8), rope k-steps -> ro[ks-32]
+        const int arow = l & 31;
+        int qo[8], ro[4];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) qo[u] = arow * G::ROWB + 16 * ((2 * u + kh) ^ (arow & 15));
+#pragma unroll
+        for (int u = 0; u < 4; ++u) ro[u] = arow * G::ROWB + 1024 + 16 * ((2 * u + kh) ^ (arow & 7));
+        auto qk_a = [&](const char* cur, int ks) -> bf16x8 {
+            return ks < 32 ? *(const bf16x8*)(cur + qo[ks & 7] + 256 * (ks >> 3))
+                           : *(const bf16x8*)(cur + ro[ks - 32]);
+        };
+        float m_run = NEG_INF;  // reference max (base 2) of this lane's head
+        float l_run = 0.f;      // this lane's share of that head's sum
+        lds_barrier();  // sub-chunk 0 landed
+#pragma unroll 1
+        for (int s = 0; s <= nsub; ++s) {
+            if (s < nsub) {
+                const char* cur = cbuf + (s & (NBUF - 1)) * G::BUF;
+                const int par = s & 1;
+                // 2 KS k-steps in operand groups of QG, double-buffered, on two
+                // accumulator chains (even / odd k-steps) so consecutive MFMAs
+                // do not wait on each other; the fences keep the scheduler from
+                // hoisting every LDS read
+                constexpr int NK = 2 * G::KS;
+                constexpr int QG = 4;
+                constexpr int NG = NK / QG;
+                f32x16 sacc[2] = {f32x16{}, f32x16{}};
+                bf16x8 ga[2][QG];
+#pragma unroll
+                for (int e = 0; e < QG; ++e) ga[0][e] = qk_a(cur, e);
+#pragma unroll
+                for (int g = 0; g < NG; ++g) {
+                    if (g + 1 < NG) {
+#pragma unroll
+                        for (int e = 0; e < QG; ++e) ga[(g + 1) & 1][e] = qk_a(cur, (g + 1) * QG + e);
+                    }
+                    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                    for (int e = 0; e < QG; ++e) {
+                        const int k = g * QG + e;
+                        sacc[k & 1] = mfma32(ga[g & 1][e], qreg[k], sacc[k & 1]);
+                    }
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+                // S^T: acc i -> key 8(i/4) + 4kh + i%4 of the sub-chunk, head hq
+                float sv[16];
+                const int rbase = row_begin + s * ROWS;
+#pragma unroll
+                for (int i = 0; i < 16; ++i) sv[i] = (sacc[0][i] + sacc[1][i]) * scale2;
+                // masking only on a sub-chunk past the split end or gathered
+                // (a wave-uniform branch: full dense sub-chunks skip it)
+                if (__builtin_amdgcn_readfirstlane(GATHER || rbase + ROWS > row_end)) {
+#pragma unroll
+                    for (int i = 0; i < 16; ++i) {
+                        const int r = rbase + 8 * (i >> 2) + 4 * kh + (i & 3);
+                        bool ok = r < row_end;
+                        if (GATHER) ok = ok && idx_s[r - row_begin] >= 0;
+                        if (!ok) sv[i] = NEG_INF;
+                    }
+                }
+                float cm = sv[0];
+#pragma unroll
+                for (int i = 1; i < 16; ++i) cm = fmaxf(cm, sv[i]);
+                cm = fmaxf(cm, __shfl_xor(cm, 32));
+                // reference max raised only when a score passes it by TAU, so
+                // O is rarely rescaled; P <= 2^TAU
+                const bool raise = cm > m_run + TAU;  // false while cm is -inf
+                const float m_new = raise ? cm : m_run;
+                const float alpha = raise ? exp2f(m_run - m_new) : 1.f;
+                m_run = m_new;
+                // while every row so far is masked, m is -inf and so is every
+                // score: a finite reference keeps exp2 at 0 (not -inf - -inf)
+                const float m_ref = m_new == NEG_INF ? 0.f : m_new;
+                float ls = 0.f;
+#pragma unroll
+                for (int i4 = 0; i4 < 4; ++i4) {
+                    float pv[4];
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) pv[e] = __builtin_amdgcn_exp2f(sv[4 * i4 + e] - m_ref);
+                    ls += (pv[0] + pv[1]) + (pv[2] + pv[3]);
+                    typedef __bf16 bf16x2v __attribute__((ext_vector_type(2)));
+                    const bf16x2v lo = {(__bf16)pv[0], (__bf16)pv[1]};
+                    const bf16x2v hi = {(__bf16)pv[2], (__bf16)pv[3]};
+                    *(u32x2*)(pbuf[par] + hq * PSTR + 2 * (8 * i4 + 4 * kh)) =
+                        u32x2{__builtin_bit_cast(uint32_t, lo), __builtin_bit_cast(uint32_t, hi)};
+                }
+                l_run = l_run * alpha + ls;
+                if (kh == 0) alpha_s[par][hq] = alpha;
+                const bool any = __builtin_amdgcn_ballot_w64(raise) != 0;
+                if (l == 0) flag_s[par][qw] = any;
+            }
+            lds_barrier();  // end of phase s
+        }
+        l_run += __shfl_xor(l_run, 32);
+        if (kh == 0) {
+            l_s[hq] = l_run;
+            const int64_t r = part_rec(p, b, hg * HGS + hq, split);
+            p.ws_ml[r * 2 + 0] = m_run;
+            p.ws_ml[r * 2 + 1] = l_run;
+        }
+        lds_barrier();  // l_s ready
+        lds_barrier();  // staging written
+    } else {
+        // ---------------------------------------------------------- PV role
+        int dma_row[G::NLD], dma_c16[G::NLD];
+#pragma unroll
+        for (int k = 0; k < G::NLD; ++k) {
+            const int slot = 64 * (pw + 4 * k) + l;
+            dma_row[k] = slot / G::CPR;
+            dma_c16[k] = 16 * swz(slot - dma_row[k] * G::CPR, dma_row[k]);
+        }
+        const uint32_t rs_b = (uint32_t)(p.lat_rs * 2);
+        // every PV lane always loads (rows past the split read a valid row and
+        // are masked), so each PV wave issues exactly NLD loads per sub-chunk
+        auto issue = [&](int s, char* base) {
+            const int rbase = row_begin + s * ROWS;
+#pragma unroll
+            for (int k = 0; k < G::NLD; ++k) {
+                int rr = dma_row[k];
+                int src_row;
+                if (GATHER) {
+                    const int v = (rbase + rr < row_end) ? idx_s[rbase + rr - row_begin] : -1;
+                    src_row = v >= 0 ? v : 0;
+                } else {
+                    if (rbase + ROWS > row_end) rr = min(rr, row_end - 1 - rbase);
+                    src_row = rbase + rr;
+                }
+                char* dst = base + 1024 * (pw + 4 * k);
+                if (PACKED) {
+                    if (GATHER)
+                        dma16_off(lat, (uint32_t)src_row * rs_b + (uint32_t)dma_c16[k], dst);
+                    else
+                        dma16_off((const char*)lat + (int64_t)rbase * rs_b, (uint32_t)rr * rs_b + (uint32_t)dma_c16[k],
+                                  dst);
+                } else {
+                    const int c = dma_c16[k] >> 4;
+                    const uint16_t* src = c < R / 8 ? lat + (int64_t)src_row * p.lat_rs + c * 8
+                                                    : rop + (int64_t)src_row * p.rope_rs + (c - R / 8) * 8;
+                    dma16(src, dst);
+                }
+            }
+        };
+        // B operand of PV (V, natural key order): lane group lg takes keys
+        // 8lg..8lg+3 (tr0) and 8lg+4..8lg+7 (tr1) of column block 16J by
+        // transposed reads; lane lc addresses key row (lc/4), columns 4(lc%4)
+        int tr0[8], tr1[8];
+        {
+            const int r0 = 8 * lg + (lc >> 2), r1 = r0 + 4;
+#pragma unroll
+            for (int J = 0; J < 8; ++J) {
+                const int c = 16 * pw + 2 * J + ((lc & 3) >> 1);  // 16-byte chunk of the column
+                tr0[J] = r0 * G::ROWB + 16 * swz(c, r0) + 8 * (lc & 1);
+                tr1[J] = r1 * G::ROWB + 16 * swz(c, r1) + 8 * (lc & 1);
+            }
+        }
+        f32x4 oacc[HT][8];  // O[HGS heads][128pw .. +127]
+#pragma unroll
+        for (int T = 0; T < HT; ++T)
+#pragma unroll
+            for (int J = 0; J < 8; ++J) oacc[T][J] = f32x4{0.f, 0.f, 0.f, 0.f};
+        // prologue: sub-chunks 0 .. NBUF-2 in flight, wait for 0
+        const int pro = min(nsub, NBUF - 1);
+        for (int s = 0; s < pro; ++s) issue(s, cbuf + s * G::BUF);
+        if (pro >= 3)
+            wait_vmcnt<2 * G::NLD>();
+        else if (pro == 2)
+            wait_vmcnt<G::NLD>();
+        else
+            wait_vmcnt<0>();
+        lds_barrier();  // sub-chunk 0 landed
+#pragma unroll 1
+        for (int s = 0; s <= nsub; ++s) {
+            // refill the buffer of s-2 (PV(s-2) ran in phase s-1) with s+2
+            if (s >= 1 && s + 2 < nsub) issue(s + 2, cbuf + ((s + 2) & (NBUF - 1)) * G::BUF);
+            if (s >= 1) {
+                const int t = s - 1;  // PV(t): P buffer t&1, rows of buffer t%4
+                const int par = t & 1;
+                const char* cur = cbuf + (t & (NBUF - 1)) * G::BUF;
+                bool rescale = false;
+#pragma unroll
+                for (int q = 0; q < QKW; ++q) rescale |= flag_s[par][q] != 0;
+                if (rescale) {
+#pragma unroll
+                    for (int T = 0; T < HT; ++T) {
+                        const f32x4 a4 = *(const f32x4*)(alpha_s[par] + 16 * T + 4 * lg);
+#pragma unroll
+                        for (int J = 0; J < 8; ++J) oacc[T][J] *= a4;
+                    }
+                }
+                bf16x8 pa[HT];
+#pragma unroll
+                for (int T = 0; T < HT; ++T) pa[T] = *(const bf16x8*)(pbuf[par] + (16 * T + lc) * PSTR + 16 * lg);
+                bf16x4 b0[8], b1[8];
+#pragma unroll
+                for (int J = 0; J < 8; ++J) {
+                    b0[J] = ds_read_tr16(cur + tr0[J]);
+                    b1[J] = ds_read_tr16(cur + tr1[J]);
+                }
+                __builtin_amdgcn_sched_barrier(0);  // all 16 reads in flight before the MFMAs
+#pragma unroll
+                for (int J = 0; J < 8; ++J) {
+                    const bf16x8 bb = __builtin_shufflevector(b0[J], b1[J], 0, 1, 2, 3, 4, 5, 6, 7);
+#pragma unroll
+                    for (int T = 0; T < HT; ++T) oacc[T][J] = mfma16(pa[T], bb, oacc[T][J]);
+                }
+            }
+            // sub-chunk s+1 must have landed before the barrier; only s+2 may
+            // still be in flight
+            if (s + 1 < nsub) {
+                if (s + 2 < nsub)
+                    wait_vmcnt<G::NLD>();
+                else
+                    wait_vmcnt<0>();
+            }
+            lds_barrier();  // end of phase s
+        }
+        lds_barrier();  // l_s ready
+        // O / l into the staging area [HGS heads][srow bytes], partial precision
+        float inv[HT][4];
+#pragma unroll
+        for (int T = 0; T < HT; ++T) {
+            const f32x4 l4 = *(const f32x4*)(l_s + 16 * T + 4 * lg);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) inv[T][i] = l4[i] > 0.f ? 1.f / l4[i] : 0.f;
+        }
+        if (p.ws_f32) {
+#pragma unroll
+            for (int T = 0; T < HT; ++T)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    float* row = (float*)(cbuf + (16 * T + 4 * lg + i) * srow) + 128 * pw + lc;
+#pragma unroll
+                    for (int J = 0; J < 8; ++J) row[16 * J] = oacc[T][J][i] * inv[T][i];
+                }
+        } else {
+#pragma unroll
+            for (int T = 0; T < HT; ++T)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    __bf16* row = (__bf16*)(cbuf + (16 * T + 4 * lg + i) * srow) + 128 * pw + lc;
+#pragma unroll
+                    for (int J = 0; J < 8; ++J) row[16 * J] = (__bf16)(oacc[T][J][i] * inv[T][i]);
+                }
+        }
+        lds_barrier();  // staging written
+    }
+    // the partial records: one row of 512 values per head, 16-byte stores
+    const int cpr = R * esz / 16;  // 16-byte chunks per row
+    for (int e = tid; e < HGS * cpr; e += NT) {
+        const int r = e / cpr, c = e - r * cpr;
+        // streamed past L2: the combine on other XCDs reads them from memory
+        __builtin_nontemporal_store(*(const u32x4*)(cbuf + r * srow + 16 * c),
+                                    (u32x4*)((char*)p.ws_o + part_rec(p, b, hg * HGS + r, split) * R * esz + 16 * c));
+    }
+}
+
+// Merge the split partials.  A partial is O_s / l_s (bf16 for bf16 output,
+// f32 for f32 output) with its running max m_s and sum l_s (fp32):
+//   out = sum_s w_s (O_s / l_s) / (sum_s w_s + sink),  w_s = l_s 2^(m_s - M).
+// One 512-thread block per (batch, head): wave w sums splits w, w+8, ... over
+// all 512 columns (eight per lane), so every load takes a whole 1 KB (bf16)
+// record and a block streams its head's contiguous records.  The first
+// COMBINE_PF loads of each wave go out before the weights are known, so the
+// block waits on memory about once.  The eight waves' sums meet in LDS.
+constexpr int COMBINE_THREADS = 512;
+constexpr int COMBINE_PF = 16;  // prefetched splits per wave (128 splits)
+
+template <bool F32>
+__global__ void __launch_bounds__(COMBINE_THREADS) mla_combine(CombineParams p) {
     __shared__ float wgt[MAX_COMBINE_SPLITS];
-    __shared__ float red_w[4];
-    __shared__ f32x4 part[3][64];
+    __shared__ float red_w[8];
+    __shared__ f32x4 part[8][64][2];
     const int bh = blockIdx.x;
     const int b = bh / p.heads;
     const int h = bh % p.heads;
     const int tid = threadIdx.x;
-    const int q = tid >> 6;
+    const int w = tid >> 6;
     const int l = tid & 63;
-    const int64_t rec0 = (int64_t)b * p.splits * p.h_pad + h;
+    const int64_t rec0 = ((int64_t)b * p.h_pad + h) * p.splits;  // the splits of (b, h) are contiguous
+    const int v = 8 * l;                                         // this lane's eight columns
+    typedef f32x4 F8[2];
+    auto ld8 = [&](int s, F8& o) {
+        const int64_t e = (rec0 + s) * R + v;
+        if (F32) {
+            o[0] = *(const f32x4*)((const float*)p.ws_o + e);
+            o[1] = *(const f32x4*)((const float*)p.ws_o + e + 4);
+        } else {
+            const u32x4 u = *(const u32x4*)((const uint16_t*)p.ws_o + e);
+            o[0] = f32x4{__uint_as_float(u[0] << 16), __uint_as_float(u[0] & 0xffff0000u), __uint_as_float(u[1] << 16),
+                         __uint_as_float(u[1] & 0xffff0000u)};
+            o[1] = f32x4{__uint_as_float(u[2] << 16), __uint_as_float(u[2] & 0xffff0000u), __uint_as_float(u[3] << 16),
+                         __uint_as_float(u[3] & 0xffff0000u)};
+        }
+    };
+    // partials first (independent of the weights), then (m, l) of every split
+    F8 x[COMBINE_PF];
+#pragma unroll
+    for (int k = 0; k < COMBINE_PF; ++k) {
+        const int s = w + 8 * k;
+        if (s < p.splits)
+            ld8(s, x[k]);
+        else
+            x[k][0] = x[k][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+    constexpr int MLK = MAX_COMBINE_SPLITS / COMBINE_THREADS;
+    float ml_m[MLK], ml_l[MLK];
+#pragma unroll
+    for (int k = 0; k < MLK; ++k) {
+        const int s = tid + COMBINE_THREADS * k;
+        ml_m[k] = NEG_INF;
+        ml_l[k] = 0.f;
+        if (s < p.splits) {
+            const f32x2 ml = *(const f32x2*)(p.ws_ml + (rec0 + s) * 2);
+            ml_m[k] = ml[0];
+            ml_l[k] = ml[1];
+        }
+    }
     float M = NEG_INF;
-    for (int s = tid; s < p.splits; s += 256) M = fmaxf(M, p.ws_ml[(rec0 + (int64_t)s * p.h_pad) * 2]);
+#pragma unroll
+    for (int k = 0; k < MLK; ++k)
+        if (ml_l[k] > 0.f) M = fmaxf(M, ml_m[k]);
     M = wave_max(M);
-    if (l == 0) red_w[q] = M;
+    if (l == 0) red_w[w] = M;
     __syncthreads();
-    M = fmaxf(fmaxf(red_w[0], red_w[1]), fmaxf(red_w[2], red_w[3]));
+    M = red_w[0];
+#pragma unroll
+    for (int k = 1; k < 8; ++k) M = fmaxf(M, red_w[k]);
     const bool any = M != NEG_INF;
     const float sink2 = p.sinks ? p.sinks[h] * LOG2E : NEG_INF;
     M = fmaxf(M, sink2);
     float L = 0.f;
-    for (int s = tid; s < p.splits; s += 256) {
-        const int64_t rec = rec0 + (int64_t)s * p.h_pad;
-        const float ms = p.ws_ml[rec * 2];
-        const float wv = ms == NEG_INF ? 0.f : exp2f(ms - M);
-        wgt[s] = wv;
-        L += wv * p.ws_ml[rec * 2 + 1];
+#pragma unroll
+    for (int k = 0; k < MLK; ++k) {
+        const int s = tid + COMBINE_THREADS * k;
+        if (s < p.splits) {
+            const float wv = ml_l[k] > 0.f ? ml_l[k] * exp2f(ml_m[k] - M) : 0.f;
+            wgt[s] = wv;
+            L += wv;
+        }
     }
     L = wave_sum(L);
     __syncthreads();
-    if (l == 0) red_w[q] = L;
+    if (l == 0) red_w[w] = L;
     __syncthreads();
-    L = (red_w[0] + red_w[1]) + (red_w[2] + red_w[3]);
+    L = red_w[0];
+#pragma unroll
+    for (int k = 1; k < 8; ++k) L += red_w[k];
     if (p.sinks) L += exp2f(sink2 - M);
-    const int v = blockIdx.y * 256 + 4 * l;
-    const float* src = p.ws_o + rec0 * R + v;
-    const int64_t step = (int64_t)p.h_pad * R;
-    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-    const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
-    int s = q;
-    // a split with no valid row has weight 0 and may hold non-finite
-    // scratch: select, never multiply it in
-    for (; s + 12 < p.splits; s += 16) {
-        const f32x4 x0 = *(const f32x4*)(src + (s + 0) * step);
-        const f32x4 x1 = *(const f32x4*)(src + (s + 4) * step);
-        const f32x4 x2 = *(const f32x4*)(src + (s + 8) * step);
-        const f32x4 x3 = *(const f32x4*)(src + (s + 12) * step);
-        acc += wgt[s] != 0.f ? wgt[s] * x0 : zero;
-        acc += wgt[s + 4] != 0.f ? wgt[s + 4] * x1 : zero;
-        acc += wgt[s + 8] != 0.f ? wgt[s + 8] * x2 : zero;
-        acc += wgt[s + 12] != 0.f ? wgt[s + 12] * x3 : zero;
+
+    f32x4 a0 = {0.f, 0.f, 0.f, 0.f}, a1 = a0;
+    const f32x4 zero = a0;
+    // a split with no valid row has weight 0: select, never multiply it in
+#pragma unroll
+    for (int k = 0; k < COMBINE_PF; ++k) {
+        const int s = w + 8 * k;
+        if (s < p.splits && wgt[s] != 0.f) {
+            a0 += wgt[s] * x[k][0];
+            a1 += wgt[s] * x[k][1];
+        }
     }
-    for (; s < p.splits; s += 4) {
-        const f32x4 x = *(const f32x4*)(src + s * step);
-        acc += wgt[s] != 0.f ? wgt[s] * x : zero;
+    for (int s = w + 8 * COMBINE_PF; s < p.splits; s += 8) {
+        F8 y;
+        ld8(s, y);
+        a0 += wgt[s] != 0.f ? wgt[s] * y[0] : zero;
+        a1 += wgt[s] != 0.f ? wgt[s] * y[1] : zero;
     }
-    if (q > 0) part[q - 1][l] = acc;
+    part[w][l][0] = a0;
+    part[w][l][1] = a1;
     __syncthreads();
-    if (q != 0) return;
-    acc += part[0][l];
-    acc += part[1][l];
-    acc += part[2][l];
-    acc *= any ? 1.f / L : 0.f;
+    if (w != 0) return;
+#pragma unroll
+    for (int k = 1; k < 8; ++k) {
+        a0 += part[k][l][0];
+        a1 += part[k][l][1];
+    }
+    const float sc = any ? 1.f / L : 0.f;
+    a0 *= sc;
+    a1 *= sc;
     const int64_t o = (int64_t)b * p.out_bs + (int64_t)h * p.out_hs + v;
     if (p.out_f32) {
-        *(f32x4*)((float*)p.out + o) = acc;
+        *(f32x4*)((float*)p.out + o) = a0;
+        *(f32x4*)((float*)p.out + o + 4) = a1;
     } else {
-        *(u32x2*)((uint16_t*)p.out + o) = u32x2{pack_bf16x2(acc[0], acc[1]), pack_bf16x2(acc[2], acc[3])};
+        *(u32x4*)((uint16_t*)p.out + o) = u32x4{pack_bf16x2(a0[0], a0[1]), pack_bf16x2(a0[2], a0[3]),
+                                                pack_bf16x2(a1[0], a1[1]), pack_bf16x2(a1[2], a1[3])};
     }
+}
+
+template <int DR, bool GATHER, bool PACKED>
+hipError_t launch_ws(const DecodeParams& p, int grid, hipStream_t st) {
+    if (p.hg_size == 64)
+        hipLaunchKernelGGL((mla_decode_ws<DR, GATHER, PACKED, 64>), dim3(grid), dim3(WsShape<64>::THREADS), 0, st, p);
+    else
+        hipLaunchKernelGGL((mla_decode_ws<DR, GATHER, PACKED, 32>), dim3(grid), dim3(WsShape<32>::THREADS), 0, st, p);
+    return hipGetLastError();
 }
 
 template <int DR, bool GATHER, bool TR>
 hipError_t launch_split(const DecodeParams& p, int grid, hipStream_t st) {
     const bool packed = DR == 0 || (p.rope == p.latent + R && p.rope_rs == p.lat_rs && p.rope_bs == p.lat_bs);
+    if (TR)  // the role-split kernel (PV by transposed reads)
+        return packed ? launch_ws<DR, GATHER, true>(p, grid, st) : launch_ws<DR, GATHER, false>(p, grid, st);
+    // 4-wave kernel with scalar PV reads (debug path), head groups of 32
     if (packed)
-        hipLaunchKernelGGL((mla_decode_split<DR, GATHER, TR, true>), dim3(grid), dim3(THREADS), 0, st, p);
+        hipLaunchKernelGGL((mla_decode_split<DR, GATHER, false, true>), dim3(grid), dim3(THREADS), 0, st, p);
     else
-        hipLaunchKernelGGL((mla_decode_split<DR, GATHER, TR, false>), dim3(grid), dim3(THREADS), 0, st, p);
+        hipLaunchKernelGGL((mla_decode_split<DR, GATHER, false, false>), dim3(grid), dim3(THREADS), 0, st, p);
     return hipGetLastError();
 }
 
@@ -580,7 +1018,7 @@ hipError_t launch_validate_indices(const int32_t* indices, int32_t batch, int32_
     return hipGetLastError();
 }
 
-int decode_head_groups(int heads) { return (heads + HG - 1) / HG; }
+int decode_head_group_size(int heads, bool transpose_reads) { return transpose_reads && heads > 32 ? 64 : 32; }
 
 hipError_t launch_mla_decode(const DecodeParams& p, const CombineParams& cp, bool transpose_reads,
                              hipEvent_t const* events, hipStream_t st) {
@@ -602,7 +1040,10 @@ hipError_t launch_mla_decode(const DecodeParams& p, const CombineParams& cp, boo
     }
     if (e != hipSuccess) return e;
     if (events && (e = hipEventRecord(events[1], st)) != hipSuccess) return e;
-    hipLaunchKernelGGL(mla_combine, dim3(p.batch * p.heads, R / 256), dim3(256), 0, st, cp);
+    if (cp.ws_f32)
+        hipLaunchKernelGGL(mla_combine<true>, dim3(p.batch * p.heads), dim3(COMBINE_THREADS), 0, st, cp);
+    else
+        hipLaunchKernelGGL(mla_combine<false>, dim3(p.batch * p.heads), dim3(COMBINE_THREADS), 0, st, cp);
     if ((e = hipGetLastError()) != hipSuccess) return e;
     if (events && (e = hipEventRecord(events[2], st)) != hipSuccess) return e;
     return hipSuccess;

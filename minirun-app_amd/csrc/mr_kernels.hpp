@@ -9,7 +9,7 @@
 
 namespace mr {
 
-constexpr int MAX_GATHER_ROWS = 1024;     // index rows one decode workgroup stages in LDS
+constexpr int MAX_GATHER_ROWS = 512;      // index rows one decode workgroup stages in LDS
 constexpr int MAX_COMBINE_SPLITS = 1024;  // context splits the combine kernel merges
 
 // ---------------------------------------------------------------- decode
@@ -27,14 +27,17 @@ struct DecodeParams {
     int32_t batch, heads, n_ctx, rope_dim;
     int32_t n_rows;          // rows attended per batch element (n_ctx or n_idx)
     int32_t splits, rows_per_split, head_groups, h_pad;
+    int32_t hg_size;         // heads per workgroup: 32 or 64
     float scale_log2;        // softmax scale * log2(e)
-    float* ws_o;             // [batch*splits][h_pad][512]
-    float* ws_ml;            // [batch*splits][h_pad][2]
+    void* ws_o;              // [batch][h_pad][splits][512]: O_s / l_s, bf16 (or f32 when ws_f32)
+    int32_t ws_f32;
+    float* ws_ml;            // [batch][h_pad][splits][2]: m_s (base 2), l_s
     int32_t* err_flag;       // optional: bit 0 set on an out-of-range index
 };
 
 struct CombineParams {
-    const float* ws_o;
+    const void* ws_o;  // bf16, or f32 when ws_f32
+    int32_t ws_f32;
     const float* ws_ml;
     const float* sinks;  // [heads] or null
     void* out;
@@ -43,7 +46,9 @@ struct CombineParams {
     int32_t out_f32;
 };
 
-int decode_head_groups(int heads);
+// Heads per decode workgroup: 64 with the role-split kernel when there are
+// more than 32 heads, else 32.
+int decode_head_group_size(int heads, bool transpose_reads);
 hipError_t launch_validate_indices(const int32_t* indices, int32_t batch, int32_t n_idx, int32_t n_rows,
                                    int32_t* result, hipStream_t st);
 hipError_t launch_mla_decode(const DecodeParams& p, const CombineParams& cp, bool transpose_reads,

@@ -71,18 +71,25 @@ def test_config2_decode_128_heads_32k(M):
     check(host_f32(out32)[0], ref, "config2-f32", scale_bar=2e-3)
 
 
-def test_bf16_output_is_rne_of_f32_output(M):
-    # the split kernel is shared; only the combine's final conversion differs,
-    # so the bf16 output must be the round-to-nearest-even of the f32 output
-    print("decode bf16 == RNE(f32)", flush=True)
+def test_bf16_output_tracks_f32_output(M):
+    # bf16 output combines bf16 split partials (O_s / l_s), f32 output f32
+    # ones; the two differ by the partials' rounding (2^-9 of a partial, each
+    # a convex combination of rows) plus the final rounding (2^-9 of the
+    # output): within 2^-8 |a| + 2^-8 max|a|
+    print("decode bf16 vs f32 output", flush=True)
     import torch
 
     ql, qr, cache = MI.decode_inputs(128, 8192, tag="rne")
-    a = run_decode(M, ql, qr, cache, out_dtype=torch.float32)
-    b = run_decode(M, ql, qr, cache)
-    exp = O.f32_to_bf16(host_f32(a))
-    got = b.cpu().view(torch.int16).numpy().view(np.uint16)
-    np.testing.assert_array_equal(got, exp)
+    a = host_f32(run_decode(M, ql, qr, cache, out_dtype=torch.float32)).astype(np.float64)
+    b = host_f32(run_decode(M, ql, qr, cache)).astype(np.float64)
+    err = np.abs(b - a)
+    assert (err <= 2.0 ** -8 * (np.abs(a) + np.abs(a).max())).all(), err.max()
+    # and one split: the single partial is O / l itself, so the bf16 output
+    # is the f32 output's bf16 rounding up to one ulp
+    a1 = host_f32(run_decode(M, ql, qr, cache, num_splits=1, out_dtype=torch.float32))
+    b1 = run_decode(M, ql, qr, cache, num_splits=1).cpu().view(torch.int16).numpy().view(np.uint16)
+    d = np.abs(b1.astype(np.int32) - O.f32_to_bf16(a1).astype(np.int32))
+    assert d.max() <= 1, d.max()
 
 
 @pytest.mark.parametrize("splits", [1, 2, 7, 64])
@@ -110,14 +117,21 @@ def test_ragged_shapes(M, H, N):
                                    rtol=1e-6)
 
 
-def test_transpose_read_equals_scalar_reads(M):
-    print("decode tr16 vs scalar", flush=True)
+def test_debug_scalar_read_path_matches(M):
+    # MR_DECODE_NO_TRANSPOSE_READ runs the 4-wave kernel with scalar PV reads;
+    # the default role-split kernel scores on 32x32x16 MFMA with another
+    # summation order, so a P value may round to a neighbouring bf16: the two
+    # agree to the bf16 rounding of P (2^-8 relative), far inside the bar
+    print("decode role-split vs 4-wave scalar-read kernel", flush=True)
     import torch
 
     ql, qr, cache = MI.decode_inputs(64, 2048, tag="tr")
-    a = run_decode(M, ql, qr, cache, out_dtype=torch.float32)
-    b = run_decode(M, ql, qr, cache, out_dtype=torch.float32, flags=M.DECODE_NO_TRANSPOSE_READ)
-    np.testing.assert_array_equal(host_f32(a), host_f32(b))
+    a = host_f32(run_decode(M, ql, qr, cache, out_dtype=torch.float32)).astype(np.float64)
+    b = host_f32(run_decode(M, ql, qr, cache, out_dtype=torch.float32, flags=M.DECODE_NO_TRANSPOSE_READ))
+    err = np.abs(a - b)
+    assert err.max() <= 2.0 ** -8 * np.abs(a).max(), err.max()
+    ref = O.mla_decode(ql, qr, cache)[0]
+    check(b[0], ref, "debug-path", scale_bar=2e-3)
 
 
 def test_separate_latent_and_rope_arrays(M):
