@@ -462,6 +462,16 @@ __global__ void __launch_bounds__(THREADS, 1) mla_decode_split(DecodeParams p) {
 // buffer (j-1)&1 with the rows of j-1 and refill the buffer of j-2 with
 // j+2.  Each role runs its own loop, so neither carries the other's
 // registers.
+// Key row behind k position p of a 32-row sub-chunk in the role-split
+// kernel: within each group of eight, positions 0..3 take the even rows and
+// 4..7 the odd ones, so the four rows of a transposed read fall on distinct
+// swizzle classes (bank-conflict free) while S^T rows and P columns keep the
+// same order.
+__device__ __forceinline__ int ksig(int p) {
+    const int j = p & 7;
+    return (p & ~7) | (j < 4 ? 2 * j : 2 * (j - 4) + 1);
+}
+
 template <int HGS>
 struct WsShape {
     static constexpr int QKW = HGS / 32;           // QK waves
@@ -538,10 +548,10 @@ __global__ void __launch_bounds__(WsShape<HGS>::THREADS, 1) mla_decode_ws(Decode
                 qreg[ks] = d < R ? *(const bf16x8*)(ql + d) : *(const bf16x8*)(qr + (d - R));
             }
         }
-        // A operand: row (key) l%32 of the sub-chunk, chunk 2ks + kh; with the
-        // row swizzle, chunk 16v + u2 sits at 256v + qo[u2/2 ...]: latent
-        // k-steps ks -> qo[ks%8] + 256 (ks/8), rope k-steps -> ro[ks-32]
-        const int arow = l & 31;
+        // A operand: row (key) ksig(l%32) of the sub-chunk, chunk 2ks + kh;
+        // with the row swizzle, chunk 16v + u2 sits at 256v + qo[u2/2 ...]:
+        // latent k-steps ks -> qo[ks%8] + 256 (ks/8), rope k-steps -> ro[ks-32]
+        const int arow = ksig(l & 31);
         int qo[8], ro[4];
 #pragma unroll
         for (int u = 0; u < 8; ++u) qo[u] = arow * G::ROWB + 16 * ((2 * u + kh) ^ (arow & 15));
@@ -594,7 +604,7 @@ __global__ void __launch_bounds__(WsShape<HGS>::THREADS, 1) mla_decode_ws(Decode
                 if (__builtin_amdgcn_readfirstlane(GATHER || rbase + ROWS > row_end)) {
 #pragma unroll
                     for (int i = 0; i < 16; ++i) {
-                        const int r = rbase + 8 * (i >> 2) + 4 * kh + (i & 3);
+                        const int r = rbase + ksig(8 * (i >> 2) + 4 * kh + (i & 3));
                         bool ok = r < row_end;
                         if (GATHER) ok = ok && idx_s[r - row_begin] >= 0;
                         if (!ok) sv[i] = NEG_INF;
@@ -603,7 +613,7 @@ __global__ void __launch_bounds__(WsShape<HGS>::THREADS, 1) mla_decode_ws(Decode
                 float cm = sv[0];
 #pragma unroll
                 for (int i = 1; i < 16; ++i) cm = fmaxf(cm, sv[i]);
-                cm = fmaxf(cm, __shfl_xor(cm, 32));
+                cm = xor32_max(cm);
                 // reference max raised only when a score passes it by TAU, so
                 // O is rarely rescaled; P <= 2^TAU
                 const bool raise = cm > m_run + TAU;  // false while cm is -inf
@@ -633,7 +643,7 @@ __global__ void __launch_bounds__(WsShape<HGS>::THREADS, 1) mla_decode_ws(Decode
             }
             lds_barrier();  // end of phase s
         }
-        l_run += __shfl_xor(l_run, 32);
+        l_run = xor32_sum(l_run);
         if (kh == 0) {
             l_s[hq] = l_run;
             const int64_t r = part_rec(p, b, hg * HGS + hq, split);
@@ -682,12 +692,13 @@ __global__ void __launch_bounds__(WsShape<HGS>::THREADS, 1) mla_decode_ws(Decode
                 }
             }
         };
-        // B operand of PV (V, natural key order): lane group lg takes keys
-        // 8lg..8lg+3 (tr0) and 8lg+4..8lg+7 (tr1) of column block 16J by
-        // transposed reads; lane lc addresses key row (lc/4), columns 4(lc%4)
+        // B operand of PV: k position p holds key row ksig(p), so lane group
+        // lg takes rows 8lg + {0,2,4,6} (tr0) and 8lg + {1,3,5,7} (tr1) of
+        // column block 16J by transposed reads; lane lc addresses row
+        // 8lg + 2(lc/4) (+1), columns 4(lc%4)
         int tr0[8], tr1[8];
         {
-            const int r0 = 8 * lg + (lc >> 2), r1 = r0 + 4;
+            const int r0 = 8 * lg + 2 * (lc >> 2), r1 = r0 + 1;
 #pragma unroll
             for (int J = 0; J < 8; ++J) {
                 const int c = 16 * pw + 2 * J + ((lc & 3) >> 1);  // 16-byte chunk of the column
@@ -799,52 +810,38 @@ __global__ void __launch_bounds__(WsShape<HGS>::THREADS, 1) mla_decode_ws(Decode
 // Merge the split partials.  A partial is O_s / l_s (bf16 for bf16 output,
 // f32 for f32 output) with its running max m_s and sum l_s (fp32):
 //   out = sum_s w_s (O_s / l_s) / (sum_s w_s + sink),  w_s = l_s 2^(m_s - M).
-// One 512-thread block per (batch, head): wave w sums splits w, w+8, ... over
-// all 512 columns (eight per lane), so every load takes a whole 1 KB (bf16)
-// record and a block streams its head's contiguous records.  The first
-// COMBINE_PF loads of each wave go out before the weights are known, so the
-// block waits on memory about once.  The eight waves' sums meet in LDS.
-constexpr int COMBINE_THREADS = 512;
-constexpr int COMBINE_PF = 16;  // prefetched splits per wave (128 splits)
+// One 256-thread block per (batch, head, 256-byte column block of the
+// record): 128 columns of bf16 partials or 64 of f32, so a (batch, head)
+// spreads over 4 or 8 blocks and the grid covers every CU.  Lane l of wave w
+// takes the 16 bytes l%16 of splits 16k + 4w + l/16: one load instruction of
+// a wave reads four whole 256-byte pieces, and the first COMBINE_PF loads of
+// every lane are in flight before the weights are computed.
+constexpr int COMBINE_THREADS = 256;
+constexpr int COMBINE_PF = 8;  // 128 splits in flight per block
 
 template <bool F32>
 __global__ void __launch_bounds__(COMBINE_THREADS) mla_combine(CombineParams p) {
+    constexpr int VPL = F32 ? 4 : 8;  // values per lane (16 bytes)
+    constexpr int CB = 16 * VPL;      // columns per block
+    constexpr int NCB = R / CB;
+    constexpr int MLK = MAX_COMBINE_SPLITS / COMBINE_THREADS;
     __shared__ float wgt[MAX_COMBINE_SPLITS];
-    __shared__ float red_w[8];
-    __shared__ f32x4 part[8][64][2];
-    const int bh = blockIdx.x;
+    __shared__ float red_m[4], red_l[4];
+    __shared__ __attribute__((aligned(16))) float part[4][16][VPL];
+    const int bh = blockIdx.x / NCB;
+    const int cb = blockIdx.x - bh * NCB;
     const int b = bh / p.heads;
-    const int h = bh % p.heads;
+    const int h = bh - b * p.heads;
     const int tid = threadIdx.x;
     const int w = tid >> 6;
     const int l = tid & 63;
+    const int sg = l >> 4;  // split within the wave's four
+    const int ch = l & 15;  // 16-byte chunk of the column block
     const int64_t rec0 = ((int64_t)b * p.h_pad + h) * p.splits;  // the splits of (b, h) are contiguous
-    const int v = 8 * l;                                         // this lane's eight columns
-    typedef f32x4 F8[2];
-    auto ld8 = [&](int s, F8& o) {
-        const int64_t e = (rec0 + s) * R + v;
-        if (F32) {
-            o[0] = *(const f32x4*)((const float*)p.ws_o + e);
-            o[1] = *(const f32x4*)((const float*)p.ws_o + e + 4);
-        } else {
-            const u32x4 u = *(const u32x4*)((const uint16_t*)p.ws_o + e);
-            o[0] = f32x4{__uint_as_float(u[0] << 16), __uint_as_float(u[0] & 0xffff0000u), __uint_as_float(u[1] << 16),
-                         __uint_as_float(u[1] & 0xffff0000u)};
-            o[1] = f32x4{__uint_as_float(u[2] << 16), __uint_as_float(u[2] & 0xffff0000u), __uint_as_float(u[3] << 16),
-                         __uint_as_float(u[3] & 0xffff0000u)};
-        }
-    };
-    // partials first (independent of the weights), then (m, l) of every split
-    F8 x[COMBINE_PF];
-#pragma unroll
-    for (int k = 0; k < COMBINE_PF; ++k) {
-        const int s = w + 8 * k;
-        if (s < p.splits)
-            ld8(s, x[k]);
-        else
-            x[k][0] = x[k][1] = f32x4{0.f, 0.f, 0.f, 0.f};
-    }
-    constexpr int MLK = MAX_COMBINE_SPLITS / COMBINE_THREADS;
+    constexpr int RB = R * (F32 ? 4 : 2);  // bytes per record
+    const char* base = (const char*)p.ws_o + rec0 * RB + 256 * cb + 16 * ch;
+
+    // (m, l) of every split first: the weights wait only on these
     float ml_m[MLK], ml_l[MLK];
 #pragma unroll
     for (int k = 0; k < MLK; ++k) {
@@ -857,16 +854,20 @@ __global__ void __launch_bounds__(COMBINE_THREADS) mla_combine(CombineParams p) 
             ml_l[k] = ml[1];
         }
     }
+    u32x4 x[COMBINE_PF];
+#pragma unroll
+    for (int k = 0; k < COMBINE_PF; ++k) {
+        const int s = 16 * k + 4 * w + sg;
+        x[k] = s < p.splits ? *(const u32x4*)(base + (int64_t)s * RB) : u32x4{0u, 0u, 0u, 0u};
+    }
     float M = NEG_INF;
 #pragma unroll
     for (int k = 0; k < MLK; ++k)
         if (ml_l[k] > 0.f) M = fmaxf(M, ml_m[k]);
     M = wave_max(M);
-    if (l == 0) red_w[w] = M;
+    if (l == 0) red_m[w] = M;
     __syncthreads();
-    M = red_w[0];
-#pragma unroll
-    for (int k = 1; k < 8; ++k) M = fmaxf(M, red_w[k]);
+    M = fmaxf(fmaxf(red_m[0], red_m[1]), fmaxf(red_m[2], red_m[3]));
     const bool any = M != NEG_INF;
     const float sink2 = p.sinks ? p.sinks[h] * LOG2E : NEG_INF;
     M = fmaxf(M, sink2);
@@ -881,50 +882,51 @@ __global__ void __launch_bounds__(COMBINE_THREADS) mla_combine(CombineParams p) 
         }
     }
     L = wave_sum(L);
+    if (l == 0) red_l[w] = L;
     __syncthreads();
-    if (l == 0) red_w[w] = L;
-    __syncthreads();
-    L = red_w[0];
-#pragma unroll
-    for (int k = 1; k < 8; ++k) L += red_w[k];
+    L = (red_l[0] + red_l[1]) + (red_l[2] + red_l[3]);
     if (p.sinks) L += exp2f(sink2 - M);
 
-    f32x4 a0 = {0.f, 0.f, 0.f, 0.f}, a1 = a0;
-    const f32x4 zero = a0;
+    float acc[VPL];
+#pragma unroll
+    for (int v = 0; v < VPL; ++v) acc[v] = 0.f;
     // a split with no valid row has weight 0: select, never multiply it in
+    auto add = [&](const u32x4& u, float wv) {
+        if (wv == 0.f) return;
+#pragma unroll
+        for (int v = 0; v < VPL; ++v) {
+            const float xv = F32 ? __uint_as_float(u[v]) : __uint_as_float(v & 1 ? u[v >> 1] & 0xffff0000u : u[v >> 1] << 16);
+            acc[v] += wv * xv;
+        }
+    };
 #pragma unroll
     for (int k = 0; k < COMBINE_PF; ++k) {
-        const int s = w + 8 * k;
-        if (s < p.splits && wgt[s] != 0.f) {
-            a0 += wgt[s] * x[k][0];
-            a1 += wgt[s] * x[k][1];
-        }
+        const int s = 16 * k + 4 * w + sg;
+        if (s < p.splits) add(x[k], wgt[s]);
     }
-    for (int s = w + 8 * COMBINE_PF; s < p.splits; s += 8) {
-        F8 y;
-        ld8(s, y);
-        a0 += wgt[s] != 0.f ? wgt[s] * y[0] : zero;
-        a1 += wgt[s] != 0.f ? wgt[s] * y[1] : zero;
-    }
-    part[w][l][0] = a0;
-    part[w][l][1] = a1;
-    __syncthreads();
-    if (w != 0) return;
+    for (int s = 16 * COMBINE_PF + 4 * w + sg; s < p.splits; s += 16) add(*(const u32x4*)(base + (int64_t)s * RB), wgt[s]);
+    // the four splits of a wave, then the four waves
 #pragma unroll
-    for (int k = 1; k < 8; ++k) {
-        a0 += part[k][l][0];
-        a1 += part[k][l][1];
+    for (int v = 0; v < VPL; ++v) {
+        acc[v] += __shfl_xor(acc[v], 16);
+        acc[v] += __shfl_xor(acc[v], 32);
     }
+    if (sg == 0) {
+#pragma unroll
+        for (int v = 0; v < VPL; ++v) part[w][ch][v] = acc[v];
+    }
+    __syncthreads();
+    if (tid >= 16) return;
     const float sc = any ? 1.f / L : 0.f;
-    a0 *= sc;
-    a1 *= sc;
-    const int64_t o = (int64_t)b * p.out_bs + (int64_t)h * p.out_hs + v;
-    if (p.out_f32) {
-        *(f32x4*)((float*)p.out + o) = a0;
-        *(f32x4*)((float*)p.out + o + 4) = a1;
+    float o[VPL];
+#pragma unroll
+    for (int v = 0; v < VPL; ++v) o[v] = ((part[0][ch][v] + part[1][ch][v]) + (part[2][ch][v] + part[3][ch][v])) * sc;
+    const int64_t oo = (int64_t)b * p.out_bs + (int64_t)h * p.out_hs + CB * cb + VPL * ch;
+    if (F32) {
+        *(f32x4*)((float*)p.out + oo) = f32x4{o[0], o[1], o[2], o[3]};
     } else {
-        *(u32x4*)((uint16_t*)p.out + o) = u32x4{pack_bf16x2(a0[0], a0[1]), pack_bf16x2(a0[2], a0[3]),
-                                                pack_bf16x2(a1[0], a1[1]), pack_bf16x2(a1[2], a1[3])};
+        *(u32x4*)((uint16_t*)p.out + oo) = u32x4{pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3]),
+                                                 pack_bf16x2(o[4], o[5]), pack_bf16x2(o[6], o[7])};
     }
 }
 
@@ -1041,9 +1043,9 @@ hipError_t launch_mla_decode(const DecodeParams& p, const CombineParams& cp, boo
     if (e != hipSuccess) return e;
     if (events && (e = hipEventRecord(events[1], st)) != hipSuccess) return e;
     if (cp.ws_f32)
-        hipLaunchKernelGGL(mla_combine<true>, dim3(p.batch * p.heads), dim3(COMBINE_THREADS), 0, st, cp);
+        hipLaunchKernelGGL(mla_combine<true>, dim3(p.batch * p.heads * (R / 64)), dim3(COMBINE_THREADS), 0, st, cp);
     else
-        hipLaunchKernelGGL(mla_combine<false>, dim3(p.batch * p.heads), dim3(COMBINE_THREADS), 0, st, cp);
+        hipLaunchKernelGGL(mla_combine<false>, dim3(p.batch * p.heads * (R / 128)), dim3(COMBINE_THREADS), 0, st, cp);
     if ((e = hipGetLastError()) != hipSuccess) return e;
     if (events && (e = hipEventRecord(events[2], st)) != hipSuccess) return e;
     return hipSuccess;

@@ -86,6 +86,19 @@ __device__ __forceinline__ bf16x8 as_bf16x8(const u32x4& v) {
     return __builtin_bit_cast(bf16x8, v);
 }
 
+// v combined with the value of lane l ^ 32 by one VALU op: after
+// v_permlane32_swap of two copies of v, the pair (r[0], r[1]) of lane l holds
+// {v[l], v[l ^ 32]} (lower-half lane first in both halves), so max and sum
+// are the same bits in lanes l and l ^ 32.
+__device__ __forceinline__ float xor32_max(float v) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float xor32_sum(float v) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
 __device__ __forceinline__ float wave_max(float v) {
     for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
     return v;

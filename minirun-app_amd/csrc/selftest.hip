@@ -57,6 +57,15 @@ __global__ void __launch_bounds__(64) k_tr16(const int32_t* offsets, uint16_t* o
     out[4 * l + 3] = (uint16_t)(u[1] >> 16);
 }
 
+// v_permlane32_swap of two copies of in[l]: out[2l] = r[0], out[2l+1] = r[1].
+__global__ void __launch_bounds__(64) k_permlane32(const uint32_t* in, uint32_t* out) {
+    const int l = threadIdx.x;
+    const uint32_t v = in[l];
+    const auto r = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+    out[2 * l] = r[0];
+    out[2 * l + 1] = r[1];
+}
+
 extern "C" {
 int mr_selftest_mfma16(const void* A, const void* B, void* D, void* stream) {
     hipLaunchKernelGGL(k_mfma16, dim3(1), dim3(64), 0, (hipStream_t)stream, (const uint16_t*)A,
@@ -66,6 +75,11 @@ int mr_selftest_mfma16(const void* A, const void* B, void* D, void* stream) {
 int mr_selftest_mfma32(const void* A, const void* B, void* D, void* stream) {
     hipLaunchKernelGGL(k_mfma32, dim3(1), dim3(64), 0, (hipStream_t)stream, (const uint16_t*)A,
                        (const uint16_t*)B, (float*)D);
+    return hipGetLastError() == hipSuccess ? 0 : 6;
+}
+int mr_selftest_permlane32(const void* d_in, void* d_out, void* stream) {
+    hipLaunchKernelGGL(k_permlane32, dim3(1), dim3(64), 0, (hipStream_t)stream, (const uint32_t*)d_in,
+                       (uint32_t*)d_out);
     return hipGetLastError() == hipSuccess ? 0 : 6;
 }
 int mr_selftest_tr16(const int32_t* host_offsets, const void* d_offsets, void* d_out, void* stream) {

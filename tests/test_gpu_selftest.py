@@ -79,3 +79,23 @@ def test_ds_read_tr16_mapping(st):
         for lane in range(64):
             print(lane, got[lane].tolist(), file=sys.stderr)
     np.testing.assert_array_equal(got, exp)
+
+
+def test_permlane32_swap_pairs(st):
+    """v_permlane32_swap of two copies of v: lane l gets (v[l], v[l+32]) for
+    l < 32 and (v[l-32], v[l]) for l >= 32, the lane-pair exchange the
+    decode softmax uses for its max and sum over the two wave halves."""
+    import torch
+
+    print("selftest permlane32", flush=True)
+    st.mr_selftest_permlane32.argtypes = [C.c_void_p] * 3
+    v = np.arange(64, dtype=np.int32) * 7 + 3
+    d_in = torch.tensor(v, device="cuda")
+    out = torch.zeros(128, dtype=torch.int32, device="cuda")
+    assert st.mr_selftest_permlane32(d_in.data_ptr(), out.data_ptr(), None) == 0
+    torch.cuda.synchronize()
+    r = out.cpu().numpy().reshape(64, 2)
+    lanes = np.arange(64)
+    lo = np.where(lanes < 32, lanes, lanes - 32)
+    np.testing.assert_array_equal(r[:, 0], v[lo])
+    np.testing.assert_array_equal(r[:, 1], v[lo + 32])
