@@ -536,18 +536,16 @@ __global__ void __launch_bounds__(WsShape<HGS>::THREADS, 1) mla_decode_ws(Decode
         // B operand of 32x32x16: head 32qw + l%32, k = 16ks + 8(l/32)..+7
         const int hq = 32 * qw + (l & 31);  // this lane's head within the group
         const int kh = l >> 5;              // k half / key half
+        // Q arrives in LDS (buffers 2-3, staged by the PV waves' DMA, chunk c
+        // of head h at slot c ^ (h & 7) of its row)
         bf16x8 qreg[2 * G::KS];
+        lds_barrier();  // Q staged
         {
-            const int h0 = hg * HGS + hq;
-            const int h = h0 < p.heads ? h0 : 0;
-            const uint16_t* ql = p.q_lat + (int64_t)b * p.q_lat_bs + (int64_t)h * p.q_lat_hs;
-            const uint16_t* qr = DR ? p.q_rope + (int64_t)b * p.q_rope_bs + (int64_t)h * p.q_rope_hs : nullptr;
+            const char* qrow = cbuf + 2 * G::BUF + hq * G::ROWB;
 #pragma unroll
-            for (int ks = 0; ks < 2 * G::KS; ++ks) {
-                const int d = 16 * ks + 8 * kh;
-                qreg[ks] = d < R ? *(const bf16x8*)(ql + d) : *(const bf16x8*)(qr + (d - R));
-            }
+            for (int ks = 0; ks < 2 * G::KS; ++ks) qreg[ks] = *(const bf16x8*)(qrow + 16 * ((2 * ks + kh) ^ (hq & 7)));
         }
+        lds_barrier();  // Q in registers: buffers 2-3 free again
         // A operand: row (key) ksig(l%32) of the sub-chunk, chunk 2ks + kh;
         // with the row swizzle, chunk 16v + u2 sits at 256v + qo[u2/2 ...]:
         // latent k-steps ks -> qo[ks%8] + 256 (ks/8), rope k-steps -> ro[ks-32]
@@ -706,14 +704,48 @@ __global__ void __launch_bounds__(WsShape<HGS>::THREADS, 1) mla_decode_ws(Decode
                 tr1[J] = r1 * G::ROWB + 16 * swz(c, r1) + 8 * (lc & 1);
             }
         }
-        f32x4 oacc[HT][8];  // O[HGS heads][128pw .. +127]
+        // O^T tiles (A = V^T from the transposed reads, B = P^T): lane holds
+        // head 16T + lc, columns 128pw + 16J + 4lg + 0..3
+        f32x4 oacc[HT][8];
 #pragma unroll
         for (int T = 0; T < HT; ++T)
 #pragma unroll
             for (int J = 0; J < 8; ++J) oacc[T][J] = f32x4{0.f, 0.f, 0.f, 0.f};
-        // prologue: sub-chunks 0 .. NBUF-2 in flight, wait for 0
+        // prologue: Q of the head group into buffers 2-3 (one 1 KB load per
+        // wave instruction instead of 32-byte pieces of 32 heads per QK
+        // load), sub-chunks 0 and 1 behind it; sub-chunk 2 goes out once the
+        // QK waves hold Q in registers
+        {
+            constexpr int QPW = HGS * G::CPR / 256;  // Q loads per PV wave
+            static_assert(QPW * 256 == HGS * G::CPR, "Q staging loads");
+            static_assert(HGS * G::ROWB <= 2 * G::BUF, "Q fits buffers 2-3");
+            char* qdst = cbuf + 2 * G::BUF;
+#pragma unroll
+            for (int k = 0; k < QPW; ++k) {
+                const int slot = 64 * (pw + 4 * k) + l;
+                const int h = slot / G::CPR;
+                const int c = (slot - h * G::CPR) ^ (h & 7);
+                const int h0 = hg * HGS + h;
+                const int hh = h0 < p.heads ? h0 : 0;
+                const uint16_t* src = c < R / 8 ? p.q_lat + (int64_t)b * p.q_lat_bs + (int64_t)hh * p.q_lat_hs + 8 * c
+                                                : p.q_rope + (int64_t)b * p.q_rope_bs + (int64_t)hh * p.q_rope_hs +
+                                                      8 * (c - R / 8);
+                dma16(src, qdst + 1024 * (pw + 4 * k));
+            }
+        }
+        const int pro2 = min(nsub, 2);
+        for (int s = 0; s < pro2; ++s) issue(s, cbuf + s * G::BUF);
+        if (pro2 == 2)
+            wait_vmcnt<2 * G::NLD>();
+        else if (pro2 == 1)
+            wait_vmcnt<G::NLD>();
+        else
+            wait_vmcnt<0>();
+        lds_barrier();  // Q staged
+        lds_barrier();  // Q in registers: buffers 2-3 free again
+        if (nsub > 2) issue(2, cbuf + 2 * G::BUF);
+        // sub-chunks 0 .. NBUF-2 in flight, wait for 0
         const int pro = min(nsub, NBUF - 1);
-        for (int s = 0; s < pro; ++s) issue(s, cbuf + s * G::BUF);
         if (pro >= 3)
             wait_vmcnt<2 * G::NLD>();
         else if (pro == 2)
@@ -735,9 +767,9 @@ __global__ void __launch_bounds__(WsShape<HGS>::THREADS, 1) mla_decode_ws(Decode
                 if (rescale) {
 #pragma unroll
                     for (int T = 0; T < HT; ++T) {
-                        const f32x4 a4 = *(const f32x4*)(alpha_s[par] + 16 * T + 4 * lg);
+                        const float a = alpha_s[par][16 * T + lc];
 #pragma unroll
-                        for (int J = 0; J < 8; ++J) oacc[T][J] *= a4;
+                        for (int J = 0; J < 8; ++J) oacc[T][J] *= a;
                     }
                 }
                 bf16x8 pa[HT];
@@ -754,7 +786,7 @@ __global__ void __launch_bounds__(WsShape<HGS>::THREADS, 1) mla_decode_ws(Decode
                 for (int J = 0; J < 8; ++J) {
                     const bf16x8 bb = __builtin_shufflevector(b0[J], b1[J], 0, 1, 2, 3, 4, 5, 6, 7);
 #pragma unroll
-                    for (int T = 0; T < HT; ++T) oacc[T][J] = mfma16(pa[T], bb, oacc[T][J]);
+                    for (int T = 0; T < HT; ++T) oacc[T][J] = mfma16(bb, pa[T], oacc[T][J]);
                 }
             }
             // sub-chunk s+1 must have landed before the barrier; only s+2 may
@@ -768,32 +800,35 @@ __global__ void __launch_bounds__(WsShape<HGS>::THREADS, 1) mla_decode_ws(Decode
             lds_barrier();  // end of phase s
         }
         lds_barrier();  // l_s ready
-        // O / l into the staging area [HGS heads][srow bytes], partial precision
-        float inv[HT][4];
+        // O / l into the staging area [HGS heads][srow bytes], partial
+        // precision: per (T, J) a lane writes its head's four consecutive
+        // columns (8 bytes bf16, 16 bytes f32)
+        float inv[HT];
 #pragma unroll
         for (int T = 0; T < HT; ++T) {
-            const f32x4 l4 = *(const f32x4*)(l_s + 16 * T + 4 * lg);
-#pragma unroll
-            for (int i = 0; i < 4; ++i) inv[T][i] = l4[i] > 0.f ? 1.f / l4[i] : 0.f;
+            const float lv = l_s[16 * T + lc];
+            inv[T] = lv > 0.f ? 1.f / lv : 0.f;
         }
         if (p.ws_f32) {
 #pragma unroll
-            for (int T = 0; T < HT; ++T)
+            for (int T = 0; T < HT; ++T) {
+                float* row = (float*)(cbuf + (16 * T + lc) * srow) + 128 * pw + 4 * lg;
 #pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    float* row = (float*)(cbuf + (16 * T + 4 * lg + i) * srow) + 128 * pw + lc;
-#pragma unroll
-                    for (int J = 0; J < 8; ++J) row[16 * J] = oacc[T][J][i] * inv[T][i];
-                }
+                for (int J = 0; J < 8; ++J) *(f32x4*)(row + 16 * J) = oacc[T][J] * inv[T];
+            }
         } else {
+            typedef __bf16 bf16x2v __attribute__((ext_vector_type(2)));
 #pragma unroll
-            for (int T = 0; T < HT; ++T)
+            for (int T = 0; T < HT; ++T) {
+                __bf16* row = (__bf16*)(cbuf + (16 * T + lc) * srow) + 128 * pw + 4 * lg;
 #pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    __bf16* row = (__bf16*)(cbuf + (16 * T + 4 * lg + i) * srow) + 128 * pw + lc;
-#pragma unroll
-                    for (int J = 0; J < 8; ++J) row[16 * J] = (__bf16)(oacc[T][J][i] * inv[T][i]);
+                for (int J = 0; J < 8; ++J) {
+                    const f32x4 o = oacc[T][J] * inv[T];
+                    const bf16x2v lo = {(__bf16)o[0], (__bf16)o[1]};
+                    const bf16x2v hi = {(__bf16)o[2], (__bf16)o[3]};
+                    *(u32x2*)(row + 16 * J) = u32x2{__builtin_bit_cast(uint32_t, lo), __builtin_bit_cast(uint32_t, hi)};
                 }
+            }
         }
         lds_barrier();  // staging written
     }

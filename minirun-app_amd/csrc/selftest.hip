@@ -66,6 +66,15 @@ __global__ void __launch_bounds__(64) k_permlane32(const uint32_t* in, uint32_t*
     out[2 * l + 1] = r[1];
 }
 
+// v_permlane16_swap of two copies of in[l]: out[2l] = r[0], out[2l+1] = r[1].
+__global__ void __launch_bounds__(64) k_permlane16(const uint32_t* in, uint32_t* out) {
+    const int l = threadIdx.x;
+    const uint32_t v = in[l];
+    const auto r = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+    out[2 * l] = r[0];
+    out[2 * l + 1] = r[1];
+}
+
 extern "C" {
 int mr_selftest_mfma16(const void* A, const void* B, void* D, void* stream) {
     hipLaunchKernelGGL(k_mfma16, dim3(1), dim3(64), 0, (hipStream_t)stream, (const uint16_t*)A,
@@ -79,6 +88,11 @@ int mr_selftest_mfma32(const void* A, const void* B, void* D, void* stream) {
 }
 int mr_selftest_permlane32(const void* d_in, void* d_out, void* stream) {
     hipLaunchKernelGGL(k_permlane32, dim3(1), dim3(64), 0, (hipStream_t)stream, (const uint32_t*)d_in,
+                       (uint32_t*)d_out);
+    return hipGetLastError() == hipSuccess ? 0 : 6;
+}
+int mr_selftest_permlane16(const void* d_in, void* d_out, void* stream) {
+    hipLaunchKernelGGL(k_permlane16, dim3(1), dim3(64), 0, (hipStream_t)stream, (const uint32_t*)d_in,
                        (uint32_t*)d_out);
     return hipGetLastError() == hipSuccess ? 0 : 6;
 }

@@ -99,3 +99,23 @@ def test_permlane32_swap_pairs(st):
     lo = np.where(lanes < 32, lanes, lanes - 32)
     np.testing.assert_array_equal(r[:, 0], v[lo])
     np.testing.assert_array_equal(r[:, 1], v[lo + 32])
+
+
+def test_permlane16_swap_pairs(st):
+    """v_permlane16_swap of two copies of v: a lane of row r (16 lanes a row)
+    gets (v[l], v[l+16]) for even r and (v[l-16], v[l]) for odd r, the
+    exchange the decode softmax uses between lanes l and l ^ 16."""
+    import torch
+
+    print("selftest permlane16", flush=True)
+    st.mr_selftest_permlane16.argtypes = [C.c_void_p] * 3
+    v = np.arange(64, dtype=np.int32) * 5 + 11
+    d_in = torch.tensor(v, device="cuda")
+    out = torch.zeros(128, dtype=torch.int32, device="cuda")
+    assert st.mr_selftest_permlane16(d_in.data_ptr(), out.data_ptr(), None) == 0
+    torch.cuda.synchronize()
+    r = out.cpu().numpy().reshape(64, 2)
+    lanes = np.arange(64)
+    lo = np.where((lanes // 16) % 2 == 0, lanes, lanes - 16)
+    np.testing.assert_array_equal(r[:, 0], v[lo])
+    np.testing.assert_array_equal(r[:, 1], v[lo + 16])
