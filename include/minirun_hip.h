@@ -108,6 +108,10 @@ typedef struct mr_mla_decode_args {
 
 #define MR_DECODE_VALIDATE_INDICES 1u  /* run mr_validate_indices first (synchronises) */
 #define MR_DECODE_NO_TRANSPOSE_READ 2u /* debug: PV operand by scalar LDS reads */
+/* Profiling aid, no reference counterpart: launch only the split kernel
+ * (the split partials land in the workspace; `out` is not written), so a
+ * caller can time that kernel over many launches between two events. */
+#define MR_DECODE_SPLIT_ONLY 4u
 
 size_t mr_mla_decode_workspace_size(const mr_mla_decode_args *args);
 mr_status mr_mla_decode(const mr_mla_decode_args *args, void *stream);

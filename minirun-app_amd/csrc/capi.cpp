@@ -270,7 +270,8 @@ mr_status mr_mla_decode(const mr_mla_decode_args* a, void* stream) {
 
     const hipError_t e =
         mr::launch_mla_decode(p, cp, (a->flags & MR_DECODE_NO_TRANSPOSE_READ) == 0,
-                              (hipEvent_t const*)a->phase_events, (hipStream_t)stream);
+                              (a->flags & MR_DECODE_SPLIT_ONLY) != 0, (hipEvent_t const*)a->phase_events,
+                              (hipStream_t)stream);
     if (e != hipSuccess) return hip_fail(e, "mla decode launch");
     return MR_OK;
 }

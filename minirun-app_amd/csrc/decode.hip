@@ -1058,7 +1058,7 @@ hipError_t launch_validate_indices(const int32_t* indices, int32_t batch, int32_
 int decode_head_group_size(int heads, bool transpose_reads) { return transpose_reads && heads > 32 ? 64 : 32; }
 
 hipError_t launch_mla_decode(const DecodeParams& p, const CombineParams& cp, bool transpose_reads,
-                             hipEvent_t const* events, hipStream_t st) {
+                             bool split_only, hipEvent_t const* events, hipStream_t st) {
     const int units = p.batch * p.splits;
     const int grid = 8 * p.head_groups * ((units + 7) / 8);
     hipError_t e;
@@ -1077,6 +1077,7 @@ hipError_t launch_mla_decode(const DecodeParams& p, const CombineParams& cp, boo
     }
     if (e != hipSuccess) return e;
     if (events && (e = hipEventRecord(events[1], st)) != hipSuccess) return e;
+    if (split_only) return events ? hipEventRecord(events[2], st) : hipSuccess;
     if (cp.ws_f32)
         hipLaunchKernelGGL(mla_combine<true>, dim3(p.batch * p.heads * (R / 64)), dim3(COMBINE_THREADS), 0, st, cp);
     else

@@ -52,7 +52,7 @@ int decode_head_group_size(int heads, bool transpose_reads);
 hipError_t launch_validate_indices(const int32_t* indices, int32_t batch, int32_t n_idx, int32_t n_rows,
                                    int32_t* result, hipStream_t st);
 hipError_t launch_mla_decode(const DecodeParams& p, const CombineParams& cp, bool transpose_reads,
-                             hipEvent_t const* events, hipStream_t st);
+                             bool split_only, hipEvent_t const* events, hipStream_t st);
 
 // ---------------------------------------------------------------- prefill
 // Up-projection (NT GEMM): kv[p][n] = sum_r latent[p][r] * kv_b[n][r], bf16

@@ -25,6 +25,7 @@ BF16, F16, F32, U32, I32 = range(5)
 
 DECODE_VALIDATE_INDICES = 1
 DECODE_NO_TRANSPOSE_READ = 2
+DECODE_SPLIT_ONLY = 4
 
 
 class MRError(RuntimeError):
