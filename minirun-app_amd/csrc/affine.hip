@@ -66,96 +66,207 @@ __global__ void __launch_bounds__(256) affine_dequant_kernel(AffineDequantParams
 }
 
 // ---------------------------------------------------------------- GEMV, 4-bit fast path
-// Rows are processed in blocks of RB by one wave; lane l owns groups
-// l, l+64, ... of those rows and reuses its staged x pairs for all RB rows.
-// Output row j reads weight row (j / A) * B + C + (j % A) and activation
-// vector (j / A) (a plain GEMV is A = O, B = 0, C = 0; the per-head W_UV
-// product is A = 128, B = 256, C = 128).  One workgroup covers rows of a
-// single activation vector, which it stages in LDS as pair words.
+// A workgroup owns a tile of tile_rows output rows of one activation vector
+// (a tile never crosses a map_a boundary; output row j reads weight row
+// (j / A) * B + C + (j % A) and activation vector j / A: a plain GEMV is
+// A = O, B = 0, C = 0, the per-head W_UV product A = 128, B = 256, C = 128).
+// It stages that vector once in LDS, one 16-byte chunk per thread and
+// pass: the pair words (x_j | x_j+4 << 16) of every packed word and the
+// per-group sums (eight chunk sums per group, combined by lane exchange).
+// With norm_w set, the staged vector is bf16(w * (x * rsqrt(mean(x^2) +
+// eps))), the RMSNorm stage's output.  tpr threads (a power of two <= 64)
+// share an output row, each dotting groups lane, lane + tpr, ...; a step of
+// the 256-thread workgroup covers 256 / tpr rows and two steps are in flight.
 constexpr int GEMV_THREADS = 256;
-constexpr int GEMV_MAX_IN = 16384;  // activation length staged per token
+constexpr int GEMV_MAX_IN = 16384;  // activation length staged per vector
+constexpr int GEMV_MAX_CH = GEMV_MAX_IN / 8 / GEMV_THREADS;
+constexpr int GEMV_NPT_MAX = 4;  // groups per thread and row: tpr * GEMV_NPT >= G
 
-template <int SDT, int RB>
+template <int SDT, int GEMV_NPT>
 __global__ void __launch_bounds__(GEMV_THREADS) affine_gemv4_kernel(AffineGemvParams p) {
     __shared__ __attribute__((aligned(16))) uint32_t xp[GEMV_MAX_IN / 2];  // (x_j, x_j+4) pairs
-    __shared__ float xs[GEMV_MAX_IN / 32];                              // per-group sums of x (group >= 32)
-    const int rows_per_wg = (GEMV_THREADS / 64) * RB;
-    const int j0 = blockIdx.x * rows_per_wg;
-    if (j0 >= p.out_rows) return;
-    const int xg = j0 / p.map_a;  // activation vector of this workgroup
+    __shared__ float xs[GEMV_MAX_IN / 64];                              // per-group sums of the staged x
+    __shared__ float red[GEMV_THREADS / 64];
+    const int tile = blockIdx.x;
+    const int xg = tile / p.tiles_per_vec;  // activation vector of this tile
+    const int r0 = xg * p.map_a + (tile - xg * p.tiles_per_vec) * p.tile_rows;
+    const int r_end = min(r0 + p.tile_rows, min((xg + 1) * p.map_a, p.out_rows));
     const int in = p.in_features;
-    const int words = in / 8;
-    const int groups = in / 64;
+    const int nch = in / 8;  // 16-byte chunks of x
+    const int G = in / 64;
+    const int t = threadIdx.x;
     const uint16_t* x = (const uint16_t*)p.x + (int64_t)xg * p.x_stride;
 
-    // stage x as pair words: word k, pair j = (x[8k+j] | x[8k+j+4] << 16)
-    for (int t = threadIdx.x; t < words * 4; t += GEMV_THREADS) {
-        const int k = t >> 2, j = t & 3;
-        xp[t] = (uint32_t)x[8 * k + j] | ((uint32_t)x[8 * k + j + 4] << 16);
+    // rows: tpr threads per row, two steps of 256 / tpr rows per iteration; a
+    // thread dots at most GEMV_NPT groups of a row (tpr * GEMV_NPT >= G)
+    const int tpr = p.tpr;
+    const int rps = GEMV_THREADS / tpr;
+    const int tr = t / tpr, tl = t - tr * tpr;
+    typedef __bf16 bf16x2v __attribute__((ext_vector_type(2)));
+    struct RowLoads {
+        u32x4 w[GEMV_NPT][2];
+        float s[GEMV_NPT], b[GEMV_NPT];
+        uint32_t ok;  // bit q: group q of this thread is a real (row, group)
+    };
+    // loads without branches (clamped to a real row and group, masked at
+    // use), so none of them waits before the dot products
+    auto load_row = [&](int j, RowLoads& L) {
+        const bool rok = j < r_end;
+        const int jj = rok ? j : r0;
+        const int64_t wr = (int64_t)(jj / p.map_a) * p.map_b + p.map_c + (jj % p.map_a);
+        const uint32_t* wrow = p.packed + wr * (int64_t)(in / 8);
+        L.ok = 0;
+#pragma unroll
+        for (int q = 0; q < GEMV_NPT; ++q) {
+            const int g = tl + tpr * q;
+            const int gg = min(g, G - 1);
+            L.ok |= (rok && g < G) ? (1u << q) : 0u;
+            L.w[q][0] = *((const u32x4*)(wrow + 8 * gg));
+            L.w[q][1] = *((const u32x4*)(wrow + 8 * gg) + 1);
+            L.s[q] = load_scale<SDT>(p.scales, wr * G + gg);
+            L.b[q] = load_scale<SDT>(p.biases, wr * G + gg);
+        }
+    };
+    // the first iteration's weights go out before x is staged: they do not
+    // depend on it
+    RowLoads la, lb;
+    load_row(r0 + tr, la);
+    load_row(r0 + rps + tr, lb);
+
+    // ---- stage the activation vector (and the norm weights beside it)
+    // every thread loads GEMV_MAX_CH chunks, clamped to the last real one
+    // (no branch, so the loads overlap); chunks k >= nch are zeroed at use
+    u32x4 xc[GEMV_MAX_CH];
+#pragma unroll
+    for (int c = 0; c < GEMV_MAX_CH; ++c) xc[c] = *(const u32x4*)(x + 8 * min(t + GEMV_THREADS * c, nch - 1));
+#pragma unroll
+    for (int c = 0; c < GEMV_MAX_CH; ++c)
+        if (t + GEMV_THREADS * c >= nch) xc[c] = u32x4{0u, 0u, 0u, 0u};
+    // norm weights of the same chunks (bf16: one 16-byte load, f32: two)
+    u32x4 wn[GEMV_MAX_CH][2];
+    if (p.norm_w) {
+#pragma unroll
+        for (int c = 0; c < GEMV_MAX_CH; ++c) {
+            const int k = min(t + GEMV_THREADS * c, nch - 1);
+            if (p.norm_w_f32) {
+                wn[c][0] = *((const u32x4*)p.norm_w + 2 * k);
+                wn[c][1] = *((const u32x4*)p.norm_w + 2 * k + 1);
+            } else {
+                wn[c][0] = *((const u32x4*)p.norm_w + k);
+            }
+        }
     }
-    for (int g = threadIdx.x; g < groups; g += GEMV_THREADS) {
-        float s = 0.f;
-        for (int i = 0; i < 64; ++i) s += bf16_bits_to_f32(x[64 * g + i]);
-        xs[g] = s;
+    float inv = 1.f;
+    if (p.norm_w) {
+        float ss = 0.f;
+#pragma unroll
+        for (int c = 0; c < GEMV_MAX_CH; ++c)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const float lo = __uint_as_float(xc[c][e] << 16), hi = __uint_as_float(xc[c][e] & 0xffff0000u);
+                ss = fmaf(lo, lo, ss);
+                ss = fmaf(hi, hi, ss);
+            }
+        ss = wave_sum(ss);
+        if ((t & 63) == 0) red[t >> 6] = ss;
+        __syncthreads();
+        ss = (red[0] + red[1]) + (red[2] + red[3]);
+        inv = 1.f / sqrtf(ss / (float)in + p.norm_eps);
+    }
+#pragma unroll
+    for (int c = 0; c < GEMV_MAX_CH; ++c) {
+        if (GEMV_THREADS * c >= nch) break;  // uniform: no chunk of this pass exists
+        const int k = t + GEMV_THREADS * c;
+        float h[8];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            h[2 * e] = __uint_as_float(xc[c][e] << 16);
+            h[2 * e + 1] = __uint_as_float(xc[c][e] & 0xffff0000u);
+        }
+        if (p.norm_w) {
+            float w[8];
+            if (p.norm_w_f32) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    w[i] = __uint_as_float(wn[c][0][i]);
+                    w[4 + i] = __uint_as_float(wn[c][1][i]);
+                }
+            } else {
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    w[2 * e] = __uint_as_float(wn[c][0][e] << 16);
+                    w[2 * e + 1] = __uint_as_float(wn[c][0][e] & 0xffff0000u);
+                }
+            }
+            // chunks past the vector carry x = 0, so h stays 0
+#pragma unroll
+            for (int i = 0; i < 8; ++i) h[i] = bf16_bits_to_f32(f32_to_bf16_bits(w[i] * (h[i] * inv)));
+        }
+        if (k < nch) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                xp[4 * k + j] = (__float_as_uint(h[j]) >> 16) | (__float_as_uint(h[j + 4]) & 0xffff0000u);
+        }
+        float cs = ((h[0] + h[1]) + (h[2] + h[3])) + ((h[4] + h[5]) + (h[6] + h[7]));
+        cs += __shfl_xor(cs, 1);
+        cs += __shfl_xor(cs, 2);
+        cs += __shfl_xor(cs, 4);
+        if ((k & 7) == 0 && k < nch) xs[k >> 3] = cs;
     }
     __syncthreads();
 
-    const int w = threadIdx.x >> 6;
-    const int l = threadIdx.x & 63;
-    const int jw = j0 + w * RB;  // first output row of this wave
-    float acc[RB];
-    int64_t wrow[RB];
-    bool rv[RB];
+    auto dot_row = [&](const RowLoads& L) {
+        float acc = 0.f;
 #pragma unroll
-    for (int r = 0; r < RB; ++r) {
-        acc[r] = 0.f;
-        const int j = jw + r;
-        rv[r] = j < p.out_rows && j / p.map_a == xg;
-        const int jj = rv[r] ? j : jw;
-        wrow[r] = (int64_t)(jj / p.map_a) * p.map_b + p.map_c + (jj % p.map_a);
-    }
-    const int64_t wpr = words;  // packed words per weight row
-    for (int g = l; g < groups; g += 64) {
-        // x pairs of group g: 8 words x 4 pairs
-        u32x4 xv[8];
-#pragma unroll
-        for (int k = 0; k < 8; ++k) xv[k] = *(const u32x4*)(xp + 4 * (8 * g + k));
-        const float xsum = xs[g];
-#pragma unroll
-        for (int r = 0; r < RB; ++r) {
-            if (!rv[r]) continue;
-            const uint32_t* wp = p.packed + wrow[r] * wpr + 8 * g;
-            const u32x4 w0 = __builtin_nontemporal_load((const u32x4*)wp);
-            const u32x4 w1 = __builtin_nontemporal_load((const u32x4*)wp + 1);
-            const float s = load_scale<SDT>(p.scales, wrow[r] * groups + g);
-            const float bb = load_scale<SDT>(p.biases, wrow[r] * groups + g);
+        for (int q = 0; q < GEMV_NPT; ++q) {
+            const int g = min(tl + tpr * q, G - 1);
             float d = 0.f;
-            typedef __bf16 bf16x2v __attribute__((ext_vector_type(2)));
 #pragma unroll
             for (int k = 0; k < 8; ++k) {
-                const uint32_t word = k < 4 ? w0[k] : w1[k - 4];
+                const uint32_t word = k < 4 ? L.w[q][0][k] : L.w[q][1][k - 4];
+                const u32x4 xv = *(const u32x4*)(xp + 4 * (8 * g + k));
 #pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    const uint32_t pr = ((word >> (4 * j)) & 0x000F000Fu) | 0x43004300u;
-                    const uint32_t xw = xv[k][j];  // bit_cast of a vector-element lvalue reads element 0
+                for (int jj = 0; jj < 4; ++jj) {
+                    const uint32_t pr = ((word >> (4 * jj)) & 0x000F000Fu) | 0x43004300u;
+                    const uint32_t xw = xv[jj];  // bit_cast of a vector-element lvalue reads element 0
                     d = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2v, pr), __builtin_bit_cast(bf16x2v, xw),
                                                        d, false);
                 }
             }
             // sum x (128 + q) = d  ->  sum x q = d - 128 sum x
-            acc[r] = fmaf(s, d, fmaf(bb - 128.f * s, xsum, acc[r]));
+            const float sv = (L.ok >> q) & 1u ? L.s[q] : 0.f;
+            const float bv = (L.ok >> q) & 1u ? L.b[q] : 0.f;
+            acc = fmaf(sv, d, fmaf(bv - 128.f * sv, xs[g], acc));
         }
-    }
-#pragma unroll
-    for (int r = 0; r < RB; ++r) {
-        const float v = wave_sum(acc[r]);
-        if (l == 0 && rv[r]) {
-            const int64_t o = (int64_t)(jw + r) * p.y_stride_row;
+        return acc;
+    };
+    auto finish = [&](int j, float acc) {
+        for (int o = tpr >> 1; o >= 1; o >>= 1) acc += __shfl_xor(acc, o);
+        if (tl == 0 && j < r_end) {
+            const int64_t o = (int64_t)j * p.y_stride_row;
             if (p.y_f32)
-                ((float*)p.y)[o] = v;
+                ((float*)p.y)[o] = acc;
             else
-                ((uint16_t*)p.y)[o] = f32_to_bf16_bits(v);
+                ((uint16_t*)p.y)[o] = f32_to_bf16_bits(acc);
         }
+    };
+    // two register sets alternate: the next two steps' weights load (rows
+    // clamped, never branched around) while this pair is dotted, and no
+    // loaded value is copied before use
+    RowLoads ya, yb;
+    for (int rb = r0;;) {
+        load_row(rb + 2 * rps + tr, ya);
+        load_row(rb + 3 * rps + tr, yb);
+        finish(rb + tr, dot_row(la));
+        if (rb + rps < r_end) finish(rb + rps + tr, dot_row(lb));  // uniform
+        rb += 2 * rps;
+        if (rb >= r_end) break;
+        load_row(rb + 2 * rps + tr, la);
+        load_row(rb + 3 * rps + tr, lb);
+        finish(rb + tr, dot_row(ya));
+        if (rb + rps < r_end) finish(rb + rps + tr, dot_row(yb));  // uniform
+        rb += 2 * rps;
+        if (rb >= r_end) break;
     }
 }
 
@@ -211,27 +322,54 @@ hipError_t launch_affine_dequant(const AffineDequantParams& p, hipStream_t st) {
 
 bool affine_gemv_fast_ok(const AffineGemvParams& p) {
     return !p.force_generic && p.bits == 4 && p.group == 64 && !p.x_f32 && p.m == 1 && p.in_features <= GEMV_MAX_IN &&
-           p.in_features % 64 == 0 && (p.map_a % 4 == 0 || p.map_a == p.out_rows);
+           p.in_features % 64 == 0 && ((uintptr_t)p.x & 15) == 0 && p.x_stride % 8 == 0 &&
+           p.in_features <= 64 * GEMV_NPT_MAX * 64 && (!p.norm_w || ((uintptr_t)p.norm_w & 15) == 0);
 }
 
-hipError_t launch_affine_gemv(const AffineGemvParams& p, hipStream_t st) {
-    if (affine_gemv_fast_ok(p)) {
-        // rows per wave: enough waves to cover the GPU, RB rows to reuse x
-        int rb = p.out_rows >= 8192 ? 4 : (p.out_rows >= 4096 ? 2 : 1);
-        while (p.map_a != p.out_rows && p.map_a % (4 * rb) != 0) rb >>= 1;
-        const int rows_per_wg = 4 * rb;  // divides map_a (a multiple of 4 ... 16) when grouped
-        const unsigned grid = (unsigned)((p.out_rows + rows_per_wg - 1) / rows_per_wg);
-#define MR_GEMV4(SDT, RB) hipLaunchKernelGGL((affine_gemv4_kernel<SDT, RB>), dim3(grid), dim3(GEMV_THREADS), 0, st, p)
-        if (rb == 4) {
-            if (p.scale_dtype == 0) MR_GEMV4(0, 4); else if (p.scale_dtype == 1) MR_GEMV4(1, 4); else MR_GEMV4(2, 4);
-        } else if (rb == 2) {
-            if (p.scale_dtype == 0) MR_GEMV4(0, 2); else if (p.scale_dtype == 1) MR_GEMV4(1, 2); else MR_GEMV4(2, 2);
-        } else {
-            if (p.scale_dtype == 0) MR_GEMV4(0, 1); else if (p.scale_dtype == 1) MR_GEMV4(1, 1); else MR_GEMV4(2, 1);
-        }
+hipError_t launch_affine_gemv(const AffineGemvParams& q, hipStream_t st) {
+    if (affine_gemv_fast_ok(q)) {
+        AffineGemvParams p = q;
+        // threads per row: about G/4 groups each, more while the grid holds
+        // fewer row steps than the GPU has CUs; tiles of whole steps, about
+        // one per CU
+        const int G = p.in_features / 64;
+        const int nvec = (p.out_rows + p.map_a - 1) / p.map_a;
+        const int per_vec = std::min(p.map_a, p.out_rows);
+        int tpr = 1;
+        while (tpr < 64 && tpr * 4 < G) tpr <<= 1;
+        auto steps = [&](int t) { return (int64_t)nvec * ((per_vec + GEMV_THREADS / t - 1) / (GEMV_THREADS / t)); };
+        while (tpr < 64 && steps(tpr) < 256) tpr <<= 1;
+        const int rps = GEMV_THREADS / tpr;
+        const int64_t total = steps(tpr);
+        const int64_t per_tile = std::max<int64_t>(1, (total + 255) / 256);
+        p.tpr = tpr;
+        p.tile_rows = (int)std::min<int64_t>(per_tile * rps, per_vec);
+        p.tiles_per_vec = (per_vec + p.tile_rows - 1) / p.tile_rows;
+        const unsigned grid = (unsigned)(nvec * p.tiles_per_vec);
+        const int npt = (G + tpr - 1) / tpr;  // 1 .. 4
+#define MR_GEMV4(SDT, NPT) hipLaunchKernelGGL((affine_gemv4_kernel<SDT, NPT>), dim3(grid), dim3(GEMV_THREADS), 0, st, p)
+#define MR_GEMV4_NPT(SDT) \
+    do {                     \
+        if (npt == 1)        \
+            MR_GEMV4(SDT, 1); \
+        else if (npt == 2)   \
+            MR_GEMV4(SDT, 2); \
+        else if (npt == 3)   \
+            MR_GEMV4(SDT, 3); \
+        else                 \
+            MR_GEMV4(SDT, 4); \
+    } while (0)
+        if (p.scale_dtype == 0)
+            MR_GEMV4_NPT(0);
+        else if (p.scale_dtype == 1)
+            MR_GEMV4_NPT(1);
+        else
+            MR_GEMV4_NPT(2);
+#undef MR_GEMV4_NPT
 #undef MR_GEMV4
         return hipGetLastError();
     }
+    const AffineGemvParams& p = q;
     const int64_t waves = (int64_t)p.m * p.out_rows;
     const unsigned grid = (unsigned)((waves + 3) / 4);
     if (p.scale_dtype == 0)

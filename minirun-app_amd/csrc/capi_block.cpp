@@ -60,6 +60,36 @@ mr_status check_weight(const mr_affine_weight* w, const char* what) {
 
 bool act_dtype_ok(mr_dtype d) { return d == MR_BF16 || d == MR_F32; }
 
+mr::AffineGemvParams gemv_params(const mr_affine_weight* w);
+
+// y = W . RMSNorm(x) (norm_w non-null) or y = W . x for one bf16 token:
+// the norm rides in the GEMV's staging of x when the 4-bit fast path takes
+// the weight, else it runs as its own stage into `norm_buf`.
+mr_status block_gemv(const void* x, int64_t in, const mr_affine_weight* w, void* y, const void* norm_w,
+                     mr_dtype norm_dtype, float eps, void* norm_buf, void* stream) {
+    mr::AffineGemvParams g = gemv_params(w);
+    g.x = x;
+    g.x_f32 = 0;
+    g.x_stride = in;
+    g.m = 1;
+    g.y = y;
+    g.y_f32 = 0;
+    g.y_stride_row = 1;
+    g.y_stride_token = w->out_features;
+    g.force_generic = !aligned16(w->packed);
+    g.norm_w = norm_w;
+    g.norm_w_f32 = norm_dtype == MR_F32;
+    g.norm_eps = eps;
+    if (norm_w && !mr::affine_gemv_fast_ok(g)) {
+        mr_status st = mr_rmsnorm(x, MR_BF16, 1, (int32_t)in, in, norm_w, norm_dtype, eps, norm_buf, MR_BF16, in, stream);
+        if (st != MR_OK) return st;
+        g.x = norm_buf;
+        g.norm_w = nullptr;
+    }
+    const hipError_t e = mr::launch_affine_gemv(g, (hipStream_t)stream);
+    return e == hipSuccess ? MR_OK : hip_fail(e, "affine matmul launch");
+}
+
 mr::AffineGemvParams gemv_params(const mr_affine_weight* w) {
     mr::AffineGemvParams g{};
     g.packed = w->packed;
@@ -422,21 +452,11 @@ mr_status mr_mla_decode_block(const mr_mla_block_args* a, void* stream) {
     void* attn = W + L.attn;
     const mr_dtype nd = a->norm_w_dtype;
 
-    // h = input norm (or x)
-    const void* hin = a->x;
-    if (a->input_norm_w) {
-        st = mr_rmsnorm(a->x, MR_BF16, 1, a->hidden, a->hidden, a->input_norm_w, nd, a->eps, h, MR_BF16, a->hidden, stream);
-        if (st != MR_OK) return st;
-        hin = h;
-    }
-    // query path: q_a -> RMSNorm -> q_b -> rotate the rope part -> absorb W_UK
-    if ((st = mr_affine_matmul(hin, MR_BF16, 1, a->hidden, &a->q_a, q_lora, MR_BF16, a->q_lora_rank, stream)) != MR_OK)
+    // query path: [input norm] -> q_a -> RMSNorm -> q_b -> rotate the rope
+    // part -> absorb W_UK (the norms ride in the GEMVs' staging of x)
+    if ((st = block_gemv(a->x, a->hidden, &a->q_a, q_lora, a->input_norm_w, nd, a->eps, h, stream)) != MR_OK)
         return st;
-    if ((st = mr_rmsnorm(q_lora, MR_BF16, 1, a->q_lora_rank, a->q_lora_rank, a->q_a_norm_w, nd, a->eps, q_lora_n,
-                         MR_BF16, a->q_lora_rank, stream)) != MR_OK)
-        return st;
-    if ((st = mr_affine_matmul(q_lora_n, MR_BF16, 1, a->q_lora_rank, &a->q_b, q, MR_BF16, int64_t(a->heads) * dq,
-                               stream)) != MR_OK)
+    if ((st = block_gemv(q_lora, a->q_lora_rank, &a->q_b, q, a->q_a_norm_w, nd, a->eps, q_lora_n, stream)) != MR_OK)
         return st;
     if ((st = mr_rope_apply(q, MR_BF16, 1, a->heads, dq, a->qk_nope_dim, a->qk_rope_dim, a->rope_cos, a->rope_sin,
                             stream)) != MR_OK)
@@ -445,9 +465,7 @@ mr_status mr_mla_decode_block(const mr_mla_block_args* a, void* stream) {
                                   stream)) != MR_OK)
         return st;
     // key path: kv_a -> cache row `position` (norm + rope), then attend
-    if ((st = mr_affine_matmul(hin, MR_BF16, 1, a->hidden, &a->kv_a, kv, MR_BF16, a->kv_rank + a->qk_rope_dim,
-                               stream)) != MR_OK)
-        return st;
+    if ((st = block_gemv(a->x, a->hidden, &a->kv_a, kv, a->input_norm_w, nd, a->eps, h, stream)) != MR_OK) return st;
     if ((st = mr_mla_cache_append(kv, MR_BF16, a->kv_rank + a->qk_rope_dim, 1, a->kv_a_norm_w, nd, a->eps, a->kv_rank,
                                   a->qk_rope_dim, a->rope_cos, a->rope_sin, a->cache_latent, a->latent_row_stride,
                                   a->cache_rope, a->rope_row_stride, a->position, stream)) != MR_OK)

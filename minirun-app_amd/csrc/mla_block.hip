@@ -147,6 +147,94 @@ __global__ void __launch_bounds__(256) absorb_q_kernel(AbsorbParams p) {
     }
 }
 
+// The same product, 256 columns of one head per workgroup (kv_rank 512,
+// nope_dim 128): the head's query values, scales and biases are staged in
+// LDS with one load per thread; lane (rs = l/8, quad wq = l%8) of wave w
+// loads the 16-byte words of rows d = 32k + 8w + rs (k < 4) and columns
+// 256 half + 32 wq .. +31, so a thread issues four weight loads.  Row sums
+// meet by lane exchange (rs) and through LDS (waves).
+template <int SDT>
+__global__ void __launch_bounds__(256) absorb_q_fast_kernel(AbsorbParams p) {
+    __shared__ float qs[128];
+    __shared__ float sc[128][8], bi[128][8];
+    __shared__ __attribute__((aligned(16))) float part[4][256];
+    const int h = blockIdx.x >> 1;
+    const int half = blockIdx.x & 1;
+    const int t = threadIdx.x;
+    const int w = t >> 6, l = t & 63;
+    const int rs = l >> 3, wq = l & 7;
+    const int64_t row0 = (int64_t)h * (p.nope_dim + p.v_dim);
+    // weights first: they do not depend on the staging
+    u32x4 wd[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const int d = 32 * k + 8 * w + rs;
+        wd[k] = *(const u32x4*)(p.packed + (row0 + d) * 64 + 32 * half + 4 * wq);
+    }
+    // scales and biases of the head's 128 nope rows (8 groups each) and q
+    {
+        const int64_t gi = row0 * 8 + 4 * t;  // four consecutive (row, group) entries
+        float sv[4], bv[4];
+        if (SDT == 2) {
+            const f32x4 a = *(const f32x4*)((const float*)p.scales + gi);
+            const f32x4 c = *(const f32x4*)((const float*)p.biases + gi);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                sv[i] = a[i];
+                bv[i] = c[i];
+            }
+        } else {
+            const u32x2 a = *(const u32x2*)((const uint16_t*)p.scales + gi);
+            const u32x2 c = *(const u32x2*)((const uint16_t*)p.biases + gi);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const uint16_t ua = (uint16_t)(a[i >> 1] >> (16 * (i & 1)));
+                const uint16_t uc = (uint16_t)(c[i >> 1] >> (16 * (i & 1)));
+                sv[i] = SDT == 1 ? f16_bits_to_f32(ua) : bf16_bits_to_f32(ua);
+                bv[i] = SDT == 1 ? f16_bits_to_f32(uc) : bf16_bits_to_f32(uc);
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            sc[(4 * t + i) >> 3][(4 * t + i) & 7] = sv[i];
+            bi[(4 * t + i) >> 3][(4 * t + i) & 7] = bv[i];
+        }
+        if (t < 128) qs[t] = bf16_bits_to_f32(p.q[(int64_t)h * p.q_head_stride + t]);
+    }
+    __syncthreads();
+    const int grp = 4 * half + (wq >> 1);  // group of this lane's 32 columns
+    float acc[32];
+#pragma unroll
+    for (int i = 0; i < 32; ++i) acc[i] = 0.f;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const int d = 32 * k + 8 * w + rs;
+        const float s = sc[d][grp], b = bi[d][grp], qd = qs[d];
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int n = 0; n < 8; ++n) {
+                const float wv = add_rn(mul_rn(s, (float)((wd[k][j] >> (4 * n)) & 15u)), b);
+                acc[8 * j + n] = fmaf(qd, wv, acc[8 * j + n]);
+            }
+    }
+    // rows of the wave: lanes l, l^8, l^16, l^32 hold the same columns
+#pragma unroll
+    for (int i = 0; i < 32; ++i) {
+        acc[i] += __shfl_xor(acc[i], 8);
+        acc[i] = xor16_sum(acc[i]);
+        acc[i] = xor32_sum(acc[i]);
+    }
+    if (rs == 0) {
+#pragma unroll
+        for (int i = 0; i < 32; i += 4)
+            *(f32x4*)&part[w][32 * wq + i] = f32x4{acc[i], acc[i + 1], acc[i + 2], acc[i + 3]};
+    }
+    __syncthreads();
+    const float v = (part[0][t] + part[1][t]) + (part[2][t] + part[3][t]);
+    p.q_lat[(int64_t)h * p.q_lat_head_stride + 256 * half + t] = f32_to_bf16_bits(v);
+}
+
 }  // namespace
 
 hipError_t launch_rmsnorm(const RmsNormParams& p, hipStream_t st) {
@@ -167,6 +255,18 @@ hipError_t launch_cache_append(const CacheAppendParams& p, hipStream_t st) {
 }
 
 hipError_t launch_absorb_q(const AbsorbParams& p, hipStream_t st) {
+    const int sz = p.scale_dtype == 2 ? 4 : 2;
+    if (p.kv_rank == 512 && p.nope_dim == 128 && ((uintptr_t)p.packed & 15) == 0 &&
+        ((uintptr_t)p.scales & (2 * sz - 1)) == 0 && ((uintptr_t)p.biases & (2 * sz - 1)) == 0) {
+        const dim3 grid((unsigned)p.heads * 2);
+        if (p.scale_dtype == 0)
+            hipLaunchKernelGGL(absorb_q_fast_kernel<0>, grid, dim3(256), 0, st, p);
+        else if (p.scale_dtype == 1)
+            hipLaunchKernelGGL(absorb_q_fast_kernel<1>, grid, dim3(256), 0, st, p);
+        else
+            hipLaunchKernelGGL(absorb_q_fast_kernel<2>, grid, dim3(256), 0, st, p);
+        return hipGetLastError();
+    }
     hipLaunchKernelGGL(absorb_q_kernel, dim3((unsigned)p.heads), dim3(256), 0, st, p);
     return hipGetLastError();
 }

@@ -137,6 +137,13 @@ struct AffineGemvParams {
     int y_f32;
     int64_t y_stride_row, y_stride_token;
     int force_generic;
+    // 4-bit fast path: optional RMSNorm of the activation vector, applied
+    // while it is staged (null = plain x), and the launch geometry the host
+    // chose (threads per output row, rows per workgroup tile)
+    const void* norm_w;
+    int norm_w_f32;
+    float norm_eps;
+    int tpr, tile_rows, tiles_per_vec;
 };
 
 hipError_t launch_affine_dequant(const AffineDequantParams& p, hipStream_t st);
