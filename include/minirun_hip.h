@@ -230,6 +230,9 @@ mr_status mr_mla_unabsorb_values(const void *ctx, int64_t ctx_head_stride, int32
  *   out = o_proj(unabsorb(ctx, kv_b))
  * The output gate is not part of this block.  All activations between the
  * projections are bf16 (the affine matmul output dtype for bf16 input).
+ * The key path (kv_a, cache append) runs on a library-owned side stream of
+ * the current device, forked from `stream` and joined back before the
+ * attention by events; the call stays ordered on `stream` as a whole.
  * ------------------------------------------------------------------------ */
 typedef struct mr_mla_block_args {
     int32_t hidden, q_lora_rank, heads, qk_nope_dim, qk_rope_dim, v_head_dim, kv_rank;

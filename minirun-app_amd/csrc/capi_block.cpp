@@ -1,11 +1,13 @@
 // C-ABI: affine weights, RMSNorm, rotary, cache append, absorption, the
 // composed decode block, and the V4 index tables.  Validation first, with
-// the reference's messages where it has them; no device allocation.
+// the reference's messages where it has them; no device memory allocation
+// (the block creates one side stream and two events per device, once).
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
 #include <cmath>
 #include <cstdio>
+#include <mutex>
 #include <string>
 
 #include "../../include/minirun_hip.h"
@@ -61,6 +63,37 @@ mr_status check_weight(const mr_affine_weight* w, const char* what) {
 bool act_dtype_ok(mr_dtype d) { return d == MR_BF16 || d == MR_F32; }
 
 mr::AffineGemvParams gemv_params(const mr_affine_weight* w);
+
+// The block's key path (kv_a projection, cache append) does not depend on
+// its query path until the attention: it runs on a side stream of the
+// device, forked from and joined back to the caller's stream by events.
+// One side stream per device for the process; calls that share it are
+// ordered on it, and every join waits for the caller's own fork point or
+// later, so sharing stays correct.
+struct SideStream {
+    hipStream_t s = nullptr;
+    hipEvent_t fork = nullptr, join = nullptr;
+};
+
+mr_status side_stream(SideStream** out) {
+    static std::mutex mu;
+    static SideStream per_dev[64];
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return hip_fail(e, "mla block: hipGetDevice");
+    if (dev < 0 || dev >= 64) return fail(MR_INVALID_ARGUMENT, "mla block: device %d out of range", dev);
+    std::lock_guard<std::mutex> lock(mu);
+    SideStream& ss = per_dev[dev];
+    if (!ss.s) {
+        if ((e = hipStreamCreateWithFlags(&ss.s, hipStreamNonBlocking)) != hipSuccess)
+            return hip_fail(e, "mla block: side stream");
+        if ((e = hipEventCreateWithFlags(&ss.fork, hipEventDisableTiming)) != hipSuccess ||
+            (e = hipEventCreateWithFlags(&ss.join, hipEventDisableTiming)) != hipSuccess)
+            return hip_fail(e, "mla block: side stream events");
+    }
+    *out = &ss;
+    return MR_OK;
+}
 
 // y = W . RMSNorm(x) (norm_w non-null) or y = W . x for one bf16 token:
 // the norm rides in the GEMV's staging of x when the 4-bit fast path takes
@@ -452,6 +485,22 @@ mr_status mr_mla_decode_block(const mr_mla_block_args* a, void* stream) {
     void* attn = W + L.attn;
     const mr_dtype nd = a->norm_w_dtype;
 
+    // key path on the side stream: [input norm] -> kv_a -> cache row
+    // `position` (norm + rope); the attention below joins it
+    SideStream* side = nullptr;
+    if ((st = side_stream(&side)) != MR_OK) return st;
+    hipError_t he;
+    if ((he = hipEventRecord(side->fork, (hipStream_t)stream)) != hipSuccess ||
+        (he = hipStreamWaitEvent(side->s, side->fork, 0)) != hipSuccess)
+        return hip_fail(he, "mla block: fork");
+    // the kv_a norm fallback writes its own buffer (q_lora_n is the query's)
+    if ((st = block_gemv(a->x, a->hidden, &a->kv_a, kv, a->input_norm_w, nd, a->eps, ctx, side->s)) != MR_OK)
+        return st;
+    if ((st = mr_mla_cache_append(kv, MR_BF16, a->kv_rank + a->qk_rope_dim, 1, a->kv_a_norm_w, nd, a->eps, a->kv_rank,
+                                  a->qk_rope_dim, a->rope_cos, a->rope_sin, a->cache_latent, a->latent_row_stride,
+                                  a->cache_rope, a->rope_row_stride, a->position, side->s)) != MR_OK)
+        return st;
+    if ((he = hipEventRecord(side->join, side->s)) != hipSuccess) return hip_fail(he, "mla block: join record");
     // query path: [input norm] -> q_a -> RMSNorm -> q_b -> rotate the rope
     // part -> absorb W_UK (the norms ride in the GEMVs' staging of x)
     if ((st = block_gemv(a->x, a->hidden, &a->q_a, q_lora, a->input_norm_w, nd, a->eps, h, stream)) != MR_OK)
@@ -464,12 +513,9 @@ mr_status mr_mla_decode_block(const mr_mla_block_args* a, void* stream) {
     if ((st = mr_mla_absorb_query(q, dq, a->heads, a->qk_nope_dim, a->v_head_dim, &a->kv_b, q_lat, a->kv_rank,
                                   stream)) != MR_OK)
         return st;
-    // key path: kv_a -> cache row `position` (norm + rope), then attend
-    if ((st = block_gemv(a->x, a->hidden, &a->kv_a, kv, a->input_norm_w, nd, a->eps, h, stream)) != MR_OK) return st;
-    if ((st = mr_mla_cache_append(kv, MR_BF16, a->kv_rank + a->qk_rope_dim, 1, a->kv_a_norm_w, nd, a->eps, a->kv_rank,
-                                  a->qk_rope_dim, a->rope_cos, a->rope_sin, a->cache_latent, a->latent_row_stride,
-                                  a->cache_rope, a->rope_row_stride, a->position, stream)) != MR_OK)
-        return st;
+    // attend once the key path has written the cache row
+    if ((he = hipStreamWaitEvent((hipStream_t)stream, side->join, 0)) != hipSuccess)
+        return hip_fail(he, "mla block: join");
     mr_mla_decode_args d = L.dec_args;
     d.q_lat = q_lat;
     d.q_rope = q + a->qk_nope_dim;
