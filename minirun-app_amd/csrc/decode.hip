@@ -67,34 +67,6 @@ __device__ __forceinline__ int sigma_row(int rt, int a) {
     return 16 * rt + 8 * (g >> 1) + (g & 1) + 2 * (a & 3);
 }
 
-// LDS-only barrier: waits for this wave's LDS traffic, not for its global
-// (DMA) loads, so prefetches stay in flight across it.
-__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
-
-// All global -> LDS traffic of the split kernel is issued with this
-// instruction from inline asm, so the compiler neither knows of it nor
-// inserts its conservative vmcnt(0) before LDS reads; the kernel waits for
-// it explicitly with wait_vmcnt.  The kernel issues no other vector-memory
-// load after the first DMA, which keeps those counts exact.  (Extra loads
-// the compiler does not see can only make its own waits stricter.)
-__device__ __forceinline__ void dma16(const void* src, const void* lds_dst_wave_base) {
-    const uint32_t m0 = (uint32_t)(uintptr_t)lds_dst_wave_base;  // LDS offset (low 32 bits)
-    asm volatile("global_load_lds_dwordx4 %0, off" ::"v"(src), "{m0}"(m0) : "memory");
-}
-
-// Same DMA with a wave-uniform 64-bit base in SGPRs and a 32-bit per-lane
-// byte offset: one VGPR per load instead of two.
-__device__ __forceinline__ void dma16_off(const void* sbase, uint32_t voff, const void* lds_dst_wave_base) {
-    const uint32_t m0 = (uint32_t)(uintptr_t)lds_dst_wave_base;
-    asm volatile("global_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase), "{m0}"(m0) : "memory");
-}
-
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-    static_assert(N >= 0 && N < 64, "vmcnt range");
-    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
-}
-
 constexpr float TAU = 8.f;  // log2 headroom before the running max is raised
 
 // Partial record of (batch b, head, split): [batch][h_pad][splits] order, so

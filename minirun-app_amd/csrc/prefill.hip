@@ -126,6 +126,7 @@ constexpr int AT_Q = 128;   // queries per workgroup (32 per wave)
 constexpr int AT_K = 64;    // keys per tile
 constexpr int AT_DK = 192;  // key width: 128 nope + 64 rope
 constexpr int AT_DV = 128;
+constexpr float AT_TAU = 8.f;  // log2 headroom of the running max
 
 // K tile [64][192] bf16 (384-byte rows, 24 chunks): chunk c of row r at
 // c ^ ((r >> 1) & 7).  V tile [64][128] (256-byte rows): chunk c of row r at
@@ -133,10 +134,11 @@ constexpr int AT_DV = 128;
 __device__ __forceinline__ int k_off(int r, int c) { return r * AT_DK + ((c ^ ((r >> 1) & 7)) << 3); }
 __device__ __forceinline__ int v_off(int r, int d) { return r * AT_DV + ((((d >> 3) ^ ((r & 3) << 1))) << 3) + (d & 7); }
 
-__global__ void __launch_bounds__(256, 1) prefill_attn_kernel(PrefillAttnParams p) {
-    __shared__ __attribute__((aligned(16))) uint16_t lds[AT_K * AT_DK + AT_K * AT_DV];  // 40 KB
-    uint16_t* ks_lds = lds;
-    uint16_t* vs_lds = lds + AT_K * AT_DK;
+constexpr int AT_TILE = AT_K * AT_DK + AT_K * AT_DV;  // elements of one K + V tile (40 KB)
+constexpr int AT_NBUF = 2;                            // tiles in LDS: one in use, one in flight
+
+__global__ void __launch_bounds__(256, 2) prefill_attn_kernel(PrefillAttnParams p) {
+    __shared__ __attribute__((aligned(1024))) uint16_t lds[AT_NBUF * AT_TILE];  // 80 KB: two workgroups per CU
     const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, lq = l & 31, hh = l >> 5;
 
     // work item: (head, query tile); one XCD takes all query tiles of a head
@@ -171,32 +173,30 @@ __global__ void __launch_bounds__(256, 1) prefill_attn_kernel(PrefillAttnParams 
     const int wave_kend = q0 + 32 * w < p.T ? off + min(q0 + 32 * w + 32, p.T) : 0;
 
     const uint16_t* kv_h = p.kv + (int64_t)head * 256;
-    u32x4 rk[6], rv[4];
-    auto gload = [&](int kt) {
+    // K / V tile kt into buffer `buf` by DMA (global_load_lds_dwordx4, 1 KB
+    // per wave instruction, 10 per wave): LDS slot s holds the swizzled
+    // chunk of k_off / v_off, so its source is the inverse-swizzled chunk.
+    // Every lane always loads (keys clamped), so each wave issues exactly 10.
+    auto issue = [&](int kt, int buf) {
+        uint16_t* kb = lds + buf * AT_TILE;
+        uint16_t* vb = kb + AT_K * AT_DK;
 #pragma unroll
         for (int i = 0; i < 6; ++i) {
-            const int q = tid + 256 * i, row = q / 24, ch = q % 24;
-            const int key = min(kt * AT_K + row, p.P - 1);
-            rk[i] = ch < 16 ? *(const u32x4*)(kv_h + (int64_t)key * p.kv_rs + ch * 8)
-                            : *(const u32x4*)(p.rope + (int64_t)key * p.rope_rs + (ch - 16) * 8);
+            const int sl = 64 * (w + 4 * i) + l;  // K slot: row sl / 24, physical chunk sl % 24
+            const int r = sl / 24, pc = sl - r * 24;
+            const int c = pc ^ ((r >> 1) & 7);
+            const int key = min(kt * AT_K + r, p.P - 1);
+            const uint16_t* src = c < 16 ? kv_h + (int64_t)key * p.kv_rs + c * 8
+                                         : p.rope + (int64_t)key * p.rope_rs + (c - 16) * 8;
+            dma16(src, kb + 512 * (w + 4 * i));
         }
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const int q = tid + 256 * i, row = q >> 4, ch = q & 15;
-            const int key = min(kt * AT_K + row, p.P - 1);
-            rv[i] = *(const u32x4*)(kv_h + (int64_t)key * p.kv_rs + 128 + ch * 8);
-        }
-    };
-    auto sstore = [&]() {
-#pragma unroll
-        for (int i = 0; i < 6; ++i) {
-            const int q = tid + 256 * i, row = q / 24, ch = q % 24;
-            *(u32x4*)(ks_lds + k_off(row, ch)) = rk[i];
-        }
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int q = tid + 256 * i, row = q >> 4, ch = q & 15;
-            *(u32x4*)(vs_lds + v_off(row, ch * 8)) = rv[i];
+            const int sl = 64 * (w + 4 * i) + l;  // V slot: row sl / 16, physical chunk sl % 16
+            const int r = sl >> 4, pc = sl & 15;
+            const int c = pc ^ ((r & 3) << 1);
+            const int key = min(kt * AT_K + r, p.P - 1);
+            dma16(kv_h + (int64_t)key * p.kv_rs + 128 + c * 8, vb + 512 * (w + 4 * i));
         }
     };
 
@@ -210,73 +210,100 @@ __global__ void __launch_bounds__(256, 1) prefill_attn_kernel(PrefillAttnParams 
     const int tr_key = 4 * (g >> 1) + (j >> 2);
     const int tr_d = 16 * (g & 1) + 4 * (j & 3);
 
-    gload(0);
+    // tile 0 in flight, wait for it
+    issue(0, 0);
+    wait_vmcnt<0>();
+    lds_barrier();
     for (int kt = 0; kt < ntiles; ++kt) {
-        if (kt > 0) __syncthreads();
-        sstore();
-        __syncthreads();
-        if (kt + 1 < ntiles) gload(kt + 1);
+        // refill the buffer of tile kt-1 (read before the last barrier)
+        if (kt + 1 < ntiles) issue(kt + 1, (kt + 1) % AT_NBUF);
+        const uint16_t* ks_lds = lds + (kt % AT_NBUF) * AT_TILE;
+        const uint16_t* vs_lds = ks_lds + AT_K * AT_DK;
         const int k0 = kt * AT_K;
-        if (k0 >= wave_kend) continue;  // every query of this wave is past this tile
+        if (k0 < wave_kend) {  // else every query of this wave is past this tile
 
-        // S^T = K . Q^T: two 32-key blocks, 12 k-steps of 16 features
-        f32x16 s[2] = {f32x16{}, f32x16{}};
+            // S^T = K . Q^T: two 32-key blocks, 12 k-steps of 16 features; the
+            // A operands come in double-buffered groups of 4 (two k-steps x
+            // both blocks), so each group's LDS reads overlap the previous
+            // group's MFMAs (the fences keep the scheduler from hoisting all)
+            f32x16 s[2] = {f32x16{}, f32x16{}};
+            bf16x8 ga[2][4];
+            auto qk_a = [&](int ks, int kb) -> bf16x8 {
+                return *(const bf16x8*)(ks_lds + k_off(kb * 32 + lq, 2 * ks + hh));
+            };
 #pragma unroll
-        for (int ks = 0; ks < 12; ++ks) {
+            for (int e = 0; e < 4; ++e) ga[0][e] = qk_a(e >> 1, e & 1);
 #pragma unroll
-            for (int kb = 0; kb < 2; ++kb) {
-                const bf16x8 a = *(const bf16x8*)(ks_lds + k_off(kb * 32 + lq, 2 * ks + hh));
-                s[kb] = mfma32(a, qf[ks], s[kb]);
-            }
-        }
-        // scale, causal mask, running max (lane = query, 32 of its keys)
-        const bool diag = k0 + AT_K - 1 > wave_first;
-        float mx = -INFINITY;
+            for (int gq = 0; gq < 6; ++gq) {
+                if (gq + 1 < 6) {
 #pragma unroll
-        for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-            for (int i = 0; i < 16; ++i) {
-                float v = s[kb][i] * p.scale_log2;
-                if (diag) {
-                    const int key = k0 + kb * 32 + 8 * (i >> 2) + 4 * hh + (i & 3);
-                    if (key > q_limit) v = -INFINITY;
+                    for (int e = 0; e < 4; ++e) ga[(gq + 1) & 1][e] = qk_a(2 * (gq + 1) + (e >> 1), e & 1);
                 }
-                s[kb][i] = v;
-                mx = fmaxf(mx, v);
+                __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) s[e & 1] = mfma32(ga[gq & 1][e], qf[2 * gq + (e >> 1)], s[e & 1]);
+                __builtin_amdgcn_sched_barrier(0);
             }
-        mx = fmaxf(mx, __shfl_xor(mx, 32));
-        const float m_new = fmaxf(m_run, mx);
-        const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
-        m_run = m_new;
-        float ls = 0.f;
+            // scale, causal mask, running max (lane = query, 32 of its keys)
+            const bool diag = k0 + AT_K - 1 > wave_first;
+            float mx = -INFINITY;
 #pragma unroll
-        for (int kb = 0; kb < 2; ++kb)
+            for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-            for (int i = 0; i < 16; ++i) {
-                const float e = __builtin_amdgcn_exp2f(s[kb][i] - m_new);
-                s[kb][i] = e;
-                ls += e;
+                for (int i = 0; i < 16; ++i) {
+                    float v = s[kb][i] * p.scale_log2;
+                    if (diag) {
+                        const int key = k0 + kb * 32 + 8 * (i >> 2) + 4 * hh + (i & 3);
+                        if (key > q_limit) v = -INFINITY;
+                    }
+                    s[kb][i] = v;
+                    mx = fmaxf(mx, v);
+                }
+            mx = fmaxf(mx, __shfl_xor(mx, 32));
+            // the reference max rises only when a score passes it by
+            // AT_TAU (log2 units), so O is rescaled on few tiles (P <=
+            // 2^AT_TAU); key 0 is visible to every query, so the first tile
+            // always sets a finite reference
+            const bool raise = mx > m_run + AT_TAU;  // false while mx is -inf
+            if (__builtin_amdgcn_ballot_w64(raise)) {
+                const float m_new = raise ? mx : m_run;
+                const float alpha = raise ? __builtin_amdgcn_exp2f(m_run - m_new) : 1.f;
+                m_run = m_new;
+                l_part *= alpha;
+#pragma unroll
+                for (int d = 0; d < 4; ++d) o[d] *= alpha;
             }
-        l_part = l_part * alpha + ls;
+            float ls = 0.f;
 #pragma unroll
-        for (int d = 0; d < 4; ++d) o[d] *= alpha;
+            for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+                for (int i = 0; i < 16; ++i) {
+                    const float e = __builtin_amdgcn_exp2f(s[kb][i] - m_run);
+                    s[kb][i] = e;
+                    ls += e;
+                }
+            l_part += ls;
 
-        // O^T += V^T . P^T: k-step t covers tile keys 16t .. 16t+15
+            // O^T += V^T . P^T: k-step t covers tile keys 16t .. 16t+15
 #pragma unroll
-        for (int t = 0; t < 4; ++t) {
-            const int kb = t >> 1, base = 8 * (t & 1);
-            bf16x8 pb;
+            for (int t = 0; t < 4; ++t) {
+                const int kb = t >> 1, base = 8 * (t & 1);
+                bf16x8 pb;
 #pragma unroll
-            for (int e = 0; e < 8; ++e) pb[e] = (__bf16)s[kb][base + e];
+                for (int e = 0; e < 8; ++e) pb[e] = (__bf16)s[kb][base + e];
 #pragma unroll
-            for (int db = 0; db < 4; ++db) {
-                const int d = 32 * db + tr_d;
-                const bf16x4 lo = ds_read_tr16(vs_lds + v_off(16 * t + tr_key, d));
-                const bf16x4 hi = ds_read_tr16(vs_lds + v_off(16 * t + 8 + tr_key, d));
-                const bf16x8 a = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-                o[db] = mfma32(a, pb, o[db]);
+                for (int db = 0; db < 4; ++db) {
+                    const int d = 32 * db + tr_d;
+                    const bf16x4 lo = ds_read_tr16(vs_lds + v_off(16 * t + tr_key, d));
+                    const bf16x4 hi = ds_read_tr16(vs_lds + v_off(16 * t + 8 + tr_key, d));
+                    const bf16x8 a = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+                    o[db] = mfma32(a, pb, o[db]);
+                }
             }
         }
+        // tile kt+1 must have landed
+        if (kt + 1 < ntiles) wait_vmcnt<0>();
+        lds_barrier();
     }
 
     // normalise: the two halves of the wave hold partial sums of one query
