@@ -44,6 +44,8 @@ mr_status check_prefill(const mr_mla_prefill_args* a) {
     if (a->q_head_stride < 192 || a->q_token_stride < 192 || a->latent_row_stride < 512 || a->rope_row_stride < 64 ||
         a->kv_b_row_stride < 512)
         return fail(MR_INVALID_ARGUMENT, "mla prefill: strides are smaller than the rows they step over");
+    if (a->rope_row_stride > (int64_t)(INT32_MAX / 64))  // a 64-key tile's offsets stay 32-bit
+        return fail(MR_INVALID_ARGUMENT, "mla prefill: rope_row_stride %lld too large", (long long)a->rope_row_stride);
     if (a->out_dtype != MR_BF16 && a->out_dtype != MR_F32)
         return fail(MR_INVALID_DTYPE, "mla prefill: out_dtype must be MR_BF16 or MR_F32");
     const int64_t vec = a->out_dtype == MR_F32 ? 4 : 8;  // 16-byte output pieces

@@ -131,6 +131,23 @@ __device__ __forceinline__ void dma16_off(const void* sbase, uint32_t voff, cons
     asm volatile("global_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase), "{m0}"(m0) : "memory");
 }
 
+// Raw (stride 0) buffer resource over `bytes` bytes from `base`: a load at a
+// byte offset at or past `bytes` returns zeros.  Word 3 holds the gfx9 data
+// format the memory-to-register loads expect (32-bit, no swizzle).
+typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ i32x4 buffer_rsrc(const void* base, uint32_t bytes) {
+    const uint64_t a = (uint64_t)(uintptr_t)base;
+    return i32x4{(int32_t)(uint32_t)a, (int32_t)((a >> 32) & 0xffff), (int32_t)bytes, 0x00020000};
+}
+
+// DMA of 16 bytes per lane from a buffer resource at a per-lane byte offset
+// (buffer_load_dwordx4 ... lds): lane i lands at lds_dst_wave_base + 16 i;
+// a lane whose offset is out of range writes zeros.  Same wait rules as dma16.
+__device__ __forceinline__ void dma16_buf(i32x4 rsrc, uint32_t voff, const void* lds_dst_wave_base) {
+    const uint32_t m0 = (uint32_t)(uintptr_t)lds_dst_wave_base;
+    asm volatile("buffer_load_dwordx4 %0, %1, 0 offen lds" ::"v"(voff), "s"(rsrc), "{m0}"(m0) : "memory");
+}
+
 template <int N>
 __device__ __forceinline__ void wait_vmcnt() {
     static_assert(N >= 0 && N < 64, "vmcnt range");
