@@ -277,9 +277,9 @@ __global__ void __launch_bounds__(THREADS, 1) mla_decode_split(DecodeParams p) {
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const int r = rbase + 16 * rt + lbase + 2 * i;
-                bool ok = r < row_end;
-                if (GATHER) ok = ok && idx_s[r - row_begin] >= 0;
-                if (!ok) sv[i] = NEG_INF;
+                const int v = GATHER ? idx_s[r - row_begin] : 0;  // inside idx_s for every sub-chunk row
+                const bool ok = (r < row_end) & (v >= 0);
+                sv[i] = ok ? sv[i] : NEG_INF;
             }
         }
         // partial max over this lane's 4 rows; the 8 partials of a head (4 lane
@@ -444,17 +444,19 @@ __device__ __forceinline__ int ksig(int p) {
     return (p & ~7) | (j < 4 ? 2 * j : 2 * (j - 4) + 1);
 }
 
-template <int HGS>
+// QK waves of 32 heads (32x32x16 MFMA) or, with QK16, of 16 heads (16x16x32
+// MFMA): a 64-head group then has one QK wave per SIMD beside each PV wave.
+template <int HGS, bool QK16>
 struct WsShape {
-    static constexpr int QKW = HGS / 32;           // QK waves
-    static constexpr int THREADS = 64 * (QKW + 4);  // + 4 PV waves
+    static constexpr int QKW = QK16 ? HGS / 16 : HGS / 32;  // QK waves
+    static constexpr int THREADS = 64 * (QKW + 4);          // + 4 PV waves
 };
 
-template <int DR, bool GATHER, bool PACKED, int HGS>
-__global__ void __launch_bounds__(WsShape<HGS>::THREADS, 1) mla_decode_ws(DecodeParams p) {
+template <int DR, bool GATHER, bool PACKED, int HGS, bool QK16>
+__global__ void __launch_bounds__((WsShape<HGS, QK16>::THREADS), 1) mla_decode_ws(DecodeParams p) {
     using G = Geo<DR>;
-    constexpr int QKW = WsShape<HGS>::QKW;
-    constexpr int NT = WsShape<HGS>::THREADS;
+    constexpr int QKW = WsShape<HGS, QK16>::QKW;
+    constexpr int NT = WsShape<HGS, QK16>::THREADS;
     constexpr int HT = HGS / 16;  // 16-head tiles of a PV wave
     __shared__ __attribute__((aligned(1024))) char cbuf[NBUF * G::BUF];
     __shared__ __attribute__((aligned(16))) char pbuf[2][HGS * PSTR];
@@ -504,6 +506,128 @@ __global__ void __launch_bounds__(WsShape<HGS>::THREADS, 1) mla_decode_ws(Decode
     const int srow = R * esz + 16;
 
     if (is_qk) {
+        if constexpr (QK16) {
+        // ---------------------------------------------------------- QK role, 16 heads
+        // B operand of 16x16x32: head 16qw + l%16, k = 32ks + 8(l/16)..+7
+        const int hq = 16 * qw + (l & 15);  // this lane's head within the group
+        const int kg = l >> 4;              // k group; output row group
+        bf16x8 qreg[G::KS];
+        lds_barrier();  // Q staged
+        {
+            const char* qrow = cbuf + 2 * G::BUF + hq * G::ROWB;
+#pragma unroll
+            for (int ks = 0; ks < G::KS; ++ks) qreg[ks] = *(const bf16x8*)(qrow + 16 * ((4 * ks + kg) ^ (hq & 7)));
+        }
+        lds_barrier();  // Q in registers: buffers 2-3 free again
+        // A operand of row tile rt: key row ksig(16rt + l%16) of the
+        // sub-chunk, chunk 4ks + kg; with the row swizzle, latent chunk
+        // 16v + 4u + kg sits at 256v + qo[rt][u], rope k-steps at ro[rt][.]
+        int qo[2][4], ro[2][2];
+#pragma unroll
+        for (int rt = 0; rt < 2; ++rt) {
+            const int ar = ksig(16 * rt + (l & 15));
+#pragma unroll
+            for (int u = 0; u < 4; ++u) qo[rt][u] = ar * G::ROWB + 16 * ((4 * u + kg) ^ (ar & 15));
+#pragma unroll
+            for (int u = 0; u < 2; ++u) ro[rt][u] = ar * G::ROWB + 1024 + 16 * ((4 * u + kg) ^ (ar & 7));
+        }
+        auto qk_a = [&](const char* cur, int ks, int rt) -> bf16x8 {
+            return ks < 16 ? *(const bf16x8*)(cur + qo[rt][ks & 3] + 256 * (ks >> 2))
+                           : *(const bf16x8*)(cur + ro[rt][ks - 16]);
+        };
+        float m_run = NEG_INF;  // reference max (base 2) of this lane's head
+        float l_run = 0.f;      // this lane's share of that head's sum
+        lds_barrier();  // sub-chunk 0 landed
+#pragma unroll 1
+        for (int s = 0; s <= nsub; ++s) {
+            if (s < nsub) {
+                const char* cur = cbuf + (s & (NBUF - 1)) * G::BUF;
+                const int par = s & 1;
+                // KS k-steps x 2 row tiles in operand groups of 4 (two k-steps
+                // x both tiles), double-buffered, on four accumulator chains
+                // (tile x k-step parity); the fences keep the scheduler from
+                // hoisting every LDS read
+                constexpr int NG = G::KS / 2;
+                f32x4 sacc[2][2] = {{f32x4{}, f32x4{}}, {f32x4{}, f32x4{}}};
+                bf16x8 ga[2][4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) ga[0][e] = qk_a(cur, e >> 1, e & 1);
+#pragma unroll
+                for (int g = 0; g < NG; ++g) {
+                    if (g + 1 < NG) {
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) ga[(g + 1) & 1][e] = qk_a(cur, 2 * (g + 1) + (e >> 1), e & 1);
+                    }
+                    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const int k = 2 * g + (e >> 1), rt = e & 1;
+                        sacc[rt][k & 1] = mfma16(ga[g & 1][e], qreg[k], sacc[rt][k & 1]);
+                    }
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+                // S^T: tile rt, acc j -> k position 16rt + 4kg + j, key row
+                // ksig of it, head hq
+                float sv[8];
+                const int rbase = row_begin + s * ROWS;
+#pragma unroll
+                for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) sv[4 * rt + j] = (sacc[rt][0][j] + sacc[rt][1][j]) * scale2;
+                // branch-free: the index entry is read whatever the row (a
+                // split's sub-chunks stay inside idx_s) and the tests combine
+                // as plain values, with no short-circuit control flow
+                if (__builtin_amdgcn_readfirstlane(GATHER || rbase + ROWS > row_end)) {
+#pragma unroll
+                    for (int i = 0; i < 8; ++i) {
+                        const int r = rbase + ksig(16 * (i >> 2) + 4 * kg + (i & 3));
+                        const int v = GATHER ? idx_s[r - row_begin] : 0;
+                        const bool ok = (r < row_end) & (v >= 0);
+                        sv[i] = ok ? sv[i] : NEG_INF;
+                    }
+                }
+                float cm = fmaxf(fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3])),
+                                 fmaxf(fmaxf(sv[4], sv[5]), fmaxf(sv[6], sv[7])));
+                cm = xor32_max(xor16_max(cm));
+                // reference max raised only when a score passes it by TAU, so
+                // O is rarely rescaled; P <= 2^TAU
+                const bool raise = cm > m_run + TAU;  // false while cm is -inf
+                const float m_new = raise ? cm : m_run;
+                const float alpha = raise ? exp2f(m_run - m_new) : 1.f;
+                m_run = m_new;
+                // while every row so far is masked, m is -inf and so is every
+                // score: a finite reference keeps exp2 at 0 (not -inf - -inf)
+                const float m_ref = m_new == NEG_INF ? 0.f : m_new;
+                float ls = 0.f;
+#pragma unroll
+                for (int rt = 0; rt < 2; ++rt) {
+                    float pv[4];
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) pv[e] = __builtin_amdgcn_exp2f(sv[4 * rt + e] - m_ref);
+                    ls += (pv[0] + pv[1]) + (pv[2] + pv[3]);
+                    typedef __bf16 bf16x2v __attribute__((ext_vector_type(2)));
+                    const bf16x2v lo = {(__bf16)pv[0], (__bf16)pv[1]};
+                    const bf16x2v hi = {(__bf16)pv[2], (__bf16)pv[3]};
+                    *(u32x2*)(pbuf[par] + hq * PSTR + 2 * (16 * rt + 4 * kg)) =
+                        u32x2{__builtin_bit_cast(uint32_t, lo), __builtin_bit_cast(uint32_t, hi)};
+                }
+                l_run = l_run * alpha + ls;
+                if (kg == 0) alpha_s[par][hq] = alpha;
+                const bool any = __builtin_amdgcn_ballot_w64(raise) != 0;
+                if (l == 0) flag_s[par][qw] = any;
+            }
+            lds_barrier();  // end of phase s
+        }
+        l_run = xor32_sum(xor16_sum(l_run));
+        if (kg == 0) {
+            l_s[hq] = l_run;
+            const int64_t r = part_rec(p, b, hg * HGS + hq, split);
+            p.ws_ml[r * 2 + 0] = m_run;
+            p.ws_ml[r * 2 + 1] = l_run;
+        }
+        lds_barrier();  // l_s ready
+        lds_barrier();  // staging written
+        } else {
         // ---------------------------------------------------------- QK role
         // B operand of 32x32x16: head 32qw + l%32, k = 16ks + 8(l/32)..+7
         const int hq = 32 * qw + (l & 31);  // this lane's head within the group
@@ -575,9 +699,9 @@ __global__ void __launch_bounds__(WsShape<HGS>::THREADS, 1) mla_decode_ws(Decode
 #pragma unroll
                     for (int i = 0; i < 16; ++i) {
                         const int r = rbase + ksig(8 * (i >> 2) + 4 * kh + (i & 3));
-                        bool ok = r < row_end;
-                        if (GATHER) ok = ok && idx_s[r - row_begin] >= 0;
-                        if (!ok) sv[i] = NEG_INF;
+                        const int v = GATHER ? idx_s[r - row_begin] : 0;  // inside idx_s for every sub-chunk row
+                        const bool ok = (r < row_end) & (v >= 0);
+                        sv[i] = ok ? sv[i] : NEG_INF;
                     }
                 }
                 float cm = sv[0];
@@ -622,6 +746,7 @@ __global__ void __launch_bounds__(WsShape<HGS>::THREADS, 1) mla_decode_ws(Decode
         }
         lds_barrier();  // l_s ready
         lds_barrier();  // staging written
+        }
     } else {
         // ---------------------------------------------------------- PV role
         int dma_row[G::NLD], dma_c16[G::NLD];
@@ -940,9 +1065,11 @@ __global__ void __launch_bounds__(COMBINE_THREADS) mla_combine(CombineParams p) 
 template <int DR, bool GATHER, bool PACKED>
 hipError_t launch_ws(const DecodeParams& p, int grid, hipStream_t st) {
     if (p.hg_size == 64)
-        hipLaunchKernelGGL((mla_decode_ws<DR, GATHER, PACKED, 64>), dim3(grid), dim3(WsShape<64>::THREADS), 0, st, p);
+        hipLaunchKernelGGL((mla_decode_ws<DR, GATHER, PACKED, 64, true>), dim3(grid), dim3(WsShape<64, true>::THREADS), 0,
+                           st, p);
     else
-        hipLaunchKernelGGL((mla_decode_ws<DR, GATHER, PACKED, 32>), dim3(grid), dim3(WsShape<32>::THREADS), 0, st, p);
+        hipLaunchKernelGGL((mla_decode_ws<DR, GATHER, PACKED, 32, false>), dim3(grid), dim3(WsShape<32, false>::THREADS),
+                           0, st, p);
     return hipGetLastError();
 }
 
