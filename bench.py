@@ -50,7 +50,7 @@ def split_kernel_bytes():
 # FETCH_SIZE x 2.0 + WRITE_SIZE x 1.0 (factors from a streaming kernel of
 # known size), measured with rocprofv3 --pmc; profiles/mla_decode_hbm_counters.md
 # holds the passes.  Of it, 16,777,216 B are the bf16 split partials written.
-SPLIT_TRAFFIC_BYTES = 56499721
+SPLIT_TRAFFIC_BYTES = 56488746
 
 
 def sparse_bytes(B=4, K=2048):
