@@ -90,6 +90,12 @@ DecodePlan plan_decode(const mr_mla_decode_args* a) {
     splits = std::min(splits, max_splits);
     int rps = (rows + splits - 1) / splits;
     rps = std::max(64, (rps + 63) / 64 * 64);
+    // gathered rows: a split of 64 rows writes as many partial bytes as it
+    // reads rows, so take at least 128 while the grid keeps half the CUs busy
+    // (measured at B=4, H=128, K=2048: 22.1 us per layer against 23.7 at 64)
+    if (a->indices && a->num_splits <= 0 && rps < 128 &&
+        int64_t(a->batch) * pl.head_groups * ((rows + 127) / 128) >= cu_count() / 2)
+        rps = 128;
     if (a->indices && rps > mr::MAX_GATHER_ROWS) rps = mr::MAX_GATHER_ROWS;
     splits = std::max(1, (rows + rps - 1) / rps);
     if (splits > mr::MAX_COMBINE_SPLITS) {  // very long contexts: fewer, longer splits
