@@ -67,12 +67,14 @@ mr::AffineGemvParams gemv_params(const mr_affine_weight* w);
 // The block's key path (kv_a projection, cache append) does not depend on
 // its query path until the attention: it runs on a side stream of the
 // device, forked from and joined back to the caller's stream by events.
-// One side stream per device for the process; calls that share it are
-// ordered on it, and every join waits for the caller's own fork point or
-// later, so sharing stays correct.
+// One side stream per device for the process, with one fork and one join
+// event.  A call holds `mu` from its fork record to its wait on the join, so
+// calls from several host threads cannot pick up each other's fork point;
+// calls that share the stream are ordered on it.
 struct SideStream {
     hipStream_t s = nullptr;
     hipEvent_t fork = nullptr, join = nullptr;
+    std::mutex mu;
 };
 
 mr_status side_stream(SideStream** out) {
@@ -489,6 +491,7 @@ mr_status mr_mla_decode_block(const mr_mla_block_args* a, void* stream) {
     // `position` (norm + rope); the attention below joins it
     SideStream* side = nullptr;
     if ((st = side_stream(&side)) != MR_OK) return st;
+    std::unique_lock<std::mutex> side_lock(side->mu);  // released after the join is waited on
     hipError_t he;
     if ((he = hipEventRecord(side->fork, (hipStream_t)stream)) != hipSuccess ||
         (he = hipStreamWaitEvent(side->s, side->fork, 0)) != hipSuccess)
@@ -516,6 +519,7 @@ mr_status mr_mla_decode_block(const mr_mla_block_args* a, void* stream) {
     // attend once the key path has written the cache row
     if ((he = hipStreamWaitEvent((hipStream_t)stream, side->join, 0)) != hipSuccess)
         return hip_fail(he, "mla block: join");
+    side_lock.unlock();
     mr_mla_decode_args d = L.dec_args;
     d.q_lat = q_lat;
     d.q_rope = q + a->qk_nope_dim;

@@ -241,3 +241,48 @@ def test_block_small_context_and_first_token(M):
         out, _ = run_block(M, d)
         ref, _ = MI.block_reference(d)
         check_block(f32(out), ref, f"block-ctx{ctx}")
+
+
+def test_block_two_host_threads(M):
+    # two host threads, two streams, one device: each call's key path (on the
+    # library's shared side stream) must wait for its own caller's stream, so
+    # every result equals the single-thread one bit for bit
+    print("block from two host threads at once", flush=True)
+    import threading
+
+    import torch
+
+    ds = [MI.block_inputs(ctx=c, tag=f"thr{c}", centred=True) for c in (71, 40)]
+    refs = [bits16(run_block(M, d)[0]) for d in ds]
+    prep = []
+    for d in ds:
+        w = {k: dev(d[k]) for k in ("input_norm", "q_a_norm", "kv_a_norm")}
+        for k in ("q_a", "q_b", "kv_a", "kv_b", "o_proj"):
+            w[k] = weights(M, d[k])
+        c, s = M.rope_table([d["position"]], M.rope_frequencies(64))
+        prep.append((dev(d["x"]), w, torch.from_numpy(c).cuda(), torch.from_numpy(s).cuda()))
+    sync()
+    outs = [[], []]
+    errors = []
+
+    def work(i):
+        try:
+            st = torch.cuda.Stream()
+            x, w, c, s = prep[i]
+            with torch.cuda.stream(st):
+                for _ in range(6):
+                    cache = torch.from_numpy(np.ascontiguousarray(ds[i]["cache"])).view(torch.bfloat16).to("cuda")
+                    outs[i].append(M.mla_decode_block(x, w, cache, ds[i]["position"], c, s, stream=st))
+            st.synchronize()
+        except Exception as e:  # surfaced below
+            errors.append(e)
+
+    th = [threading.Thread(target=work, args=(i,)) for i in range(2)]
+    for t in th:
+        t.start()
+    for t in th:
+        t.join()
+    assert not errors, errors
+    for i in range(2):
+        for o in outs[i]:
+            np.testing.assert_array_equal(bits16(o), refs[i])
