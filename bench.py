@@ -296,6 +296,35 @@ def time_sparse(torch, M, steps, warmup):
             "split_kernel_ms": time_split_only(torch, M, args, steps)}
 
 
+def mfma_probe(torch, M):
+    """On-box MFMA rate: one 256-thread workgroup per CU, each wave 8
+    independent 32x32x16 bf16 MFMA chains for 4000 rounds, no memory traffic
+    in the loop.  Returns the dense bf16 rate and the shader clock it ran at
+    (s_memtime cycles over 100 MHz wall-clock ticks, mean over workgroups)."""
+    import ctypes as C
+
+    lib = C.CDLL(M.SELFTEST_PATH)
+    lib.mr_selftest_mfma_rate.argtypes = [C.c_int, C.c_int, C.c_void_p, C.c_void_p, C.c_void_p]
+    blocks, iters = 256, 4000
+    sink = torch.empty(blocks * 256, dtype=torch.float32, device="cuda")
+    stamps = torch.zeros(2 * blocks, dtype=torch.int64, device="cuda")
+    sp = M._stream(torch.cuda.current_stream())
+    for _ in range(2):
+        assert lib.mr_selftest_mfma_rate(blocks, iters, sink.data_ptr(), stamps.data_ptr(), sp) == 0
+    torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record()
+    assert lib.mr_selftest_mfma_rate(blocks, iters, sink.data_ptr(), stamps.data_ptr(), sp) == 0
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1)
+    flop = blocks * 4 * iters * 8 * 2 * 32 * 32 * 16
+    st = stamps.view(blocks, 2).double().cpu()
+    clock_ghz = float(st[:, 0].mean() / (st[:, 1].mean() * 10.0))
+    return {"tflops": round(flop / (ms * 1e-3) / 1e12, 1), "clock_ghz": round(clock_ghz, 3)}
+
+
 def cpu_baseline(budget_s=12.0):
     """The oracle (scalar C, OpenMP over heads) on the same workload, timed on
     this host's cores; a bounded sample: whole config-2 decode calls until the
@@ -362,6 +391,8 @@ def main():
     log("bench: causal prefill T=4096 H=128")
     pf = time_prefill(torch, M, max(args.steps // 20, 5), 3)
     log(f"bench: prefill {pf}")
+    mp = mfma_probe(torch, M)
+    log(f"bench: mfma probe {mp}")
 
     layer_us = d["wall_ms"] * 1e3
     split_s = d["split_kernel_ms"] * 1e-3
@@ -396,6 +427,8 @@ def main():
         "prefill_upproj_us": round(pf["upproj_ms"] * 1e3, 2),
         "prefill_attn_us": round(pf["attn_ms"] * 1e3, 2),
         "prefill_attn_mfma_fraction": round(ATTN_FLOP / (pf["attn_ms"] * 1e-3) / 1e12 / MFMA_PEAK_TFLOPS, 4),
+        "mfma_probe_tflops": mp["tflops"],
+        "mfma_probe_clock_ghz": mp["clock_ghz"],
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": SPLIT_TRAFFIC_BYTES,
                      "kernel": "mla_decode_ws", "algorithmic_bytes": split_kernel_bytes()},

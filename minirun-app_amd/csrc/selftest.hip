@@ -75,6 +75,39 @@ __global__ void __launch_bounds__(64) k_permlane16(const uint32_t* in, uint32_t*
     out[2 * l + 1] = r[1];
 }
 
+
+// MFMA rate probe: every wave runs `iters` rounds of 8 independent 32x32x16
+// bf16 MFMA chains (no memory traffic in the loop).  Thread 0 of each
+// workgroup writes the loop's shader cycles (s_memtime) and 100 MHz wall
+// ticks to stamps[2 block], [2 block + 1]; every thread writes one value of
+// its accumulators to sink[global thread] so the chains stay live.
+__global__ void __launch_bounds__(256) k_mfma_rate(int iters, float* sink, uint64_t* stamps) {
+    const int t = threadIdx.x;
+    bf16x8 a, b;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        a[j] = (__bf16)(0.0009765625f * (float)((t + j) & 7));
+        b[j] = (__bf16)(0.0009765625f * (float)((t * 3 + j) & 7));
+    }
+    f32x16 acc[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) acc[k] = f32x16{};
+    const uint64_t c0 = clock64(), w0 = wall_clock64();
+    for (int i = 0; i < iters; ++i) {
+#pragma unroll
+        for (int k = 0; k < 8; ++k) acc[k] = mfma32(a, b, acc[k]);
+    }
+    const uint64_t c1 = clock64(), w1 = wall_clock64();
+    float v = 0.f;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) v += acc[k][t & 15];
+    sink[(int64_t)blockIdx.x * 256 + t] = v;
+    if (t == 0) {
+        stamps[2 * blockIdx.x] = c1 - c0;
+        stamps[2 * blockIdx.x + 1] = w1 - w0;
+    }
+}
+
 extern "C" {
 int mr_selftest_mfma16(const void* A, const void* B, void* D, void* stream) {
     hipLaunchKernelGGL(k_mfma16, dim3(1), dim3(64), 0, (hipStream_t)stream, (const uint16_t*)A,
@@ -101,6 +134,13 @@ int mr_selftest_tr16(const int32_t* host_offsets, const void* d_offsets, void* d
         if (host_offsets[i] < 0 || host_offsets[i] > 4096 - 8 || (host_offsets[i] % 8) != 0) return 1;
     hipLaunchKernelGGL(k_tr16, dim3(1), dim3(64), 0, (hipStream_t)stream, (const int32_t*)d_offsets,
                        (uint16_t*)d_out);
+    return hipGetLastError() == hipSuccess ? 0 : 6;
+}
+// sink: blocks * 256 floats, stamps: 2 * blocks uint64 (device)
+int mr_selftest_mfma_rate(int blocks, int iters, void* sink, void* stamps, void* stream) {
+    if (blocks <= 0 || iters <= 0) return 1;
+    hipLaunchKernelGGL(k_mfma_rate, dim3(blocks), dim3(256), 0, (hipStream_t)stream, iters, (float*)sink,
+                       (uint64_t*)stamps);
     return hipGetLastError() == hipSuccess ? 0 : 6;
 }
 }

@@ -119,3 +119,22 @@ def test_permlane16_swap_pairs(st):
     lo = np.where((lanes // 16) % 2 == 0, lanes, lanes - 16)
     np.testing.assert_array_equal(r[:, 0], v[lo])
     np.testing.assert_array_equal(r[:, 1], v[lo + 16])
+
+
+def test_mfma_rate_probe_runs():
+    # the bench's on-box MFMA rate probe: plausible rate and clock (wide
+    # bounds: a sanity check of the probe, not a performance gate)
+    print("selftest mfma rate probe", flush=True)
+    import os
+
+    import torch
+
+    import minirun_hip as M
+
+    sys.path.insert(0, os.path.dirname(os.path.dirname(os.path.abspath(__file__))))
+    import bench
+
+    r = bench.mfma_probe(torch, M)
+    print(r, flush=True)
+    assert 100.0 < r["tflops"] < 5000.0, r
+    assert 0.5 < r["clock_ghz"] < 3.5, r
