@@ -106,19 +106,21 @@ __global__ void __launch_bounds__(NT) topk_select_kernel(TopkParams p) {
         const uint32_t fixed = top >= 32 ? 0u : (0xffffffffu << top);  // no shift by 32
         for (int i = tid; i < TK_BINS; i += NT) hist[i] = 0;
         __syncthreads();
+        if (pass == 0) {
+            // every key counts: no branch, padding keys add 0
 #pragma unroll
-        for (int j = 0; j < KPT; ++j) {
-            const uint32_t key = (uint32_t)(NT * j + tid);
-            bool match;
-            uint32_t bin;
-            if (on_img) {
-                match = ((img[j] ^ dimg) & fixed) == 0u;
-                bin = (img[j] >> sh) & ((1u << wd) - 1u);
-            } else {
-                match = img[j] == dimg && ((key ^ dkey) & fixed) == 0u;
-                bin = (key >> sh) & ((1u << wd) - 1u);
+            for (int j = 0; j < KPT; ++j) atomicAdd(&hist[img[j] >> 21], valid(j) ? 1u : 0u);
+        } else if (on_img) {
+#pragma unroll
+            for (int j = 0; j < KPT; ++j)
+                if (valid(j) && ((img[j] ^ dimg) & fixed) == 0u) atomicAdd(&hist[(img[j] >> sh) & ((1u << wd) - 1u)], 1u);
+        } else {
+#pragma unroll
+            for (int j = 0; j < KPT; ++j) {
+                const uint32_t key = (uint32_t)(NT * j + tid);
+                if (valid(j) && img[j] == dimg && ((key ^ dkey) & fixed) == 0u)
+                    atomicAdd(&hist[(key >> sh) & ((1u << wd) - 1u)], 1u);
             }
-            if (valid(j) && match) atomicAdd(&hist[bin], 1u);
         }
         __syncthreads();
         uint32_t h[BPT], sum = 0;
