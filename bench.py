@@ -296,6 +296,40 @@ def time_sparse(torch, M, steps, warmup):
             "split_kernel_ms": time_split_only(torch, M, args, steps)}
 
 
+def time_topk(torch, M, steps=200):
+    """Lightning-indexer selection of one decode token: 2048 of 32768
+    compressed keys (position 131071, ratio 4), scores ~N(0,1) f32; average
+    of `steps` launches between two events (no NaN check, no sync)."""
+    import ctypes as C
+
+    lib = M.load()
+    rows, cols, k, ratio, start = 1, 32768, 2048, 4, 131071
+    g = torch.Generator(device="cuda")
+    g.manual_seed(0x4D4C410004)
+    scores = torch.randn(rows, cols, generator=g, device="cuda")
+    sel = M.topk_geometry(rows, cols, k, ratio, start, 0)
+    out = torch.empty(rows, sel, dtype=torch.int32, device="cuda")
+    ws = torch.empty(max(lib.mr_topk_workspace_size(rows), 1), dtype=torch.uint8, device="cuda")
+    a = M.TopkArgs()
+    a.scores, a.score_row_stride, a.rows, a.cols = scores.data_ptr(), scores.stride(0), rows, cols
+    a.top_k, a.ratio, a.start_pos, a.offset = k, ratio, start, 0
+    a.out, a.out_row_stride = out.data_ptr(), out.stride(0)
+    a.status, a.flags = None, 0
+    a.workspace, a.workspace_bytes = ws.data_ptr(), ws.numel()
+    sp = M._stream(torch.cuda.current_stream())
+    for _ in range(20):
+        M._check(lib.mr_topk_select(C.byref(a), sp))
+    torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(steps):
+        M._check(lib.mr_topk_select(C.byref(a), sp))
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / steps
+
+
 def mfma_probe(torch, M):
     """On-box MFMA rate: one 256-thread workgroup per CU, each wave 8
     independent 32x32x16 bf16 MFMA chains for 4000 rounds, no memory traffic
@@ -391,6 +425,8 @@ def main():
     log("bench: causal prefill T=4096 H=128")
     pf = time_prefill(torch, M, max(args.steps // 20, 5), 3)
     log(f"bench: prefill {pf}")
+    tk_ms = time_topk(torch, M)
+    log(f"bench: top-k 2048 of 32768 {tk_ms * 1e3:.2f} us")
     mp = mfma_probe(torch, M)
     log(f"bench: mfma probe {mp}")
 
@@ -427,6 +463,7 @@ def main():
         "prefill_upproj_us": round(pf["upproj_ms"] * 1e3, 2),
         "prefill_attn_us": round(pf["attn_ms"] * 1e3, 2),
         "prefill_attn_mfma_fraction": round(ATTN_FLOP / (pf["attn_ms"] * 1e-3) / 1e12 / MFMA_PEAK_TFLOPS, 4),
+        "topk_2048_of_32768_us": round(tk_ms * 1e3, 2),
         "mfma_probe_tflops": mp["tflops"],
         "mfma_probe_clock_ghz": mp["clock_ghz"],
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
