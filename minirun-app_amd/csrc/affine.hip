@@ -13,6 +13,7 @@
 // (x_j, x_j+4) staged in LDS in that order; the 128 * sum(x) offset is folded
 // into the bias term.  Products are exact in fp32, accumulation is fp32.
 #include <algorithm>
+#include <type_traits>
 
 #include "mr_kernels.hpp"
 
@@ -76,15 +77,21 @@ __global__ void __launch_bounds__(256) affine_dequant_kernel(AffineDequantParams
 // With norm_w set, the staged vector is bf16(w * (x * rsqrt(mean(x^2) +
 // eps))), the RMSNorm stage's output.  tpr threads (a power of two <= 64)
 // share an output row, each dotting groups lane, lane + tpr, ...; a step of
-// the 256-thread workgroup covers 256 / tpr rows and two steps are in flight.
+// the 256-thread workgroup covers 256 / tpr rows, and while one step is
+// dotted the next two steps' weights are in flight.  Every load goes through
+// a buffer descriptor, so rows past the tile and groups past the row take an
+// out-of-buffer offset: they read zeros without a memory request or a branch.
 constexpr int GEMV_THREADS = 256;
 constexpr int GEMV_MAX_IN = 16384;  // activation length staged per vector
 constexpr int GEMV_MAX_CH = GEMV_MAX_IN / 8 / GEMV_THREADS;
 constexpr int GEMV_NPT_MAX = 4;  // groups per thread and row: tpr * GEMV_NPT >= G
 
 template <int SDT, int GEMV_NPT>
-__global__ void __launch_bounds__(GEMV_THREADS) affine_gemv4_kernel(AffineGemvParams p) {
-    __shared__ __attribute__((aligned(16))) uint32_t xp[GEMV_MAX_IN / 2];  // (x_j, x_j+4) pairs
+__global__ void __launch_bounds__(GEMV_THREADS) affine_gemv4_kernel(AffineGemvParams p, uint32_t wbytes, uint32_t sbytes) {
+    // (x_j, x_j+4) pairs, 16 bytes per packed word; a group's 128 bytes are
+    // followed by 16 bytes of padding, so lanes reading consecutive groups
+    // start on different banks
+    __shared__ __attribute__((aligned(16))) uint32_t xp[GEMV_MAX_IN / 2 + GEMV_MAX_IN / 16];
     __shared__ float xs[GEMV_MAX_IN / 64];                              // per-group sums of the staged x
     __shared__ float red[GEMV_THREADS / 64];
     const int tile = blockIdx.x;
@@ -97,65 +104,105 @@ __global__ void __launch_bounds__(GEMV_THREADS) affine_gemv4_kernel(AffineGemvPa
     const int t = threadIdx.x;
     const uint16_t* x = (const uint16_t*)p.x + (int64_t)xg * p.x_stride;
 
-    // rows: tpr threads per row, two steps of 256 / tpr rows per iteration; a
-    // thread dots at most GEMV_NPT groups of a row (tpr * GEMV_NPT >= G)
+    // rows: tpr threads per row, steps of 256 / tpr rows; a thread dots at
+    // most GEMV_NPT groups of a row (tpr * GEMV_NPT >= G)
     const int tpr = p.tpr;
     const int rps = GEMV_THREADS / tpr;
     const int tr = t / tpr, tl = t - tr * tpr;
     typedef __bf16 bf16x2v __attribute__((ext_vector_type(2)));
+    // weight, scale and bias rows through buffer descriptors: 32-bit offsets,
+    // and a load whose offset is past the buffer returns 0 without a memory
+    // request (rows past the tile and groups past the row point there)
+    const __amdgpu_buffer_rsrc_t wres = __builtin_amdgcn_make_buffer_rsrc((void*)p.packed, 0, (int)wbytes, 0x00020000);
+    const __amdgpu_buffer_rsrc_t sres = __builtin_amdgcn_make_buffer_rsrc((void*)p.scales, 0, (int)sbytes, 0x00020000);
+    const __amdgpu_buffer_rsrc_t bres = __builtin_amdgcn_make_buffer_rsrc((void*)p.biases, 0, (int)sbytes, 0x00020000);
+    constexpr uint32_t SB = SDT == 2 ? 4 : 2;
+    constexpr uint32_t OOB = 0x80000000u;
+    // a tile stays inside one activation vector, so output row j reads weight
+    // row wbase + j
+    const int wbase = (int)(xg * p.map_b + p.map_c) - xg * p.map_a;
+    typedef typename std::conditional<SB == 2, uint16_t, uint32_t>::type SRaw;
     struct RowLoads {
         u32x4 w[GEMV_NPT][2];
-        float s[GEMV_NPT], b[GEMV_NPT];
+        SRaw s[GEMV_NPT], b[GEMV_NPT];  // raw scale / bias words, converted at use
         uint32_t ok;  // bit q: group q of this thread is a real (row, group)
     };
-    // loads without branches (clamped to a real row and group, masked at
-    // use), so none of them waits before the dot products
+    // byte offsets of this thread's groups inside a weight row / scale row
+    uint32_t woq[GEMV_NPT], soq[GEMV_NPT];
+    bool gq[GEMV_NPT];
+#pragma unroll
+    for (int q = 0; q < GEMV_NPT; ++q) {
+        const int g = tl + tpr * q;
+        gq[q] = g < G;
+        woq[q] = 32u * (uint32_t)g;
+        soq[q] = SB * (uint32_t)g;
+    }
+    const uint32_t wrow_bytes = (uint32_t)(in / 2), srow_bytes = (uint32_t)G * SB;
     auto load_row = [&](int j, RowLoads& L) {
         const bool rok = j < r_end;
-        const int jj = rok ? j : r0;
-        const int64_t wr = (int64_t)(jj / p.map_a) * p.map_b + p.map_c + (jj % p.map_a);
-        const uint32_t* wrow = p.packed + wr * (int64_t)(in / 8);
+        const uint32_t wr = (uint32_t)(wbase + j);  // < 2^24 (host check)
+        const uint32_t wrow = __umul24(wr, wrow_bytes), srow = __umul24(wr, srow_bytes);
         L.ok = 0;
 #pragma unroll
         for (int q = 0; q < GEMV_NPT; ++q) {
-            const int g = tl + tpr * q;
-            const int gg = min(g, G - 1);
-            L.ok |= (rok && g < G) ? (1u << q) : 0u;
-            L.w[q][0] = *((const u32x4*)(wrow + 8 * gg));
-            L.w[q][1] = *((const u32x4*)(wrow + 8 * gg) + 1);
-            L.s[q] = load_scale<SDT>(p.scales, wr * G + gg);
-            L.b[q] = load_scale<SDT>(p.biases, wr * G + gg);
+            const bool ok = rok && gq[q];
+            L.ok |= ok ? (1u << q) : 0u;
+            const uint32_t wo = ok ? wrow + woq[q] : OOB;
+            const uint32_t so = ok ? srow + soq[q] : OOB;
+            L.w[q][0] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(wres, wo, 0, 0));
+            L.w[q][1] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(wres, wo + 16, 0, 0));
+            if (SB == 2) {
+                L.s[q] = __builtin_amdgcn_raw_buffer_load_b16(sres, so, 0, 0);
+                L.b[q] = __builtin_amdgcn_raw_buffer_load_b16(bres, so, 0, 0);
+            } else {
+                L.s[q] = __builtin_amdgcn_raw_buffer_load_b32(sres, so, 0, 0);
+                L.b[q] = __builtin_amdgcn_raw_buffer_load_b32(bres, so, 0, 0);
+            }
         }
+    };
+    auto cvt = [&](SRaw raw) -> float {
+        if (SDT == 0) return __uint_as_float((uint32_t)raw << 16);
+        if (SDT == 1) return f16_bits_to_f32((uint16_t)raw);
+        return __uint_as_float(raw);
     };
     // the first iteration's weights go out before x is staged: they do not
     // depend on it
-    RowLoads la, lb;
-    load_row(r0 + tr, la);
-    load_row(r0 + rps + tr, lb);
 
     // ---- stage the activation vector (and the norm weights beside it)
     // every thread loads GEMV_MAX_CH chunks, clamped to the last real one
     // (no branch, so the loads overlap); chunks k >= nch are zeroed at use
+    // chunk k of x (and of the norm weights) through buffer descriptors; a
+    // chunk past the vector has an out-of-buffer offset and loads as zeros
+    // with no memory request, so no select waits on the loads
+    const __amdgpu_buffer_rsrc_t xres = __builtin_amdgcn_make_buffer_rsrc((void*)x, 0, in * 2, 0x00020000);
     u32x4 xc[GEMV_MAX_CH];
 #pragma unroll
-    for (int c = 0; c < GEMV_MAX_CH; ++c) xc[c] = *(const u32x4*)(x + 8 * min(t + GEMV_THREADS * c, nch - 1));
-#pragma unroll
-    for (int c = 0; c < GEMV_MAX_CH; ++c)
-        if (t + GEMV_THREADS * c >= nch) xc[c] = u32x4{0u, 0u, 0u, 0u};
+    for (int c = 0; c < GEMV_MAX_CH; ++c) {
+        const int k = t + GEMV_THREADS * c;
+        xc[c] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(xres, k < nch ? 16u * k : OOB, 0, 0));
+    }
     // norm weights of the same chunks (bf16: one 16-byte load, f32: two)
     u32x4 wn[GEMV_MAX_CH][2];
     if (p.norm_w) {
+        const __amdgpu_buffer_rsrc_t nres =
+            __builtin_amdgcn_make_buffer_rsrc((void*)p.norm_w, 0, in * (p.norm_w_f32 ? 4 : 2), 0x00020000);
 #pragma unroll
         for (int c = 0; c < GEMV_MAX_CH; ++c) {
-            const int k = min(t + GEMV_THREADS * c, nch - 1);
+            const int k = t + GEMV_THREADS * c;
             if (p.norm_w_f32) {
-                wn[c][0] = *((const u32x4*)p.norm_w + 2 * k);
-                wn[c][1] = *((const u32x4*)p.norm_w + 2 * k + 1);
+                const uint32_t o = k < nch ? 32u * k : OOB;
+                wn[c][0] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(nres, o, 0, 0));
+                wn[c][1] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(nres, o + 16, 0, 0));
             } else {
-                wn[c][0] = *((const u32x4*)p.norm_w + k);
+                wn[c][0] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(nres, k < nch ? 16u * k : OOB, 0, 0));
             }
         }
     }
+    // the first two row steps' weights go out behind x: a wait for x does
+    // not wait for them
+    RowLoads l0, l1, l2;
+    load_row(r0 + tr, l0);
+    load_row(r0 + rps + tr, l1);
     float inv = 1.f;
     if (p.norm_w) {
         float ss = 0.f;
@@ -205,43 +252,55 @@ __global__ void __launch_bounds__(GEMV_THREADS) affine_gemv4_kernel(AffineGemvPa
         if (k < nch) {
 #pragma unroll
             for (int j = 0; j < 4; ++j)
-                xp[4 * k + j] = (__float_as_uint(h[j]) >> 16) | (__float_as_uint(h[j + 4]) & 0xffff0000u);
+                xp[4 * (k + (k >> 3)) + j] = (__float_as_uint(h[j]) >> 16) | (__float_as_uint(h[j + 4]) & 0xffff0000u);
         }
         float cs = ((h[0] + h[1]) + (h[2] + h[3])) + ((h[4] + h[5]) + (h[6] + h[7]));
-        cs += __shfl_xor(cs, 1);
-        cs += __shfl_xor(cs, 2);
-        cs += __shfl_xor(cs, 4);
+        cs = group_sum(cs, 8);
         if ((k & 7) == 0 && k < nch) xs[k >> 3] = cs;
     }
     __syncthreads();
 
+    // and-or operands: a VOP3 takes no literal and reads one scalar at most,
+    // so the mask sits in an SGPR and the bf16 pair 128|128 in a VGPR
+    uint32_t nib_mask, bf_128;
+    asm volatile("s_mov_b32 %0, 0x000f000f" : "=s"(nib_mask));
+    asm volatile("v_mov_b32 %0, 0x43004300" : "=v"(bf_128));
     auto dot_row = [&](const RowLoads& L) {
-        float acc = 0.f;
+        float acc = 0.f, hist[GEMV_NPT + 1];
+        hist[0] = 0.f;
 #pragma unroll
         for (int q = 0; q < GEMV_NPT; ++q) {
-            const int g = min(tl + tpr * q, G - 1);
-            float d = 0.f;
+            int g = min(tl + tpr * q, G - 1);
+            // a group's x is read from LDS once the group two back is dotted:
+            // two groups of x in registers at a time, none held across rows
+            if (q >= 2) asm volatile("" : "+v"(g) : "v"(hist[q - 1]));
+            else asm volatile("" : "+v"(g));
+            float d4[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int k = 0; k < 8; ++k) {
                 const uint32_t word = k < 4 ? L.w[q][0][k] : L.w[q][1][k - 4];
-                const u32x4 xv = *(const u32x4*)(xp + 4 * (8 * g + k));
+                const u32x4 xv = *(const u32x4*)(xp + 4 * (9 * g + k));
 #pragma unroll
                 for (int jj = 0; jj < 4; ++jj) {
-                    const uint32_t pr = ((word >> (4 * jj)) & 0x000F000Fu) | 0x43004300u;
-                    const uint32_t xw = xv[jj];  // bit_cast of a vector-element lvalue reads element 0
-                    d = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2v, pr), __builtin_bit_cast(bf16x2v, xw),
-                                                       d, false);
+                    const uint32_t sh = word >> (4 * jj);
+                    uint32_t pr;
+                    asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(pr) : "v"(sh), "s"(nib_mask), "v"(bf_128));
+                    const uint32_t xw = xv[jj];
+                    d4[jj] = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2v, pr), __builtin_bit_cast(bf16x2v, xw),
+                                                            d4[jj], false);
                 }
             }
+            const float d = (d4[0] + d4[1]) + (d4[2] + d4[3]);
             // sum x (128 + q) = d  ->  sum x q = d - 128 sum x
-            const float sv = (L.ok >> q) & 1u ? L.s[q] : 0.f;
-            const float bv = (L.ok >> q) & 1u ? L.b[q] : 0.f;
+            const float sv = (L.ok >> q) & 1u ? cvt(L.s[q]) : 0.f;
+            const float bv = (L.ok >> q) & 1u ? cvt(L.b[q]) : 0.f;
             acc = fmaf(sv, d, fmaf(bv - 128.f * sv, xs[g], acc));
+            hist[q + 1] = acc;
         }
         return acc;
     };
     auto finish = [&](int j, float acc) {
-        for (int o = tpr >> 1; o >= 1; o >>= 1) acc += __shfl_xor(acc, o);
+        acc = group_sum(acc, tpr);
         if (tl == 0 && j < r_end) {
             const int64_t o = (int64_t)j * p.y_stride_row;
             if (p.y_f32)
@@ -250,24 +309,24 @@ __global__ void __launch_bounds__(GEMV_THREADS) affine_gemv4_kernel(AffineGemvPa
                 ((uint16_t*)p.y)[o] = f32_to_bf16_bits(acc);
         }
     };
-    // two register sets alternate: the next two steps' weights load (rows
-    // clamped, never branched around) while this pair is dotted, and no
-    // loaded value is copied before use
-    RowLoads ya, yb;
-    for (int rb = r0;;) {
-        load_row(rb + 2 * rps + tr, ya);
-        load_row(rb + 3 * rps + tr, yb);
-        finish(rb + tr, dot_row(la));
-        if (rb + rps < r_end) finish(rb + rps + tr, dot_row(lb));  // uniform
-        rb += 2 * rps;
-        if (rb >= r_end) break;
-        load_row(rb + 2 * rps + tr, la);
-        load_row(rb + 3 * rps + tr, lb);
-        finish(rb + tr, dot_row(ya));
-        if (rb + rps < r_end) finish(rb + rps + tr, dot_row(yb));  // uniform
-        rb += 2 * rps;
-        if (rb >= r_end) break;
+    // three register sets rotate: while one row step is dotted the next two
+    // are in flight, and no loaded value is copied before use.  Loads of
+    // steps past the tile end are out-of-buffer offsets: no memory request.
+    const int nsteps = (r_end - r0 + rps - 1) / rps;
+    int rb = r0, i = 0;
+    for (; i + 3 <= nsteps; i += 3) {
+        load_row(rb + 2 * rps + tr, l2);
+        finish(rb + tr, dot_row(l0));
+        rb += rps;
+        load_row(rb + 2 * rps + tr, l0);
+        finish(rb + tr, dot_row(l1));
+        rb += rps;
+        load_row(rb + 2 * rps + tr, l1);
+        finish(rb + tr, dot_row(l2));
+        rb += rps;
     }
+    if (i < nsteps) finish(rb + tr, dot_row(l0));
+    if (i + 1 < nsteps) finish(rb + rps + tr, dot_row(l1));
 }
 
 // ---------------------------------------------------------------- GEMV, generic
@@ -320,10 +379,23 @@ hipError_t launch_affine_dequant(const AffineDequantParams& p, hipStream_t st) {
     return hipGetLastError();
 }
 
+// Weight rows the fast path addresses: the last activation vector's rows end
+// at (nvec - 1) * map_b + map_c + (its row count).
+static int64_t gemv_weight_rows(const AffineGemvParams& p) {
+    const int64_t nvec = (p.out_rows + p.map_a - 1) / p.map_a;
+    const int64_t last_rows = std::min<int64_t>(p.map_a, p.out_rows - (nvec - 1) * p.map_a);
+    return (nvec - 1) * p.map_b + p.map_c + last_rows;
+}
+
 bool affine_gemv_fast_ok(const AffineGemvParams& p) {
     return !p.force_generic && p.bits == 4 && p.group == 64 && !p.x_f32 && p.m == 1 && p.in_features <= GEMV_MAX_IN &&
            p.in_features % 64 == 0 && ((uintptr_t)p.x & 15) == 0 && p.x_stride % 8 == 0 &&
-           p.in_features <= 64 * GEMV_NPT_MAX * 64 && (!p.norm_w || ((uintptr_t)p.norm_w & 15) == 0);
+           p.in_features <= 64 * GEMV_NPT_MAX * 64 && (!p.norm_w || ((uintptr_t)p.norm_w & 15) == 0) &&
+           // 32-bit buffer offsets (24-bit row numbers) reach every weight and
+           // scale byte, with 2^31 free above them for the out-of-buffer offset
+           gemv_weight_rows(p) < (int64_t(1) << 24) &&
+           gemv_weight_rows(p) * (p.in_features / 2) < (int64_t(1) << 31) &&
+           gemv_weight_rows(p) * (p.in_features / 64) * (p.scale_dtype == 2 ? 4 : 2) < (int64_t(1) << 31);
 }
 
 hipError_t launch_affine_gemv(const AffineGemvParams& q, hipStream_t st) {
@@ -347,7 +419,10 @@ hipError_t launch_affine_gemv(const AffineGemvParams& q, hipStream_t st) {
         p.tiles_per_vec = (per_vec + p.tile_rows - 1) / p.tile_rows;
         const unsigned grid = (unsigned)(nvec * p.tiles_per_vec);
         const int npt = (G + tpr - 1) / tpr;  // 1 .. 4
-#define MR_GEMV4(SDT, NPT) hipLaunchKernelGGL((affine_gemv4_kernel<SDT, NPT>), dim3(grid), dim3(GEMV_THREADS), 0, st, p)
+        const int64_t w_rows = gemv_weight_rows(p);
+        const uint32_t wbytes = (uint32_t)(w_rows * (p.in_features / 2));
+        const uint32_t sbytes = (uint32_t)(w_rows * G * (p.scale_dtype == 2 ? 4 : 2));
+#define MR_GEMV4(SDT, NPT) hipLaunchKernelGGL((affine_gemv4_kernel<SDT, NPT>), dim3(grid), dim3(GEMV_THREADS), 0, st, p, wbytes, sbytes)
 #define MR_GEMV4_NPT(SDT) \
     do {                     \
         if (npt == 1)        \

@@ -109,6 +109,24 @@ __device__ __forceinline__ float xor16_sum(float v) {
     return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
+// Sum of v over aligned groups of n lanes (n a power of two <= 64, uniform):
+// every lane of a group ends with the group's sum.  Butterflies run from
+// lane distance 1 upward on DPP and permlane swaps, with no LDS round trip:
+// quad_perm(1,0,3,2) (0xB1) and quad_perm(2,3,0,1) (0x4E) are xor 1 and
+// xor 2; once the steps below distance d are done, all lanes of a d-group
+// hold the same value, so row_half_mirror (0x141) and row_mirror (0x140),
+// which map every lane into the neighbouring 4- / 8-lane group, act as xor 4
+// and xor 8.
+__device__ __forceinline__ float group_sum(float v, int n) {
+    if (n > 1) v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xf, 0xf, false));
+    if (n > 2) v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4E, 0xf, 0xf, false));
+    if (n > 4) v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x141, 0xf, 0xf, false));
+    if (n > 8) v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x140, 0xf, 0xf, false));
+    if (n > 16) v = xor16_sum(v);
+    if (n > 32) v = xor32_sum(v);
+    return v;
+}
+
 // LDS-only barrier: waits for this wave's LDS traffic, not for its global
 // (DMA) loads, so prefetches stay in flight across it.
 __device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
