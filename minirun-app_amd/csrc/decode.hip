@@ -939,6 +939,16 @@ __global__ void __launch_bounds__((WsShape<HGS, QK16>::THREADS), 1) mla_decode_w
     }
 }
 
+// Full-wave max on DPP and permlane swaps, no LDS round trips (the same
+// butterfly as group_sum): every lane ends with the result.
+__device__ __forceinline__ float wave_max_dpp(float v) {
+    v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xf, 0xf, false)));
+    v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4E, 0xf, 0xf, false)));
+    v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x141, 0xf, 0xf, false)));
+    v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x140, 0xf, 0xf, false)));
+    return xor32_max(xor16_max(v));
+}
+
 // Merge the split partials.  A partial is O_s / l_s (bf16 for bf16 output,
 // f32 for f32 output) with its running max m_s and sum l_s (fp32):
 //   out = sum_s w_s (O_s / l_s) / (sum_s w_s + sink),  w_s = l_s 2^(m_s - M).
@@ -996,7 +1006,7 @@ __global__ void __launch_bounds__(COMBINE_THREADS) mla_combine(CombineParams p) 
 #pragma unroll
     for (int k = 0; k < MLK; ++k)
         if (ml_l[k] > 0.f) M = fmaxf(M, ml_m[k]);
-    M = wave_max(M);
+    M = wave_max_dpp(M);
     if (l == 0) red_m[w] = M;
     __syncthreads();
     M = fmaxf(fmaxf(red_m[0], red_m[1]), fmaxf(red_m[2], red_m[3]));
@@ -1013,7 +1023,7 @@ __global__ void __launch_bounds__(COMBINE_THREADS) mla_combine(CombineParams p) 
             L += wv;
         }
     }
-    L = wave_sum(L);
+    L = group_sum(L, 64);
     if (l == 0) red_l[w] = L;
     __syncthreads();
     L = (red_l[0] + red_l[1]) + (red_l[2] + red_l[3]);
@@ -1040,8 +1050,7 @@ __global__ void __launch_bounds__(COMBINE_THREADS) mla_combine(CombineParams p) 
     // the four splits of a wave, then the four waves
 #pragma unroll
     for (int v = 0; v < VPL; ++v) {
-        acc[v] += __shfl_xor(acc[v], 16);
-        acc[v] += __shfl_xor(acc[v], 32);
+        acc[v] = xor32_sum(xor16_sum(acc[v]));
     }
     if (sg == 0) {
 #pragma unroll
