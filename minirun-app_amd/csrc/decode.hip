@@ -376,8 +376,7 @@ __global__ void __launch_bounds__(THREADS, 1) mla_decode_split(DecodeParams p) {
     }
 
     // ---- epilogue: l over lane groups and the two row tiles
-    l_run += __shfl_xor(l_run, 16);
-    l_run += __shfl_xor(l_run, 32);
+    l_run = xor32_sum(xor16_sum(l_run));
     lds_barrier();  // every wave is past its last LDS read of the buffers
     if (lg == 0) red[w][lc] = l_run;
     lds_barrier();
@@ -939,16 +938,6 @@ __global__ void __launch_bounds__((WsShape<HGS, QK16>::THREADS), 1) mla_decode_w
     }
 }
 
-// Full-wave max on DPP and permlane swaps, no LDS round trips (the same
-// butterfly as group_sum): every lane ends with the result.
-__device__ __forceinline__ float wave_max_dpp(float v) {
-    v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xf, 0xf, false)));
-    v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4E, 0xf, 0xf, false)));
-    v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x141, 0xf, 0xf, false)));
-    v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x140, 0xf, 0xf, false)));
-    return xor32_max(xor16_max(v));
-}
-
 // Merge the split partials.  A partial is O_s / l_s (bf16 for bf16 output,
 // f32 for f32 output) with its running max m_s and sum l_s (fp32):
 //   out = sum_s w_s (O_s / l_s) / (sum_s w_s + sink),  w_s = l_s 2^(m_s - M).
@@ -1006,7 +995,7 @@ __global__ void __launch_bounds__(COMBINE_THREADS) mla_combine(CombineParams p) 
 #pragma unroll
     for (int k = 0; k < MLK; ++k)
         if (ml_l[k] > 0.f) M = fmaxf(M, ml_m[k]);
-    M = wave_max_dpp(M);
+    M = wave_max(M);
     if (l == 0) red_m[w] = M;
     __syncthreads();
     M = fmaxf(fmaxf(red_m[0], red_m[1]), fmaxf(red_m[2], red_m[3]));
@@ -1023,7 +1012,7 @@ __global__ void __launch_bounds__(COMBINE_THREADS) mla_combine(CombineParams p) 
             L += wv;
         }
     }
-    L = group_sum(L, 64);
+    L = wave_sum(L);
     if (l == 0) red_l[w] = L;
     __syncthreads();
     L = (red_l[0] + red_l[1]) + (red_l[2] + red_l[3]);

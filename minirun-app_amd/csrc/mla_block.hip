@@ -221,7 +221,7 @@ __global__ void __launch_bounds__(256) absorb_q_fast_kernel(AbsorbParams p) {
     // rows of the wave: lanes l, l^8, l^16, l^32 hold the same columns
 #pragma unroll
     for (int i = 0; i < 32; ++i) {
-        acc[i] += __shfl_xor(acc[i], 8);
+        acc[i] = xor8_sum(acc[i]);
         acc[i] = xor16_sum(acc[i]);
         acc[i] = xor32_sum(acc[i]);
     }

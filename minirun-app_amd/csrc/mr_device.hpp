@@ -172,14 +172,22 @@ __device__ __forceinline__ void wait_vmcnt() {
     asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
 
+// Full-wave max and sum: the group_sum butterfly over all 64 lanes (DPP and
+// permlane swaps, no LDS round trips); every lane ends with the result.
 __device__ __forceinline__ float wave_max(float v) {
-    for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
-    return v;
+    v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xf, 0xf, false)));
+    v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4E, 0xf, 0xf, false)));
+    v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x141, 0xf, 0xf, false)));
+    v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x140, 0xf, 0xf, false)));
+    return xor32_max(xor16_max(v));
 }
 
-__device__ __forceinline__ float wave_sum(float v) {
-    for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o);
-    return v;
+__device__ __forceinline__ float wave_sum(float v) { return group_sum(v, 64); }
+
+// v plus the value of lane l ^ 8 (DPP row_ror:8 rotates each 16-lane row by
+// 8, which is xor 8 there).
+__device__ __forceinline__ float xor8_sum(float v) {
+    return v + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x128, 0xf, 0xf, false));
 }
 
 }  // namespace mr
