@@ -489,6 +489,29 @@ __global__ void __launch_bounds__((WsShape<HGS, QK16>::THREADS), 1) mla_decode_w
     const uint16_t* lat = p.latent + (int64_t)b * p.lat_bs;
     const uint16_t* rop = DR ? p.rope + (int64_t)b * p.rope_bs : nullptr;
 
+    // Q of the head group into buffers 2-3 by the PV waves, first of all (one
+    // 1 KB load per wave instruction instead of 32-byte pieces of 32 heads
+    // per QK load): in the gathered form it is in flight while the split's
+    // indices load
+    if (!is_qk) {
+        constexpr int QPW = HGS * G::CPR / 256;  // Q loads per PV wave
+        static_assert(QPW * 256 == HGS * G::CPR, "Q staging loads");
+        static_assert(HGS * G::ROWB <= 2 * G::BUF, "Q fits buffers 2-3");
+        char* qdst = cbuf + 2 * G::BUF;
+#pragma unroll
+        for (int k = 0; k < QPW; ++k) {
+            const int slot = 64 * (pw + 4 * k) + l;
+            const int h = slot / G::CPR;
+            const int c = (slot - h * G::CPR) ^ (h & 7);
+            const int h0 = hg * HGS + h;
+            const int hh = h0 < p.heads ? h0 : 0;
+            const uint16_t* src = c < R / 8 ? p.q_lat + (int64_t)b * p.q_lat_bs + (int64_t)hh * p.q_lat_hs + 8 * c
+                                            : p.q_rope + (int64_t)b * p.q_rope_bs + (int64_t)hh * p.q_rope_hs +
+                                                  8 * (c - R / 8);
+            dma16(src, qdst + 1024 * (pw + 4 * k));
+        }
+    }
+
     if (GATHER) {
         const int32_t* ind = p.indices + (int64_t)b * p.n_idx;
         for (int i = tid; i < nrows; i += NT) {
@@ -807,28 +830,9 @@ __global__ void __launch_bounds__((WsShape<HGS, QK16>::THREADS), 1) mla_decode_w
         for (int T = 0; T < HT; ++T)
 #pragma unroll
             for (int J = 0; J < 8; ++J) oacc[T][J] = f32x4{0.f, 0.f, 0.f, 0.f};
-        // prologue: Q of the head group into buffers 2-3 (one 1 KB load per
-        // wave instruction instead of 32-byte pieces of 32 heads per QK
-        // load), sub-chunks 0 and 1 behind it; sub-chunk 2 goes out once the
+        // prologue: Q of the head group went into buffers 2-3 at the start
+        // (see above); sub-chunks 0 and 1 go behind it, sub-chunk 2 once the
         // QK waves hold Q in registers
-        {
-            constexpr int QPW = HGS * G::CPR / 256;  // Q loads per PV wave
-            static_assert(QPW * 256 == HGS * G::CPR, "Q staging loads");
-            static_assert(HGS * G::ROWB <= 2 * G::BUF, "Q fits buffers 2-3");
-            char* qdst = cbuf + 2 * G::BUF;
-#pragma unroll
-            for (int k = 0; k < QPW; ++k) {
-                const int slot = 64 * (pw + 4 * k) + l;
-                const int h = slot / G::CPR;
-                const int c = (slot - h * G::CPR) ^ (h & 7);
-                const int h0 = hg * HGS + h;
-                const int hh = h0 < p.heads ? h0 : 0;
-                const uint16_t* src = c < R / 8 ? p.q_lat + (int64_t)b * p.q_lat_bs + (int64_t)hh * p.q_lat_hs + 8 * c
-                                                : p.q_rope + (int64_t)b * p.q_rope_bs + (int64_t)hh * p.q_rope_hs +
-                                                      8 * (c - R / 8);
-                dma16(src, qdst + 1024 * (pw + 4 * k));
-            }
-        }
         const int pro2 = min(nsub, 2);
         for (int s = 0; s < pro2; ++s) issue(s, cbuf + s * G::BUF);
         if (pro2 == 2)

@@ -114,6 +114,36 @@ def test_affine_gemv_config5_shapes(M, name, out_f, in_f, centred):
     check(f32(y), ref, f"gemv-{name}{'-centred' if centred else ''}", scale_bar=1e-4)
 
 
+@pytest.mark.parametrize("sdt", ["bf16", "f16", "f32"])
+@pytest.mark.parametrize("out_f,in_f", [(1000, 832), (37, 64), (129, 4096), (3, 16384), (300, 512)])
+def test_affine_gemv_fast_path_edges(M, out_f, in_f, sdt):
+    """The 4-bit fast path on shapes whose rows do not fill the last row step,
+    whose groups do not fill the last lane pass (13 groups, 1 group), a
+    single-tile matrix and every scale dtype."""
+    print(f"gemv fast edges {out_f}x{in_f} scales={sdt}", flush=True)
+    import torch
+
+    packed = O.u32(f"ge.p.{out_f}.{in_f}", (out_f, in_f // 8))
+    s = O.bf16_to_f32(O.abs_normal_bf16(f"ge.s.{out_f}.{in_f}", (out_f, in_f // 64), std=0.01))
+    b = O.bf16_to_f32(O.normal_bf16(f"ge.b.{out_f}.{in_f}", (out_f, in_f // 64), std=0.01))
+    if sdt == "bf16":
+        sa, ba, code, tdt = O.f32_to_bf16(s), O.f32_to_bf16(b), O.BF16, torch.bfloat16
+        st, bt = dev(sa), dev(ba)
+    elif sdt == "f16":
+        sa, ba, code = np.float16(s).view(np.uint16), np.float16(b).view(np.uint16), O.F16
+        st = torch.from_numpy(sa).view(torch.float16).cuda()
+        bt = torch.from_numpy(ba).view(torch.float16).cuda()
+    else:
+        sa, ba, code = s.astype(np.float32), b.astype(np.float32), O.F32
+        st, bt = torch.from_numpy(sa).cuda(), torch.from_numpy(ba).cuda()
+    w = M.AffineWeights(dev(packed), st, bt)
+    x = O.normal_bf16(f"ge.x.{out_f}.{in_f}", (in_f,))
+    y = M.affine_mm(dev(x), w, out_dtype=torch.float32)
+    sync()
+    ref = O.affine_matmul(O.bf16_to_f32(x)[None], packed, sa, ba, group=64, bits=4, scale_dtype=code, acc=1)[0]
+    check(f32(y), ref, f"gemv-fast-{out_f}x{in_f}-{sdt}", scale_bar=1e-4)
+
+
 def test_affine_matmul_generic_paths(M):
     print("gemv generic: 3 tokens, f32 x, 8-bit, f16 scales", flush=True)
     import torch
