@@ -330,6 +330,42 @@ def time_topk(torch, M, steps=200):
     return e0.elapsed_time(e1) / steps
 
 
+def time_indexer(torch, M, steps=200, nbuf=8):
+    """Lightning-index scores of one decode token: 64 index heads of dim 128
+    over 32768 compressed keys (bf16, 8 MiB), weights f32; the keys rotate
+    over `nbuf` copies so each launch streams them from HBM; average of
+    `steps` launches between two events."""
+    import ctypes as C
+
+    lib = M.load()
+    S, H, D, T = 1, 64, 128, 32768
+    g = torch.Generator(device="cuda")
+    g.manual_seed(0x4D4C410005)
+    q = torch.randn(S, H, D, generator=g, device="cuda").to(torch.bfloat16)
+    keys = [torch.randn(T, D, generator=g, device="cuda").to(torch.bfloat16) for _ in range(nbuf)]
+    w = torch.randn(S, H, generator=g, device="cuda") * (D * H) ** -0.5
+    out = torch.empty(S, T, dtype=torch.float32, device="cuda")
+    sp = M._stream(torch.cuda.current_stream())
+
+    def run(i):
+        k = keys[i % nbuf]
+        M._check(lib.mr_indexer_scores(q.data_ptr(), M.BF16, S, H, D, q.stride(0), q.stride(1), k.data_ptr(), M.BF16,
+                                       T, D, k.stride(0), w.data_ptr(), M.F32, S, H, w.stride(0), out.data_ptr(),
+                                       out.stride(0), sp))
+
+    for i in range(20):
+        run(i)
+    torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for i in range(steps):
+        run(i)
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / steps
+
+
 def mfma_probe(torch, M):
     """On-box MFMA rate: one 256-thread workgroup per CU, each wave 8
     independent 32x32x16 bf16 MFMA chains for 4000 rounds, no memory traffic
@@ -427,6 +463,9 @@ def main():
     log(f"bench: prefill {pf}")
     tk_ms = time_topk(torch, M)
     log(f"bench: top-k 2048 of 32768 {tk_ms * 1e3:.2f} us")
+    log("bench: lightning-index scores, 64 heads x 128, 32768 keys")
+    ix_ms = time_indexer(torch, M)
+    log(f"bench: indexer scores {ix_ms * 1e3:.2f} us")
     mp = mfma_probe(torch, M)
     log(f"bench: mfma probe {mp}")
 
@@ -464,6 +503,8 @@ def main():
         "prefill_attn_us": round(pf["attn_ms"] * 1e3, 2),
         "prefill_attn_mfma_fraction": round(ATTN_FLOP / (pf["attn_ms"] * 1e-3) / 1e12 / MFMA_PEAK_TFLOPS, 4),
         "topk_2048_of_32768_us": round(tk_ms * 1e3, 2),
+        "indexer_scores_32768_us": round(ix_ms * 1e3, 2),
+        "indexer_hbm_fraction": round(32768 * 128 * 2 / (ix_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
         "mfma_probe_tflops": mp["tflops"],
         "mfma_probe_clock_ghz": mp["clock_ghz"],
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",

@@ -308,6 +308,26 @@ mr_status mr_attention_indices_compressed(int32_t ratio, int32_t seq_len, int32_
                                           int32_t *out, int32_t *rows, int32_t *cols);
 
 /* ------------------------------------------------------------------------
+ * Lightning-index scores (DeepSeekV4LightningIndexer.scores,
+ * DeepSeekV4Attention.swift:530-549): scores[s][t] = sum_h w[s][h] *
+ * max(q[s][h] . k[t], 0) in fp32 (NaN propagates), the producer of the
+ * score matrix mr_topk_select ranks.  queries [seq][heads][dim] bf16 or f32
+ * (strides in elements), keys [n_keys][key_dim] bf16 or f32 (row stride),
+ * weights [w_rows][w_cols] f32 or bf16 (row stride), scores
+ * [seq][out_row_stride] f32.  The geometry check is the reference's
+ * (:533-541: seq, heads, dim > 0, key_dim == dim, weights [seq, heads]);
+ * n_keys == 0 writes nothing (the reference returns [seq, 0]).  bf16 inputs
+ * with dim 128 and heads a multiple of 16 up to 64 run on MFMA; other
+ * shapes run a generic kernel.  Scores match the reference to fp32
+ * rounding (its reduction order is MLX's), not bit for bit.
+ * ------------------------------------------------------------------------ */
+mr_status mr_indexer_scores(const void *queries, mr_dtype q_dtype, int32_t seq, int32_t heads, int32_t dim,
+                            int64_t q_seq_stride, int64_t q_head_stride, const void *keys, mr_dtype k_dtype,
+                            int32_t n_keys, int32_t key_dim, int64_t k_row_stride, const void *weights,
+                            mr_dtype w_dtype, int32_t w_rows, int32_t w_cols, int64_t w_row_stride, float *scores,
+                            int64_t out_row_stride, void *stream);
+
+/* ------------------------------------------------------------------------
  * Lightning-indexer top-k selection (DeepSeekV4LightningIndexer.selecting,
  * DeepSeekV4Attention.swift:582-645), on the device, bit-exact.
  * scores [rows][cols] f32.  available = (start_pos + rows) / ratio keys are

@@ -1,6 +1,6 @@
-// C-ABI of the lightning-indexer top-k selection: the reference's geometry
-// checks (DeepSeekV4Attention.swift:590-612) on the host, the selection on
-// the device.
+// C-ABI of the lightning indexer: the scores (DeepSeekV4Attention.swift:
+// 530-549) and the top-k selection, with the reference's geometry checks
+// (:533-541, :590-612) on the host and the work on the device.
 #include <hip/hip_runtime.h>
 
 #include <vector>
@@ -15,6 +15,44 @@ using mrc::hip_fail;
 }  // namespace
 
 extern "C" {
+
+mr_status mr_indexer_scores(const void* queries, mr_dtype q_dtype, int32_t seq, int32_t heads, int32_t dim,
+                            int64_t q_seq_stride, int64_t q_head_stride, const void* keys, mr_dtype k_dtype,
+                            int32_t n_keys, int32_t key_dim, int64_t k_row_stride, const void* weights,
+                            mr_dtype w_dtype, int32_t w_rows, int32_t w_cols, int64_t w_row_stride, float* scores,
+                            int64_t out_row_stride, void* stream) {
+    // DeepSeekV4Attention.swift:533-541
+    if (!(seq > 0 && heads > 0 && dim > 0 && n_keys >= 0 && key_dim == dim && w_rows == seq && w_cols == heads))
+        return fail(MR_INVALID_SHAPE, "index queries, keys, and weights have incompatible geometry");
+    auto act = [](mr_dtype d) { return d == MR_BF16 || d == MR_F32; };
+    if (!act(q_dtype) || !act(k_dtype) || !act(w_dtype))
+        return fail(MR_INVALID_DTYPE, "lightning-index scores: queries, keys and weights must be bf16 or f32");
+    if (n_keys == 0) return MR_OK;  // :542-544
+    if (!queries || !keys || !weights || !scores)
+        return fail(MR_INVALID_ARGUMENT, "lightning-index scores: NULL pointer");
+    if (q_head_stride < dim || q_seq_stride < int64_t(heads) * q_head_stride || k_row_stride < dim ||
+        w_row_stride < heads || out_row_stride < n_keys)
+        return fail(MR_INVALID_ARGUMENT, "lightning-index scores: strides are smaller than the rows");
+    mr::IndexerParams p{};
+    p.q = queries;
+    p.q_f32 = q_dtype == MR_F32;
+    p.q_ss = q_seq_stride;
+    p.q_hs = q_head_stride;
+    p.k = keys;
+    p.k_f32 = k_dtype == MR_F32;
+    p.k_rs = k_row_stride;
+    p.w = weights;
+    p.w_f32 = w_dtype == MR_F32;
+    p.w_ss = w_row_stride;
+    p.out = scores;
+    p.out_ss = out_row_stride;
+    p.S = seq;
+    p.H = heads;
+    p.D = dim;
+    p.T = n_keys;
+    const hipError_t e = mr::launch_indexer_scores(p, (hipStream_t)stream);
+    return e == hipSuccess ? MR_OK : hip_fail(e, "lightning-index scores launch");
+}
 
 mr_status mr_topk_geometry(int32_t rows, int32_t cols, int32_t top_k, int32_t ratio, int32_t start_pos,
                            int32_t offset, int32_t* selected) {

@@ -146,6 +146,26 @@ struct AffineGemvParams {
     int tpr, tile_rows, tiles_per_vec;
 };
 
+// Lightning-index scores: out[s][t] = sum_h w[s][h] * max(q[s][h] . k[t], 0).
+// Strides in elements; k_bytes is set by the launcher.
+struct IndexerParams {
+    const void* q;  // [S][H][D]
+    int q_f32;
+    int64_t q_ss, q_hs;
+    const void* k;  // [T][D]
+    int k_f32;
+    int64_t k_rs;
+    const void* w;  // [S][H]
+    int w_f32;
+    int64_t w_ss;
+    float* out;     // [S][out_ss]
+    int64_t out_ss;
+    int32_t S, H, D, T;
+    uint32_t k_bytes;
+};
+bool indexer_mfma_ok(const IndexerParams& p);
+hipError_t launch_indexer_scores(const IndexerParams& p, hipStream_t st);
+
 hipError_t launch_affine_dequant(const AffineDequantParams& p, hipStream_t st);
 bool affine_gemv_fast_ok(const AffineGemvParams& p);
 hipError_t launch_affine_gemv(const AffineGemvParams& p, hipStream_t st);

@@ -140,6 +140,9 @@ SIGNATURES = {
     "mr_topk_geometry": (C.c_int, [C.c_int32, C.c_int32, C.c_int32, C.c_int32, C.c_int32, C.c_int32, _I32P]),
     "mr_topk_workspace_size": (C.c_size_t, [C.c_int32]),
     "mr_topk_select": (C.c_int, [C.POINTER(TopkArgs), _P]),
+    "mr_indexer_scores": (C.c_int, [_P, C.c_int, C.c_int32, C.c_int32, C.c_int32, C.c_int64, C.c_int64, _P, C.c_int,
+                                    C.c_int32, C.c_int32, C.c_int64, _P, C.c_int, C.c_int32, C.c_int32, C.c_int64,
+                                    _P, C.c_int64, _P]),
     "mr_attention_indices_window": (C.c_int, [C.c_int32, C.c_int32, C.c_int32, _P, _I32P, _I32P]),
     "mr_attention_indices_compressed": (C.c_int, [C.c_int32, C.c_int32, C.c_int32, C.c_int32, _P, _I32P, _I32P]),
 }
@@ -514,6 +517,36 @@ def topk_geometry(rows, cols, top_k, ratio, start_pos, offset):
     sel = C.c_int32()
     _check(load().mr_topk_geometry(rows, cols, top_k, ratio, start_pos, offset, C.byref(sel)))
     return sel.value
+
+
+def lightning_index_scores(queries, compressed_keys, head_weights, *, out=None, stream=None):
+    """DeepSeekV4LightningIndexer.scores (DeepSeekV4Attention.swift:530-549):
+    queries [S, H, D], compressed_keys [T, D], head_weights [S, H] (bf16 or
+    f32, weights already scaled) -> f32 [S, T], sum_h w * max(q . k, 0).
+    Geometry errors are the reference's (MRError INVALID_SHAPE)."""
+    torch = _torch()
+    if queries.dim() != 3 or compressed_keys.dim() != 2 or head_weights.dim() != 2:
+        # a zero geometry makes the library raise the reference's error
+        _check(load().mr_indexer_scores(None, BF16, 0, 0, 0, 0, 0, None, BF16, 0, 0, 0, None, BF16, 0, 0, 0, None, 0,
+                                        None))
+    S, H, D = queries.shape
+    T, KD = compressed_keys.shape
+    WR, WC = head_weights.shape
+    codes = {torch.bfloat16: BF16, torch.float32: F32}
+    for t, n in ((queries, "queries"), (compressed_keys, "compressed_keys"), (head_weights, "head_weights")):
+        if t.dtype not in codes:
+            raise ValueError(f"{n} must be bf16 or f32")
+        if t.numel() and t.stride(-1) != 1:
+            raise ValueError(f"{n} must have a unit last-dimension stride")
+    if out is None:
+        out = torch.empty(max(S, 0), max(T, 0), dtype=torch.float32, device=queries.device)
+    _check(load().mr_indexer_scores(queries.data_ptr(), codes[queries.dtype], S, H, D,
+                                    queries.stride(0) if S else 0, queries.stride(1) if H else 0,
+                                    compressed_keys.data_ptr(), codes[compressed_keys.dtype], T, KD,
+                                    compressed_keys.stride(0) if T else 0, head_weights.data_ptr(),
+                                    codes[head_weights.dtype], WR, WC, head_weights.stride(0) if WR else 0,
+                                    out.data_ptr(), out.stride(0) if out.numel() else max(T, 0), _stream(stream)))
+    return out
 
 
 def lightning_select(scores, top_k, ratio, start_pos, offset, *, check=True, status=None, stream=None):

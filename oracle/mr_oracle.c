@@ -24,6 +24,8 @@
  *                            form bitwise, validation error order
  *   topk_select              brute force with the stated comparator, ties,
  *                            NaN, masking
+ *   indexer_scores           numpy fp64 brute force, w = 0, negative dots,
+ *                            linearity in w, positive key scaling, NaN
  *   window/compressed        hand-written tables from the reference's rules
  *   MLX reduction order      parity unpinned (needs MLX; tolerance instead)
  */
@@ -589,6 +591,27 @@ int mro_affine_matmul(const float *x, int64_t M, const uint32_t *packed, const u
         }
     }
     free(w);
+    return MRO_OK;
+}
+
+/* DeepSeekV4Attention.swift:545-548: perHead = einsum("shd,td->sht") in
+ * fp32, then sum over h of maximum(perHead, 0) * w[s, h]. */
+int mro_indexer_scores(const float *q, int32_t S, int32_t H, int32_t D, const float *k, int32_t T,
+                       const float *w, float *out) {
+    if (!(S > 0 && H > 0 && D > 0 && T >= 0)) return MRO_INVALID_SHAPE;
+#pragma omp parallel for schedule(static)
+    for (int64_t st = 0; st < (int64_t)S * T; ++st) {
+        const int64_t s = st / T, t = st % T;
+        float acc = 0.f;
+        for (int32_t h = 0; h < H; ++h) {
+            const float *qr = q + (s * H + h) * D, *kr = k + t * D;
+            float d = 0.f;
+            for (int32_t i = 0; i < D; ++i) d += qr[i] * kr[i];
+            const float r = d > 0.f ? d : (d != d ? d : 0.f);
+            acc += r * w[s * H + h];
+        }
+        out[st] = acc;
+    }
     return MRO_OK;
 }
 

@@ -136,6 +136,12 @@ int mro_affine_matmul(const float *x, int64_t M, const uint32_t *packed,
 int mro_topk_select(const float *scores, int32_t rows, int32_t cols, int32_t top_k,
                     int32_t ratio, int32_t start_pos, int32_t offset, int32_t *out,
                     int32_t *out_count);
+/* DeepSeekV4LightningIndexer.scores (DeepSeekV4Attention.swift:530-549):
+ * out[s][t] = sum_h w[s][h] * max(q[s][h] . k[t], 0) in fp32; the dot is
+ * summed over d in order, the heads in order; NaN propagates through the
+ * max.  q [S][H][D], k [T][D], w [S][H], out [S][T], all dense fp32. */
+int mro_indexer_scores(const float *q, int32_t S, int32_t H, int32_t D, const float *k, int32_t T,
+                       const float *w, float *out);
 int mro_window_indices(int32_t window, int32_t seq_len, int32_t start_pos, int32_t *out,
                        int32_t *out_rows, int32_t *out_cols);
 int mro_compressed_indices(int32_t ratio, int32_t seq_len, int32_t start_pos, int32_t offset,

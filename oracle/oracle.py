@@ -71,6 +71,7 @@ def _declare(L):
         "mro_affine_dequantize": (C.c_int, [P, P, P, i32, i64, i64, i32, i32, P, C.c_int]),
         "mro_affine_matmul": (C.c_int, [P, i64, P, P, P, i32, i64, i64, i32, i32, C.c_int, P, C.c_int]),
         "mro_topk_select": (C.c_int, [P, i32, i32, i32, i32, i32, i32, P, P]),
+        "mro_indexer_scores": (C.c_int, [P, i32, i32, i32, P, i32, P, P]),
         "mro_window_indices": (C.c_int, [i32, i32, i32, P, P, P]),
         "mro_compressed_indices": (C.c_int, [i32, i32, i32, i32, P, P, P]),
     }
@@ -279,6 +280,21 @@ def affine_matmul(x, packed, scales, biases, group=64, bits=4, scale_dtype=BF16,
 
 
 # ---------------------------------------------------------------- indices
+def indexer_scores(q, k, w):
+    """DeepSeekV4LightningIndexer.scores (DeepSeekV4Attention.swift:530-549):
+    q [S, H, D], k [T, D], w [S, H] -> [S, T] fp32."""
+    q = _c(q, np.float32)
+    k = _c(k, np.float32)
+    w = _c(w, np.float32)
+    S, H, D = q.shape
+    T = k.shape[0]
+    out = np.empty((S, T), np.float32)
+    st = lib().mro_indexer_scores(_p(q), S, H, D, _p(k), T, _p(w), _p(out))
+    if st != OK:
+        raise ValueError(f"indexer_scores status {st}")
+    return out
+
+
 def topk_select(scores, top_k, ratio, start_pos, offset):
     s = _c(scores, np.float32)
     rows, cols = s.shape

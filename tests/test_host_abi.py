@@ -136,3 +136,33 @@ def test_topk_geometry_counts():
     assert M.topk_geometry(1, 32768, 2048, 4, 131071, 0) == 2048
     assert M.topk_geometry(300, 75, 16, 4, 0, 128) == 16
     assert M.topk_geometry(3, 4, 16, 4, 0, 0) == 0   # fewer than ratio tokens: empty rows
+
+
+# ---------------------------------------------------------------- lightning-index scores
+def _scores_call(seq, heads, dim, n_keys, key_dim, w_rows, w_cols, qdt=M.BF16):
+    """Geometry-only calls: every case below returns before any launch."""
+    return M.load().mr_indexer_scores(None, qdt, seq, heads, dim, heads * dim, dim, None, M.BF16, n_keys, key_dim,
+                                      key_dim, None, M.F32, w_rows, w_cols, w_cols, None, n_keys, None)
+
+
+@pytest.mark.parametrize("args", [
+    (0, 4, 8, 5, 8, 0, 4),     # empty sequence
+    (2, 0, 8, 5, 8, 2, 0),     # no heads
+    (2, 4, 0, 5, 0, 2, 4),     # zero dimension
+    (2, 4, 8, 5, 16, 2, 4),    # key dimension differs from the queries'
+    (2, 4, 8, 5, 8, 1, 4),     # weights not [seq, heads]
+    (2, 4, 8, 5, 8, 2, 5),
+])
+def test_indexer_scores_geometry_errors(args):
+    """DeepSeekV4Attention.swift:533-541: one error for every geometry
+    mismatch, raised before any work."""
+    st = _scores_call(*args)
+    assert st == O.INVALID_SHAPE
+    assert "incompatible geometry" in M.last_error()
+
+
+def test_indexer_scores_no_keys_and_dtypes():
+    # no compressed keys: nothing to compute (:542-544), not an error
+    assert _scores_call(2, 4, 8, 0, 8, 2, 4) == 0
+    st = _scores_call(2, 4, 8, 0, 8, 2, 4, qdt=M.F16)
+    assert st == O.INVALID_DTYPE and "bf16 or f32" in M.last_error()
