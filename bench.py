@@ -366,6 +366,46 @@ def time_indexer(torch, M, steps=200, nbuf=8):
     return e0.elapsed_time(e1) / steps
 
 
+def time_gather(torch, M, steps=200, nbuf=4):
+    """Routed-expert affine GEMV of one decode token: 8 of 128 experts of a
+    4-bit, group-64 [768, 2048] stack (bf16 scales), random distinct ids per
+    launch set; stacks rotate over `nbuf` copies; average of `steps` launches
+    between two events."""
+    import ctypes as C
+
+    lib = M.load()
+    E, K, out_f, in_f = 128, 8, 768, 2048
+    g = torch.Generator(device="cuda")
+    g.manual_seed(0x4D4C410006)
+    ws = []
+    for _ in range(nbuf):
+        packed = torch.randint(-2**31, 2**31 - 1, (E, out_f, in_f // 8), generator=g, dtype=torch.int32, device="cuda")
+        scales = (torch.rand(E, out_f, in_f // 64, generator=g, device="cuda") * 0.01).to(torch.bfloat16)
+        biases = (torch.randn(E, out_f, in_f // 64, generator=g, device="cuda") * 0.01).to(torch.bfloat16)
+        ws.append(M.AffineWeights(packed, scales, biases))
+    descs = [w.desc() for w in ws]
+    x = torch.randn(1, in_f, generator=g, device="cuda").to(torch.bfloat16)
+    ids = [torch.randperm(E, generator=g, device="cuda")[:K].to(torch.int32).reshape(1, K) for _ in range(16)]
+    y = torch.empty(1, K, out_f, dtype=torch.bfloat16, device="cuda")
+    sp = M._stream(torch.cuda.current_stream())
+
+    def run(i):
+        M._check(lib.mr_affine_gather_matmul(x.data_ptr(), M.BF16, 1, x.stride(0), C.byref(descs[i % nbuf]), E,
+                                             ids[i % 16].data_ptr(), K, y.data_ptr(), M.BF16, sp))
+
+    for i in range(20):
+        run(i)
+    torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for i in range(steps):
+        run(i)
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / steps
+
+
 def mfma_probe(torch, M):
     """On-box MFMA rate: one 256-thread workgroup per CU, each wave 8
     independent 32x32x16 bf16 MFMA chains for 4000 rounds, no memory traffic
@@ -466,6 +506,9 @@ def main():
     log("bench: lightning-index scores, 64 heads x 128, 32768 keys")
     ix_ms = time_indexer(torch, M)
     log(f"bench: indexer scores {ix_ms * 1e3:.2f} us")
+    log("bench: routed-expert GEMV, 8 of 128 experts of [768, 2048] 4-bit")
+    gx_ms = time_gather(torch, M)
+    log(f"bench: gather {gx_ms * 1e3:.2f} us")
     mp = mfma_probe(torch, M)
     log(f"bench: mfma probe {mp}")
 
@@ -505,6 +548,8 @@ def main():
         "topk_2048_of_32768_us": round(tk_ms * 1e3, 2),
         "indexer_scores_32768_us": round(ix_ms * 1e3, 2),
         "indexer_hbm_fraction": round(32768 * 128 * 2 / (ix_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+        "gather_8x768x2048_us": round(gx_ms * 1e3, 2),
+        "gather_hbm_fraction": round(8 * 768 * (2048 // 2 + 4 * 2048 // 64) / (gx_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
         "mfma_probe_tflops": mp["tflops"],
         "mfma_probe_clock_ghz": mp["clock_ghz"],
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",

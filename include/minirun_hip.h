@@ -172,6 +172,20 @@ mr_status mr_affine_matmul(const void *x, mr_dtype x_dtype, int32_t tokens, int6
                            const mr_affine_weight *w, void *y, mr_dtype y_dtype, int64_t y_stride,
                            void *stream);
 
+/* affineGatherMM (AffineWeights.swift:255-318): routed experts,
+ * y[t, j, :] = x[t, :] . dequant(W[rhs[t, j]])^T.  w describes one expert
+ * (out_features x in_features) of a stack of `experts` laid out back to back
+ * (packed [experts][out][in*bits/32], scales/biases [experts][out][in/group]);
+ * rhs_indices: device int32 [tokens][experts_per_token], need not be sorted,
+ * may repeat; y: [tokens][experts_per_token][out] bf16 or f32, dense.  The
+ * reference's preconditions (a stacked weight, indices matching the token
+ * count) return MR_INVALID_ARGUMENT with its message.  An expert id outside
+ * [0, experts) yields a zero row (MLX leaves it undefined).  4-bit /
+ * group-64 / bf16 x runs the fused dequant-GEMV per (token, slot). */
+mr_status mr_affine_gather_matmul(const void *x, mr_dtype x_dtype, int32_t tokens, int64_t x_stride,
+                                  const mr_affine_weight *w, int64_t experts, const int32_t *rhs_indices,
+                                  int32_t experts_per_token, void *y, mr_dtype y_dtype, void *stream);
+
 /* K3Norm.rms (Sources/ModelAdapters/Operators/Normalization.swift:15-19):
  * out = weight * (x * rsqrt(mean(x^2) + eps)) per row, fp32 arithmetic. */
 mr_status mr_rmsnorm(const void *x, mr_dtype x_dtype, int64_t rows, int32_t dim, int64_t x_stride,

@@ -102,7 +102,7 @@ __global__ void __launch_bounds__(GEMV_THREADS) affine_gemv4_kernel(AffineGemvPa
     const int nch = in / 8;  // 16-byte chunks of x
     const int G = in / 64;
     const int t = threadIdx.x;
-    const uint16_t* x = (const uint16_t*)p.x + (int64_t)xg * p.x_stride;
+    const uint16_t* x = (const uint16_t*)p.x + (int64_t)(xg / p.x_div) * p.x_stride;
 
     // rows: tpr threads per row, steps of 256 / tpr rows; a thread dots at
     // most GEMV_NPT groups of a row (tpr * GEMV_NPT >= G)
@@ -120,7 +120,15 @@ __global__ void __launch_bounds__(GEMV_THREADS) affine_gemv4_kernel(AffineGemvPa
     constexpr uint32_t OOB = 0x80000000u;
     // a tile stays inside one activation vector, so output row j reads weight
     // row wbase + j
-    const int wbase = (int)(xg * p.map_b + p.map_c) - xg * p.map_a;
+    // (routed: the expert's rows; an expert id out of range loads nothing)
+    int64_t wfirst = xg * p.map_b + p.map_c;
+    bool evalid = true;
+    if (p.rhs_idx) {
+        const int32_t e = p.rhs_idx[xg];
+        evalid = e >= 0 && e < p.experts;
+        wfirst = evalid ? (int64_t)e * p.map_a : 0;
+    }
+    const int wbase = (int)wfirst - xg * p.map_a;
     typedef typename std::conditional<SB == 2, uint16_t, uint32_t>::type SRaw;
     struct RowLoads {
         u32x4 w[GEMV_NPT][2];
@@ -139,7 +147,7 @@ __global__ void __launch_bounds__(GEMV_THREADS) affine_gemv4_kernel(AffineGemvPa
     }
     const uint32_t wrow_bytes = (uint32_t)(in / 2), srow_bytes = (uint32_t)G * SB;
     auto load_row = [&](int j, RowLoads& L) {
-        const bool rok = j < r_end;
+        const bool rok = j < r_end && evalid;
         const uint32_t wr = (uint32_t)(wbase + j);  // < 2^24 (host check)
         const uint32_t wrow = __umul24(wr, wrow_bytes), srow = __umul24(wr, srow_bytes);
         L.ok = 0;
@@ -340,8 +348,22 @@ __global__ void __launch_bounds__(256) affine_gemv_generic_kernel(AffineGemvPara
     if (wave >= total) return;
     const int m = wave / p.out_rows;
     const int j = wave - m * p.out_rows;
-    const int64_t wr = (int64_t)(j / p.map_a) * p.map_b + p.map_c + (j % p.map_a);
-    const int xrow = m * (p.out_rows / p.map_a) + j / p.map_a;
+    int64_t wr = (int64_t)(j / p.map_a) * p.map_b + p.map_c + (j % p.map_a);
+    const int xrow = (m * (p.out_rows / p.map_a) + j / p.map_a) / p.x_div;
+    if (p.rhs_idx) {  // routed: the expert's rows, zeros for an id out of range
+        const int32_t e = p.rhs_idx[j / p.map_a];
+        if (e < 0 || e >= p.experts) {
+            if (l == 0) {
+                const int64_t o = (int64_t)m * p.y_stride_token + (int64_t)j * p.y_stride_row;
+                if (p.y_f32)
+                    ((float*)p.y)[o] = 0.f;
+                else
+                    ((uint16_t*)p.y)[o] = 0;
+            }
+            return;
+        }
+        wr = (int64_t)e * p.map_a + (j % p.map_a);
+    }
     const int per = 32 / p.bits;
     const uint32_t mask = p.bits == 32 ? 0xffffffffu : ((1u << p.bits) - 1u);
     const int64_t wpr = p.in_features / per;
@@ -382,6 +404,7 @@ hipError_t launch_affine_dequant(const AffineDequantParams& p, hipStream_t st) {
 // Weight rows the fast path addresses: the last activation vector's rows end
 // at (nvec - 1) * map_b + map_c + (its row count).
 static int64_t gemv_weight_rows(const AffineGemvParams& p) {
+    if (p.rhs_idx) return p.experts * p.map_a;
     const int64_t nvec = (p.out_rows + p.map_a - 1) / p.map_a;
     const int64_t last_rows = std::min<int64_t>(p.map_a, p.out_rows - (nvec - 1) * p.map_a);
     return (nvec - 1) * p.map_b + p.map_c + last_rows;

@@ -138,6 +138,7 @@ mr::AffineGemvParams gemv_params(const mr_affine_weight* w) {
     g.map_a = (int)w->out_features;
     g.map_b = 0;
     g.map_c = 0;
+    g.x_div = 1;
     return g;
 }
 
@@ -244,6 +245,45 @@ mr_status mr_affine_matmul(const void* x, mr_dtype x_dtype, int32_t tokens, int6
     g.force_generic = !aligned16(w->packed);  // the fused kernel loads 16-byte row chunks
     const hipError_t e = mr::launch_affine_gemv(g, (hipStream_t)stream);
     return e == hipSuccess ? MR_OK : hip_fail(e, "affine matmul launch");
+}
+
+mr_status mr_affine_gather_matmul(const void* x, mr_dtype x_dtype, int32_t tokens, int64_t x_stride,
+                                  const mr_affine_weight* w, int64_t experts, const int32_t* rhs_indices,
+                                  int32_t experts_per_token, void* y, mr_dtype y_dtype, void* stream) {
+    // AffineWeights.swift:283-318: the reference's preconditions, as errors
+    if (experts <= 0)
+        return fail(MR_INVALID_ARGUMENT,
+                    "affineGatherMM needs a stacked AffineWeights; use affineMM for a single matrix");
+    if (tokens < 0 || experts_per_token <= 0)
+        return fail(MR_INVALID_ARGUMENT, "rhsIndices must be [tokens, expertsPerToken] matching x's token count");
+    mr_status st = check_weight(w, "affine gather matmul");
+    if (st != MR_OK) return st;
+    if (tokens == 0) return MR_OK;
+    if (!x || !y || !rhs_indices)
+        return fail(MR_INVALID_ARGUMENT, "affine gather matmul: x, rhs_indices and y must be non-NULL");
+    if (!act_dtype_ok(x_dtype) || !act_dtype_ok(y_dtype))
+        return fail(MR_INVALID_DTYPE, "affine gather matmul: x and y must be bf16 or f32");
+    if (x_stride < w->in_features)
+        return fail(MR_INVALID_SHAPE, "affine gather matmul: x rows need %lld features", (long long)w->in_features);
+    const int64_t pairs = int64_t(tokens) * experts_per_token;
+    if (w->in_features > INT32_MAX || pairs * w->out_features > INT32_MAX || experts * w->out_features > INT32_MAX)
+        return fail(MR_INVALID_SHAPE, "affine gather matmul: dimensions exceed int32");
+    mr::AffineGemvParams g = gemv_params(w);
+    g.x = x;
+    g.x_f32 = x_dtype == MR_F32;
+    g.x_stride = x_stride;
+    g.x_div = experts_per_token;
+    g.m = 1;
+    g.out_rows = (int)(pairs * w->out_features);  // [tokens][experts_per_token][out]
+    g.rhs_idx = rhs_indices;
+    g.experts = experts;
+    g.y = y;
+    g.y_f32 = y_dtype == MR_F32;
+    g.y_stride_row = 1;
+    g.y_stride_token = g.out_rows;
+    g.force_generic = !aligned16(w->packed);
+    const hipError_t e = mr::launch_affine_gemv(g, (hipStream_t)stream);
+    return e == hipSuccess ? MR_OK : hip_fail(e, "affine gather matmul launch");
 }
 
 mr_status mr_rmsnorm(const void* x, mr_dtype x_dtype, int64_t rows, int32_t dim, int64_t x_stride, const void* weight,

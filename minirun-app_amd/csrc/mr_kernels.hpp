@@ -144,6 +144,12 @@ struct AffineGemvParams {
     int norm_w_f32;
     float norm_eps;
     int tpr, tile_rows, tiles_per_vec;
+    // routed experts (affineGatherMM): activation vector v reads x row
+    // v / x_div and the weight rows of expert rhs_idx[v] (map_a rows each);
+    // an expert id outside [0, experts) gives zeros.  Null = the map above.
+    const int32_t* rhs_idx;
+    int32_t x_div;
+    int64_t experts;
 };
 
 // Lightning-index scores: out[s][t] = sum_h w[s][h] * max(q[s][h] . k[t], 0).

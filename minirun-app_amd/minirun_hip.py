@@ -122,6 +122,8 @@ SIGNATURES = {
     "mr_affine_dequantize": (C.c_int, [C.POINTER(AffineWeightDesc), _P, C.c_int, _P]),
     "mr_affine_matmul": (C.c_int, [_P, C.c_int, C.c_int32, C.c_int64, C.POINTER(AffineWeightDesc), _P, C.c_int,
                                    C.c_int64, _P]),
+    "mr_affine_gather_matmul": (C.c_int, [_P, C.c_int, C.c_int32, C.c_int64, C.POINTER(AffineWeightDesc), C.c_int64,
+                                          _P, C.c_int32, _P, C.c_int, _P]),
     "mr_rmsnorm": (C.c_int, [_P, C.c_int, C.c_int64, C.c_int32, C.c_int64, _P, C.c_int, C.c_float, _P, C.c_int,
                              C.c_int64, _P]),
     "mr_rope_frequencies": (C.c_int, [C.c_int32, C.c_int32, C.c_double, C.c_double, C.c_double, C.c_double, _P]),
@@ -360,6 +362,29 @@ def affine_mm(x, w: AffineWeights, out_dtype=None, stream=None):
     _check(load().mr_affine_matmul(_ptr(x2), _dtype_code(x2.dtype), x2.shape[0], x2.stride(0), C.byref(w.desc()),
                                    _ptr(y), _dtype_code(y.dtype), y.stride(0), _stream(stream)))
     return y if x.dim() == 2 else y.reshape(w.out_features)
+
+
+def affine_gather_mm(x, w: AffineWeights, rhs_indices, out_dtype=None, stream=None):
+    """affineGatherMM (AffineWeights.swift:255-318): x [tokens, in], a
+    stacked w (experts != None), rhs_indices int32 [tokens, experts_per_token]
+    -> [tokens, experts_per_token, out], row (t, j) = W[rhs[t, j]] . x[t].
+    The reference's preconditions raise MRError (INVALID_ARGUMENT)."""
+    torch = _torch()
+    _need(x, "x")
+    experts = w.experts or 0
+    if x.dim() != 2:
+        raise ValueError("x must be [tokens, inFeatures]; this function inserts the broadcast axes itself")
+    if rhs_indices.dim() != 2 or rhs_indices.shape[0] != x.shape[0]:
+        _check(load().mr_affine_gather_matmul(None, 0, -1, 0, C.byref(w.desc()), max(experts, 1), None, 0, None, 0,
+                                              None))  # raises the reference's message
+    if rhs_indices.dtype != torch.int32 or not rhs_indices.is_contiguous():
+        raise ValueError("rhs_indices must be contiguous int32")
+    T, K = rhs_indices.shape
+    y = torch.empty(T, K, w.out_features, dtype=out_dtype or x.dtype, device=x.device)
+    _check(load().mr_affine_gather_matmul(_ptr(x), _dtype_code(x.dtype), T, x.stride(0) if T else w.in_features,
+                                          C.byref(w.desc()), experts, _ptr(rhs_indices), K, _ptr(y),
+                                          _dtype_code(y.dtype), _stream(stream)))
+    return y
 
 
 def rms_norm(x, weight, eps=1e-6, out_dtype=None, stream=None):

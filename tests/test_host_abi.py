@@ -166,3 +166,17 @@ def test_indexer_scores_no_keys_and_dtypes():
     assert _scores_call(2, 4, 8, 0, 8, 2, 4) == 0
     st = _scores_call(2, 4, 8, 0, 8, 2, 4, qdt=M.F16)
     assert st == O.INVALID_DTYPE and "bf16 or f32" in M.last_error()
+
+
+# ---------------------------------------------------------------- routed experts
+def test_affine_gather_preconditions():
+    """AffineWeights.swift:290-298: the reference traps on a single matrix and
+    on indices that do not match the token count; the ABI returns those
+    messages as MR_INVALID_ARGUMENT before any work."""
+    w = M.AffineWeightDesc(256, 256, 256, M.BF16, 8, 64, 64, 4)  # dummy aligned pointers: never dereferenced
+    st = M.load().mr_affine_gather_matmul(None, M.BF16, 1, 64, C.byref(w), 0, None, 1, None, M.BF16, None)
+    assert st == M.INVALID_ARGUMENT and "needs a stacked AffineWeights" in M.last_error()
+    st = M.load().mr_affine_gather_matmul(None, M.BF16, 1, 64, C.byref(w), 4, None, 0, None, M.BF16, None)
+    assert st == M.INVALID_ARGUMENT and "rhsIndices must be [tokens, expertsPerToken]" in M.last_error()
+    # no tokens: nothing to do
+    assert M.load().mr_affine_gather_matmul(None, M.BF16, 0, 64, C.byref(w), 4, None, 2, None, M.BF16, None) == 0
