@@ -83,3 +83,25 @@ def test_prefill_rejects_bad_arguments_before_any_gpu_call():
     assert lib.mr_mla_prefill(C.byref(a), None) == M.INVALID_ARGUMENT  # NULL pointers
     assert lib.mr_mla_prefill(None, None) == M.INVALID_ARGUMENT
     assert lib.mr_mla_prefill_workspace_size(C.byref(a)) == 4096 * 128 * 512
+
+
+def test_header_compiles_as_c_and_host_entry_points_work_from_c(tmp_path):
+    """include/minirun_hip.h as a C11 translation unit (what a Swift module
+    map imports): a C program links the library and checks the host-side
+    entry points.  Built in a temporary directory; no GPU call."""
+    import shutil
+    import subprocess
+
+    cc = shutil.which("gcc") or shutil.which("cc")
+    if cc is None:
+        pytest.skip("no C compiler")
+    lib_dir = os.path.dirname(M.LIB_PATH)
+    exe = str(tmp_path / "abi_from_c")
+    src = os.path.join(ROOT, "tests", "c_abi", "abi_from_c.c")
+    r = subprocess.run([cc, "-std=c11", "-Wall", "-Wextra", "-Werror", "-pedantic", "-I", os.path.join(ROOT, "include"),
+                        src, "-o", exe, "-L", lib_dir, "-lminirun_hip", f"-Wl,-rpath,{lib_dir}"],
+                       capture_output=True, text=True)
+    assert r.returncode == 0, r.stderr
+    r = subprocess.run([exe], capture_output=True, text=True, timeout=60)
+    assert r.returncode == 0, r.stdout + r.stderr
+    assert "abi_from_c: ok" in r.stdout
