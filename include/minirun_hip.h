@@ -172,6 +172,19 @@ mr_status mr_affine_matmul(const void *x, mr_dtype x_dtype, int32_t tokens, int6
                            const mr_affine_weight *w, void *y, mr_dtype y_dtype, int64_t y_stride,
                            void *stream);
 
+/* Fixed-buffer hand-off of a StorageCore affine tile (QuantizedTileContainer
+ * .swift:219-343; layout rules :496-640): one slot holds [packed | scales |
+ * biases] for `rows` output rows of `cols` inputs, each sub-region a whole
+ * number of 16 KiB units, so each can be adopted as its own operand without
+ * a copy.  mr_affine_tile_view fills an mr_affine_weight over the slot's
+ * bytes (pinned host memory the device reads, or device memory) and the
+ * slot size; the geometry errors are the container's.  mr_tile_upload
+ * copies a slot from pinned host memory to device memory on the stream
+ * (asynchronous; the host slot must stay alive until the stream reaches it). */
+mr_status mr_affine_tile_view(const void *tile, int64_t rows, int64_t cols, int32_t group, int32_t bits,
+                              mr_dtype scale_dtype, mr_affine_weight *out, int64_t *tile_bytes);
+mr_status mr_tile_upload(void *device_dst, const void *pinned_src, int64_t bytes, void *stream);
+
 /* affineGatherMM (AffineWeights.swift:255-318): routed experts,
  * y[t, j, :] = x[t, :] . dequant(W[rhs[t, j]])^T.  w describes one expert
  * (out_features x in_features) of a stack of `experts` laid out back to back

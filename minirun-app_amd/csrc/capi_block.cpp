@@ -247,6 +247,64 @@ mr_status mr_affine_matmul(const void* x, mr_dtype x_dtype, int32_t tokens, int6
     return e == hipSuccess ? MR_OK : hip_fail(e, "affine matmul launch");
 }
 
+mr_status mr_affine_tile_view(const void* tile, int64_t rows, int64_t cols, int32_t group, int32_t bits,
+                              mr_dtype scale_dtype, mr_affine_weight* out, int64_t* tile_bytes) {
+    // QuantizedTileContainer.swift:560-620, affine mode, one scale row per row
+    constexpr int64_t kAlign = 16384;
+    if (!out) return fail(MR_INVALID_ARGUMENT, "affine tile view: out is NULL");
+    if (rows <= 0 || cols <= 0 || group <= 0 || bits <= 0 || 32 % bits != 0)
+        return fail(MR_INVALID_SHAPE, "affine tile view: rows %lld, cols %lld, group %d, bits %d", (long long)rows,
+                    (long long)cols, group, bits);
+    if (!is_float_dtype(scale_dtype))
+        return fail(MR_INVALID_DTYPE, "affine scales are a floating-point type; e8m0 is an MX encoding");
+    if (cols % group != 0)
+        return fail(MR_INVALID_SHAPE,
+                    "cols %lld must be a multiple of the group size %d; partial final groups are not supported",
+                    (long long)cols, group);
+    const int per_word = 32 / bits;
+    if (cols % per_word != 0)
+        return fail(MR_INVALID_SHAPE, "cols %lld must be a multiple of %d (%d %d-bit elements per uint32)",
+                    (long long)cols, per_word, per_word, bits);
+    const int64_t packed_bytes = rows * cols * bits / 8;
+    const int64_t scale_bytes = rows * (cols / group) * (scale_dtype == MR_F32 ? 4 : 2);
+    if (packed_bytes % kAlign != 0)
+        return fail(MR_INVALID_SHAPE,
+                    "packed bytes per tile (%lld) must be a multiple of %lld so the scale sub-region starts aligned "
+                    "and can be adopted as its own zero-copy array; try rows*cols*bits divisible by %lld",
+                    (long long)packed_bytes, (long long)kAlign, (long long)kAlign * 8);
+    if (scale_bytes % kAlign != 0)
+        return fail(MR_INVALID_SHAPE,
+                    "scale bytes per tile (%lld) must be a multiple of %lld; try rows*cols divisible by %lld",
+                    (long long)scale_bytes, (long long)kAlign,
+                    (long long)(kAlign * group / (scale_dtype == MR_F32 ? 4 : 2)));
+    if (!tile) return fail(MR_INVALID_ARGUMENT, "affine tile view: tile is NULL");
+    const char* base = (const char*)tile;
+    out->packed = (const uint32_t*)base;
+    out->scales = base + packed_bytes;
+    out->biases = base + packed_bytes + scale_bytes;
+    out->scale_dtype = scale_dtype;
+    out->out_features = rows;
+    out->in_features = cols;
+    out->group = group;
+    out->bits = bits;
+    if (tile_bytes) *tile_bytes = packed_bytes + 2 * scale_bytes;
+    return MR_OK;
+}
+
+mr_status mr_tile_upload(void* device_dst, const void* pinned_src, int64_t bytes, void* stream) {
+    if (bytes < 0) return fail(MR_INVALID_ARGUMENT, "tile upload: negative size");
+    if (bytes == 0) return MR_OK;
+    if (!device_dst || !pinned_src) return fail(MR_INVALID_ARGUMENT, "tile upload: NULL pointer");
+    hipPointerAttribute_t at{};
+    if (hipPointerGetAttributes(&at, pinned_src) != hipSuccess || at.type != hipMemoryTypeHost) {
+        (void)hipGetLastError();  // clear the query's error for the next call
+        return fail(MR_INVALID_ARGUMENT, "tile upload: the source is not pinned host memory");
+    }
+    const hipError_t e = hipMemcpyAsync(device_dst, pinned_src, size_t(bytes), hipMemcpyHostToDevice,
+                                        (hipStream_t)stream);
+    return e == hipSuccess ? MR_OK : hip_fail(e, "tile upload");
+}
+
 mr_status mr_affine_gather_matmul(const void* x, mr_dtype x_dtype, int32_t tokens, int64_t x_stride,
                                   const mr_affine_weight* w, int64_t experts, const int32_t* rhs_indices,
                                   int32_t experts_per_token, void* y, mr_dtype y_dtype, void* stream) {

@@ -122,6 +122,9 @@ SIGNATURES = {
     "mr_affine_dequantize": (C.c_int, [C.POINTER(AffineWeightDesc), _P, C.c_int, _P]),
     "mr_affine_matmul": (C.c_int, [_P, C.c_int, C.c_int32, C.c_int64, C.POINTER(AffineWeightDesc), _P, C.c_int,
                                    C.c_int64, _P]),
+    "mr_affine_tile_view": (C.c_int, [_P, C.c_int64, C.c_int64, C.c_int32, C.c_int32, C.c_int,
+                                      C.POINTER(AffineWeightDesc), C.POINTER(C.c_int64)]),
+    "mr_tile_upload": (C.c_int, [_P, _P, C.c_int64, _P]),
     "mr_affine_gather_matmul": (C.c_int, [_P, C.c_int, C.c_int32, C.c_int64, C.POINTER(AffineWeightDesc), C.c_int64,
                                           _P, C.c_int32, _P, C.c_int, _P]),
     "mr_rmsnorm": (C.c_int, [_P, C.c_int, C.c_int64, C.c_int32, C.c_int64, _P, C.c_int, C.c_float, _P, C.c_int,
@@ -362,6 +365,15 @@ def affine_mm(x, w: AffineWeights, out_dtype=None, stream=None):
     _check(load().mr_affine_matmul(_ptr(x2), _dtype_code(x2.dtype), x2.shape[0], x2.stride(0), C.byref(w.desc()),
                                    _ptr(y), _dtype_code(y.dtype), y.stride(0), _stream(stream)))
     return y if x.dim() == 2 else y.reshape(w.out_features)
+
+
+def affine_tile_view(tile_ptr, rows, cols, group=64, bits=4, scale_dtype=BF16):
+    """A StorageCore affine tile [packed | scales | biases] (QuantizedTileContainer
+    .swift:219-343) as a weight descriptor over its bytes, and the tile size."""
+    d = AffineWeightDesc()
+    n = C.c_int64()
+    _check(load().mr_affine_tile_view(tile_ptr, rows, cols, group, bits, scale_dtype, C.byref(d), C.byref(n)))
+    return d, n.value
 
 
 def affine_gather_mm(x, w: AffineWeights, rhs_indices, out_dtype=None, stream=None):

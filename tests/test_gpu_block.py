@@ -144,6 +144,37 @@ def test_affine_gemv_fast_path_edges(M, out_f, in_f, sdt):
     check(f32(y), ref, f"gemv-fast-{out_f}x{in_f}-{sdt}", scale_bar=1e-4)
 
 
+def test_storage_tile_handoff(M):
+    """A StorageCore tile [packed | scales | biases] in pinned host memory,
+    uploaded to HBM as one slot and viewed as a weight without a copy: the
+    GEMV over the view equals the GEMV over separately allocated operands
+    bit for bit (same kernel, same bytes)."""
+    print("tile hand-off: 512 x 1024 4-bit tile, pinned -> HBM -> view", flush=True)
+    import ctypes as C
+    import torch
+
+    rows, cols = 512, 1024
+    w = MI.affine_weight("tile.w", rows, cols)
+    slot = np.concatenate([w[0].view(np.uint8).ravel(), w[1].view(np.uint8).ravel(), w[2].view(np.uint8).ravel()])
+    host = torch.from_numpy(slot).pin_memory()
+    dev_slot = torch.empty(slot.size, dtype=torch.uint8, device="cuda")
+    sp = M._stream(torch.cuda.current_stream())
+    M._check(M.load().mr_tile_upload(dev_slot.data_ptr(), host.data_ptr(), slot.size, sp))
+    d, n = M.affine_tile_view(dev_slot.data_ptr(), rows, cols)
+    assert n == slot.size
+    x = O.normal_bf16("tile.x", (cols,))
+    xd = dev(x)
+    y_view = torch.empty(1, rows, dtype=torch.float32, device="cuda")
+    M._check(M.load().mr_affine_matmul(xd.data_ptr(), M.BF16, 1, cols, C.byref(d), y_view.data_ptr(), M.F32, rows,
+                                       sp))
+    y_sep = M.affine_mm(xd, weights(M, w), out_dtype=torch.float32)
+    sync()
+    assert torch.equal(y_view[0], y_sep)
+    # a pageable (not pinned) source is refused
+    st = M.load().mr_tile_upload(dev_slot.data_ptr(), slot.ctypes.data, slot.size, sp)
+    assert st == M.INVALID_ARGUMENT and "not pinned" in M.last_error()
+
+
 def test_affine_matmul_generic_paths(M):
     print("gemv generic: 3 tokens, f32 x, 8-bit, f16 scales", flush=True)
     import torch

@@ -180,3 +180,23 @@ def test_affine_gather_preconditions():
     assert st == M.INVALID_ARGUMENT and "rhsIndices must be [tokens, expertsPerToken]" in M.last_error()
     # no tokens: nothing to do
     assert M.load().mr_affine_gather_matmul(None, M.BF16, 0, 64, C.byref(w), 4, None, 2, None, M.BF16, None) == 0
+
+
+# ---------------------------------------------------------------- StorageCore tile hand-off
+def test_affine_tile_view_layout_and_errors():
+    """QuantizedTileContainer.swift:560-620 (affine, one scale row per row):
+    [packed | scales | biases], each a whole number of 16 KiB."""
+    base = 1 << 20  # never dereferenced
+    d, n = M.affine_tile_view(base, 512, 1024)
+    assert (d.packed, d.scales, d.biases) == (base, base + 262144, base + 262144 + 16384)
+    assert (d.out_features, d.in_features, d.group, d.bits, n) == (512, 1024, 64, 4, 262144 + 2 * 16384)
+    d, n = M.affine_tile_view(base, 256, 1024, scale_dtype=M.F32)  # f32 scales: 16 KiB from 256 rows
+    assert d.scales == base + 131072 and n == 131072 + 2 * 16384
+    for args, needle in [((512, 1000), "multiple of the group size"),
+                         ((16, 1024), "packed bytes per tile (8192) must be a multiple of 16384"),
+                         ((256, 1024), "scale bytes per tile (8192) must be a multiple of 16384")]:
+        with pytest.raises(M.MRError) as e:
+            M.affine_tile_view(base, *args)
+        assert needle in e.value.message, e.value.message
+    with pytest.raises(M.MRError):
+        M.affine_tile_view(base, 512, 1024, scale_dtype=M.U32)
