@@ -41,11 +41,15 @@ __device__ __forceinline__ uint32_t ordered_bits(float f) {
 template <int NT>
 __device__ __forceinline__ uint32_t block_scan_incl(uint32_t v, uint32_t* sh) {
     const int l = threadIdx.x & 63, w = threadIdx.x >> 6;
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-        const uint32_t t = __shfl_up(v, o);
-        if (l >= o) v += t;
-    }
+    // wave scan on DPP: row_shr 1, 2, 4, 8 inside rows of 16 lanes (lanes
+    // shifted in from outside the row add 0), then row_bcast 15 / 31 carry
+    // each row's total into the rows above it
+    v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x111, 0xf, 0xf, true);
+    v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x112, 0xf, 0xf, true);
+    v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x114, 0xf, 0xf, true);
+    v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x118, 0xf, 0xf, true);
+    v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x142, 0xa, 0xf, false);
+    v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x143, 0xc, 0xf, false);
     if (l == 63) sh[w] = v;
     __syncthreads();
     uint32_t base = 0;
