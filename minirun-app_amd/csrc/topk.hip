@@ -38,18 +38,23 @@ __device__ __forceinline__ uint32_t ordered_bits(float f) {
 
 // Inclusive scan of one value per thread over the block; `sh` holds one
 // word per wave.  Every thread of the block must call it.
-template <int NT>
-__device__ __forceinline__ uint32_t block_scan_incl(uint32_t v, uint32_t* sh) {
-    const int l = threadIdx.x & 63, w = threadIdx.x >> 6;
-    // wave scan on DPP: row_shr 1, 2, 4, 8 inside rows of 16 lanes (lanes
-    // shifted in from outside the row add 0), then row_bcast 15 / 31 carry
-    // each row's total into the rows above it
+// Inclusive scan over the 64 lanes of a wave on DPP: row_shr 1, 2, 4, 8
+// inside rows of 16 lanes (lanes shifted in from outside the row add 0),
+// then row_bcast 15 / 31 carry each row's total into the rows above it.
+__device__ __forceinline__ uint32_t wave_scan_incl(uint32_t v) {
     v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x111, 0xf, 0xf, true);
     v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x112, 0xf, 0xf, true);
     v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x114, 0xf, 0xf, true);
     v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x118, 0xf, 0xf, true);
     v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x142, 0xa, 0xf, false);
     v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x143, 0xc, 0xf, false);
+    return v;
+}
+
+template <int NT>
+__device__ __forceinline__ uint32_t block_scan_incl(uint32_t v, uint32_t* sh) {
+    const int l = threadIdx.x & 63, w = threadIdx.x >> 6;
+    v = wave_scan_incl(v);
     if (l == 63) sh[w] = v;
     __syncthreads();
     uint32_t base = 0;
@@ -63,8 +68,9 @@ constexpr unsigned long long TK_NONE = ~0ull;  // padding: past every composite
 
 template <int NT, int KPT>
 __global__ void __launch_bounds__(NT) topk_select_kernel(TopkParams p) {
-    constexpr int BPT = TK_BINS / NT;  // histogram bins per thread in the scan
-    __shared__ uint32_t hist[TK_BINS];
+    // two histograms: a pass counts into one while the other is cleared for
+    // the next pass
+    __shared__ __attribute__((aligned(16))) uint32_t hist[2][TK_BINS];
     __shared__ uint32_t scan_sh[NT / 64];
     __shared__ uint32_t pick[3];  // bin, count before it, count in it
     __shared__ unsigned long long comp[TOPK_MAX];
@@ -101,6 +107,8 @@ __global__ void __launch_bounds__(NT) topk_select_kernel(TopkParams p) {
     // 15..8, 7..0 (all in 32-bit arithmetic)
     uint32_t dimg = 0, dkey = 0;
     uint32_t remaining = (uint32_t)k;  // rank of D among the still-matching composites
+    for (int i = tid; i < TK_BINS; i += NT) hist[0][i] = 0;
+    __syncthreads();
 #pragma unroll 1
     for (int pass = 0; pass < 5; ++pass) {
         const bool on_img = pass < 3;
@@ -108,40 +116,57 @@ __global__ void __launch_bounds__(NT) topk_select_kernel(TopkParams p) {
         const int wd = pass == 0 ? 11 : pass == 1 ? 11 : pass == 2 ? 10 : 8;
         const int top = sh + wd;  // bits at and above `top` of the current field are fixed
         const uint32_t fixed = top >= 32 ? 0u : (0xffffffffu << top);  // no shift by 32
-        for (int i = tid; i < TK_BINS; i += NT) hist[i] = 0;
-        __syncthreads();
+        uint32_t* hc = hist[pass & 1];
+        for (int i = tid; i < TK_BINS; i += NT) hist[(pass & 1) ^ 1][i] = 0;  // the next pass's
         if (pass == 0) {
             // every key counts: no branch, padding keys add 0
 #pragma unroll
-            for (int j = 0; j < KPT; ++j) atomicAdd(&hist[img[j] >> 21], valid(j) ? 1u : 0u);
+            for (int j = 0; j < KPT; ++j) atomicAdd(&hc[img[j] >> 21], valid(j) ? 1u : 0u);
         } else if (on_img) {
 #pragma unroll
             for (int j = 0; j < KPT; ++j)
-                if (valid(j) && ((img[j] ^ dimg) & fixed) == 0u) atomicAdd(&hist[(img[j] >> sh) & ((1u << wd) - 1u)], 1u);
+                if (valid(j) && ((img[j] ^ dimg) & fixed) == 0u) atomicAdd(&hc[(img[j] >> sh) & ((1u << wd) - 1u)], 1u);
         } else {
 #pragma unroll
             for (int j = 0; j < KPT; ++j) {
                 const uint32_t key = (uint32_t)(NT * j + tid);
                 if (valid(j) && img[j] == dimg && ((key ^ dkey) & fixed) == 0u)
-                    atomicAdd(&hist[(key >> sh) & ((1u << wd) - 1u)], 1u);
+                    atomicAdd(&hc[(key >> sh) & ((1u << wd) - 1u)], 1u);
             }
         }
         __syncthreads();
-        uint32_t h[BPT], sum = 0;
+        // wave 0 finds the bin where the running count reaches `remaining`:
+        // lane l sums bins 32l .. 32l+31, a wave scan places the lanes, and
+        // the one lane whose range crosses the rank walks its bins
+        if (tid < 64) {
+            uint32_t tot = 0;
 #pragma unroll
-        for (int b = 0; b < BPT; ++b) {
-            h[b] = hist[BPT * tid + b];
-            sum += h[b];
-        }
-        uint32_t before = block_scan_incl<NT>(sum, scan_sh) - sum;
-#pragma unroll
-        for (int b = 0; b < BPT; ++b) {
-            if (before < remaining && before + h[b] >= remaining) {
-                pick[0] = (uint32_t)(BPT * tid + b);
-                pick[1] = before;
-                pick[2] = h[b];
+            for (int i = 0; i < 8; ++i) {
+                const u32x4 q = *(const u32x4*)(hc + 32 * tid + 4 * i);
+                tot += (q[0] + q[1]) + (q[2] + q[3]);
             }
-            before += h[b];
+            const uint32_t incl = wave_scan_incl(tot);
+            uint32_t before = incl - tot;
+            if (before < remaining && remaining <= incl) {
+                // this lane's range holds the crossing: walk it, four bins a read
+#pragma unroll 1
+                for (int i = 0; i < 8; ++i) {
+                    const u32x4 q = *(const u32x4*)(hc + 32 * tid + 4 * i);
+                    const uint32_t q4 = (q[0] + q[1]) + (q[2] + q[3]);
+                    if (before + q4 >= remaining) {
+                        int b = 0;
+                        uint32_t cb = q[0];
+                        if (before + cb < remaining) { before += cb; b = 1; cb = q[1]; }
+                        if (b == 1 && before + cb < remaining) { before += cb; b = 2; cb = q[2]; }
+                        if (b == 2 && before + cb < remaining) { before += cb; b = 3; cb = q[3]; }
+                        pick[0] = (uint32_t)(32 * tid + 4 * i + b);
+                        pick[1] = before;
+                        pick[2] = cb;
+                        break;
+                    }
+                    before += q4;
+                }
+            }
         }
         __syncthreads();
         if (on_img)
@@ -150,7 +175,6 @@ __global__ void __launch_bounds__(NT) topk_select_kernel(TopkParams p) {
             dkey |= pick[0] << sh;
         remaining -= pick[1];
         const uint32_t in_bin = pick[2];
-        __syncthreads();
         // image complete and every key with that image is taken: D's key
         // part is past them all (ties need the key digits)
         if (pass == 2 && remaining == in_bin) {
