@@ -608,12 +608,19 @@ mr_status mr_mla_decode_block(const mr_mla_block_args* a, void* stream) {
         return st;
     if ((st = block_gemv(q_lora, a->q_lora_rank, &a->q_b, q, a->q_a_norm_w, nd, a->eps, q_lora_n, stream)) != MR_OK)
         return st;
-    if ((st = mr_rope_apply(q, MR_BF16, 1, a->heads, dq, a->qk_nope_dim, a->qk_rope_dim, a->rope_cos, a->rope_sin,
-                            stream)) != MR_OK)
-        return st;
-    if ((st = mr_mla_absorb_query(q, dq, a->heads, a->qk_nope_dim, a->v_head_dim, &a->kv_b, q_lat, a->kv_rank,
-                                  stream)) != MR_OK)
-        return st;
+    // query rotary + absorb W_UK in one launch (the rotation touches only
+    // the rope columns, the absorption reads only the nope columns)
+    if ((st = check_kv_b(&a->kv_b, a->heads, a->qk_nope_dim, a->v_head_dim)) != MR_OK) return st;
+    {
+        mr::AbsorbParams ap{(const uint16_t*)q, dq, a->kv_b.packed, a->kv_b.scales, a->kv_b.biases,
+                            scale_code(a->kv_b.scale_dtype), a->heads, a->qk_nope_dim, a->v_head_dim, 512,
+                            (uint16_t*)q_lat, a->kv_rank};
+        ap.rope_cos = a->rope_cos;
+        ap.rope_sin = a->rope_sin;
+        ap.rope_dim = a->qk_rope_dim;
+        ap.rope_col0 = a->qk_nope_dim;
+        if ((he = mr::launch_absorb_q(ap, (hipStream_t)stream)) != hipSuccess) return hip_fail(he, "absorb launch");
+    }
     // attend once the key path has written the cache row
     if ((he = hipStreamWaitEvent((hipStream_t)stream, side->join, 0)) != hipSuccess)
         return hip_fail(he, "mla block: join");

@@ -164,6 +164,15 @@ __global__ void __launch_bounds__(256) absorb_q_fast_kernel(AbsorbParams p) {
     const int w = t >> 6, l = t & 63;
     const int rs = l >> 3, wq = l & 7;
     const int64_t row0 = (int64_t)h * (p.nope_dim + p.v_dim);
+    if (p.rope_cos && half == 0 && t < p.rope_dim / 2) {
+        // this head's rotary part, in place (the block reads only the nope
+        // part): the arithmetic of rope_kernel at one position
+        uint16_t* xr = (uint16_t*)p.q + (int64_t)h * p.q_head_stride + p.rope_col0 + 2 * t;
+        const float e = bf16_bits_to_f32(xr[0]), o = bf16_bits_to_f32(xr[1]);
+        const float c = p.rope_cos[t], sn = p.rope_sin[t];
+        xr[0] = f32_to_bf16_bits(sub_rn(mul_rn(e, c), mul_rn(o, sn)));
+        xr[1] = f32_to_bf16_bits(add_rn(mul_rn(e, sn), mul_rn(o, c)));
+    }
     // weights first: they do not depend on the staging
     u32x4 wd[4];
 #pragma unroll
@@ -256,8 +265,25 @@ hipError_t launch_cache_append(const CacheAppendParams& p, hipStream_t st) {
 
 hipError_t launch_absorb_q(const AbsorbParams& p, hipStream_t st) {
     const int sz = p.scale_dtype == 2 ? 4 : 2;
-    if (p.kv_rank == 512 && p.nope_dim == 128 && ((uintptr_t)p.packed & 15) == 0 &&
-        ((uintptr_t)p.scales & (2 * sz - 1)) == 0 && ((uintptr_t)p.biases & (2 * sz - 1)) == 0) {
+    const bool fast = p.kv_rank == 512 && p.nope_dim == 128 && ((uintptr_t)p.packed & 15) == 0 &&
+                      ((uintptr_t)p.scales & (2 * sz - 1)) == 0 && ((uintptr_t)p.biases & (2 * sz - 1)) == 0;
+    if (p.rope_cos && (!fast || p.rope_dim > 512)) {  // the rotation as its own launch
+        RopeParams r{};
+        r.x = (void*)p.q;
+        r.n_pos = 1;
+        r.inner = p.heads;
+        r.row_stride = p.q_head_stride;
+        r.col0 = p.rope_col0;
+        r.dim = p.rope_dim;
+        r.cos_t = p.rope_cos;
+        r.sin_t = p.rope_sin;
+        const hipError_t e = launch_rope(r, st);
+        if (e != hipSuccess) return e;
+        AbsorbParams q = p;
+        q.rope_cos = q.rope_sin = nullptr;
+        return launch_absorb_q(q, st);
+    }
+    if (fast) {
         const dim3 grid((unsigned)p.heads * 2);
         if (p.scale_dtype == 0)
             hipLaunchKernelGGL(absorb_q_fast_kernel<0>, grid, dim3(256), 0, st, p);

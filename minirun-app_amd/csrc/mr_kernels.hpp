@@ -227,6 +227,12 @@ struct AbsorbParams {
     int heads, nope_dim, v_dim, kv_rank;
     uint16_t* q_lat;
     int64_t q_lat_head_stride;
+    // optional: rotate each head's rotary part (one position, adjacent pairs,
+    // cos/sin [rope_dim/2]) in place in the same launch; null = none
+    const float* rope_cos;
+    const float* rope_sin;
+    int rope_dim;
+    int64_t rope_col0;
 };
 
 hipError_t launch_rmsnorm(const RmsNormParams& p, hipStream_t st);
