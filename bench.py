@@ -481,7 +481,8 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported "
-              "(the decode path is single-GPU; context sharding is described in DESIGN.md)", file=sys.stderr)
+              "(the decode path runs on one GPU; sharding the context across GPUs is a design sketch, not built)",
+              file=sys.stderr)
         sys.exit(2)
 
     import torch

@@ -4,8 +4,8 @@
  * A drop-in for the MLX calls that Minirun's attention hot path makes.  Each
  * entry point names the reference interface it replaces (paths relative to
  * the nanguoyu/minirun-app tree).  The Swift side binds this header through a
- * module map (a HIPBridge module shaped like MLXBridge); INTEGRATION.md shows
- * that binding.
+ * module map (a HIPBridge module shaped like MLXBridge); every declaration
+ * is plain C11.
  *
  * Conventions
  *  - Every tensor is caller-owned device memory, passed as a plain pointer
