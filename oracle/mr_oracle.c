@@ -1,7 +1,8 @@
 /*
  * mr_oracle.c -- CPU restatement of the Minirun MLA attention path.
  *
- * TEST INFRASTRUCTURE ONLY (the checker, never the product): see mr_oracle.h.
+ * TEST INFRASTRUCTURE ONLY (the tests check the library against it; it is
+ * never part of the product): see mr_oracle.h.
  * Build: oracle/Makefile (gcc -O2 -fopenmp -ffp-contract=off).
  *
  * Pinning status, by function (the tests that pin each one are named in

@@ -70,7 +70,7 @@ def within_block_tolerance(got, ref, rtol=2e-2, scale_tol=1e-2):
     return bool(ok), float(err.max()), float(err.max() / top)
 
 
-# ---------------------------------------------------------------- config 5: the block
+# ---------------------------------------------------------------- the decode block workload
 def affine_weight(tag, out, inp, group=64, centred=False):
     """MLX affine 4-bit operand, bf16 scales and biases.
 

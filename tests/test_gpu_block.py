@@ -1,7 +1,7 @@
 """Parity of the HIP projection path against the oracle: affine dequantize
 (bit-exact in f32), the fused dequant-GEMV (tolerance), RMSNorm, RoPE,
 the latent-cache append, query absorption / value un-absorption and the
-whole decode block of the fifth workload (hidden 7168, 128 heads, 32K
+whole decode block workload (hidden 7168, 128 heads, 32K
 context, 4-bit group-64 affine projections).
 
 Bars: bit-exact where the arithmetic is exact or identical by construction
@@ -102,7 +102,7 @@ def test_dequantize_bit_exact(M, bits, group, sdt):
 @pytest.mark.parametrize("centred", [False, True])
 @pytest.mark.parametrize("name,out_f,in_f", [("q_a", 1536, 7168), ("q_b", 24576, 1536), ("kv_a", 576, 7168),
                                              ("o_proj", 7168, 16384), ("kv_b", 32768, 512)])
-def test_affine_gemv_config5_shapes(M, name, out_f, in_f, centred):
+def test_affine_gemv_block_shapes(M, name, out_f, in_f, centred):
     print(f"gemv {name} {out_f}x{in_f} centred={centred}", flush=True)
     import torch
 
@@ -284,15 +284,15 @@ def check_block(got, ref, tag):
 
 
 @pytest.mark.parametrize("centred", [False, True])
-def test_block_config5_full(M, centred):
-    print(f"block config5 hidden=7168 H=128 ctx=32768 centred={centred}", flush=True)
+def test_block_full(M, centred):
+    print(f"block hidden=7168 H=128 ctx=32768 centred={centred}", flush=True)
     d = MI.block_inputs(centred=centred)
     out, cache = run_block(M, d)
     ref, row = MI.block_reference(d)
     got_row = bits16(cache)[d["position"]]
     np.testing.assert_array_equal(got_row[512:], row[512:])   # rotary key: bit-exact
     assert np.abs(got_row[:512].astype(np.int32) - row[:512].astype(np.int32)).max() <= 1
-    check_block(f32(out), ref, f"block-config5{'-centred' if centred else ''}")
+    check_block(f32(out), ref, f"block-full{'-centred' if centred else ''}")
 
 
 def test_block_small_context_and_first_token(M):

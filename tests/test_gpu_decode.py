@@ -53,22 +53,22 @@ def run_decode(M, q_lat, q_rope, cache, **kw):
     return out
 
 
-def test_config1_decode_16_heads_512_ctx(M):
-    print("decode config1 H=16 N=512", flush=True)
+def test_decode_16_heads_512_ctx(M):
+    print("decode H=16 N=512", flush=True)
     ql, qr, cache = MI.decode_inputs(16, 512, tag="c1", rope=False)
     ref = O.mla_decode(ql, qr, cache)[0]
     out = run_decode(M, ql, qr, cache)
-    check(host_f32(out)[0], ref, "config1")
+    check(host_f32(out)[0], ref, "decode-16x512")
 
 
-def test_config2_decode_128_heads_32k(M):
-    print("decode config2 H=128 N=32768", flush=True)
+def test_decode_128_heads_32k(M):
+    print("decode H=128 N=32768", flush=True)
     ql, qr, cache = MI.decode_inputs(128, 32768, tag="c2")
     ref = O.mla_decode(ql, qr, cache)[0]
     out = run_decode(M, ql, qr, cache)
-    check(host_f32(out)[0], ref, "config2")
+    check(host_f32(out)[0], ref, "decode-128x32768")
     out32 = run_decode(M, ql, qr, cache, out_dtype=__import__("torch").float32)
-    check(host_f32(out32)[0], ref, "config2-f32", scale_bar=2e-3)
+    check(host_f32(out32)[0], ref, "decode-128x32768-f32", scale_bar=2e-3)
 
 
 def test_bf16_output_tracks_f32_output(M):
@@ -157,13 +157,13 @@ def run_sparse(M, q_lat, q_rope, cache, idx, sinks=None, **kw):
     return out
 
 
-def test_config4_sparse_top2048_128k(M):
-    print("sparse config4 B=4 H=128 N=131072 K=2048", flush=True)
+def test_sparse_top2048_128k(M):
+    print("sparse B=4 H=128 N=131072 K=2048", flush=True)
     ql, qr, cache, idx = MI.sparse_inputs(4, 128, 131072, 2048)
     st, ref = O.sparse_attention(ql, qr, cache, idx)
     assert st == O.OK
     out = run_sparse(M, ql, qr, cache, idx)
-    check(host_f32(out), ref, "config4")
+    check(host_f32(out), ref, "sparse-4x2048")
 
 
 def test_sparse_sentinels_sinks_and_empty(M):

@@ -109,10 +109,10 @@ def test_prefill_first_query_is_first_value(M):
     np.testing.assert_allclose(got[0], v0.reshape(8, 128), rtol=8e-3, atol=1e-6)
 
 
-def test_prefill_config3_sampled(M):
+def test_prefill_4096_tokens_128_heads_sampled(M):
     T = P = 4096
     H = 128
-    print(f"prefill config3 T={T} H={H}", flush=True)
+    print(f"prefill T={T} H={H}", flush=True)
     q, cache, w_uk, w_uv, kv_b = prefill_inputs(T, P, H, "c3")
     got = run(M, q, cache, kv_b)
     assert np.isfinite(got).all()
@@ -121,4 +121,4 @@ def test_prefill_config3_sampled(M):
     t, h = np.meshgrid(rows, heads, indexing="ij")
     st, sh = t.ravel().astype(np.int32), h.ravel().astype(np.int32)
     ref = O.mla_prefill_rows(q, cache, w_uk, w_uv, st, sh, round_kv=True)
-    check_rows(got[st, sh], ref, "prefill-config3")
+    check_rows(got[st, sh], ref, "prefill-4096x128")

@@ -44,7 +44,7 @@ def test_decode_matches_numpy_fp64_and_fp32_path():
     np.testing.assert_allclose(got32, ref, rtol=1e-4, atol=1e-5)
 
 
-def test_decode_config1_shape():
+def test_decode_16_heads_512_ctx_shape():
     ql = O.normal_bf16("c1.q_lat", (16, 512))
     qr = O.normal_bf16("c1.q_rope", (16, 64))
     cache = O.normal_bf16("c1.cache", (512, 576), std=0.5)

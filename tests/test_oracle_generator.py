@@ -146,7 +146,7 @@ def test_sparse_indices_structure_and_fisher_yates():
 
 
 def test_sparse_indices_full_config_shape():
-    idx = O.sparse_topk_indices("cfg4.idx.0", 131072, 2048, 128)
+    idx = O.sparse_topk_indices("sparse.idx.0", 131072, 2048, 128)
     assert idx.size == 2048 and (np.diff(idx) > 0).all()
     assert idx[-128:].tolist() == list(range(130944, 131072))
     assert idx[:1920].max() < 130944
