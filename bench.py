@@ -260,9 +260,13 @@ def time_split_only(torch, M, args, steps):
             a.flags &= ~M.DECODE_SPLIT_ONLY
 
 
-def time_sparse(torch, M, steps, warmup):
+def time_sparse(torch, M, steps, warmup, checked=True):
+    """Sparse top-2048 decode, B=4, H=128, 128K-row caches.  checked: the
+    index lists are checked on the device in the same launch (a status
+    buffer, the C-ABI's asynchronous form); else MR_DECODE_UNCHECKED."""
     q_lat, q_rope, caches, sets = make_sparse_inputs(torch, 2, 16)
     out = torch.empty(4, H, R, dtype=torch.bfloat16, device="cuda")
+    status = torch.zeros(4, 3, dtype=torch.int32, device="cuda")
     import ctypes as C
 
     lib = M.load()
@@ -271,7 +275,8 @@ def time_sparse(torch, M, steps, warmup):
     for i in range(32):
         c = caches[i % 2]
         a, _, ws = M.decode_args(q_lat, q_rope, c[..., :R], c[..., R:], scale=SCALE, indices=sets[i % 16], out=out,
-                                 workspace=ws)
+                                 workspace=ws, index_status=status if checked else None,
+                                 flags=0 if checked else M.DECODE_UNCHECKED)
         args.append(a)
     for i in range(warmup):
         M._check(lib.mr_mla_decode(C.byref(args[i % 32]), sp))
@@ -496,6 +501,8 @@ def main():
     log("bench: sparse B=4 H=128 N=131072 K=2048")
     s = time_sparse(torch, M, args.steps, args.warmup)
     log(f"bench: sparse {s}")
+    su = time_sparse(torch, M, args.steps, args.warmup, checked=False)
+    log(f"bench: sparse, no index checks {su}")
     log("bench: decode block, hidden 7168, affine 4-bit g64, ctx 32768")
     blk = time_block(torch, M, max(args.steps // 4, 10), max(args.warmup // 4, 5))
     log(f"bench: block {blk}")
@@ -538,6 +545,7 @@ def main():
         "split_us_events": round(d["split_ms"] * 1e3, 3),
         "sparse_top2048_us": round(s["wall_ms"] * 1e3, 3),
         "sparse_split_kernel_us": round(s["split_kernel_ms"] * 1e3, 3),
+        "sparse_unchecked_us": round(su["wall_ms"] * 1e3, 3),
         "sparse_hbm_fraction": round(sparse_bytes() / (s["wall_ms"] * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
         "block_us": round(blk["wall_ms"] * 1e3, 3),
         "block_hbm_fraction": round(block_bytes() / (blk["wall_ms"] * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),

@@ -71,6 +71,21 @@ const char *mr_get_last_error(void);
  * An index list with no valid entry gives zeros (:896-899).  The sink, when
  * given, enters the max and the denominator only (:908-913).
  *
+ * Index checks (the reference throws on an entry outside [0, n_ctx) other
+ * than -1, and on a repeated entry, :884-895), chosen by the caller:
+ *  - index_status != NULL: checked on the device in the same launch, no
+ *    host synchronisation.  index_status[3*b .. 3*b+2] receives (MR_OK, -1,
+ *    -1) for a valid list of token b, else (MR_INDEX_OUT_OF_RANGE or
+ *    MR_DUPLICATE_INDEX, position, value) of the first bad entry in the
+ *    reference's order.  `out` of a token whose list is bad is unspecified.
+ *  - index_status == NULL (the default): the same check runs first and the
+ *    call returns its error (synchronises `stream`), as the reference's
+ *    throwing call does.  MR_DECODE_VALIDATE_INDICES asks for this form even
+ *    when index_status is given.
+ *  - MR_DECODE_UNCHECKED: no check; a bad entry is skipped like -1 and a
+ *    repeated one counts once per occurrence.
+ * Checked lists hold at most 8192 entries; n_idx is at most 524288.
+ *
  * Layout: the cache is one bf16 row per position; the latent part and the
  * shared rope key are given as two (pointer, row stride) pairs so that both
  * the packed [P, 576] row and the reference's two arrays [P,512] + [P,64]
@@ -104,14 +119,15 @@ typedef struct mr_mla_decode_args {
      * three hipEvent_t recorded on `stream` before the split kernel, between
      * it and the combine kernel, and after the combine kernel. */
     void *const *phase_events;
+    int32_t *index_status; /* optional device int32 [batch][3]: see the index checks above */
 } mr_mla_decode_args;
 
-#define MR_DECODE_VALIDATE_INDICES 1u  /* run mr_validate_indices first (synchronises) */
-#define MR_DECODE_NO_TRANSPOSE_READ 2u /* debug: PV operand by scalar LDS reads */
+#define MR_DECODE_VALIDATE_INDICES 1u /* check the indices first and return the error (synchronises) */
 /* Profiling aid, no reference counterpart: launch only the split kernel
  * (the split partials land in the workspace; `out` is not written), so a
  * caller can time that kernel over many launches between two events. */
 #define MR_DECODE_SPLIT_ONLY 4u
+#define MR_DECODE_UNCHECKED 8u /* no index checks (trusted producers) */
 
 size_t mr_mla_decode_workspace_size(const mr_mla_decode_args *args);
 mr_status mr_mla_decode(const mr_mla_decode_args *args, void *stream);
@@ -121,7 +137,7 @@ mr_status mr_mla_decode(const mr_mla_decode_args *args, void *stream);
  * order, -1 skips, an entry outside [0, n_rows) is INDEX_OUT_OF_RANGE, a
  * repeat of an earlier entry is DUPLICATE_INDEX.  Synchronises `stream`.
  * bad_token / bad_position (optional host pointers) receive the location.
- * Needs n_idx <= 4096 and a workspace of mr_validate_indices_workspace_size. */
+ * Needs n_idx <= 8192 and a workspace of mr_validate_indices_workspace_size. */
 size_t mr_validate_indices_workspace_size(int32_t batch, int32_t n_idx);
 mr_status mr_validate_indices(const int32_t *indices, int32_t batch, int32_t n_idx,
                               int32_t n_rows, void *workspace, size_t workspace_bytes,

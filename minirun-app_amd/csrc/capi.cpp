@@ -49,6 +49,7 @@ const char* dtype_name(mr_dtype d) {
 
 namespace {
 using mrc::aligned16;
+using mrc::aligned4;
 using mrc::align256;
 using mrc::fail;
 using mrc::hip_fail;
@@ -75,7 +76,7 @@ struct DecodePlan {
 DecodePlan plan_decode(const mr_mla_decode_args* a) {
     DecodePlan pl{};
     pl.n_rows = a->indices ? a->n_idx : a->n_ctx;
-    pl.hg_size = mr::decode_head_group_size(a->heads, (a->flags & MR_DECODE_NO_TRANSPOSE_READ) == 0);
+    pl.hg_size = mr::decode_head_group_size(a->heads);
     pl.head_groups = (a->heads + pl.hg_size - 1) / pl.hg_size;
     pl.h_pad = pl.head_groups * pl.hg_size;
     const int rows = std::max(pl.n_rows, 0);
@@ -126,6 +127,14 @@ mr_status check_decode(const mr_mla_decode_args* a) {
     if (a->indices) {
         if (a->n_idx < 0) return fail(MR_INVALID_SHAPE, "mla decode: n_idx %d is negative", a->n_idx);
         if (a->n_ctx <= 0) return fail(MR_INVALID_SHAPE, "mla decode: the cache has no rows (n_ctx %d)", a->n_ctx);
+        // a gathered split stages at most MAX_GATHER_ROWS indices in LDS and
+        // the combine merges at most MAX_COMBINE_SPLITS splits
+        if (int64_t(a->n_idx) > int64_t(mr::MAX_GATHER_ROWS) * mr::MAX_COMBINE_SPLITS)
+            return fail(MR_INVALID_SHAPE, "mla decode: n_idx %d exceeds %d", a->n_idx,
+                        mr::MAX_GATHER_ROWS * mr::MAX_COMBINE_SPLITS);
+        if (!(a->flags & MR_DECODE_UNCHECKED) && a->n_idx > mr::validate_max_indices())
+            return fail(MR_INVALID_SHAPE, "mla decode: index checks take at most %d entries per token, got %d "
+                        "(MR_DECODE_UNCHECKED skips them)", mr::validate_max_indices(), a->n_idx);
     } else if (a->n_ctx <= 0) {
         return fail(MR_INVALID_SHAPE, "mla decode: n_ctx %d must be positive", a->n_ctx);
     }
@@ -177,7 +186,7 @@ size_t mr_mla_decode_workspace_size(const mr_mla_decode_args* args) {
 
 size_t mr_validate_indices_workspace_size(int32_t batch, int32_t n_idx) {
     (void)n_idx;
-    return align256(size_t(std::max(batch, 0)) * 2 * sizeof(int32_t));
+    return align256(size_t(std::max(batch, 0)) * 3 * sizeof(int32_t));
 }
 
 mr_status mr_validate_indices(const int32_t* indices, int32_t batch, int32_t n_idx, int32_t n_rows,
@@ -188,7 +197,8 @@ mr_status mr_validate_indices(const int32_t* indices, int32_t batch, int32_t n_i
     if (batch <= 0 || n_idx < 0 || n_rows < 0)
         return fail(MR_INVALID_SHAPE, "index validation: batch %d, n_idx %d, n_rows %d", batch, n_idx, n_rows);
     if (n_idx == 0) return MR_OK;
-    if (n_idx > 4096) return fail(MR_INVALID_SHAPE, "index validation: n_idx %d exceeds 4096", n_idx);
+    if (n_idx > mr::validate_max_indices())
+        return fail(MR_INVALID_SHAPE, "index validation: n_idx %d exceeds %d", n_idx, mr::validate_max_indices());
     if (!indices || !workspace) return fail(MR_INVALID_ARGUMENT, "index validation: NULL indices or workspace");
     if (workspace_bytes < mr_validate_indices_workspace_size(batch, n_idx))
         return fail(MR_WORKSPACE_TOO_SMALL, "index validation: workspace %zu bytes < %zu", workspace_bytes,
@@ -197,20 +207,17 @@ mr_status mr_validate_indices(const int32_t* indices, int32_t batch, int32_t n_i
     int32_t* res = (int32_t*)workspace;
     hipError_t e = mr::launch_validate_indices(indices, batch, n_idx, n_rows, res, st);
     if (e != hipSuccess) return hip_fail(e, "index validation launch");
-    std::vector<int32_t> host(size_t(batch) * 2);
+    std::vector<int32_t> host(size_t(batch) * 3);
     e = hipMemcpyAsync(host.data(), res, host.size() * sizeof(int32_t), hipMemcpyDeviceToHost, st);
     if (e == hipSuccess) e = hipStreamSynchronize(st);
     if (e != hipSuccess) return hip_fail(e, "index validation readback");
-    std::vector<int32_t> idx_host(1);
     for (int32_t b = 0; b < batch; ++b) {
-        const int32_t rp = host[2 * b], dp = host[2 * b + 1];
-        if (rp == 0x7fffffff && dp == 0x7fffffff) continue;
-        const int32_t pos = std::min(rp, dp);
+        const int32_t code = host[3 * b], pos = host[3 * b + 1], v = host[3 * b + 2];
+        if (code == MR_OK) continue;
         if (bad_token) *bad_token = b;
         if (bad_position) *bad_position = pos;
-        e = hipMemcpy(idx_host.data(), indices + int64_t(b) * n_idx + pos, sizeof(int32_t), hipMemcpyDeviceToHost);
-        const int32_t v = e == hipSuccess ? idx_host[0] : -1;
-        if (rp <= dp)
+        // DeepSeekV4Attention.swift:888-893
+        if (code == MR_INDEX_OUT_OF_RANGE)
             return fail(MR_INDEX_OUT_OF_RANGE, "token %d names KV row %d, outside the cache", b, v);
         return fail(MR_DUPLICATE_INDEX, "token %d names KV row %d more than once", b, v);
     }
@@ -224,11 +231,17 @@ mr_status mr_mla_decode(const mr_mla_decode_args* a, void* stream) {
     if (!a->workspace || a->workspace_bytes < pl.total)
         return fail(MR_WORKSPACE_TOO_SMALL, "mla decode: workspace %zu bytes < %zu required", a->workspace_bytes, pl.total);
     if (!aligned16(a->workspace)) return fail(MR_INVALID_ARGUMENT, "mla decode: workspace must be 16-byte aligned");
-    if (a->indices && (a->flags & MR_DECODE_VALIDATE_INDICES) && a->n_idx > 0) {
+    // index checks: on the device in the split launch when the caller gives
+    // a status buffer, else synchronously before it (the reference throws)
+    const bool checked = a->indices && !(a->flags & MR_DECODE_UNCHECKED);
+    const bool sync_check = checked && (!a->index_status || (a->flags & MR_DECODE_VALIDATE_INDICES));
+    if (sync_check && a->n_idx > 0) {
         st = mr_validate_indices(a->indices, a->batch, a->n_idx, a->n_ctx, a->workspace, a->workspace_bytes, nullptr,
                                  nullptr, stream);
         if (st != MR_OK) return st;
     }
+    if (checked && !sync_check && !aligned4(a->index_status))
+        return fail(MR_INVALID_ARGUMENT, "mla decode: index_status must be 4-byte aligned");
     mr::DecodeParams p{};
     p.q_lat = (const uint16_t*)a->q_lat;
     p.q_lat_bs = a->q_lat_batch_stride;
@@ -258,7 +271,10 @@ mr_status mr_mla_decode(const mr_mla_decode_args* a, void* stream) {
     p.ws_o = a->workspace;
     p.ws_f32 = a->out_dtype == MR_F32;
     p.ws_ml = (float*)((char*)a->workspace + pl.o_bytes);
-    p.err_flag = nullptr;
+    // one check workgroup per token, in front of a multiple of 8 so the
+    // attention workgroups keep their XCD placement (blockIdx % 8)
+    p.check_blocks = (checked && !sync_check) ? (a->batch + 7) / 8 * 8 : 0;
+    p.index_status = p.check_blocks ? a->index_status : nullptr;
 
     mr::CombineParams cp{};
     cp.ws_o = p.ws_o;
@@ -275,8 +291,7 @@ mr_status mr_mla_decode(const mr_mla_decode_args* a, void* stream) {
     cp.out_f32 = a->out_dtype == MR_F32;
 
     const hipError_t e =
-        mr::launch_mla_decode(p, cp, (a->flags & MR_DECODE_NO_TRANSPOSE_READ) == 0,
-                              (a->flags & MR_DECODE_SPLIT_ONLY) != 0, (hipEvent_t const*)a->phase_events,
+        mr::launch_mla_decode(p, cp, (a->flags & MR_DECODE_SPLIT_ONLY) != 0, (hipEvent_t const*)a->phase_events,
                               (hipStream_t)stream);
     if (e != hipSuccess) return hip_fail(e, "mla decode launch");
     return MR_OK;

@@ -490,7 +490,7 @@ mr_status mr_mla_unabsorb_values(const void* ctx, int64_t ctx_head_stride, int32
 namespace {
 
 struct BlockLayout {
-    size_t h, q_lora, q_lora_n, q, q_lat, kv, ctx, attn, dec, total;
+    size_t h, h_kv, q_lora, q_lora_n, q, q_lat, kv, ctx, attn, dec, total;
     mr_mla_decode_args dec_args;
 };
 
@@ -503,6 +503,7 @@ bool block_layout(const mr_mla_block_args* a, BlockLayout* L) {
     };
     const int dq = a->qk_nope_dim + a->qk_rope_dim;
     L->h = take(size_t(a->hidden) * 2);
+    L->h_kv = take(size_t(a->hidden) * 2);  // the key path's normed x (it runs beside the query path)
     L->q_lora = take(size_t(a->q_lora_rank) * 2);
     L->q_lora_n = take(size_t(a->q_lora_rank) * 2);
     L->q = take(size_t(a->heads) * dq * 2);
@@ -576,6 +577,7 @@ mr_status mr_mla_decode_block(const mr_mla_block_args* a, void* stream) {
     if (!aligned16(a->workspace)) return fail(MR_INVALID_ARGUMENT, "mla block: workspace must be 16-byte aligned");
     char* W = (char*)a->workspace;
     void* h = W + L.h;
+    void* h_kv = W + L.h_kv;
     void* q_lora = W + L.q_lora;
     void* q_lora_n = W + L.q_lora_n;
     uint16_t* q = (uint16_t*)(W + L.q);
@@ -594,8 +596,8 @@ mr_status mr_mla_decode_block(const mr_mla_block_args* a, void* stream) {
     if ((he = hipEventRecord(side->fork, (hipStream_t)stream)) != hipSuccess ||
         (he = hipStreamWaitEvent(side->s, side->fork, 0)) != hipSuccess)
         return hip_fail(he, "mla block: fork");
-    // the kv_a norm fallback writes its own buffer (q_lora_n is the query's)
-    if ((st = block_gemv(a->x, a->hidden, &a->kv_a, kv, a->input_norm_w, nd, a->eps, ctx, side->s)) != MR_OK)
+    // the kv_a norm fallback writes its own buffer (h is the query path's)
+    if ((st = block_gemv(a->x, a->hidden, &a->kv_a, kv, a->input_norm_w, nd, a->eps, h_kv, side->s)) != MR_OK)
         return st;
     if ((st = mr_mla_cache_append(kv, MR_BF16, a->kv_rank + a->qk_rope_dim, 1, a->kv_a_norm_w, nd, a->eps, a->kv_rank,
                                   a->qk_rope_dim, a->rope_cos, a->rope_sin, a->cache_latent, a->latent_row_stride,

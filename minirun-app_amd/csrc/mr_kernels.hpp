@@ -32,7 +32,11 @@ struct DecodeParams {
     void* ws_o;              // [batch][h_pad][splits][512]: O_s / l_s, bf16 (or f32 when ws_f32)
     int32_t ws_f32;
     float* ws_ml;            // [batch][h_pad][splits][2]: m_s (base 2), l_s
-    int32_t* err_flag;       // optional: bit 0 set on an out-of-range index
+    // gathered form: the first check_blocks workgroups check the index list
+    // of token blockIdx.x (< batch) and write (status, position, value) to
+    // index_status[3 * token]; 0 = no check
+    int32_t check_blocks;
+    int32_t* index_status;
 };
 
 struct CombineParams {
@@ -46,13 +50,16 @@ struct CombineParams {
     int32_t out_f32;
 };
 
-// Heads per decode workgroup: 64 with the role-split kernel when there are
-// more than 32 heads, else 32.
-int decode_head_group_size(int heads, bool transpose_reads);
+// Heads per decode workgroup: 64 when there are more than 32 heads, else 32.
+int decode_head_group_size(int heads);
+// Index checks (DeepSeekV4Attention.swift:884-895), one workgroup per token:
+// result[3 * b] = (status, position, value); lists of at most
+// validate_max_indices() entries.
+int validate_max_indices();
 hipError_t launch_validate_indices(const int32_t* indices, int32_t batch, int32_t n_idx, int32_t n_rows,
                                    int32_t* result, hipStream_t st);
-hipError_t launch_mla_decode(const DecodeParams& p, const CombineParams& cp, bool transpose_reads,
-                             bool split_only, hipEvent_t const* events, hipStream_t st);
+hipError_t launch_mla_decode(const DecodeParams& p, const CombineParams& cp, bool split_only,
+                             hipEvent_t const* events, hipStream_t st);
 
 // ---------------------------------------------------------------- prefill
 // Up-projection (NT GEMM): kv[p][n] = sum_r latent[p][r] * kv_b[n][r], bf16

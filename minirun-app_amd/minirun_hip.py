@@ -24,8 +24,8 @@ OK, INVALID_SHAPE, INVALID_DTYPE, INDEX_OUT_OF_RANGE, DUPLICATE_INDEX, NONFINITE
 BF16, F16, F32, U32, I32 = range(5)
 
 DECODE_VALIDATE_INDICES = 1
-DECODE_NO_TRANSPOSE_READ = 2
 DECODE_SPLIT_ONLY = 4
+DECODE_UNCHECKED = 8
 
 
 class MRError(RuntimeError):
@@ -50,6 +50,7 @@ class DecodeArgs(C.Structure):
         ("workspace", C.c_void_p), ("workspace_bytes", C.c_size_t),
         ("num_splits", C.c_int32), ("flags", C.c_uint32),
         ("phase_events", C.c_void_p),
+        ("index_status", C.c_void_p),
     ]
 
 
@@ -217,12 +218,13 @@ def _need(t, name, dtype=None):
 
 
 def decode_args(q_lat, q_rope, latent, rope_keys, *, scale, indices=None, sinks=None, out=None,
-                out_dtype=None, num_splits=0, flags=0, workspace=None):
+                out_dtype=None, num_splits=0, flags=0, workspace=None, index_status=None):
     """Fill a DecodeArgs from torch tensors.
 
     q_lat [B,H,512] bf16; q_rope [B,H,64] bf16 or None; latent [B,N,*] or [N,*]
     bf16 rows (first 512 columns used); rope_keys likewise (64 columns) or
-    None; indices [B,K] int32 or None; sinks [H] f32 or None.
+    None; indices [B,K] int32 or None; sinks [H] f32 or None; index_status
+    int32 [B,3] device tensor or None (the device-side index check).
     """
     torch = _torch()
     _need(q_lat, "q_lat", torch.bfloat16)
@@ -273,6 +275,11 @@ def decode_args(q_lat, q_rope, latent, rope_keys, *, scale, indices=None, sinks=
     o3 = out if out.dim() == 3 else out.unsqueeze(0)
     a.out_batch_stride, a.out_head_stride = o3.stride(0), o3.stride(1)
     a.num_splits, a.flags = int(num_splits), int(flags)
+    if index_status is not None:
+        _need(index_status, "index_status", torch.int32)
+        if index_status.numel() < 3 * B or not index_status.is_contiguous():
+            raise ValueError("index_status must be a contiguous int32 tensor of at least 3 * batch entries")
+        a.index_status = index_status.data_ptr()
     need = load().mr_mla_decode_workspace_size(C.byref(a))
     if workspace is None:
         workspace = torch.empty(max(need, 256), dtype=torch.uint8, device=q_lat.device)
@@ -281,20 +288,28 @@ def decode_args(q_lat, q_rope, latent, rope_keys, *, scale, indices=None, sinks=
 
 
 def mla_decode(q_lat, q_rope, latent, rope_keys, *, scale, indices=None, sinks=None, out=None,
-               out_dtype=None, num_splits=0, flags=0, workspace=None, stream=None):
-    """Absorbed MLA decode / sparse decode.  Returns the [B,H,512] context."""
+               out_dtype=None, num_splits=0, flags=0, workspace=None, index_status=None, stream=None):
+    """Absorbed MLA decode / sparse decode.  Returns the [B,H,512] context.
+
+    With indices, the lists are checked as the reference does: by default
+    before the launch (a bad list raises MRError, the call synchronises);
+    with an index_status tensor on the device in the same launch (read it
+    later: per token (status, position, value)); not at all with
+    DECODE_UNCHECKED in flags."""
     a, out, ws = decode_args(q_lat, q_rope, latent, rope_keys, scale=scale, indices=indices, sinks=sinks,
-                             out=out, out_dtype=out_dtype, num_splits=num_splits, flags=flags, workspace=workspace)
+                             out=out, out_dtype=out_dtype, num_splits=num_splits, flags=flags, workspace=workspace,
+                             index_status=index_status)
     _check(load().mr_mla_decode(C.byref(a), _stream(stream)))
     return out
 
 
 def sparse_attention(queries_lat, queries_rope, cache, indices, *, scale, sinks=None, validate=True, **kw):
     """DeepSeekV4SparseAttention.forward over a [B, N, 512+dr] cache (rows
-    shared by all heads, K = row[0:512+dr], V = row[0:512])."""
+    shared by all heads, K = row[0:512+dr], V = row[0:512]).  validate=False
+    skips the index checks (DECODE_UNCHECKED)."""
     lat = cache[..., :512]
     rk = cache[..., 512:] if queries_rope is not None else None
-    flags = kw.pop("flags", 0) | (DECODE_VALIDATE_INDICES if validate else 0)
+    flags = kw.pop("flags", 0) | (0 if validate else DECODE_UNCHECKED)
     return mla_decode(queries_lat, queries_rope, lat, rk, scale=scale, indices=indices, sinks=sinks,
                       flags=flags, **kw)
 

@@ -63,8 +63,27 @@ def test_workspace_size_is_deterministic_and_covers_partials():
 
 def test_validate_indices_rejects_oversize_without_gpu():
     lib = M.load()
-    st = lib.mr_validate_indices(None, 1, 5000, 10, None, 0, None, None, None)
+    st = lib.mr_validate_indices(None, 1, 8193, 10, None, 0, None, None, None)
     assert st == M.INVALID_SHAPE
+    assert lib.mr_validate_indices(None, 1, 8192, 10, None, 0, None, None, None) == M.INVALID_ARGUMENT
+
+
+def test_sparse_decode_bounds_the_index_count_without_gpu():
+    # a gathered split stages at most 512 indices and the combine merges at
+    # most 1024 splits: longer lists are refused before any launch; checked
+    # lists hold at most 8192 entries unless the caller opts out of checks
+    lib = M.load()
+    a = M.DecodeArgs()
+    a.batch, a.heads, a.n_ctx, a.kv_rank, a.rope_dim, a.scale = 1, 128, 1 << 20, 512, 64, 0.07
+    a.indices = 256  # never dereferenced: the shape checks come first
+    a.n_idx = 512 * 1024 + 1
+    assert lib.mr_mla_decode(C.byref(a), None) == M.INVALID_SHAPE and "exceeds 524288" in M.last_error()
+    a.flags = M.DECODE_UNCHECKED
+    assert lib.mr_mla_decode(C.byref(a), None) == M.INVALID_SHAPE
+    a.n_idx = 9000
+    assert lib.mr_mla_decode(C.byref(a), None) == M.INVALID_ARGUMENT  # past the shape checks: NULL q
+    a.flags = 0
+    assert lib.mr_mla_decode(C.byref(a), None) == M.INVALID_SHAPE and "8192" in M.last_error()
 
 
 def test_prefill_rejects_bad_arguments_before_any_gpu_call():

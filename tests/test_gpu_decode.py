@@ -117,23 +117,6 @@ def test_ragged_shapes(M, H, N):
                                    rtol=1e-6)
 
 
-def test_debug_scalar_read_path_matches(M):
-    # MR_DECODE_NO_TRANSPOSE_READ runs the 4-wave kernel with scalar PV reads;
-    # the default role-split kernel scores on 32x32x16 MFMA with another
-    # summation order, so a P value may round to a neighbouring bf16: the two
-    # agree to the bf16 rounding of P (2^-8 relative), far inside the bar
-    print("decode role-split vs 4-wave scalar-read kernel", flush=True)
-    import torch
-
-    ql, qr, cache = MI.decode_inputs(64, 2048, tag="tr")
-    a = host_f32(run_decode(M, ql, qr, cache, out_dtype=torch.float32)).astype(np.float64)
-    b = host_f32(run_decode(M, ql, qr, cache, out_dtype=torch.float32, flags=M.DECODE_NO_TRANSPOSE_READ))
-    err = np.abs(a - b)
-    assert err.max() <= 2.0 ** -8 * np.abs(a).max(), err.max()
-    ref = O.mla_decode(ql, qr, cache)[0]
-    check(b[0], ref, "debug-path", scale_bar=2e-3)
-
-
 def test_separate_latent_and_rope_arrays(M):
     # the reference's State keeps two arrays, [P,512] and [P,64] (MLA.swift:28-36)
     print("decode two-array cache", flush=True)
@@ -231,6 +214,108 @@ def test_index_validation(M, row, status, pos):
     if status:
         assert (tok, p) == (1, pos) and opos == pos
         assert ("outside the cache" in msg) if status == 3 else ("more than once" in msg)
+
+
+def raw_sparse(M, ql, qr, cache, idx, **kw):
+    """One mr_mla_decode call through ctypes (the C-ABI itself, not the
+    Python wrapper's defaults); returns (status, out, index_status)."""
+    import ctypes as C
+
+    import torch
+
+    keep = [dev(ql), dev(qr), dev(cache), dev(np.ascontiguousarray(idx, np.int32))]
+    status = kw.pop("index_status", None)
+    a, out, ws = M.decode_args(keep[0], keep[1], keep[2][..., :512], keep[2][..., 512:], scale=MI.SCALE,
+                               indices=keep[3], out_dtype=torch.float32, index_status=status, **kw)
+    st = M.load().mr_mla_decode(C.byref(a), M._stream(None))
+    torch.cuda.synchronize()
+    return st, out, keep, ws
+
+
+def bad_lists(N, K, seed):
+    """Four token lists: valid; a repeat; an out-of-range entry before a
+    repeat; a -2 (out of range, not the -1 sentinel)."""
+    rng = np.random.default_rng(seed)
+    idx = np.stack([rng.permutation(N)[:K] for _ in range(4)]).astype(np.int32)
+    idx[0, ::9] = -1
+    idx[1, K - 40] = idx[1, 12]
+    idx[2, 20] = N
+    idx[2, 100] = idx[2, 5]
+    idx[3, 3] = -2
+    return idx
+
+
+def test_sparse_device_index_status_matches_oracle(M):
+    # the C-ABI default with a status buffer: checked on the device in the
+    # same launch, per token (status, position, value) in the reference's
+    # order (DeepSeekV4Attention.swift:884-895); valid tokens still attend
+    print("sparse device index status", flush=True)
+    import torch
+
+    B, H, N, K = 4, 32, 5000, 300
+    ql, qr, cache, _ = MI.sparse_inputs(B, H, N, K, window=16, tag="ds")
+    idx = bad_lists(N, K, 11)
+    status = torch.full((B, 3), 77, dtype=torch.int32, device="cuda")
+    st, out, _, _ = raw_sparse(M, ql, qr, cache, idx, index_status=status)
+    assert st == M.OK, M.last_error()
+    got = status.cpu().numpy()
+    for b in range(B):
+        ost, opos = O.validate_indices(idx[b], N)
+        want = (ost, opos, idx[b, opos] if opos >= 0 else -1)
+        print(f"token {b}: device {tuple(got[b])} oracle {want}", flush=True)
+        assert tuple(got[b]) == want
+    assert [g[0] for g in got] == [M.OK, M.DUPLICATE_INDEX, M.INDEX_OUT_OF_RANGE, M.INDEX_OUT_OF_RANGE]
+    st0, ref0 = O.sparse_attention(ql[:1], qr[:1], cache[:1], idx[:1])
+    assert st0 == O.OK
+    check(host_f32(out)[:1], ref0, "sparse-status-token0", scale_bar=2e-3)
+    # the status is rewritten by every call: a valid batch reads all OK
+    good = idx.copy()
+    good[1:] = good[0]
+    st, _, _, _ = raw_sparse(M, ql, qr, cache, good, index_status=status)
+    assert st == M.OK and (status.cpu().numpy() == np.array([0, -1, -1])).all()
+
+
+def test_sparse_default_call_rejects_bad_lists(M):
+    # no status buffer and no flag: the call itself returns the reference's
+    # error for the first bad token; MR_DECODE_UNCHECKED skips the checks
+    print("sparse default call", flush=True)
+    B, H, N, K = 4, 32, 5000, 300
+    ql, qr, cache, _ = MI.sparse_inputs(B, H, N, K, window=16, tag="dd")
+    idx = bad_lists(N, K, 12)
+    st, _, _, _ = raw_sparse(M, ql, qr, cache, idx)
+    assert st == M.DUPLICATE_INDEX
+    assert M.last_error() == f"token 1 names KV row {idx[1, 12]} more than once"
+    st, _, _, _ = raw_sparse(M, ql, qr, cache, idx[2:])
+    assert st == M.INDEX_OUT_OF_RANGE and M.last_error() == f"token 0 names KV row {N}, outside the cache"
+    st, _, _, _ = raw_sparse(M, ql, qr, cache, idx, flags=M.DECODE_UNCHECKED)
+    assert st == M.OK
+
+
+@pytest.mark.parametrize("n_ctx,n_idx,where", [(1 << 20, 8192, 8191), (1 << 20, 8192, None), (262144, 2176, 2000)])
+def test_device_index_check_long_lists(M, n_ctx, n_idx, where):
+    # V4-sized caches (up to 2^20 positions) and the longest checked list;
+    # a repeat at the very end, or none
+    print(f"device index check n_ctx={n_ctx} n_idx={n_idx} repeat at {where}", flush=True)
+    import ctypes as C
+
+    import torch
+
+    rng = np.random.default_rng(n_idx)
+    B = 2
+    idx = np.stack([rng.choice(n_ctx, n_idx, replace=False) for _ in range(B)]).astype(np.int32)
+    if where is not None:
+        idx[1, where] = idx[1, 0]
+    ws = torch.zeros(4096, dtype=torch.uint8, device="cuda")
+    bt, bp = C.c_int32(-9), C.c_int32(-9)
+    st = M.load().mr_validate_indices(M._ptr(dev(idx)), B, n_idx, n_ctx, M._ptr(ws), ws.numel(), C.byref(bt),
+                                      C.byref(bp), M._stream(None))
+    for b in range(B):
+        print(b, O.validate_indices(idx[b], n_ctx), flush=True)
+    want = O.validate_indices(idx[1], n_ctx)
+    assert O.validate_indices(idx[0], n_ctx) == (O.OK, -1)
+    assert st == want[0]
+    if where is not None:
+        assert (bt.value, bp.value) == (1, where) == (1, want[1])
 
 
 def test_sparse_validation_flag_rejects_before_compute(M):
