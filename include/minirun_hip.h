@@ -132,6 +132,21 @@ typedef struct mr_mla_decode_args {
 size_t mr_mla_decode_workspace_size(const mr_mla_decode_args *args);
 mr_status mr_mla_decode(const mr_mla_decode_args *args, void *stream);
 
+/* mr_mla_decode with no workspace argument and no allocation.  No
+ * counterpart in the reference: it is for callers that cannot allocate
+ * device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  The caller passes inputs and outputs;
+ * args->workspace / workspace_bytes are ignored.  Scratch is a
+ * library-owned device array of MR_DECODE_NOALLOC_SCRATCH_BYTES per GPU
+ * (held until the process ends); a call needing more
+ * (mr_mla_decode_workspace_size) returns MR_WORKSPACE_TOO_SMALL.  Index
+ * lists need index_status or MR_DECODE_UNCHECKED (no synchronous check).
+ * Every call on one GPU shares that GPU's array: calls that overlap on one
+ * GPU (concurrent streams or threads) race and must be serialised by the
+ * caller. */
+#define MR_DECODE_NOALLOC_SCRATCH_BYTES (48u * 1024u * 1024u)
+mr_status mr_mla_decode_noalloc(const mr_mla_decode_args *args, void *stream);
+
 /* Index validation with the reference's rules and error order
  * (DeepSeekV4Attention.swift:884-895): per token b in order, per entry in
  * order, -1 skips, an entry outside [0, n_rows) is INDEX_OUT_OF_RANGE, a

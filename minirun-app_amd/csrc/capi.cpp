@@ -7,6 +7,7 @@
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
+#include <mutex>
 #include <string>
 #include <vector>
 
@@ -298,3 +299,57 @@ mr_status mr_mla_decode(const mr_mla_decode_args* a, void* stream) {
 }
 
 }  // extern "C"
+
+// ---------------------------------------------------------------- no-allocation decode
+// Scratch of mr_mla_decode_noalloc: a file-scope device array, one copy per
+// GPU, held until the process ends.  In host code `scratch` names a host-side
+// stand-in, not device memory: kernels and copies get the device address
+// that hipGetSymbolAddress returns for the current device, looked up once
+// per device and kept in g_scratch.  The decode writes every byte of the
+// scratch it reads in the same call (split partials, then the combine), so
+// nothing in it has to start at zero.
+namespace {
+static __device__ __align__(256) unsigned char scratch[MR_DECODE_NOALLOC_SCRATCH_BYTES];
+std::atomic<void*> g_scratch[kMaxDevices];
+std::mutex g_scratch_mu;
+
+mr_status scratch_address(void** out) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return hip_fail(e, "mla decode (no-alloc): hipGetDevice");
+    if (dev < 0 || dev >= kMaxDevices) return fail(MR_INVALID_ARGUMENT, "mla decode (no-alloc): device %d", dev);
+    void* p = g_scratch[dev].load(std::memory_order_acquire);
+    if (!p) {
+        std::lock_guard<std::mutex> lock(g_scratch_mu);
+        p = g_scratch[dev].load(std::memory_order_acquire);
+        if (!p) {
+            e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+            if (e != hipSuccess || !p) return hip_fail(e, "mla decode (no-alloc): hipGetSymbolAddress(scratch)");
+            g_scratch[dev].store(p, std::memory_order_release);
+        }
+    }
+    *out = p;
+    return MR_OK;
+}
+}  // namespace
+
+extern "C" mr_status mr_mla_decode_noalloc(const mr_mla_decode_args* a, void* stream) {
+    mr_status st = check_decode(a);
+    if (st != MR_OK) return st;
+    mr_mla_decode_args d = *a;
+    d.workspace = nullptr;
+    d.workspace_bytes = 0;
+    // a synchronous index check reads its result on the host: not here
+    if (d.indices && !(d.flags & MR_DECODE_UNCHECKED) && (!d.index_status || (d.flags & MR_DECODE_VALIDATE_INDICES)))
+        return fail(MR_INVALID_ARGUMENT, "mla decode (no-alloc): index lists need index_status (device check) or "
+                                         "MR_DECODE_UNCHECKED");
+    const size_t need = plan_decode(&d).total;
+    if (need > MR_DECODE_NOALLOC_SCRATCH_BYTES)
+        return fail(MR_WORKSPACE_TOO_SMALL, "mla decode (no-alloc): needs %zu bytes of scratch, the library holds %zu",
+                    need, (size_t)MR_DECODE_NOALLOC_SCRATCH_BYTES);
+    void* ptr = nullptr;
+    if ((st = scratch_address(&ptr)) != MR_OK) return st;
+    d.workspace = ptr;
+    d.workspace_bytes = MR_DECODE_NOALLOC_SCRATCH_BYTES;
+    return mr_mla_decode(&d, stream);
+}

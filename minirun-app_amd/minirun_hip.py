@@ -26,6 +26,7 @@ BF16, F16, F32, U32, I32 = range(5)
 DECODE_VALIDATE_INDICES = 1
 DECODE_SPLIT_ONLY = 4
 DECODE_UNCHECKED = 8
+DECODE_NOALLOC_SCRATCH_BYTES = 48 * 1024 * 1024
 
 
 class MRError(RuntimeError):
@@ -115,6 +116,7 @@ SIGNATURES = {
     "mr_get_last_error": (C.c_char_p, []),
     "mr_mla_decode_workspace_size": (C.c_size_t, [C.POINTER(DecodeArgs)]),
     "mr_mla_decode": (C.c_int, [C.POINTER(DecodeArgs), C.c_void_p]),
+    "mr_mla_decode_noalloc": (C.c_int, [C.POINTER(DecodeArgs), C.c_void_p]),
     "mr_validate_indices_workspace_size": (C.c_size_t, [C.c_int32, C.c_int32]),
     "mr_validate_indices": (C.c_int, [C.c_void_p, C.c_int32, C.c_int32, C.c_int32, C.c_void_p, C.c_size_t,
                                       C.POINTER(C.c_int32), C.POINTER(C.c_int32), C.c_void_p]),
