@@ -117,14 +117,90 @@ def make_block_inputs(torch, M, nset):
     return x, sets
 
 
-def time_block(torch, M, steps, warmup):
+K3_BLOCK = dict(hidden=7168, q_lora_rank=1536, heads=96, nope=128, rope=64, v=128, kv_rank=512)
+K3_SHAPES = {"q_a": (1536, 7168), "q_b": (96 * 192, 1536), "kv_a": (576, 7168), "kv_b": (96 * 256, 512),
+             "g_proj": (96 * 128, 7168), "o_proj": (7168, 96 * 128)}
+
+
+def k3_block_bytes():
+    """Algorithmic HBM bytes of one K3 attention block for one token: every
+    dense bf16 weight once, the cache rows, and the activations (x, the
+    projections' outputs, q_lat, ctx, merged, gate, out: 0.4 MB)."""
+    w = sum(o * i * 2 for o, i in K3_SHAPES.values())
+    act = 2 * (7168 + 1536 * 2 + 96 * 192 + 576 + 96 * 512 * 2 + 96 * 128 * 3 + 7168)
+    return w + N * (R + DR) * 2 + act
+
+
+def time_k3_block(torch, M, steps, warmup, nset=2):
+    """The K3 flagship attention layer for one token at position 32767: dense
+    bf16 projections (K3 keeps self_attn weights unquantized), NoPE, the
+    sigmoid output gate, 96 heads; `nset` weight/cache sets of 502 MB rotate."""
+    import ctypes as C
+
+    g = torch.Generator(device="cuda")
+    g.manual_seed(0x4D4C41000B)
+    sets = []
+    for _ in range(nset):
+        w = {n: M.DenseWeights((torch.randn(o, i, generator=g, device="cuda") * i ** -0.5).to(torch.bfloat16))
+             for n, (o, i) in K3_SHAPES.items()}
+        w["input_norm"] = None
+        for name, n in (("q_a_norm", 1536), ("kv_a_norm", 512)):
+            w[name] = (1 + 0.02 * torch.randn(n, generator=g, device="cuda")).to(torch.bfloat16)
+        cache = (0.5 * torch.randn(N, R + DR, generator=g, device="cuda")).to(torch.bfloat16)
+        sets.append((w, cache))
+    x = torch.randn(7168, generator=g, device="cuda").to(torch.bfloat16)
+    out = torch.empty(7168, dtype=torch.bfloat16, device="cuda")
+    args, ws = [], None
+    for w, cache in sets:
+        a, ws = M.block_args(x, w, cache, N - 1, None, None, out, workspace=ws, eps=1e-5, **K3_BLOCK)
+        args.append(a)
+    lib = M.load()
+    sp = M._stream(torch.cuda.current_stream())
+    for i in range(warmup):
+        M._check(lib.mr_mla_decode_block(C.byref(args[i % nset]), sp))
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(steps):
+        M._check(lib.mr_mla_decode_block(C.byref(args[i % nset]), sp))
+    torch.cuda.synchronize()
+    return {"wall_ms": (time.perf_counter() - t0) / steps * 1e3}
+
+
+def time_decode_96(torch, M, steps, warmup, nbuf=10):
+    """Absorbed decode at the K3 flagship's 96 heads over 32768 rows (the
+    rows rotate over nbuf caches)."""
+    import ctypes as C
+
+    g = torch.Generator(device="cuda")
+    g.manual_seed(0x4D4C410096)
+    q_lat = torch.randn(1, 96, R, generator=g, device="cuda").to(torch.bfloat16)
+    q_rope = torch.randn(1, 96, DR, generator=g, device="cuda").to(torch.bfloat16)
+    caches = [(0.5 * torch.randn(N, R + DR, generator=g, device="cuda")).to(torch.bfloat16) for _ in range(nbuf)]
+    out = torch.empty(1, 96, R, dtype=torch.bfloat16, device="cuda")
+    args, ws = [], None
+    for c in caches:
+        a, _, ws = M.decode_args(q_lat, q_rope, c[:, :R], c[:, R:], scale=SCALE, out=out, workspace=ws)
+        args.append(a)
+    lib = M.load()
+    sp = M._stream(torch.cuda.current_stream())
+    for i in range(warmup):
+        M._check(lib.mr_mla_decode(C.byref(args[i % nbuf]), sp))
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(steps):
+        M._check(lib.mr_mla_decode(C.byref(args[i % nbuf]), sp))
+    torch.cuda.synchronize()
+    return {"wall_ms": (time.perf_counter() - t0) / steps * 1e3}
+
+
+def time_block(torch, M, steps, warmup, nset=4):
     """The decode block (affine 4-bit projections + absorbed attention over a
-    32768-row cache) for one token at position 32767; two weight/cache sets
-    (2 x 143 MB) rotate so the Infinity Cache cannot hold the operands."""
+    32768-row cache) for one token at position 32767; `nset` weight/cache
+    sets (143 MB each) rotate so the Infinity Cache cannot hold the operands."""
     import ctypes as C
     import numpy as np
 
-    x, sets = make_block_inputs(torch, M, 2)
+    x, sets = make_block_inputs(torch, M, nset)
     pos = N - 1
     c, s = M.rope_table(np.array([pos]), M.rope_frequencies(DR))
     cos_t, sin_t = torch.from_numpy(c).cuda(), torch.from_numpy(s).cuda()
@@ -136,11 +212,11 @@ def time_block(torch, M, steps, warmup):
     lib = M.load()
     sp = M._stream(torch.cuda.current_stream())
     for i in range(warmup):
-        M._check(lib.mr_mla_decode_block(C.byref(args[i % 2]), sp))
+        M._check(lib.mr_mla_decode_block(C.byref(args[i % nset]), sp))
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for i in range(steps):
-        M._check(lib.mr_mla_decode_block(C.byref(args[i % 2]), sp))
+        M._check(lib.mr_mla_decode_block(C.byref(args[i % nset]), sp))
     torch.cuda.synchronize()
     return {"wall_ms": (time.perf_counter() - t0) / steps * 1e3}
 
@@ -506,6 +582,11 @@ def main():
     log("bench: decode block, hidden 7168, affine 4-bit g64, ctx 32768")
     blk = time_block(torch, M, max(args.steps // 4, 10), max(args.warmup // 4, 5))
     log(f"bench: block {blk}")
+    log("bench: K3 attention block, dense bf16, 96 heads, NoPE, gated, ctx 32768")
+    k3 = time_k3_block(torch, M, max(args.steps // 4, 10), max(args.warmup // 4, 5))
+    log(f"bench: k3 block {k3}")
+    d96 = time_decode_96(torch, M, args.steps, args.warmup)
+    log(f"bench: decode 96 heads {d96}")
     log("bench: causal prefill T=4096 H=128")
     pf = time_prefill(torch, M, max(args.steps // 20, 5), 3)
     log(f"bench: prefill {pf}")
@@ -549,6 +630,9 @@ def main():
         "sparse_hbm_fraction": round(sparse_bytes() / (s["wall_ms"] * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
         "block_us": round(blk["wall_ms"] * 1e3, 3),
         "block_hbm_fraction": round(block_bytes() / (blk["wall_ms"] * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+        "k3_block_us": round(k3["wall_ms"] * 1e3, 3),
+        "k3_block_hbm_fraction": round(k3_block_bytes() / (k3["wall_ms"] * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+        "decode_96_heads_us": round(d96["wall_ms"] * 1e3, 3),
         "prefill_us": round(pf["wall_ms"] * 1e3, 2),
         "prefill_mfma_fraction": round((UPPROJ_FLOP + ATTN_FLOP) / (pf["wall_ms"] * 1e-3) / 1e12 / MFMA_PEAK_TFLOPS, 4),
         "prefill_upproj_us": round(pf["upproj_ms"] * 1e3, 2),

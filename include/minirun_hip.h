@@ -230,6 +230,34 @@ mr_status mr_affine_gather_matmul(const void *x, mr_dtype x_dtype, int32_t token
                                   const mr_affine_weight *w, int64_t experts, const int32_t *rhs_indices,
                                   int32_t experts_per_token, void *y, mr_dtype y_dtype, void *stream);
 
+/* ------------------------------------------------------------------------
+ * Dense projections: k3Linear (Sources/ModelAdapters/Operators/Linear.swift:
+ * 47-57), y = x . W^T with W stored output-major [out_features, in_features]
+ * (the checkpoint's orientation; no transpose flag).  W is bf16 or f32 with
+ * a row stride in elements (a multiple of 8, 16-byte aligned rows).
+ * ------------------------------------------------------------------------ */
+typedef struct mr_dense_weight {
+    const void *weight;
+    mr_dtype dtype; /* MR_BF16 or MR_F32 */
+    int64_t out_features, in_features, row_stride;
+} mr_dense_weight;
+
+/* y[t, :] = x[t, :] . W^T for `tokens` rows of x (bf16 or f32, row stride
+ * x_stride) into y (bf16 or f32, row stride y_stride), fp32 accumulation.
+ * Every weight byte is read once per tile of up to 8 tokens. */
+mr_status mr_linear(const void *x, mr_dtype x_dtype, int32_t tokens, int64_t x_stride, const mr_dense_weight *w,
+                    void *y, mr_dtype y_dtype, int64_t y_stride, void *stream);
+
+/* One projection in either storage, as K3Projection holds a dense or a
+ * quantized weight (Linear.swift:20-49; here the quantized form is the MLX
+ * affine one).  MR_PROJ_NONE marks an absent optional projection. */
+typedef enum mr_proj_kind { MR_PROJ_NONE = 0, MR_PROJ_AFFINE = 1, MR_PROJ_DENSE = 2 } mr_proj_kind;
+typedef struct mr_projection {
+    mr_proj_kind kind;
+    mr_affine_weight affine; /* MR_PROJ_AFFINE */
+    mr_dense_weight dense;   /* MR_PROJ_DENSE */
+} mr_projection;
+
 /* K3Norm.rms (Sources/ModelAdapters/Operators/Normalization.swift:15-19):
  * out = weight * (x * rsqrt(mean(x^2) + eps)) per row, fp32 arithmetic. */
 mr_status mr_rmsnorm(const void *x, mr_dtype x_dtype, int64_t rows, int32_t dim, int64_t x_stride,
@@ -255,7 +283,8 @@ mr_status mr_rope_apply(void *x, mr_dtype dtype, int64_t n_pos, int64_t inner, i
 /* Latent-cache append (K3MLA.forward, MLA.swift:142-157): for each of
  * `tokens` kv_a rows [kv_rank ++ rope_dim] (bf16 or f32), write
  * RMSNorm(latent) * norm_w as bf16 to latent[start_row + t] and the rope
- * key, rotated with cos_t/sin_t [tokens, rope_dim/2], to rope[start_row + t]. */
+ * key, rotated with cos_t/sin_t [tokens, rope_dim/2], to rope[start_row + t].
+ * cos_t = sin_t = NULL stores the key unrotated (K3's NoPE, MLA.swift:5-13). */
 mr_status mr_mla_cache_append(const void *kv, mr_dtype kv_dtype, int64_t kv_stride, int64_t tokens,
                               const void *norm_w, mr_dtype w_dtype, float eps, int32_t kv_rank,
                               int32_t rope_dim, const float *cos_t, const float *sin_t, void *latent,
@@ -263,34 +292,42 @@ mr_status mr_mla_cache_append(const void *kv, mr_dtype kv_dtype, int64_t kv_stri
                               int64_t start_row, void *stream);
 
 /* Query absorption (MLA.swift:180-188): q_lat[h] = q_nope[h] . W_UK[h] with
- * W_UK the rows h*(nope+v) .. +nope of the affine kv_b_proj
- * [heads*(nope+v), kv_rank] (4-bit, group 64, kv_rank 512).  q: bf16 heads
- * of q_head_stride elements, nope part first; q_lat: bf16 [heads, kv_rank]. */
+ * W_UK the rows h*(nope+v) .. +nope of kv_b_proj [heads*(nope+v), kv_rank]
+ * (kv_rank 512), affine 4-bit group 64 or dense.  q: bf16 heads of
+ * q_head_stride elements, nope part first; q_lat: bf16 [heads, kv_rank]. */
 mr_status mr_mla_absorb_query(const void *q, int64_t q_head_stride, int32_t heads, int32_t nope_dim,
-                              int32_t v_dim, const mr_affine_weight *kv_b, void *q_lat,
+                              int32_t v_dim, const mr_projection *kv_b, void *q_lat,
                               int64_t q_lat_head_stride, void *stream);
 
 /* Value un-absorption (MLA.swift:196-197): out[h] = ctx[h] . W_UV[h]^T with
- * W_UV the rows h*(nope+v)+nope .. +v of kv_b; ctx bf16 [heads, kv_rank],
- * out [heads, v_dim] bf16 or f32 (contiguous). */
+ * W_UV the rows h*(nope+v)+nope .. +v of kv_b (affine or dense); ctx bf16
+ * [heads, kv_rank], out [heads, v_dim] bf16 or f32 (contiguous). */
 mr_status mr_mla_unabsorb_values(const void *ctx, int64_t ctx_head_stride, int32_t heads, int32_t nope_dim,
-                                 int32_t v_dim, const mr_affine_weight *kv_b, void *out, mr_dtype out_dtype,
+                                 int32_t v_dim, const mr_projection *kv_b, void *out, mr_dtype out_dtype,
                                  void *stream);
 
 /* ------------------------------------------------------------------------
- * One decode token through the whole MLA block with affine projections
- * (K3MLA.forwardWithoutTrace, MLA.swift:91-98 -> :124-229, absorbed branch):
- *   h = RMSNorm(x) (input norm; skipped when input_norm_w is NULL)
- *   q = q_b(RMSNorm(q_a(h)))  [heads, nope + rope]; rope part rotated
+ * One decode token through the whole MLA block, absorbed branch of
+ * K3MLA.forwardWithoutTrace (MLA.swift:91-98 -> :124-229):
+ *   h = RMSNorm(x) (input norm; skipped when input_norm_w is NULL: K3 applies
+ *       input_layernorm before the block)
+ *   q = q_b(RMSNorm(q_a(h)))  [heads, nope + rope]
  *   kv = kv_a(h) -> cache row `position` (mr_mla_cache_append)
  *   q_lat = absorb(q_nope, kv_b)
  *   ctx = mr_mla_decode over rows [0, position]   (append, then attend)
- *   out = o_proj(unabsorb(ctx, kv_b))
- * The output gate is not part of this block.  All activations between the
- * projections are bf16 (the affine matmul output dtype for bf16 input).
- * The key path (kv_a, cache append) runs on a library-owned side stream of
- * the current device, forked from `stream` and joined back before the
- * attention by events; the call stays ordered on `stream` as a whole.
+ *   merged = unabsorb(ctx, kv_b)                   [heads * v]
+ *   out = o_proj(merged * sigmoid(g_proj(h)))      (gate when g_proj is given,
+ *                                                   MLA.swift:209-211)
+ * Rotary: with rope_cos/rope_sin (device [qk_rope_dim/2], the angle table at
+ * `position`) the query's rope slice and the cached key are rotated
+ * (DeepSeek-style MLA); with both NULL nothing is rotated (K3 is NoPE,
+ * MLA.swift:5-13: the slice is carried through unrotated).
+ * Each projection is affine (MLX 4-bit) or dense (k3Linear); K3's attention
+ * weights are dense bf16.  All activations between the projections are bf16.
+ * The key path (kv_a, cache append) and the gate projection run on a
+ * library-owned side stream of the current device, forked from `stream` and
+ * joined back by events (before the attention and before o_proj); the call
+ * stays ordered on `stream` as a whole.
  * ------------------------------------------------------------------------ */
 typedef struct mr_mla_block_args {
     int32_t hidden, q_lora_rank, heads, qk_nope_dim, qk_rope_dim, v_head_dim, kv_rank;
@@ -298,13 +335,14 @@ typedef struct mr_mla_block_args {
     const void *x; /* bf16 [hidden], one token */
     const void *input_norm_w, *q_a_norm_w, *kv_a_norm_w;
     mr_dtype norm_w_dtype; /* bf16 or f32, all three */
-    mr_affine_weight q_a, q_b, kv_a, kv_b, o_proj;
+    mr_projection q_a, q_b, kv_a, kv_b, o_proj;
+    mr_projection g_proj; /* MR_PROJ_NONE: no output gate */
     void *cache_latent; /* bf16 rows, kv_rank wide */
     int64_t latent_row_stride;
     void *cache_rope; /* bf16 rows, qk_rope_dim wide */
     int64_t rope_row_stride;
     int32_t position, capacity; /* rows cached before this token; rows available */
-    const float *rope_cos, *rope_sin; /* device [qk_rope_dim/2]: angle table at `position` */
+    const float *rope_cos, *rope_sin; /* device [qk_rope_dim/2] at `position`, or both NULL (NoPE) */
     void *out; /* bf16 [hidden] */
     void *workspace;
     size_t workspace_bytes;

@@ -58,6 +58,9 @@ using mrc::hip_fail;
 constexpr int kMaxDevices = 64;
 std::atomic<int> g_cu_count[kMaxDevices];
 
+}  // namespace
+
+namespace mrc {
 int cu_count() {
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return 256;
@@ -68,9 +71,14 @@ int cu_count() {
     g_cu_count[dev].store(n, std::memory_order_relaxed);
     return n;
 }
+}  // namespace mrc
+
+namespace {
+using mrc::cu_count;
 
 struct DecodePlan {
     int n_rows, hg_size, head_groups, h_pad, splits, rows_per_split;
+    bool ws_f32;
     size_t o_bytes, ml_bytes, total;
 };
 
@@ -107,8 +115,11 @@ DecodePlan plan_decode(const mr_mla_decode_args* a) {
     pl.splits = splits;
     pl.rows_per_split = rps;
     const size_t recs = size_t(std::max(a->batch, 0)) * size_t(splits) * size_t(pl.h_pad);
-    // split partials in the output's precision: bf16 for bf16 output, f32 for f32
-    pl.o_bytes = align256(recs * 512 * (a->out_dtype == MR_F32 ? sizeof(float) : sizeof(uint16_t)));
+    // split partials in fp32 for f32 output and for small grids (up to 4096
+    // records, 8 MB: short contexts, where each partial carries a large share
+    // of the output), else bf16 (half the bytes the combine reads back)
+    pl.ws_f32 = a->out_dtype == MR_F32 || recs <= 4096;
+    pl.o_bytes = align256(recs * 512 * (pl.ws_f32 ? sizeof(float) : sizeof(uint16_t)));
     pl.ml_bytes = align256(recs * 2 * sizeof(float));
     pl.total = pl.o_bytes + pl.ml_bytes;
     return pl;
@@ -270,7 +281,7 @@ mr_status mr_mla_decode(const mr_mla_decode_args* a, void* stream) {
     p.hg_size = pl.hg_size;
     p.scale_log2 = a->scale * 1.4426950408889634f;
     p.ws_o = a->workspace;
-    p.ws_f32 = a->out_dtype == MR_F32;
+    p.ws_f32 = pl.ws_f32;
     p.ws_ml = (float*)((char*)a->workspace + pl.o_bytes);
     // one check workgroup per token, in front of a multiple of 8 so the
     // attention workgroups keep their XCD placement (blockIdx % 8)

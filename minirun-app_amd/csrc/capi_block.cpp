@@ -67,13 +67,13 @@ mr::AffineGemvParams gemv_params(const mr_affine_weight* w);
 // The block's key path (kv_a projection, cache append) does not depend on
 // its query path until the attention: it runs on a side stream of the
 // device, forked from and joined back to the caller's stream by events.
-// One side stream per device for the process, with one fork and one join
-// event.  A call holds `mu` from its fork record to its wait on the join, so
+// One side stream per device for the process, with one fork and two join
+// events (the key path; the gate projection).  A call holds `mu` from its fork record to its wait on the join, so
 // calls from several host threads cannot pick up each other's fork point;
 // calls that share the stream are ordered on it.
 struct SideStream {
     hipStream_t s = nullptr;
-    hipEvent_t fork = nullptr, join = nullptr;
+    hipEvent_t fork = nullptr, join = nullptr, join_gate = nullptr;
     std::mutex mu;
 };
 
@@ -90,7 +90,8 @@ mr_status side_stream(SideStream** out) {
         if ((e = hipStreamCreateWithFlags(&ss.s, hipStreamNonBlocking)) != hipSuccess)
             return hip_fail(e, "mla block: side stream");
         if ((e = hipEventCreateWithFlags(&ss.fork, hipEventDisableTiming)) != hipSuccess ||
-            (e = hipEventCreateWithFlags(&ss.join, hipEventDisableTiming)) != hipSuccess)
+            (e = hipEventCreateWithFlags(&ss.join, hipEventDisableTiming)) != hipSuccess ||
+            (e = hipEventCreateWithFlags(&ss.join_gate, hipEventDisableTiming)) != hipSuccess)
             return hip_fail(e, "mla block: side stream events");
     }
     *out = &ss;
@@ -123,6 +124,94 @@ mr_status block_gemv(const void* x, int64_t in, const mr_affine_weight* w, void*
     }
     const hipError_t e = mr::launch_affine_gemv(g, (hipStream_t)stream);
     return e == hipSuccess ? MR_OK : hip_fail(e, "affine matmul launch");
+}
+
+mr_status check_dense(const mr_dense_weight* w, const char* what) {
+    if (!w) return fail(MR_INVALID_ARGUMENT, "%s: weight descriptor is NULL", what);
+    if (!w->weight) return fail(MR_INVALID_ARGUMENT, "%s: weight is NULL", what);
+    if (w->dtype != MR_BF16 && w->dtype != MR_F32)
+        return fail(MR_INVALID_DTYPE, "%s: a dense weight is bf16 or f32, got %s", what, dtype_name(w->dtype));
+    if (w->out_features <= 0 || w->in_features <= 0 || w->out_features > INT32_MAX || w->in_features > INT32_MAX)
+        return fail(MR_INVALID_SHAPE, "%s: out_features %lld and in_features %lld must be positive int32", what,
+                    (long long)w->out_features, (long long)w->in_features);
+    const int vpc = w->dtype == MR_F32 ? 4 : 8;  // values per 16-byte chunk
+    if (w->in_features % vpc)
+        return fail(MR_INVALID_SHAPE, "%s: in_features %lld must be a multiple of %d (16-byte row chunks)", what,
+                    (long long)w->in_features, vpc);
+    if (w->row_stride < w->in_features || w->row_stride % vpc || !aligned16(w->weight))
+        return fail(MR_INVALID_ARGUMENT, "%s: rows must be 16-byte aligned with a row stride >= in_features", what);
+    return MR_OK;
+}
+
+mr_status check_projection(const mr_projection* p, const char* what) {
+    if (!p) return fail(MR_INVALID_ARGUMENT, "%s: projection is NULL", what);
+    if (p->kind == MR_PROJ_AFFINE) return check_weight(&p->affine, what);
+    if (p->kind == MR_PROJ_DENSE) return check_dense(&p->dense, what);
+    return fail(MR_INVALID_ARGUMENT, "%s: projection kind %d is not MR_PROJ_AFFINE or MR_PROJ_DENSE", what,
+                (int)p->kind);
+}
+
+int64_t proj_out(const mr_projection* p) { return p->kind == MR_PROJ_AFFINE ? p->affine.out_features : p->dense.out_features; }
+int64_t proj_in(const mr_projection* p) { return p->kind == MR_PROJ_AFFINE ? p->affine.in_features : p->dense.in_features; }
+
+mr::DenseGemvParams dense_params(const mr_dense_weight* w) {
+    mr::DenseGemvParams g{};
+    g.w = w->weight;
+    g.w_f32 = w->dtype == MR_F32;
+    g.w_rs = w->row_stride;
+    g.out_rows = (int)w->out_features;
+    g.in = (int)w->in_features;
+    g.map_a = (int)w->out_features;
+    g.m = 1;
+    return g;
+}
+
+// x_eff = x * sigmoid(g) as bf16 into out (the gate as its own stage, for
+// projections whose kernel cannot apply it while staging x)
+mr_status gate_stage(const void* x, const void* g, int64_t n, void* out, void* stream) {
+    const hipError_t e = mr::launch_gate_mul((const uint16_t*)x, (const uint16_t*)g, n, (uint16_t*)out,
+                                             (hipStream_t)stream);
+    return e == hipSuccess ? MR_OK : hip_fail(e, "gate launch");
+}
+
+// y = W . x_eff for one bf16 token, x_eff = x, RMSNorm(x) (norm_w) or
+// x * sigmoid(gate) (gate): fused into the projection's staging of x where
+// its kernel can, else as a stage of its own into `stage_buf` (in elements).
+mr_status block_proj(const void* x, int64_t in, const mr_projection* w, void* y, const void* norm_w,
+                     mr_dtype norm_dtype, float eps, const void* gate, void* stage_buf, void* stream) {
+    if (w->kind == MR_PROJ_AFFINE) {
+        if (gate) {
+            mr_status st = gate_stage(x, gate, in, stage_buf, stream);
+            if (st != MR_OK) return st;
+            x = stage_buf;
+        }
+        return block_gemv(x, in, &w->affine, y, norm_w, norm_dtype, eps, stage_buf, stream);
+    }
+    mr::DenseGemvParams g = dense_params(&w->dense);
+    g.x = x;
+    g.x_f32 = 0;
+    g.x_stride = in;
+    g.y = y;
+    g.y_f32 = 0;
+    g.y_stride_row = 1;
+    g.y_stride_token = w->dense.out_features;
+    const bool staged = in <= mr::DENSE_STAGE_FLOATS;
+    if (staged) {
+        g.norm_w = norm_w;
+        g.norm_w_f32 = norm_dtype == MR_F32;
+        g.norm_eps = eps;
+        g.gate = gate;
+        g.gate_f32 = 0;
+        g.gate_stride = in;
+    } else if (norm_w || gate) {
+        mr_status st = norm_w ? mr_rmsnorm(x, MR_BF16, 1, (int32_t)in, in, norm_w, norm_dtype, eps, stage_buf, MR_BF16,
+                                           in, stream)
+                              : gate_stage(x, gate, in, stage_buf, stream);
+        if (st != MR_OK) return st;
+        g.x = stage_buf;
+    }
+    const hipError_t e = mr::launch_dense_gemv(g, staged, mrc::cu_count(), (hipStream_t)stream);
+    return e == hipSuccess ? MR_OK : hip_fail(e, "dense projection launch");
 }
 
 mr::AffineGemvParams gemv_params(const mr_affine_weight* w) {
@@ -245,6 +334,31 @@ mr_status mr_affine_matmul(const void* x, mr_dtype x_dtype, int32_t tokens, int6
     g.force_generic = !aligned16(w->packed);  // the fused kernel loads 16-byte row chunks
     const hipError_t e = mr::launch_affine_gemv(g, (hipStream_t)stream);
     return e == hipSuccess ? MR_OK : hip_fail(e, "affine matmul launch");
+}
+
+mr_status mr_linear(const void* x, mr_dtype x_dtype, int32_t tokens, int64_t x_stride, const mr_dense_weight* w,
+                    void* y, mr_dtype y_dtype, int64_t y_stride, void* stream) {
+    // k3Linear, Linear.swift:55-57
+    mr_status st = check_dense(w, "linear");
+    if (st != MR_OK) return st;
+    if (!x || !y) return fail(MR_INVALID_ARGUMENT, "linear: x and y must be non-NULL");
+    if (!act_dtype_ok(x_dtype) || !act_dtype_ok(y_dtype)) return fail(MR_INVALID_DTYPE, "linear: x and y must be bf16 or f32");
+    if (tokens <= 0) return fail(MR_INVALID_SHAPE, "linear: tokens %d must be positive", tokens);
+    if (x_stride < w->in_features || y_stride < w->out_features)
+        return fail(MR_INVALID_SHAPE, "linear: x rows need %lld features, y rows %lld", (long long)w->in_features,
+                    (long long)w->out_features);
+    mr::DenseGemvParams g = dense_params(w);
+    g.x = x;
+    g.x_f32 = x_dtype == MR_F32;
+    g.x_stride = x_stride;
+    g.m = tokens;
+    g.y = y;
+    g.y_f32 = y_dtype == MR_F32;
+    g.y_stride_row = 1;
+    g.y_stride_token = y_stride;
+    const bool staged = w->in_features <= mr::DENSE_STAGE_FLOATS;
+    const hipError_t e = mr::launch_dense_gemv(g, staged, mrc::cu_count(), (hipStream_t)stream);
+    return e == hipSuccess ? MR_OK : hip_fail(e, "linear launch");
 }
 
 mr_status mr_affine_tile_view(const void* tile, int64_t rows, int64_t cols, int32_t group, int32_t bits,
@@ -425,8 +539,9 @@ mr_status mr_mla_cache_append(const void* kv, mr_dtype kv_dtype, int64_t kv_stri
                               mr_dtype w_dtype, float eps, int32_t kv_rank, int32_t rope_dim, const float* cos_t,
                               const float* sin_t, void* latent, int64_t latent_row_stride, void* rope,
                               int64_t rope_row_stride, int64_t start_row, void* stream) {
-    if (!kv || !norm_w || !latent || (rope_dim && (!rope || !cos_t || !sin_t)))
+    if (!kv || !norm_w || !latent || (rope_dim && !rope))
         return fail(MR_INVALID_ARGUMENT, "cache append: NULL pointer");
+    if (!cos_t != !sin_t) return fail(MR_INVALID_ARGUMENT, "cache append: give both rotary tables or neither (NoPE)");
     if (!act_dtype_ok(kv_dtype) || !act_dtype_ok(w_dtype)) return fail(MR_INVALID_DTYPE, "cache append: dtypes");
     if (tokens <= 0 || kv_rank <= 0 || rope_dim < 0 || rope_dim % 2 || kv_stride < kv_rank + rope_dim ||
         latent_row_stride < kv_rank || (rope_dim && rope_row_stride < rope_dim) || start_row < 0 || tokens > INT32_MAX)
@@ -438,51 +553,110 @@ mr_status mr_mla_cache_append(const void* kv, mr_dtype kv_dtype, int64_t kv_stri
     return e == hipSuccess ? MR_OK : hip_fail(e, "cache append launch");
 }
 
-static mr_status check_kv_b(const mr_affine_weight* kv_b, int32_t heads, int32_t nope_dim, int32_t v_dim) {
-    mr_status st = check_weight(kv_b, "kv_b_proj");
+static mr_status check_kv_b(const mr_projection* kv_b, int32_t heads, int32_t nope_dim, int32_t v_dim) {
+    mr_status st = check_projection(kv_b, "kv_b_proj");
     if (st != MR_OK) return st;
-    if (kv_b->bits != 4 || kv_b->group != 64 || kv_b->in_features != 512)
-        return fail(MR_INVALID_SHAPE, "kv_b_proj: the absorbed path needs 4-bit, group 64, kv_rank 512 (got %d/%d/%lld)",
-                    kv_b->bits, kv_b->group, (long long)kv_b->in_features);
-    if (heads <= 0 || nope_dim <= 0 || v_dim <= 0 || kv_b->out_features != int64_t(heads) * (nope_dim + v_dim))
+    if (kv_b->kind == MR_PROJ_AFFINE) {
+        const mr_affine_weight* w = &kv_b->affine;
+        if (w->bits != 4 || w->group != 64)
+            return fail(MR_INVALID_SHAPE, "kv_b_proj: the absorbed path needs a 4-bit, group-64 affine weight (got %d/%d)",
+                        w->bits, w->group);
+    }
+    if (proj_in(kv_b) != 512)
+        return fail(MR_INVALID_SHAPE, "kv_b_proj: in_features must be kv_rank 512, got %lld", (long long)proj_in(kv_b));
+    if (heads <= 0 || nope_dim <= 0 || v_dim <= 0 || proj_out(kv_b) != int64_t(heads) * (nope_dim + v_dim))
         return fail(MR_INVALID_SHAPE, "kv_b_proj has %lld rows; heads %d x (nope %d + v %d) expected",
-                    (long long)kv_b->out_features, heads, nope_dim, v_dim);
+                    (long long)proj_out(kv_b), heads, nope_dim, v_dim);
     return MR_OK;
 }
 
+// q_lat[h] = q_nope[h] . W_UK[h], optionally rotating q's rope slice
+// (rope_cos non-null) in the same launch
+static mr_status absorb(const void* q, int64_t q_head_stride, int32_t heads, int32_t nope_dim, int32_t v_dim,
+                        const mr_projection* kv_b, void* q_lat, int64_t q_lat_head_stride, const float* rope_cos,
+                        const float* rope_sin, int32_t rope_dim, void* stream) {
+    hipError_t e;
+    if (kv_b->kind == MR_PROJ_AFFINE) {
+        const mr_affine_weight* w = &kv_b->affine;
+        mr::AbsorbParams p{(const uint16_t*)q, q_head_stride, w->packed, w->scales, w->biases,
+                           scale_code(w->scale_dtype), heads, nope_dim, v_dim, 512, (uint16_t*)q_lat, q_lat_head_stride};
+        p.rope_cos = rope_cos;
+        p.rope_sin = rope_sin;
+        p.rope_dim = rope_dim;
+        p.rope_col0 = nope_dim;
+        e = mr::launch_absorb_q(p, (hipStream_t)stream);
+    } else {
+        const mr_dense_weight* w = &kv_b->dense;
+        mr::DenseAbsorbParams p{};
+        p.q = (uint16_t*)q;
+        p.q_head_stride = q_head_stride;
+        p.w = w->weight;
+        p.w_f32 = w->dtype == MR_F32;
+        p.w_rs = w->row_stride;
+        p.heads = heads;
+        p.nope_dim = nope_dim;
+        p.v_dim = v_dim;
+        p.q_lat = (uint16_t*)q_lat;
+        p.q_lat_head_stride = q_lat_head_stride;
+        p.rope_cos = rope_cos;
+        p.rope_sin = rope_sin;
+        p.rope_dim = rope_dim;
+        p.rope_col0 = nope_dim;
+        e = mr::launch_dense_absorb(p, (hipStream_t)stream);
+    }
+    return e == hipSuccess ? MR_OK : hip_fail(e, "absorb launch");
+}
+
 mr_status mr_mla_absorb_query(const void* q, int64_t q_head_stride, int32_t heads, int32_t nope_dim, int32_t v_dim,
-                              const mr_affine_weight* kv_b, void* q_lat, int64_t q_lat_head_stride, void* stream) {
+                              const mr_projection* kv_b, void* q_lat, int64_t q_lat_head_stride, void* stream) {
     mr_status st = check_kv_b(kv_b, heads, nope_dim, v_dim);
     if (st != MR_OK) return st;
     if (!q || !q_lat || q_head_stride < nope_dim || q_lat_head_stride < 512)
         return fail(MR_INVALID_ARGUMENT, "absorb query: bad q / q_lat");
-    mr::AbsorbParams p{(const uint16_t*)q, q_head_stride, kv_b->packed, kv_b->scales, kv_b->biases,
-                       scale_code(kv_b->scale_dtype), heads, nope_dim, v_dim, 512, (uint16_t*)q_lat, q_lat_head_stride};
-    const hipError_t e = mr::launch_absorb_q(p, (hipStream_t)stream);
-    return e == hipSuccess ? MR_OK : hip_fail(e, "absorb launch");
+    if (kv_b->kind == MR_PROJ_DENSE && nope_dim > 1024)
+        return fail(MR_INVALID_SHAPE, "absorb query: nope_dim %d exceeds 1024", nope_dim);
+    return absorb(q, q_head_stride, heads, nope_dim, v_dim, kv_b, q_lat, q_lat_head_stride, nullptr, nullptr, 0, stream);
 }
 
 mr_status mr_mla_unabsorb_values(const void* ctx, int64_t ctx_head_stride, int32_t heads, int32_t nope_dim,
-                                 int32_t v_dim, const mr_affine_weight* kv_b, void* out, mr_dtype out_dtype,
+                                 int32_t v_dim, const mr_projection* kv_b, void* out, mr_dtype out_dtype,
                                  void* stream) {
     mr_status st = check_kv_b(kv_b, heads, nope_dim, v_dim);
     if (st != MR_OK) return st;
     if (!ctx || !out || ctx_head_stride < 512) return fail(MR_INVALID_ARGUMENT, "unabsorb values: bad ctx / out");
     if (!act_dtype_ok(out_dtype)) return fail(MR_INVALID_DTYPE, "unabsorb values: out must be bf16 or f32");
-    mr::AffineGemvParams g = gemv_params(kv_b);
-    g.out_rows = heads * v_dim;
-    g.map_a = v_dim;
-    g.map_b = nope_dim + v_dim;
-    g.map_c = nope_dim;
-    g.x = ctx;
-    g.x_f32 = 0;
-    g.x_stride = ctx_head_stride;
-    g.m = 1;
-    g.y = out;
-    g.y_f32 = out_dtype == MR_F32;
-    g.y_stride_row = 1;
-    g.y_stride_token = int64_t(heads) * v_dim;
-    const hipError_t e = mr::launch_affine_gemv(g, (hipStream_t)stream);
+    hipError_t e;
+    if (kv_b->kind == MR_PROJ_AFFINE) {
+        mr::AffineGemvParams g = gemv_params(&kv_b->affine);
+        g.out_rows = heads * v_dim;
+        g.map_a = v_dim;
+        g.map_b = nope_dim + v_dim;
+        g.map_c = nope_dim;
+        g.x = ctx;
+        g.x_f32 = 0;
+        g.x_stride = ctx_head_stride;
+        g.m = 1;
+        g.y = out;
+        g.y_f32 = out_dtype == MR_F32;
+        g.y_stride_row = 1;
+        g.y_stride_token = int64_t(heads) * v_dim;
+        e = mr::launch_affine_gemv(g, (hipStream_t)stream);
+    } else {
+        mr::DenseGemvParams g = dense_params(&kv_b->dense);
+        g.out_rows = heads * v_dim;
+        g.map_a = v_dim;
+        g.map_b = nope_dim + v_dim;
+        g.map_c = nope_dim;
+        g.x = ctx;
+        g.x_f32 = 0;
+        g.x_vec_stride = ctx_head_stride;
+        g.m = 1;
+        g.y = out;
+        g.y_f32 = out_dtype == MR_F32;
+        g.y_stride_row = 1;
+        g.y_stride_token = int64_t(heads) * v_dim;
+        e = mr::launch_dense_gemv(g, false, mrc::cu_count(), (hipStream_t)stream);
+    }
     return e == hipSuccess ? MR_OK : hip_fail(e, "unabsorb launch");
 }
 
@@ -490,7 +664,7 @@ mr_status mr_mla_unabsorb_values(const void* ctx, int64_t ctx_head_stride, int32
 namespace {
 
 struct BlockLayout {
-    size_t h, h_kv, q_lora, q_lora_n, q, q_lat, kv, ctx, attn, dec, total;
+    size_t h, h_kv, q_lora, q_lora_n, q, q_lat, kv, ctx, attn, gate, stage, dec, total;
     mr_mla_decode_args dec_args;
 };
 
@@ -502,6 +676,7 @@ bool block_layout(const mr_mla_block_args* a, BlockLayout* L) {
         return at;
     };
     const int dq = a->qk_nope_dim + a->qk_rope_dim;
+    const size_t hv = size_t(a->heads) * a->v_head_dim;
     L->h = take(size_t(a->hidden) * 2);
     L->h_kv = take(size_t(a->hidden) * 2);  // the key path's normed x (it runs beside the query path)
     L->q_lora = take(size_t(a->q_lora_rank) * 2);
@@ -510,7 +685,9 @@ bool block_layout(const mr_mla_block_args* a, BlockLayout* L) {
     L->q_lat = take(size_t(a->heads) * a->kv_rank * 2);
     L->kv = take(size_t(a->kv_rank + a->qk_rope_dim) * 2);
     L->ctx = take(size_t(a->heads) * a->kv_rank * 2);
-    L->attn = take(size_t(a->heads) * a->v_head_dim * 2);
+    L->attn = take(hv * 2);
+    L->gate = take(hv * 2);
+    L->stage = take(hv * 2);  // the gated o_proj input when the gate is its own stage
     mr_mla_decode_args& d = L->dec_args;
     d = mr_mla_decode_args{};
     d.batch = 1;
@@ -548,28 +725,35 @@ mr_status mr_mla_decode_block(const mr_mla_block_args* a, void* stream) {
         return fail(MR_INVALID_SHAPE, "mla block: kv_rank 512, rope 64 and positive dims required");
     if (a->position < 0 || a->position >= a->capacity)
         return fail(MR_INVALID_SHAPE, "mla block: position %d outside the cache capacity %d", a->position, a->capacity);
-    if (!a->x || !a->q_a_norm_w || !a->kv_a_norm_w || !a->cache_latent || !a->cache_rope || !a->rope_cos ||
-        !a->rope_sin || !a->out || !a->workspace)
+    if (!a->x || !a->q_a_norm_w || !a->kv_a_norm_w || !a->cache_latent || !a->cache_rope || !a->out || !a->workspace)
         return fail(MR_INVALID_ARGUMENT, "mla block: NULL pointer");
+    if (!a->rope_cos != !a->rope_sin)
+        return fail(MR_INVALID_ARGUMENT, "mla block: give both rotary tables (rotated MLA) or neither (NoPE)");
     if (!act_dtype_ok(a->norm_w_dtype)) return fail(MR_INVALID_DTYPE, "mla block: norm weights must be bf16 or f32");
     const int dq = a->qk_nope_dim + a->qk_rope_dim;
+    const bool gated = a->g_proj.kind != MR_PROJ_NONE;
+    const int64_t hv = int64_t(a->heads) * a->v_head_dim;
     struct {
-        const mr_affine_weight* w;
+        const mr_projection* w;
         int64_t out, in;
         const char* name;
     } ws[] = {{&a->q_a, a->q_lora_rank, a->hidden, "q_a_proj"},
               {&a->q_b, int64_t(a->heads) * dq, a->q_lora_rank, "q_b_proj"},
               {&a->kv_a, a->kv_rank + a->qk_rope_dim, a->hidden, "kv_a_proj_with_mqa"},
-              {&a->o_proj, a->hidden, int64_t(a->heads) * a->v_head_dim, "o_proj"}};
+              {&a->o_proj, a->hidden, hv, "o_proj"},
+              {&a->g_proj, hv, a->hidden, "g_proj"}};
     for (auto& e : ws) {
-        mr_status st = check_weight(e.w, e.name);
+        if (e.w == &a->g_proj && !gated) continue;
+        mr_status st = check_projection(e.w, e.name);
         if (st != MR_OK) return st;
-        if (e.w->out_features != e.out || e.w->in_features != e.in)
+        if (proj_out(e.w) != e.out || proj_in(e.w) != e.in)
             return fail(MR_INVALID_SHAPE, "mla block: %s is [%lld, %lld], expected [%lld, %lld]", e.name,
-                        (long long)e.w->out_features, (long long)e.w->in_features, (long long)e.out, (long long)e.in);
+                        (long long)proj_out(e.w), (long long)proj_in(e.w), (long long)e.out, (long long)e.in);
     }
     mr_status st = check_kv_b(&a->kv_b, a->heads, a->qk_nope_dim, a->v_head_dim);
     if (st != MR_OK) return st;
+    if (a->kv_b.kind == MR_PROJ_DENSE && a->qk_nope_dim > 1024)
+        return fail(MR_INVALID_SHAPE, "mla block: nope dim %d exceeds 1024", a->qk_nope_dim);
     BlockLayout L;
     block_layout(a, &L);
     if (a->workspace_bytes < L.total)
@@ -585,48 +769,51 @@ mr_status mr_mla_decode_block(const mr_mla_block_args* a, void* stream) {
     void* kv = W + L.kv;
     void* ctx = W + L.ctx;
     void* attn = W + L.attn;
+    void* gate = W + L.gate;
+    void* stage = W + L.stage;
     const mr_dtype nd = a->norm_w_dtype;
 
-    // key path on the side stream: [input norm] -> kv_a -> cache row
-    // `position` (norm + rope); the attention below joins it
+    // side stream: [input norm] -> kv_a -> cache row `position` (norm +
+    // rope), joined before the attention; then the gate projection, joined
+    // before o_proj
     SideStream* side = nullptr;
     if ((st = side_stream(&side)) != MR_OK) return st;
-    std::unique_lock<std::mutex> side_lock(side->mu);  // released after the join is waited on
+    std::unique_lock<std::mutex> side_lock(side->mu);  // released after the joins are waited on
     hipError_t he;
     if ((he = hipEventRecord(side->fork, (hipStream_t)stream)) != hipSuccess ||
         (he = hipStreamWaitEvent(side->s, side->fork, 0)) != hipSuccess)
         return hip_fail(he, "mla block: fork");
-    // the kv_a norm fallback writes its own buffer (h is the query path's)
-    if ((st = block_gemv(a->x, a->hidden, &a->kv_a, kv, a->input_norm_w, nd, a->eps, h_kv, side->s)) != MR_OK)
+    if ((st = block_proj(a->x, a->hidden, &a->kv_a, kv, a->input_norm_w, nd, a->eps, nullptr, h_kv, side->s)) != MR_OK)
         return st;
     if ((st = mr_mla_cache_append(kv, MR_BF16, a->kv_rank + a->qk_rope_dim, 1, a->kv_a_norm_w, nd, a->eps, a->kv_rank,
                                   a->qk_rope_dim, a->rope_cos, a->rope_sin, a->cache_latent, a->latent_row_stride,
                                   a->cache_rope, a->rope_row_stride, a->position, side->s)) != MR_OK)
         return st;
     if ((he = hipEventRecord(side->join, side->s)) != hipSuccess) return hip_fail(he, "mla block: join record");
+    if (gated) {
+        if ((st = block_proj(a->x, a->hidden, &a->g_proj, gate, a->input_norm_w, nd, a->eps, nullptr, h_kv, side->s)) !=
+            MR_OK)
+            return st;
+        if ((he = hipEventRecord(side->join_gate, side->s)) != hipSuccess)
+            return hip_fail(he, "mla block: gate join record");
+    }
     // query path: [input norm] -> q_a -> RMSNorm -> q_b -> rotate the rope
-    // part -> absorb W_UK (the norms ride in the GEMVs' staging of x)
-    if ((st = block_gemv(a->x, a->hidden, &a->q_a, q_lora, a->input_norm_w, nd, a->eps, h, stream)) != MR_OK)
+    // part (unless NoPE) -> absorb W_UK (norms ride in the projections'
+    // staging of x where they can)
+    if ((st = block_proj(a->x, a->hidden, &a->q_a, q_lora, a->input_norm_w, nd, a->eps, nullptr, h, stream)) != MR_OK)
         return st;
-    if ((st = block_gemv(q_lora, a->q_lora_rank, &a->q_b, q, a->q_a_norm_w, nd, a->eps, q_lora_n, stream)) != MR_OK)
+    if ((st = block_proj(q_lora, a->q_lora_rank, &a->q_b, q, a->q_a_norm_w, nd, a->eps, nullptr, q_lora_n, stream)) !=
+        MR_OK)
         return st;
     // query rotary + absorb W_UK in one launch (the rotation touches only
     // the rope columns, the absorption reads only the nope columns)
-    if ((st = check_kv_b(&a->kv_b, a->heads, a->qk_nope_dim, a->v_head_dim)) != MR_OK) return st;
-    {
-        mr::AbsorbParams ap{(const uint16_t*)q, dq, a->kv_b.packed, a->kv_b.scales, a->kv_b.biases,
-                            scale_code(a->kv_b.scale_dtype), a->heads, a->qk_nope_dim, a->v_head_dim, 512,
-                            (uint16_t*)q_lat, a->kv_rank};
-        ap.rope_cos = a->rope_cos;
-        ap.rope_sin = a->rope_sin;
-        ap.rope_dim = a->qk_rope_dim;
-        ap.rope_col0 = a->qk_nope_dim;
-        if ((he = mr::launch_absorb_q(ap, (hipStream_t)stream)) != hipSuccess) return hip_fail(he, "absorb launch");
-    }
+    if ((st = absorb(q, dq, a->heads, a->qk_nope_dim, a->v_head_dim, &a->kv_b, q_lat, a->kv_rank, a->rope_cos,
+                     a->rope_sin, a->qk_rope_dim, stream)) != MR_OK)
+        return st;
     // attend once the key path has written the cache row
     if ((he = hipStreamWaitEvent((hipStream_t)stream, side->join, 0)) != hipSuccess)
         return hip_fail(he, "mla block: join");
-    side_lock.unlock();
+    if (!gated) side_lock.unlock();
     mr_mla_decode_args d = L.dec_args;
     d.q_lat = q_lat;
     d.q_rope = q + a->qk_nope_dim;
@@ -636,12 +823,17 @@ mr_status mr_mla_decode_block(const mr_mla_block_args* a, void* stream) {
     d.workspace = W + L.dec;
     d.workspace_bytes = L.total - L.dec;
     if ((st = mr_mla_decode(&d, stream)) != MR_OK) return st;
-    // values: un-absorb W_UV per head, then o_proj
+    // values: un-absorb W_UV per head, then o_proj of merged (* gate)
     if ((st = mr_mla_unabsorb_values(ctx, a->kv_rank, a->heads, a->qk_nope_dim, a->v_head_dim, &a->kv_b, attn, MR_BF16,
                                      stream)) != MR_OK)
         return st;
-    return mr_affine_matmul(attn, MR_BF16, 1, int64_t(a->heads) * a->v_head_dim, &a->o_proj, a->out, MR_BF16,
-                            a->hidden, stream);
+    // the gate projection ran beside the attention
+    if (gated) {
+        if ((he = hipStreamWaitEvent((hipStream_t)stream, side->join_gate, 0)) != hipSuccess)
+            return hip_fail(he, "mla block: gate join");
+        side_lock.unlock();
+    }
+    return block_proj(attn, hv, &a->o_proj, a->out, nullptr, nd, a->eps, gated ? gate : nullptr, stage, stream);
 }
 
 // ---------------------------------------------------------------- V4 index tables (host)

@@ -15,5 +15,6 @@ inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 
 inline bool aligned4(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 3u) == 0; }
 inline size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 const char* dtype_name(mr_dtype d);
+int cu_count();  // compute units of the current device (cached per device)
 
 }  // namespace mrc

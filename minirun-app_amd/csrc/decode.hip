@@ -350,10 +350,13 @@ __global__ void __launch_bounds__((WsShape<HGS, QK16>::THREADS), 1) mla_decode_w
                     float pv[4];
 #pragma unroll
                     for (int e = 0; e < 4; ++e) pv[e] = __builtin_amdgcn_exp2f(sv[4 * rt + e] - m_ref);
-                    ls += (pv[0] + pv[1]) + (pv[2] + pv[3]);
                     typedef __bf16 bf16x2v __attribute__((ext_vector_type(2)));
                     const bf16x2v lo = {(__bf16)pv[0], (__bf16)pv[1]};
                     const bf16x2v hi = {(__bf16)pv[2], (__bf16)pv[3]};
+                    // the sum of the P values the PV product uses (bf16), so
+                    // each output is a weighted mean of its rows with no bias
+                    // from the rounding of P
+                    ls += ((float)lo[0] + (float)lo[1]) + ((float)hi[0] + (float)hi[1]);
                     *(u32x2*)(pbuf[par] + hq * PSTR + 2 * (16 * rt + 4 * kg)) =
                         u32x2{__builtin_bit_cast(uint32_t, lo), __builtin_bit_cast(uint32_t, hi)};
                 }
@@ -469,10 +472,13 @@ __global__ void __launch_bounds__((WsShape<HGS, QK16>::THREADS), 1) mla_decode_w
                     float pv[4];
 #pragma unroll
                     for (int e = 0; e < 4; ++e) pv[e] = __builtin_amdgcn_exp2f(sv[4 * i4 + e] - m_ref);
-                    ls += (pv[0] + pv[1]) + (pv[2] + pv[3]);
                     typedef __bf16 bf16x2v __attribute__((ext_vector_type(2)));
                     const bf16x2v lo = {(__bf16)pv[0], (__bf16)pv[1]};
                     const bf16x2v hi = {(__bf16)pv[2], (__bf16)pv[3]};
+                    // the sum of the P values the PV product uses (bf16), so
+                    // each output is a weighted mean of its rows with no bias
+                    // from the rounding of P
+                    ls += ((float)lo[0] + (float)lo[1]) + ((float)hi[0] + (float)hi[1]);
                     *(u32x2*)(pbuf[par] + hq * PSTR + 2 * (8 * i4 + 4 * kh)) =
                         u32x2{__builtin_bit_cast(uint32_t, lo), __builtin_bit_cast(uint32_t, hi)};
                 }
@@ -780,8 +786,11 @@ __global__ void __launch_bounds__(COMBINE_THREADS) mla_combine(CombineParams p) 
 #pragma unroll
     for (int v = 0; v < VPL; ++v) o[v] = ((part[0][ch][v] + part[1][ch][v]) + (part[2][ch][v] + part[3][ch][v])) * sc;
     const int64_t oo = (int64_t)b * p.out_bs + (int64_t)h * p.out_hs + CB * cb + VPL * ch;
-    if (F32) {
-        *(f32x4*)((float*)p.out + oo) = f32x4{o[0], o[1], o[2], o[3]};
+    if (p.out_f32) {
+#pragma unroll
+        for (int v = 0; v < VPL; v += 4) *(f32x4*)((float*)p.out + oo + v) = f32x4{o[v], o[v + 1], o[v + 2], o[v + 3]};
+    } else if (F32) {  // fp32 partials, bf16 output: 8 bytes per lane
+        *(u32x2*)((uint16_t*)p.out + oo) = u32x2{pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3])};
     } else {
         *(u32x4*)((uint16_t*)p.out + oo) = u32x4{pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3]),
                                                  pack_bf16x2(o[4], o[5]), pack_bf16x2(o[6], o[7])};

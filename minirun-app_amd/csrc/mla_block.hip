@@ -100,6 +100,11 @@ __global__ void __launch_bounds__(256) cache_append_kernel(CacheAppendParams p) 
     for (int i = threadIdx.x; i < half; i += 256) {
         const float e = ld(p.kv, p.kv_f32, t * p.kv_stride + p.kv_rank + 2 * i);
         const float o = ld(p.kv, p.kv_f32, t * p.kv_stride + p.kv_rank + 2 * i + 1);
+        if (!p.cos_t) {  // NoPE (MLA.swift:5-13): the shared key slice is kept as it is
+            rk[2 * i] = f32_to_bf16_bits(e);
+            rk[2 * i + 1] = f32_to_bf16_bits(o);
+            continue;
+        }
         const float c = p.cos_t[t * half + i];
         const float s = p.sin_t[t * half + i];
         rk[2 * i] = f32_to_bf16_bits(sub_rn(mul_rn(e, c), mul_rn(o, s)));

@@ -179,6 +179,61 @@ struct IndexerParams {
 bool indexer_mfma_ok(const IndexerParams& p);
 hipError_t launch_indexer_scores(const IndexerParams& p, hipStream_t st);
 
+// ---------------------------------------------------------------- dense projections
+// y[t][j] = sum_i x_eff[t, xvec(j)][i] * W[wrow(j)][i], W [rows][in] bf16 or
+// f32 (row stride w_rs elements), with
+//   wrow(j) = (j / map_a) * map_b + map_c + j % map_a,  xvec(j) = j / map_a.
+// Staged launches (one activation vector per token: map_a == out_rows)
+// apply the optional RMSNorm or sigmoid gate to x once, in LDS.
+constexpr int MAX_GEMV_TOKENS = 8;         // tokens per launch tile
+constexpr int DENSE_STAGE_FLOATS = 16384;  // staged fp32 x values per workgroup (64 KB)
+struct DenseGemvParams {
+    const void* x;
+    int x_f32;
+    int64_t x_stride;      // elements between tokens
+    int64_t x_vec_stride;  // elements between the activation vectors of a token (direct mode)
+    int m;
+    const void* w;
+    int w_f32;
+    int64_t w_rs;
+    int out_rows, in;
+    int map_a;
+    int64_t map_b, map_c;
+    void* y;
+    int y_f32;
+    int64_t y_stride_row, y_stride_token;
+    const void* norm_w;  // optional: x_eff = norm_w * (x * rsqrt(mean(x^2) + eps))
+    int norm_w_f32;
+    float norm_eps;
+    const void* gate;    // optional: x_eff = x * sigmoid(gate[t * gate_stride + i])
+    int gate_f32;
+    int64_t gate_stride;
+    int tpr, steps_per_wg, mt;  // set by the launcher
+};
+// staged: map_a == out_rows and tokens_per_tile(in) * in fits LDS
+int dense_gemv_tokens_per_tile(int in, int m);
+hipError_t launch_dense_gemv(DenseGemvParams p, bool staged, int cus, hipStream_t st);
+
+// q_lat[h][r] = sum_{d < nope} q[h][d] * W[h*(nope+v) + d][r], r < 512
+// (W_UK of a dense kv_b_proj); optional rotation of q's rotary columns.
+struct DenseAbsorbParams {
+    uint16_t* q;  // bf16 [heads][q_head_stride], nope part first
+    int64_t q_head_stride;
+    const void* w;
+    int w_f32;
+    int64_t w_rs;
+    int heads, nope_dim, v_dim;
+    uint16_t* q_lat;
+    int64_t q_lat_head_stride;
+    const float* rope_cos;  // [rope_dim/2] or null
+    const float* rope_sin;
+    int rope_dim;
+    int64_t rope_col0;
+};
+hipError_t launch_dense_absorb(const DenseAbsorbParams& p, hipStream_t st);
+// out[i] = bf16(x[i] * sigmoid(g[i])), bf16 vectors of n elements
+hipError_t launch_gate_mul(const uint16_t* x, const uint16_t* g, int64_t n, uint16_t* out, hipStream_t st);
+
 hipError_t launch_affine_dequant(const AffineDequantParams& p, hipStream_t st);
 bool affine_gemv_fast_ok(const AffineGemvParams& p);
 hipError_t launch_affine_gemv(const AffineGemvParams& p, hipStream_t st);
@@ -215,7 +270,7 @@ struct CacheAppendParams {
     int w_f32;
     float eps;
     int kv_rank, rope_dim;
-    const float* cos_t;  // [tokens, rope_dim/2]
+    const float* cos_t;  // [tokens, rope_dim/2]; null: the key is stored unrotated (NoPE)
     const float* sin_t;
     uint16_t* latent;
     int64_t latent_stride;

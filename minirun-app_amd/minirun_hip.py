@@ -62,6 +62,20 @@ class AffineWeightDesc(C.Structure):
     ]
 
 
+class DenseWeightDesc(C.Structure):
+    _fields_ = [
+        ("weight", C.c_void_p), ("dtype", C.c_int), ("out_features", C.c_int64), ("in_features", C.c_int64),
+        ("row_stride", C.c_int64),
+    ]
+
+
+PROJ_NONE, PROJ_AFFINE, PROJ_DENSE = 0, 1, 2
+
+
+class ProjectionDesc(C.Structure):
+    _fields_ = [("kind", C.c_int), ("affine", AffineWeightDesc), ("dense", DenseWeightDesc)]
+
+
 class BlockArgs(C.Structure):
     _fields_ = [
         ("hidden", C.c_int32), ("q_lora_rank", C.c_int32), ("heads", C.c_int32), ("qk_nope_dim", C.c_int32),
@@ -69,8 +83,8 @@ class BlockArgs(C.Structure):
         ("eps", C.c_float), ("scale", C.c_float),
         ("x", C.c_void_p), ("input_norm_w", C.c_void_p), ("q_a_norm_w", C.c_void_p), ("kv_a_norm_w", C.c_void_p),
         ("norm_w_dtype", C.c_int),
-        ("q_a", AffineWeightDesc), ("q_b", AffineWeightDesc), ("kv_a", AffineWeightDesc), ("kv_b", AffineWeightDesc),
-        ("o_proj", AffineWeightDesc),
+        ("q_a", ProjectionDesc), ("q_b", ProjectionDesc), ("kv_a", ProjectionDesc), ("kv_b", ProjectionDesc),
+        ("o_proj", ProjectionDesc), ("g_proj", ProjectionDesc),
         ("cache_latent", C.c_void_p), ("latent_row_stride", C.c_int64),
         ("cache_rope", C.c_void_p), ("rope_row_stride", C.c_int64),
         ("position", C.c_int32), ("capacity", C.c_int32),
@@ -137,10 +151,12 @@ SIGNATURES = {
     "mr_rope_apply": (C.c_int, [_P, C.c_int, C.c_int64, C.c_int64, C.c_int64, C.c_int64, C.c_int32, _P, _P, _P]),
     "mr_mla_cache_append": (C.c_int, [_P, C.c_int, C.c_int64, C.c_int64, _P, C.c_int, C.c_float, C.c_int32, C.c_int32,
                                       _P, _P, _P, C.c_int64, _P, C.c_int64, C.c_int64, _P]),
-    "mr_mla_absorb_query": (C.c_int, [_P, C.c_int64, C.c_int32, C.c_int32, C.c_int32, C.POINTER(AffineWeightDesc), _P,
+    "mr_mla_absorb_query": (C.c_int, [_P, C.c_int64, C.c_int32, C.c_int32, C.c_int32, C.POINTER(ProjectionDesc), _P,
                                       C.c_int64, _P]),
-    "mr_mla_unabsorb_values": (C.c_int, [_P, C.c_int64, C.c_int32, C.c_int32, C.c_int32, C.POINTER(AffineWeightDesc),
+    "mr_mla_unabsorb_values": (C.c_int, [_P, C.c_int64, C.c_int32, C.c_int32, C.c_int32, C.POINTER(ProjectionDesc),
                                          _P, C.c_int, _P]),
+    "mr_linear": (C.c_int, [_P, C.c_int, C.c_int32, C.c_int64, C.POINTER(DenseWeightDesc), _P, C.c_int, C.c_int64,
+                            _P]),
     "mr_mla_decode_block_workspace_size": (C.c_size_t, [C.POINTER(BlockArgs)]),
     "mr_mla_decode_block": (C.c_int, [C.POINTER(BlockArgs), _P]),
     "mr_mla_prefill_workspace_size": (C.c_size_t, [C.POINTER(PrefillArgs)]),
@@ -365,6 +381,48 @@ class AffineWeights:
                                 self.scale_dtype, self.out_features, self.in_features, self.group_size, self.bits)
 
 
+class DenseWeights:
+    """A dense projection weight for k3Linear (Linear.swift:55-57): output-major
+    [out, in] bf16 or f32 on the device."""
+
+    def __init__(self, weight):
+        torch = _torch()
+        _need(weight, "weight")
+        if weight.dim() != 2 or weight.dtype not in (torch.bfloat16, torch.float32):
+            raise ValueError("a dense weight is a 2-D bf16 or f32 [out_features, in_features] tensor")
+        self.weight = weight
+        self.out_features, self.in_features = weight.shape
+
+    def desc(self):
+        return DenseWeightDesc(self.weight.data_ptr(), _dtype_code(self.weight.dtype), self.out_features,
+                               self.in_features, self.weight.stride(0))
+
+
+def projection(w):
+    """ProjectionDesc of an AffineWeights, a DenseWeights, or None (absent)."""
+    p = ProjectionDesc()
+    if w is None:
+        p.kind = PROJ_NONE
+    elif isinstance(w, AffineWeights):
+        p.kind, p.affine = PROJ_AFFINE, w.desc()
+    elif isinstance(w, DenseWeights):
+        p.kind, p.dense = PROJ_DENSE, w.desc()
+    else:
+        raise TypeError("a projection is AffineWeights, DenseWeights or None")
+    return p
+
+
+def linear(x, w: DenseWeights, out_dtype=None, stream=None):
+    """k3Linear (Linear.swift:55-57): x [tokens, in] -> x . W^T [tokens, out]."""
+    torch = _torch()
+    _need(x, "x")
+    x2 = x if x.dim() == 2 else x.reshape(1, -1)
+    y = torch.empty(x2.shape[0], w.out_features, dtype=out_dtype or x.dtype, device=x.device)
+    _check(load().mr_linear(_ptr(x2), _dtype_code(x2.dtype), x2.shape[0], x2.stride(0), C.byref(w.desc()), _ptr(y),
+                            _dtype_code(y.dtype), y.stride(0), _stream(stream)))
+    return y if x.dim() == 2 else y.reshape(w.out_features)
+
+
 def affine_dequantize(w: AffineWeights, dtype=None, stream=None):
     """affineDequantize (AffineWeights.swift:328-342): dense [out, in], f32 by default."""
     torch = _torch()
@@ -472,26 +530,29 @@ def mla_cache_append(kv, norm_w, eps, cos_t, sin_t, latent, rope, start_row, kv_
                                       _stream(stream)))
 
 
-def mla_absorb_query(q, heads, nope_dim, v_dim, kv_b: AffineWeights, stream=None):
+def mla_absorb_query(q, heads, nope_dim, v_dim, kv_b, stream=None):
+    """q_lat = q_nope . W_UK per head (MLA.swift:180-188); kv_b AffineWeights or DenseWeights."""
     torch = _torch()
     q_lat = torch.empty(heads, 512, dtype=torch.bfloat16, device=q.device)
-    _check(load().mr_mla_absorb_query(_ptr(q), q.stride(0), heads, nope_dim, v_dim, C.byref(kv_b.desc()), _ptr(q_lat),
-                                      512, _stream(stream)))
+    _check(load().mr_mla_absorb_query(_ptr(q), q.stride(0), heads, nope_dim, v_dim, C.byref(projection(kv_b)),
+                                      _ptr(q_lat), 512, _stream(stream)))
     return q_lat
 
 
-def mla_unabsorb_values(ctx, heads, nope_dim, v_dim, kv_b: AffineWeights, out_dtype=None, stream=None):
+def mla_unabsorb_values(ctx, heads, nope_dim, v_dim, kv_b, out_dtype=None, stream=None):
+    """out = ctx . W_UV^T per head (MLA.swift:196-197); kv_b AffineWeights or DenseWeights."""
     torch = _torch()
     out = torch.empty(heads, v_dim, dtype=out_dtype or torch.bfloat16, device=ctx.device)
-    _check(load().mr_mla_unabsorb_values(_ptr(ctx), ctx.stride(0), heads, nope_dim, v_dim, C.byref(kv_b.desc()),
+    _check(load().mr_mla_unabsorb_values(_ptr(ctx), ctx.stride(0), heads, nope_dim, v_dim, C.byref(projection(kv_b)),
                                          _ptr(out), _dtype_code(out.dtype), _stream(stream)))
     return out
 
 
 def block_args(x, weights, cache, position, rope_cos, rope_sin, out, *, hidden=7168, q_lora_rank=1536, heads=128,
                nope=128, rope=64, v=128, kv_rank=512, eps=1e-6, scale=None, workspace=None):
-    """Fill BlockArgs; `weights` is a dict with input_norm, q_a_norm, kv_a_norm
-    (tensors) and q_a, q_b, kv_a, kv_b, o_proj (AffineWeights)."""
+    """Fill BlockArgs; `weights` is a dict with input_norm (or None), q_a_norm,
+    kv_a_norm (tensors) and q_a, q_b, kv_a, kv_b, o_proj, optional g_proj
+    (AffineWeights or DenseWeights).  rope_cos = rope_sin = None: NoPE."""
     torch = _torch()
     a = BlockArgs()
     a.hidden, a.q_lora_rank, a.heads, a.qk_nope_dim, a.qk_rope_dim, a.v_head_dim, a.kv_rank = \
@@ -503,12 +564,13 @@ def block_args(x, weights, cache, position, rope_cos, rope_sin, out, *, hidden=7
     a.q_a_norm_w = weights["q_a_norm"].data_ptr()
     a.kv_a_norm_w = weights["kv_a_norm"].data_ptr()
     a.norm_w_dtype = _dtype_code(weights["q_a_norm"].dtype)
-    for n in ("q_a", "q_b", "kv_a", "kv_b", "o_proj"):
-        setattr(a, n, weights[n].desc())
+    for n in ("q_a", "q_b", "kv_a", "kv_b", "o_proj", "g_proj"):
+        setattr(a, n, projection(weights.get(n)))
     a.cache_latent, a.latent_row_stride = cache.data_ptr(), cache.stride(0)
     a.cache_rope, a.rope_row_stride = cache[:, kv_rank:].data_ptr(), cache.stride(0)
     a.position, a.capacity = position, cache.shape[0]
-    a.rope_cos, a.rope_sin = rope_cos.data_ptr(), rope_sin.data_ptr()
+    a.rope_cos = rope_cos.data_ptr() if rope_cos is not None else None
+    a.rope_sin = rope_sin.data_ptr() if rope_sin is not None else None
     a.out = out.data_ptr()
     need = load().mr_mla_decode_block_workspace_size(C.byref(a))
     if workspace is None:
@@ -518,7 +580,8 @@ def block_args(x, weights, cache, position, rope_cos, rope_sin, out, *, hidden=7
 
 
 def mla_decode_block(x, weights, cache, position, rope_cos, rope_sin, stream=None, **kw):
-    """K3MLA.forwardWithoutTrace for one decode token with affine projections."""
+    """K3MLA.forwardWithoutTrace for one decode token (affine or dense
+    projections, optional gate, rotary or NoPE)."""
     torch = _torch()
     out = torch.empty(kw.get("hidden", 7168), dtype=torch.bfloat16, device=x.device)
     a, ws = block_args(x, weights, cache, position, rope_cos, rope_sin, out, **kw)

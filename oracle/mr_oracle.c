@@ -729,3 +729,34 @@ int mro_compressed_indices(int32_t ratio, int32_t seq_len, int32_t start_pos, in
     }
     return MRO_OK;
 }
+
+/* Linear.swift:55-57: matmul(x, weight.transposed(1, 0)), weight [out, in]. */
+void mro_linear(const float *x, int64_t M, const void *w, int w_f32, int64_t out_features,
+                int64_t in_features, int64_t w_rs, int acc, float *y, int threads) {
+    threads = pick_threads(threads);
+#pragma omp parallel for num_threads(threads) schedule(static)
+    for (int64_t o = 0; o < out_features; ++o) {
+        for (int64_t m = 0; m < M; ++m) {
+            const float *xr = x + m * in_features;
+            double a64 = 0;
+            float a32 = 0.f;
+            for (int64_t i = 0; i < in_features; ++i) {
+                const float wv = w_f32 ? ((const float *)w)[o * w_rs + i]
+                                       : mro_bf16_to_f32(((const uint16_t *)w)[o * w_rs + i]);
+                if (acc)
+                    a64 += (double)xr[i] * (double)wv;
+                else
+                    a32 += xr[i] * wv;
+            }
+            y[m * out_features + o] = acc ? (float)a64 : a32;
+        }
+    }
+}
+
+/* MLA.swift:209-211: merged * sigmoid(k3Linear(x, gProj)). */
+void mro_sigmoid_gate(const float *merged, const float *g, int64_t n, float *out) {
+    for (int64_t i = 0; i < n; ++i) {
+        const float s = 1.0f / (1.0f + expf(-g[i]));
+        out[i] = merged[i] * s;
+    }
+}

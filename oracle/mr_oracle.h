@@ -79,6 +79,20 @@ int mro_rope_table(const int64_t *positions, int64_t n_pos, const double *freqs,
 void mro_rope_apply_bf16(uint16_t *x, int64_t n_pos, int64_t inner, int64_t row_stride,
                          int64_t col0, int32_t dim, const float *cos_t, const float *sin_t);
 
+/* ---- Dense projection, k3Linear (Linear.swift:55-57) ----
+ * y[m, o] = sum_i x[m, i] * W[o, i], W output-major [out, in] with row
+ * stride w_rs, bf16 bits (w_f32 = 0) or float (w_f32 = 1).  Pinned by
+ * tests/test_oracle_math.py (identity and one-hot weights, linearity, an
+ * fp64 product in numpy). */
+void mro_linear(const float *x, int64_t M, const void *w, int w_f32, int64_t out_features,
+                int64_t in_features, int64_t w_rs, int acc, float *y, int threads);
+
+/* ---- K3MLA output gate (MLA.swift:209-211): out = merged * sigmoid(g),
+ * sigmoid(g) = 1 / (1 + exp(-g)) in fp32.  Pinned by closed forms (g = 0
+ * halves, large |g| passes or zeroes, sigmoid(-g) = 1 - sigmoid(g)) in
+ * tests/test_oracle_math.py. */
+void mro_sigmoid_gate(const float *merged, const float *g, int64_t n, float *out);
+
 /* ---- RMSNorm (Normalization.swift:15-19) ---- */
 void mro_rmsnorm(const float *x, int64_t rows, int64_t dim, const float *weight, float eps,
                  int acc, float *out);

@@ -70,6 +70,8 @@ def _declare(L):
         "mro_affine_validate": (C.c_int, [i64, i64, i64, i32, i32, P]),
         "mro_affine_dequantize": (C.c_int, [P, P, P, i32, i64, i64, i32, i32, P, C.c_int]),
         "mro_affine_matmul": (C.c_int, [P, i64, P, P, P, i32, i64, i64, i32, i32, C.c_int, P, C.c_int]),
+        "mro_linear": (None, [P, i64, P, C.c_int, i64, i64, i64, C.c_int, P, C.c_int]),
+        "mro_sigmoid_gate": (None, [P, P, i64, P]),
         "mro_topk_select": (C.c_int, [P, i32, i32, i32, i32, i32, i32, P, P]),
         "mro_indexer_scores": (C.c_int, [P, i32, i32, i32, P, i32, P, P]),
         "mro_window_indices": (C.c_int, [i32, i32, i32, P, P, P]),
@@ -277,6 +279,28 @@ def affine_matmul(x, packed, scales, biases, group=64, bits=4, scale_dtype=BF16,
     if st != OK:
         raise ValueError(f"affine_matmul status {st}")
     return y.reshape(x.shape[:-1] + (O,))
+
+
+def linear(x, w, acc=1, threads=0):
+    """k3Linear (Linear.swift:55-57): x float [..., in] . W^T, W [out, in]
+    as bf16 bits (uint16) or float32."""
+    x = _c(x, np.float32)
+    x2 = x.reshape(-1, x.shape[-1])
+    w_f32 = int(w.dtype == np.float32)
+    w = _c(w, np.float32 if w_f32 else np.uint16)
+    O, I = w.shape
+    y = np.empty((x2.shape[0], O), np.float32)
+    lib().mro_linear(_p(x2), x2.shape[0], _p(w), w_f32, O, I, I, acc, _p(y), threads)
+    return y.reshape(x.shape[:-1] + (O,))
+
+
+def sigmoid_gate(merged, g):
+    """MLA.swift:209-211: merged * sigmoid(g), fp32."""
+    m = _c(merged, np.float32)
+    g = _c(g, np.float32)
+    out = np.empty_like(m)
+    lib().mro_sigmoid_gate(_p(m), _p(g), m.size, _p(out))
+    return out
 
 
 # ---------------------------------------------------------------- indices

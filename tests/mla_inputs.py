@@ -118,6 +118,38 @@ def block_inputs(ctx=32768, tag="c5", hidden=7168, q_lora_rank=1536, heads=128, 
     return d
 
 
+K3_DIMS = dict(hidden=7168, q_lora_rank=1536, heads=96, nope=128, rope=64, v=128, kv_rank=512)
+
+
+def k3_block_inputs(ctx=32768, tag="k3", hidden=7168, q_lora_rank=1536, heads=96, nope=128, rope=64, v=128,
+                    kv_rank=512):
+    """The K3 flagship attention block (config.json: hidden 7168, 96 heads,
+    q_lora 1536, kv_lora 512, nope 128, rope 64 carried unrotated, v 128,
+    mla_use_nope, mla_use_output_gate; self_attn weights dense bf16, not
+    quantized): dense weights ~N(0, 1/in) so activations keep unit scale,
+    RMSNorm weights ~1+N(0,0.02); x is already through input_layernorm, so
+    the block has no input norm.  Cache rows ~N(0,0.5), unrotated (NoPE)."""
+    norm = lambda name, n: O.f32_to_bf16(1 + 0.02 * O.bf16_to_f32(O.normal_bf16(f"{tag}.{name}", (n,))))
+    dense = lambda name, out, inp: O.normal_bf16(f"{tag}.{name}", (out, inp), std=inp ** -0.5)
+    d = {
+        "x": O.normal_bf16(f"{tag}.x", (hidden,)),
+        "input_norm": None,
+        "q_a_norm": norm("q_a_norm", q_lora_rank),
+        "kv_a_norm": norm("kv_a_norm", kv_rank),
+        "q_a": dense("q_a", q_lora_rank, hidden),
+        "q_b": dense("q_b", heads * (nope + rope), q_lora_rank),
+        "kv_a": dense("kv_a", kv_rank + rope, hidden),
+        "kv_b": dense("kv_b", heads * (nope + v), kv_rank),
+        "g_proj": dense("g_proj", heads * v, hidden),
+        "o_proj": dense("o_proj", hidden, heads * v),
+    }
+    cache = O.normal_bf16(f"{tag}.cache", (ctx, kv_rank + rope), std=0.5)
+    cache[ctx - 1] = 0
+    d["cache"] = cache
+    d["position"] = ctx - 1
+    return d
+
+
 def _bf(a):
     return O.bf16_to_f32(O.f32_to_bf16(np.asarray(a, np.float32)))
 
@@ -127,15 +159,35 @@ def _mm(x, w):
     return O.affine_matmul(np.asarray(x, np.float32)[None], packed, s, b, acc=1)[0]
 
 
+def _lin(x, w):
+    return O.linear(np.asarray(x, np.float32)[None], w, acc=1)[0]
+
+
+def _proj(x, w):
+    """A block projection: affine (packed, scales, biases) or dense [out, in]."""
+    return _mm(x, w) if isinstance(w, tuple) else _lin(x, w)
+
+
+def _dequant_kv_b(w, heads, nope, v, kv_rank):
+    dense = O.affine_dequantize(*w) if isinstance(w, tuple) else O.bf16_to_f32(w)
+    return dense.reshape(heads, nope + v, kv_rank).astype(np.float64)
+
+
 PLANTS = ("query_not_rotated", "scale_without_rope_dims", "uk_uv_swapped", "position_off_by_one",
           "q_a_norm_skipped")
 
 
 def block_reference(d, hidden=7168, q_lora_rank=1536, heads=128, nope=128, rope=64, v=128, kv_rank=512, eps=1e-6,
-                    plant=None):
+                    plant=None, rotary=True):
     """The block on the oracle, rounding to bf16 where the HIP path stores
     bf16 (every projection output, the normed activations, the cache row).
     Returns (out [hidden] f32 of bf16 values, the written cache row).
+
+    Projections are affine or dense (d's entries); d["input_norm"] None skips
+    the input norm; d["g_proj"], when present, gates merged by
+    sigmoid(g_proj(h)) before o_proj (MLA.swift:209-211); rotary=False is
+    K3's NoPE (MLA.swift:5-13: the rope slice of the query and the shared
+    key are carried through unrotated).
 
     plant (one of PLANTS) puts a plausible mistake into the oracle's block,
     so a test can show that the parity bar would catch it."""
@@ -145,24 +197,29 @@ def block_reference(d, hidden=7168, q_lora_rank=1536, heads=128, nope=128, rope=
     freqs = O.rope_frequencies(rope)
     cos, sin = O.rope_table([pos], freqs)
     qcos, qsin = O.rope_table([pos + 1], freqs) if plant == "position_off_by_one" else (cos, sin)
-    h = _bf(O.rmsnorm(f(d["x"])[None], f(d["input_norm"]), eps)[0])
-    q_lora = _bf(_mm(h, d["q_a"]))
+    x = f(d["x"])
+    h = x if d.get("input_norm") is None else _bf(O.rmsnorm(x[None], f(d["input_norm"]), eps)[0])
+    q_lora = _bf(_proj(h, d["q_a"]))
     q_lora_n = q_lora if plant == "q_a_norm_skipped" else _bf(O.rmsnorm(q_lora[None], f(d["q_a_norm"]), eps)[0])
-    q = O.f32_to_bf16(_mm(q_lora_n, d["q_b"])).reshape(heads, nope + rope)
-    if plant != "query_not_rotated":
+    q = O.f32_to_bf16(_proj(q_lora_n, d["q_b"])).reshape(heads, nope + rope)
+    if rotary and plant != "query_not_rotated":
         q = O.rope_apply_bf16(q.reshape(1, heads, nope + rope), qcos, qsin, nope, rope).reshape(heads, nope + rope)
-    kvb = O.affine_dequantize(*d["kv_b"]).reshape(heads, nope + v, kv_rank).astype(np.float64)
+    kvb = _dequant_kv_b(d["kv_b"], heads, nope, v, kv_rank)
     w_uk, w_uv = (kvb[:, nope:], kvb[:, :nope]) if plant == "uk_uv_swapped" else (kvb[:, :nope], kvb[:, nope:])
     q_lat = O.f32_to_bf16(np.einsum("hd,hdr->hr", f(q[:, :nope]).astype(np.float64), w_uk).astype(np.float32))
-    kv = O.f32_to_bf16(_mm(h, d["kv_a"]))
+    kv = O.f32_to_bf16(_proj(h, d["kv_a"]))
     row = np.empty(kv_rank + rope, np.uint16)
     row[:kv_rank] = O.f32_to_bf16(O.rmsnorm(f(kv[:kv_rank])[None], f(d["kv_a_norm"]), eps)[0])
-    row[kv_rank:] = O.rope_apply_bf16(kv[kv_rank:].reshape(1, 1, rope), cos, sin, 0, rope).reshape(rope)
+    row[kv_rank:] = (O.rope_apply_bf16(kv[kv_rank:].reshape(1, 1, rope), cos, sin, 0, rope).reshape(rope)
+                     if rotary else kv[kv_rank:])
     cache = d["cache"].copy()
     cache[pos] = row
     scale = nope ** -0.5 if plant == "scale_without_rope_dims" else (nope + rope) ** -0.5
     ctx = O.mla_decode(q_lat, q[:, nope:], cache[: pos + 1], kv_rank=kv_rank, rope_dim=rope, scale=scale)[0]
     ctx = _bf(ctx).astype(np.float64)
-    attn = _bf(np.einsum("hr,hvr->hv", ctx, w_uv).astype(np.float32))
-    out = _bf(_mm(attn.reshape(-1), d["o_proj"]))
+    attn = _bf(np.einsum("hr,hvr->hv", ctx, w_uv).astype(np.float32)).reshape(-1)
+    if d.get("g_proj") is not None:
+        g = _bf(_proj(h, d["g_proj"]))
+        attn = _bf(O.sigmoid_gate(attn, g))
+    out = _bf(_proj(attn, d["o_proj"]))
     return out, row

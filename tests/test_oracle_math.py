@@ -287,3 +287,46 @@ def test_topk_select_errors_and_empty():
     # signed zeros tie
     z = np.array([[0.0, -0.0, 0.0]], np.float32)
     assert O.topk_select(z, 3, 1, 2, 0)[1].tolist() == [[0, 1, 2]]
+
+
+# ---------------------------------------------------------------- k3Linear and the output gate
+def test_linear_identity_one_hot_and_fp64_product():
+    # k3Linear (Linear.swift:55-57): y = x . W^T with W output-major
+    rng = np.random.default_rng(5)
+    x = O.bf16_to_f32(O.f32_to_bf16(rng.standard_normal((3, 64)).astype(np.float32)))
+    eye = O.f32_to_bf16(np.eye(64, dtype=np.float32))
+    np.testing.assert_array_equal(O.linear(x, eye), x)
+    perm = rng.permutation(64)
+    sel = O.f32_to_bf16(np.eye(64, dtype=np.float32)[perm])   # row o picks x[perm[o]]
+    np.testing.assert_array_equal(O.linear(x, sel), x[:, perm])
+    w = O.normal_bf16("lin.w", (40, 64), std=0.1)
+    want = x.astype(np.float64) @ O.bf16_to_f32(w).astype(np.float64).T
+    np.testing.assert_allclose(O.linear(x, w, acc=1), want, rtol=1e-6, atol=1e-7)
+    np.testing.assert_allclose(O.linear(x, w, acc=0), want, rtol=1e-4, atol=1e-5)
+    # f32 weights, and a transposed reading would fail: W is not symmetric
+    wf = O.bf16_to_f32(w)
+    np.testing.assert_allclose(O.linear(x, wf), want, rtol=1e-6, atol=1e-7)
+    assert not np.allclose(O.linear(x[:, :40], O.f32_to_bf16(wf[:, :40].T.copy())), want[:, :40], atol=1e-3)
+
+
+def test_linear_is_linear():
+    rng = np.random.default_rng(6)
+    w = O.normal_bf16("lin.l", (17, 96), std=0.1)
+    a = rng.standard_normal(96).astype(np.float32)
+    b = rng.standard_normal(96).astype(np.float32)
+    lhs = O.linear((2 * a + 3 * b)[None], w).astype(np.float64)
+    rhs = 2 * O.linear(a[None], w).astype(np.float64) + 3 * O.linear(b[None], w).astype(np.float64)
+    np.testing.assert_allclose(lhs, rhs, rtol=1e-5, atol=1e-5)
+
+
+def test_sigmoid_gate_closed_forms():
+    # MLA.swift:209-211: merged * sigmoid(g)
+    m = np.array([1.0, -3.0, 7.5, 2.0], np.float32)
+    np.testing.assert_array_equal(O.sigmoid_gate(m, np.zeros(4)), m * 0.5)        # sigmoid(0) = 1/2
+    np.testing.assert_array_equal(O.sigmoid_gate(m, np.full(4, 100.0)), m)        # saturates to 1
+    np.testing.assert_array_equal(O.sigmoid_gate(m, np.full(4, -200.0)), 0 * m)   # and to 0
+    g = np.linspace(-6, 6, 25).astype(np.float32)
+    s_pos = O.sigmoid_gate(np.ones(25), g).astype(np.float64)
+    s_neg = O.sigmoid_gate(np.ones(25), -g).astype(np.float64)
+    np.testing.assert_allclose(s_pos + s_neg, 1.0, atol=2e-7)                      # sigmoid(-g) = 1 - sigmoid(g)
+    np.testing.assert_allclose(s_pos, 1 / (1 + np.exp(-g.astype(np.float64))), rtol=3e-7)
