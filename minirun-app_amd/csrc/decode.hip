@@ -14,7 +14,8 @@
 //                  so they run on one XCD and read the same rows through its L2
 //   sub-chunk   = 32 cache rows, global -> LDS by DMA (global_load_lds_dwordx4),
 //                 4 buffers; 16-byte chunks XOR-swizzled
-//   QK waves    = S^T = K . Q^T on MFMA, online base-2 softmax, P to LDS
+//   QK waves    = Q straight from global memory into registers, then
+//                 S^T = K . Q^T on MFMA, online base-2 softmax, P to LDS
 //   PV waves    = O^T = V^T . P^T on MFMA (V^T by ds_read_b64_tr_b16), one
 //                 sub-chunk behind the QK waves; they issue all the DMA
 //   epilogue    = O_s / l_s and (m_s, l_s) per (unit, head) into the
@@ -213,29 +214,6 @@ __global__ void __launch_bounds__((WsShape<HGS, QK16>::THREADS), 1) mla_decode_w
     const uint16_t* lat = p.latent + (int64_t)b * p.lat_bs;
     const uint16_t* rop = DR ? p.rope + (int64_t)b * p.rope_bs : nullptr;
 
-    // Q of the head group into buffers 2-3 by the PV waves, first of all (one
-    // 1 KB load per wave instruction instead of 32-byte pieces of 32 heads
-    // per QK load): in the gathered form it is in flight while the split's
-    // indices load
-    if (!is_qk) {
-        constexpr int QPW = HGS * G::CPR / 256;  // Q loads per PV wave
-        static_assert(QPW * 256 == HGS * G::CPR, "Q staging loads");
-        static_assert(HGS * G::ROWB <= 2 * G::BUF, "Q fits buffers 2-3");
-        char* qdst = cbuf + 2 * G::BUF;
-#pragma unroll
-        for (int k = 0; k < QPW; ++k) {
-            const int slot = 64 * (pw + 4 * k) + l;
-            const int h = slot / G::CPR;
-            const int c = (slot - h * G::CPR) ^ (h & 7);
-            const int h0 = hg * HGS + h;
-            const int hh = h0 < p.heads ? h0 : 0;
-            const uint16_t* src = c < R / 8 ? p.q_lat + (int64_t)b * p.q_lat_bs + (int64_t)hh * p.q_lat_hs + 8 * c
-                                            : p.q_rope + (int64_t)b * p.q_rope_bs + (int64_t)hh * p.q_rope_hs +
-                                                  8 * (c - R / 8);
-            dma16(src, qdst + 1024 * (pw + 4 * k));
-        }
-    }
-
     if (GATHER) {
         const int32_t* ind = p.indices + (int64_t)b * p.n_idx;
         for (int i = tid; i < nrows; i += NT) {
@@ -257,14 +235,20 @@ __global__ void __launch_bounds__((WsShape<HGS, QK16>::THREADS), 1) mla_decode_w
         // B operand of 16x16x32: head 16qw + l%16, k = 32ks + 8(l/16)..+7
         const int hq = 16 * qw + (l & 15);  // this lane's head within the group
         const int kg = l >> 4;              // k group; output row group
+        // Q straight from global memory into registers, in flight with the
+        // PV waves' first row loads (16-byte pieces: chunk 4ks + kg of head hq)
         bf16x8 qreg[G::KS];
-        lds_barrier();  // Q staged
         {
-            const char* qrow = cbuf + 2 * G::BUF + hq * G::ROWB;
+            const int h0 = hg * HGS + hq;
+            const int hh = h0 < p.heads ? h0 : 0;  // padding heads score head 0's query
+            const uint16_t* ql = p.q_lat + (int64_t)b * p.q_lat_bs + (int64_t)hh * p.q_lat_hs;
+            const uint16_t* qr = DR ? p.q_rope + (int64_t)b * p.q_rope_bs + (int64_t)hh * p.q_rope_hs : nullptr;
 #pragma unroll
-            for (int ks = 0; ks < G::KS; ++ks) qreg[ks] = *(const bf16x8*)(qrow + 16 * ((4 * ks + kg) ^ (hq & 7)));
+            for (int ks = 0; ks < G::KS; ++ks) {
+                const int c = 4 * ks + kg;
+                qreg[ks] = c < R / 8 ? *(const bf16x8*)(ql + 8 * c) : *(const bf16x8*)(qr + 8 * (c - R / 8));
+            }
         }
-        lds_barrier();  // Q in registers: buffers 2-3 free again
         // A operand of row tile rt: key row ksig(16rt + l%16) of the
         // sub-chunk, chunk 4ks + kg; with the row swizzle, latent chunk
         // 16v + 4u + kg sits at 256v + qo[rt][u], rope k-steps at ro[rt][.]
@@ -381,16 +365,20 @@ __global__ void __launch_bounds__((WsShape<HGS, QK16>::THREADS), 1) mla_decode_w
         // B operand of 32x32x16: head 32qw + l%32, k = 16ks + 8(l/32)..+7
         const int hq = 32 * qw + (l & 31);  // this lane's head within the group
         const int kh = l >> 5;              // k half / key half
-        // Q arrives in LDS (buffers 2-3, staged by the PV waves' DMA, chunk c
-        // of head h at slot c ^ (h & 7) of its row)
+        // Q straight from global memory into registers (chunk 2ks + kh of
+        // head hq), in flight with the PV waves' first row loads
         bf16x8 qreg[2 * G::KS];
-        lds_barrier();  // Q staged
         {
-            const char* qrow = cbuf + 2 * G::BUF + hq * G::ROWB;
+            const int h0 = hg * HGS + hq;
+            const int hh = h0 < p.heads ? h0 : 0;  // padding heads score head 0's query
+            const uint16_t* ql = p.q_lat + (int64_t)b * p.q_lat_bs + (int64_t)hh * p.q_lat_hs;
+            const uint16_t* qr = DR ? p.q_rope + (int64_t)b * p.q_rope_bs + (int64_t)hh * p.q_rope_hs : nullptr;
 #pragma unroll
-            for (int ks = 0; ks < 2 * G::KS; ++ks) qreg[ks] = *(const bf16x8*)(qrow + 16 * ((2 * ks + kh) ^ (hq & 7)));
+            for (int ks = 0; ks < 2 * G::KS; ++ks) {
+                const int c = 2 * ks + kh;
+                qreg[ks] = c < R / 8 ? *(const bf16x8*)(ql + 8 * c) : *(const bf16x8*)(qr + 8 * (c - R / 8));
+            }
         }
-        lds_barrier();  // Q in registers: buffers 2-3 free again
         // A operand: row (key) ksig(l%32) of the sub-chunk, chunk 2ks + kh;
         // with the row swizzle, chunk 16v + u2 sits at 256v + qo[u2/2 ...]:
         // latent k-steps ks -> qo[ks%8] + 256 (ks/8), rope k-steps -> ro[ks-32]
@@ -560,21 +548,10 @@ __global__ void __launch_bounds__((WsShape<HGS, QK16>::THREADS), 1) mla_decode_w
         for (int T = 0; T < HT; ++T)
 #pragma unroll
             for (int J = 0; J < 8; ++J) oacc[T][J] = f32x4{0.f, 0.f, 0.f, 0.f};
-        // prologue: Q of the head group went into buffers 2-3 at the start
-        // (see above); sub-chunks 0 and 1 go behind it, sub-chunk 2 once the
-        // QK waves hold Q in registers
-        const int pro2 = min(nsub, 2);
-        for (int s = 0; s < pro2; ++s) issue(s, cbuf + s * G::BUF);
-        if (pro2 == 2)
-            wait_vmcnt<2 * G::NLD>();
-        else if (pro2 == 1)
-            wait_vmcnt<G::NLD>();
-        else
-            wait_vmcnt<0>();
-        lds_barrier();  // Q staged
-        lds_barrier();  // Q in registers: buffers 2-3 free again
-        if (nsub > 2) issue(2, cbuf + 2 * G::BUF);
-        // sub-chunks 0 .. NBUF-2 in flight, wait for 0
+        // prologue: sub-chunks 0 .. NBUF-2 at once (the QK waves load Q
+        // themselves), wait for 0
+        const int pro0 = min(nsub, NBUF - 1);
+        for (int s = 0; s < pro0; ++s) issue(s, cbuf + s * G::BUF);
         const int pro = min(nsub, NBUF - 1);
         if (pro >= 3)
             wait_vmcnt<2 * G::NLD>();
