@@ -390,12 +390,13 @@ def time_topk(torch, M, steps=200):
     scores = torch.randn(rows, cols, generator=g, device="cuda")
     sel = M.topk_geometry(rows, cols, k, ratio, start, 0)
     out = torch.empty(rows, sel, dtype=torch.int32, device="cuda")
-    ws = torch.empty(max(lib.mr_topk_workspace_size(rows), 1), dtype=torch.uint8, device="cuda")
+    ws = torch.empty(max(lib.mr_topk_workspace_size(rows, cols, k), 1), dtype=torch.uint8, device="cuda")
     a = M.TopkArgs()
     a.scores, a.score_row_stride, a.rows, a.cols = scores.data_ptr(), scores.stride(0), rows, cols
     a.top_k, a.ratio, a.start_pos, a.offset = k, ratio, start, 0
     a.out, a.out_row_stride = out.data_ptr(), out.stride(0)
-    a.status, a.flags = None, 0
+    status = torch.zeros(1, dtype=torch.int32, device="cuda")
+    a.status, a.flags = status.data_ptr(), 0   # NaN status on the device, no host read
     a.workspace, a.workspace_bytes = ws.data_ptr(), ws.numel()
     sp = M._stream(torch.cuda.current_stream())
     for _ in range(20):

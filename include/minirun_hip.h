@@ -433,12 +433,16 @@ mr_status mr_indexer_scores(const void *queries, mr_dtype q_dtype, int32_t seq, 
  * available) keys are written as offset + key, or -1 for a key >= visible.
  * Geometry errors are the reference's (:590-612), checked on the host; a
  * NaN score (anywhere in the matrix, :622-624) is reported through `status`
- * (device int32: 0 or MR_NONFINITE) and, with MR_TOPK_CHECK, by a
- * synchronising read that returns MR_NONFINITE.  Limits: top_k selected
- * <= 4096, available <= 65535, offset + available - 1 <= INT32_MAX.
- * Workspace: 4 * rows bytes (per-row NaN flags).
+ * (device int32: 0 or MR_NONFINITE), with no host synchronisation; without
+ * a status buffer (or with MR_TOPK_CHECK) the call reads the flags back and
+ * returns MR_NONFINITE, as the reference throws; MR_TOPK_UNCHECKED skips
+ * that read.  Limits: top_k selected
+ * <= 4096, offset + available - 1 <= INT32_MAX.  Rows of more than 32768
+ * keys are ranked in slices of 32768 on as many workgroups and merged.
+ * Workspace: mr_topk_workspace_size(rows, cols, top_k) bytes (per-row NaN
+ * flags; for rows of more than 32768 columns also the slices' candidates).
  * ------------------------------------------------------------------------ */
-enum { MR_TOPK_CHECK = 1 };
+enum { MR_TOPK_CHECK = 1, MR_TOPK_UNCHECKED = 2 };
 
 typedef struct mr_topk_args {
     const float *scores;
@@ -457,7 +461,7 @@ typedef struct mr_topk_args {
  * each row receives. */
 mr_status mr_topk_geometry(int32_t rows, int32_t cols, int32_t top_k, int32_t ratio, int32_t start_pos,
                            int32_t offset, int32_t *selected);
-size_t mr_topk_workspace_size(int32_t rows);
+size_t mr_topk_workspace_size(int32_t rows, int32_t cols, int32_t top_k);
 mr_status mr_topk_select(const mr_topk_args *args, void *stream);
 
 #ifdef __cplusplus

@@ -68,16 +68,16 @@ mr_status mr_topk_geometry(int32_t rows, int32_t cols, int32_t top_k, int32_t ra
     const int32_t sel = top_k < available ? top_k : available;
     if (sel > mr::TOPK_MAX)
         return fail(MR_INVALID_SHAPE, "top-k selection: %d keys per row exceed the limit of %d", sel, mr::TOPK_MAX);
-    if (available > mr::TOPK_MAX_KEYS)
-        return fail(MR_INVALID_SHAPE, "top-k selection: %d available keys exceed the limit of %d", available,
-                    mr::TOPK_MAX_KEYS);
     if (available > 0 && int64_t(offset) + available - 1 > INT32_MAX)
         return fail(MR_INVALID_SHAPE, "lightning cache index overflows Int");
     if (selected) *selected = sel;
     return MR_OK;
 }
 
-size_t mr_topk_workspace_size(int32_t rows) { return rows > 0 ? mrc::align256(size_t(rows) * 4) : 0; }
+size_t mr_topk_workspace_size(int32_t rows, int32_t cols, int32_t top_k) {
+    if (rows <= 0 || cols < 0 || top_k <= 0) return 0;
+    return mr::topk_workspace_bytes(rows, cols, top_k < mr::TOPK_MAX ? top_k : mr::TOPK_MAX);
+}
 
 mr_status mr_topk_select(const mr_topk_args* a, void* stream) {
     if (!a) return fail(MR_INVALID_ARGUMENT, "mr_topk_select: args is NULL");
@@ -88,7 +88,7 @@ mr_status mr_topk_select(const mr_topk_args* a, void* stream) {
         return fail(MR_INVALID_ARGUMENT, "top-k selection: scores and out must be non-NULL");
     if (a->score_row_stride < a->cols || (selected > 0 && a->out_row_stride < selected))
         return fail(MR_INVALID_ARGUMENT, "top-k selection: row strides are smaller than the rows");
-    const size_t need = mr_topk_workspace_size(a->rows);
+    const size_t need = mr::topk_workspace_bytes(a->rows, a->cols, selected);
     if (!a->workspace || a->workspace_bytes < need)
         return fail(MR_WORKSPACE_TOO_SMALL, "top-k selection: workspace %zu bytes < %zu required", a->workspace_bytes,
                     need);
@@ -107,9 +107,11 @@ mr_status mr_topk_select(const mr_topk_args* a, void* stream) {
     p.out = a->out;
     p.out_stride = a->out_row_stride;
     p.nan_flags = (int32_t*)a->workspace;
-    hipError_t e = mr::launch_topk_select(p, a->status, s);
+    hipError_t e = mr::launch_topk_select(p, a->workspace, a->status, s);
     if (e != hipSuccess) return hip_fail(e, "top-k selection launch");
-    if (a->flags & MR_TOPK_CHECK) {
+    // the reference throws on a NaN score: check on the host unless the
+    // caller takes the device status or opts out
+    if ((a->flags & MR_TOPK_CHECK) || (!a->status && !(a->flags & MR_TOPK_UNCHECKED))) {
         std::vector<int32_t> flags(size_t(a->rows));
         e = hipMemcpyAsync(flags.data(), p.nan_flags, size_t(a->rows) * 4, hipMemcpyDeviceToHost, s);
         if (e == hipSuccess) e = hipStreamSynchronize(s);

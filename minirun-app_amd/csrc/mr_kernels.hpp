@@ -97,7 +97,7 @@ hipError_t launch_prefill_attn(const PrefillAttnParams& p, hipStream_t st);
 
 // ---------------------------------------------------------------- top-k
 constexpr int TOPK_MAX = 4096;          // selected keys per row
-constexpr int TOPK_MAX_KEYS = 65535;    // available keys per row
+constexpr int TOPK_SLICE = 32768;       // keys one workgroup ranks in registers
 
 struct TopkParams {
     const float* scores;  // [rows][cols], row stride row_stride
@@ -108,9 +108,20 @@ struct TopkParams {
     int32_t* out;  // [rows][selected], row stride out_stride
     int64_t out_stride;
     int32_t* nan_flags;  // [rows]: 1 when the row holds a NaN
+    // rows of more than TOPK_SLICE keys: `slices` workgroups per row each
+    // rank TOPK_SLICE keys and write their first `selected` composites
+    // (score image << 32 | key, ascending; ~0 past the slice's keys) to
+    // cand[row][slice][selected], and their NaN flag to slice_nan[row][slice];
+    // merge rounds then reduce the sorted lists pairwise (set by the launcher)
+    int32_t slices;
+    unsigned long long* cand;
+    int32_t* slice_nan;
 };
 
-hipError_t launch_topk_select(const TopkParams& p, int32_t* status, hipStream_t st);
+// Workspace of a selection: per-row NaN flags, and for rows of more than
+// TOPK_SLICE keys the slice flags and two candidate buffers.
+size_t topk_workspace_bytes(int32_t rows, int32_t cols, int32_t selected);
+hipError_t launch_topk_select(const TopkParams& p, void* workspace, int32_t* status, hipStream_t st);
 
 // ---------------------------------------------------------------- affine
 struct AffineDequantParams {

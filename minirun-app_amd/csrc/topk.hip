@@ -19,6 +19,14 @@
 //      block scan (exactly `selected` of them);
 //   3. a bitonic sort of those composites in LDS gives the final order.
 // The row's NaN flag (any NaN among all `cols` scores) goes to nan_flags.
+//
+// Rows of more than 32768 keys split into slices of 32768, one workgroup
+// each (the same kernel, in parallel), which emit their own first
+// `selected` keys as sorted 64-bit composites (image << 32 | key); merge
+// rounds (topk_merge_kernel) then take the first `selected` of the merge of
+// two sorted lists, each output position finding its split by a merge-path
+// binary search, until one list is left; the last round writes the keys.
+// The order is the same total order, so the result is the same.
 #include <math.h>
 
 #include <type_traits>
@@ -78,10 +86,14 @@ __global__ void __launch_bounds__(NT) topk_select_kernel(TopkParams p) {
 
     const int row = blockIdx.x;
     const int tid = threadIdx.x;
-    const float* sr = p.scores + (int64_t)row * p.row_stride;
-    const int visible = p.start_pos == 0 ? (row + 1) / p.ratio : p.available;
-    const int n = p.available;
-    const int k = p.selected;
+    // the slice of the row this workgroup ranks (the whole row when slices == 1)
+    const int slice = blockIdx.y;
+    const int key0 = slice * (NT * KPT);
+    const float* sr = p.scores + (int64_t)row * p.row_stride + key0;
+    const int visible = (p.start_pos == 0 ? (row + 1) / p.ratio : p.available) - key0;
+    const int n = min(max(p.available - key0, 0), NT * KPT);  // keys of this slice
+    const int cols = p.cols - key0;
+    const int k = min(p.selected, n);
 
     if (tid == 0) nan_seen = 0;
     // this thread's keys j NT + tid (coalesced loads): the 32-bit images in
@@ -91,14 +103,15 @@ __global__ void __launch_bounds__(NT) topk_select_kernel(TopkParams p) {
 #pragma unroll
     for (int j = 0; j < KPT; ++j) {
         const int key = NT * j + tid;
-        const float f = key < p.cols ? sr[min(key, p.cols - 1)] : 0.f;
-        nan_here |= key < p.cols && isnan(f);
+        const float f = key < cols ? sr[min(key, cols - 1)] : 0.f;
+        nan_here |= key < cols && isnan(f);
         img[j] = ~ordered_bits(key < visible ? f : -INFINITY);
     }
     auto valid = [&](int j) { return NT * j + tid < n; };
     // NaN anywhere in the row (all columns, as the reference checks the
-    // whole matrix): columns past the registers' range
-    for (int i = KPT * NT + tid; i < p.cols; i += NT) nan_here |= isnan(sr[i]);
+    // whole matrix): the last slice checks the columns past every slice
+    if (slice == (int)gridDim.y - 1)
+        for (int i = KPT * NT + tid; i < cols; i += NT) nan_here |= isnan(sr[i]);
     __syncthreads();
     if (nan_here) nan_seen = 1;
 
@@ -338,6 +351,17 @@ __global__ void __launch_bounds__(NT) topk_select_kernel(TopkParams p) {
         }
     }
 
+    if (p.slices > 1) {  // this slice's sorted composites, ~0 past its keys
+        unsigned long long* crow = p.cand + ((int64_t)row * p.slices + slice) * p.selected;
+#pragma unroll
+        for (int e = 0; e < EPT; ++e) {
+            const int i = EPT * tid + e;
+            if (i < p.selected)
+                crow[i] = i < k ? ((x[e] >> 16) << 32) | (uint32_t)(key0 + (int)(uint32_t)(x[e] & 0xffffull)) : TK_NONE;
+        }
+        if (tid == 0) p.slice_nan[row * p.slices + slice] = nan_seen;
+        return;
+    }
     int32_t* orow = p.out + (int64_t)row * p.out_stride;
 #pragma unroll
     for (int e = 0; e < EPT; ++e) {
@@ -350,136 +374,54 @@ __global__ void __launch_bounds__(NT) topk_select_kernel(TopkParams p) {
     if (tid == 0) p.nan_flags[row] = nan_seen;
 }
 
-// Rows of more than 32768 keys (up to 65535): the same selection with the
-// row re-read from global memory on every pass (one 1024-thread workgroup,
-// 4 radix passes of 8 bits on the 32-bit image, then a chunked sweep that
-// takes the keys below the selected value and the first equal ones in key
-// order).
-constexpr int TK_THREADS = 1024;
-
-// Sorting ascending by this image sorts scores descending.
-__device__ __forceinline__ uint32_t desc_image(const float* row, int key, int visible) {
-    const float f = key < visible ? row[key] : -INFINITY;
-    return ~ordered_bits(f);
-}
-
-// Inclusive scan over a 1024-thread block; `sh` holds >= 16 words.
-__device__ __forceinline__ uint32_t block_scan_incl_1024(uint32_t v, uint32_t* sh) {
-    const int l = threadIdx.x & 63, w = threadIdx.x >> 6;
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-        const uint32_t t = __shfl_up(v, o);
-        if (l >= o) v += t;
-    }
-    if (l == 63) sh[w] = v;
-    __syncthreads();
-    uint32_t base = 0;
-    for (int i = 0; i < w; ++i) base += sh[i];
-    __syncthreads();
-    return v + base;
-}
-
-__global__ void __launch_bounds__(TK_THREADS) topk_select_gmem_kernel(TopkParams p) {
-    __shared__ uint32_t hist[256];
-    __shared__ uint32_t scan_sh[16];
-    __shared__ uint32_t pick[3];  // bin, count before it, count in it
-    __shared__ unsigned long long comp[TOPK_MAX];
-    __shared__ int nan_seen;
-
-    const int row = blockIdx.x;
-    const int tid = threadIdx.x;
-    const float* sr = p.scores + (int64_t)row * p.row_stride;
+// One merge round over rows of sorted composite lists: list pair q of a row
+// (lists 2q and 2q+1 of `lists`, each `len` long; an odd last list passes
+// through) -> the first `len` of their merge.  Output position i takes its
+// split from a merge-path binary search over global memory (the lists are
+// short and cached).  The last round (one pair left) writes the keys
+// instead, offset + key or -1 past `visible`, and the row's NaN flag.
+__global__ void __launch_bounds__(256) topk_merge_kernel(TopkParams p, const unsigned long long* in, int lists,
+                                                          unsigned long long* outc) {
+    const int row = blockIdx.y;
+    const int q = blockIdx.x;
+    const int len = p.selected;
+    const unsigned long long* A = in + ((int64_t)row * lists + 2 * q) * len;
+    const bool pair = 2 * q + 1 < lists;
+    const unsigned long long* B = A + len;
+    const int nout = (lists + 1) / 2;
+    const bool last = nout == 1;
     const int visible = p.start_pos == 0 ? (row + 1) / p.ratio : p.available;
-    const int n = p.available;
-    const int k = p.selected;
-
-    // NaN anywhere in the row (all columns, as the reference checks the
-    // whole matrix)
-    if (tid == 0) nan_seen = 0;
-    __syncthreads();
-    bool nan_here = false;
-    for (int i = tid; i < p.cols; i += TK_THREADS) nan_here |= isnan(sr[i]);
-    if (nan_here) nan_seen = 1;
-
-    // 1. radix select on the 32-bit image: the k-th smallest value D
-    uint32_t prefix = 0, mask = 0;
-    uint32_t remaining = (uint32_t)k;  // how many of the still-tied keys to take
-#pragma unroll 1
-    for (int shift = 24; shift >= 0; shift -= 8) {
-        if (tid < 256) hist[tid] = 0;
-        __syncthreads();
-        for (int i = tid; i < n; i += TK_THREADS) {
-            const uint32_t d = desc_image(sr, i, visible);
-            if ((d & mask) == prefix) atomicAdd(&hist[(d >> shift) & 255u], 1u);
-        }
-        __syncthreads();
-        const uint32_t h = tid < 256 ? hist[tid] : 0u;
-        const uint32_t incl = block_scan_incl_1024(h, scan_sh);
-        if (tid < 256 && incl >= remaining && incl - h < remaining) {
-            pick[0] = (uint32_t)tid;
-            pick[1] = incl - h;
-        }
-        __syncthreads();
-        prefix |= pick[0] << shift;
-        mask |= 255u << shift;
-        remaining -= pick[1];
-        __syncthreads();
-    }
-    const uint32_t D = prefix;
-    const uint32_t n_less = (uint32_t)k - remaining;  // keys strictly before D
-
-    // 2. collection: thread t sweeps keys [t*C, (t+1)*C) in order
-    const int C = (n + TK_THREADS - 1) / TK_THREADS;
-    const int lo = min(tid * C, n), hi = min(lo + C, n);
-    uint32_t c_less = 0, c_eq = 0;
-    for (int i = lo; i < hi; ++i) {
-        const uint32_t d = desc_image(sr, i, visible);
-        c_less += d < D;
-        c_eq += d == D;
-    }
-    // both counts fit 16 bits (n <= 65535)
-    const uint32_t both = block_scan_incl_1024(c_less | (c_eq << 16), scan_sh) - (c_less | (c_eq << 16));
-    uint32_t pos_less = both & 0xffffu, rank_eq = both >> 16;
-    for (int i = lo; i < hi; ++i) {
-        const uint32_t d = desc_image(sr, i, visible);
-        const unsigned long long cv = ((unsigned long long)d << 32) | (uint32_t)i;
-        if (d < D) {
-            comp[pos_less++] = cv;
-        } else if (d == D) {
-            if (rank_eq < remaining) comp[n_less + rank_eq] = cv;
-            ++rank_eq;
-        }
-    }
-    // pad to a power of two for the sort
-    int npow = 1;
-    while (npow < k) npow <<= 1;
-    for (int i = k + tid; i < npow; i += TK_THREADS) comp[i] = ~0ull;
-    __syncthreads();
-
-    // 3. bitonic sort, ascending
-    for (int size = 2; size <= npow; size <<= 1) {
-        for (int stride = size >> 1; stride > 0; stride >>= 1) {
-            for (int i = tid; i < npow; i += TK_THREADS) {
-                const int j = i ^ stride;
-                if (j > i) {
-                    const unsigned long long a = comp[i], b = comp[j];
-                    const bool up = (i & size) == 0;
-                    if ((a > b) == up) {
-                        comp[i] = b;
-                        comp[j] = a;
-                    }
-                }
+    for (int i = threadIdx.x; i < len; i += 256) {
+        unsigned long long v;
+        if (pair) {
+            // a = number of the first i + 1 outputs taken from A
+            int lo = max(0, i + 1 - len), hi = min(i + 1, len);
+            while (lo < hi) {
+                const int mid = (lo + hi) >> 1;
+                if (A[mid] < B[i - mid])
+                    lo = mid + 1;
+                else
+                    hi = mid;
             }
-            __syncthreads();
+            // output i is the larger of A[lo - 1] and B[i - lo] (the last taken)
+            const unsigned long long a = lo > 0 ? A[lo - 1] : 0ull;
+            const unsigned long long b = i - lo >= 0 ? B[i - lo] : 0ull;
+            v = lo == 0 ? b : (i - lo < 0 ? a : (a > b ? a : b));
+        } else {
+            v = A[i];
+        }
+        if (last) {
+            const int key = (int)(uint32_t)(v & 0xffffffffull);
+            p.out[(int64_t)row * p.out_stride + i] = key >= visible ? -1 : p.offset + key;
+        } else {
+            outc[((int64_t)row * nout + q) * len + i] = v;
         }
     }
-
-    int32_t* orow = p.out + (int64_t)row * p.out_stride;
-    for (int i = tid; i < k; i += TK_THREADS) {
-        const int key = (int)(uint32_t)(comp[i] & 0xffffffffull);
-        orow[i] = key >= visible ? -1 : p.offset + key;
+    if (last && threadIdx.x == 0) {
+        int f = 0;
+        for (int sl = 0; sl < p.slices; ++sl) f |= p.slice_nan[row * p.slices + sl];
+        p.nan_flags[row] = f;
     }
-    if (tid == 0) p.nan_flags[row] = nan_seen;
 }
 
 // status = MR_NONFINITE (5) when any row flagged a NaN, else 0
@@ -496,17 +438,52 @@ __global__ void __launch_bounds__(256) topk_status_kernel(const int32_t* flags, 
 
 }  // namespace
 
-hipError_t launch_topk_select(const TopkParams& p, int32_t* status, hipStream_t st) {
+size_t topk_workspace_bytes(int32_t rows, int32_t cols, int32_t selected) {
+    auto a256 = [](size_t x) { return (x + 255) & ~size_t(255); };
+    size_t bytes = a256(size_t(rows) * 4);
+    if (cols > TOPK_SLICE) {
+        const size_t slices = (size_t(cols) + TOPK_SLICE - 1) / TOPK_SLICE;
+        bytes += a256(size_t(rows) * slices * 4);
+        bytes += 2 * a256(size_t(rows) * slices * size_t(selected) * 8);
+    }
+    return bytes;
+}
+
+hipError_t launch_topk_select(const TopkParams& p0, void* workspace, int32_t* status, hipStream_t st) {
+    TopkParams p = p0;
+    p.slices = 1;
     // keys per thread: the row's ranked keys in registers
-    const dim3 g((unsigned)p.rows);
-    if (p.available <= 256 * 4)
-        hipLaunchKernelGGL((topk_select_kernel<256, 4>), g, dim3(256), 0, st, p);
-    else if (p.available <= 1024 * 16)
-        hipLaunchKernelGGL((topk_select_kernel<1024, 16>), g, dim3(1024), 0, st, p);
-    else if (p.available <= 1024 * 32)
-        hipLaunchKernelGGL((topk_select_kernel<1024, 32>), g, dim3(1024), 0, st, p);
-    else
-        hipLaunchKernelGGL(topk_select_gmem_kernel, g, dim3(TK_THREADS), 0, st, p);
+    if (p.available <= 256 * 4) {
+        hipLaunchKernelGGL((topk_select_kernel<256, 4>), dim3((unsigned)p.rows), dim3(256), 0, st, p);
+    } else if (p.available <= 1024 * 16) {
+        hipLaunchKernelGGL((topk_select_kernel<1024, 16>), dim3((unsigned)p.rows), dim3(1024), 0, st, p);
+    } else if (p.available <= TOPK_SLICE) {
+        hipLaunchKernelGGL((topk_select_kernel<1024, 32>), dim3((unsigned)p.rows), dim3(1024), 0, st, p);
+    } else {
+        // slices of 32768 keys in parallel, then pairwise merge rounds
+        auto a256 = [](size_t x) { return (x + 255) & ~size_t(255); };
+        char* ws = (char*)workspace + a256(size_t(p.rows) * 4);
+        const int slices = (p.available + TOPK_SLICE - 1) / TOPK_SLICE;
+        const int max_slices = (p.cols + TOPK_SLICE - 1) / TOPK_SLICE;
+        p.slices = slices;
+        p.slice_nan = (int32_t*)ws;
+        ws += a256(size_t(p.rows) * max_slices * 4);
+        unsigned long long* buf[2] = {(unsigned long long*)ws,
+                                      (unsigned long long*)(ws + a256(size_t(p.rows) * max_slices * size_t(p.selected) * 8))};
+        p.cand = buf[0];
+        hipLaunchKernelGGL((topk_select_kernel<1024, 32>), dim3((unsigned)p.rows, (unsigned)slices), dim3(1024), 0, st, p);
+        hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+        int lists = slices, cur = 0;
+        while (lists > 1) {
+            const int nout = (lists + 1) / 2;
+            hipLaunchKernelGGL(topk_merge_kernel, dim3((unsigned)nout, (unsigned)p.rows), dim3(256), 0, st, p,
+                               (const unsigned long long*)buf[cur], lists, buf[cur ^ 1]);
+            if ((e = hipGetLastError()) != hipSuccess) return e;
+            lists = nout;
+            cur ^= 1;
+        }
+    }
     hipError_t e = hipGetLastError();
     if (e == hipSuccess && status) {
         hipLaunchKernelGGL(topk_status_kernel, dim3(1), dim3(256), 0, st, p.nan_flags, p.rows, status);

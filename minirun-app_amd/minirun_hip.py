@@ -119,6 +119,7 @@ class TopkArgs(C.Structure):
 
 
 TOPK_CHECK = 1
+TOPK_UNCHECKED = 2
 
 _P = C.c_void_p
 _I32P = C.POINTER(C.c_int32)
@@ -162,7 +163,7 @@ SIGNATURES = {
     "mr_mla_prefill_workspace_size": (C.c_size_t, [C.POINTER(PrefillArgs)]),
     "mr_mla_prefill": (C.c_int, [C.POINTER(PrefillArgs), _P]),
     "mr_topk_geometry": (C.c_int, [C.c_int32, C.c_int32, C.c_int32, C.c_int32, C.c_int32, C.c_int32, _I32P]),
-    "mr_topk_workspace_size": (C.c_size_t, [C.c_int32]),
+    "mr_topk_workspace_size": (C.c_size_t, [C.c_int32, C.c_int32, C.c_int32]),
     "mr_topk_select": (C.c_int, [C.POINTER(TopkArgs), _P]),
     "mr_indexer_scores": (C.c_int, [_P, C.c_int, C.c_int32, C.c_int32, C.c_int32, C.c_int64, C.c_int64, _P, C.c_int,
                                     C.c_int32, C.c_int32, C.c_int64, _P, C.c_int, C.c_int32, C.c_int32, C.c_int64,
@@ -676,13 +677,14 @@ def lightning_select(scores, top_k, ratio, start_pos, offset, *, check=True, sta
     rows, cols = scores.shape
     sel = topk_geometry(rows, cols, top_k, ratio, start_pos, offset)
     out = torch.empty(rows, max(sel, 1), dtype=torch.int32, device=scores.device)
-    ws = torch.empty(max(load().mr_topk_workspace_size(rows), 1), dtype=torch.uint8, device=scores.device)
+    ws = torch.empty(max(load().mr_topk_workspace_size(rows, cols, top_k), 1), dtype=torch.uint8,
+                     device=scores.device)
     a = TopkArgs()
     a.scores, a.score_row_stride, a.rows, a.cols = scores.data_ptr(), scores.stride(0), rows, cols
     a.top_k, a.ratio, a.start_pos, a.offset = top_k, ratio, start_pos, offset
     a.out, a.out_row_stride = out.data_ptr(), out.stride(0)
     a.status = status.data_ptr() if status is not None else None
-    a.flags = TOPK_CHECK if check else 0
+    a.flags = TOPK_CHECK if check else (0 if status is not None else TOPK_UNCHECKED)
     a.workspace, a.workspace_bytes = ws.data_ptr(), ws.numel()
     _check(load().mr_topk_select(C.byref(a), _stream(stream)))
     return out[:, :sel]

@@ -68,8 +68,44 @@ def test_prefill_rows_with_masking(M, rows, cols, top_k, ratio, offset):
 
 
 def test_limits(M):
-    compare(M, normal("tk.max", (1, 65535)), 4096, 1, 65534, 0, "max-keys")
+    compare(M, normal("tk.max", (1, 65535)), 4096, 1, 65534, 0, "two-slices")
     compare(M, normal("tk.one", (1, 1)), 1, 1, 0, 0, "one-key")
+
+
+def test_v4_full_size_row(M):
+    # DeepSeek V4: max_position_embeddings 1048576 at compression ratio 4
+    # (Tests/Fixtures/deepseek-v4/current-official-config.json:22) -> 262144
+    # compressed keys for the last token: 8 slices of 32768, 3 merge rounds
+    compare(M, normal("tk.v4", (1, 262144)), 2048, 4, 1048575, 0, "v4-262144")
+    compare(M, normal("tk.v4k", (1, 262144)), 4096, 4, 1048575, 5, "v4-262144-k4096")
+
+
+def test_slices_ties_odd_counts_and_masking(M):
+    # ties across slice boundaries break by ascending key id; three slices
+    # (an odd list passes a merge round unmerged); keys past `visible`
+    # (-1) when the row has more columns than the position ranks
+    s = np.floor(normal("tk.sl", (1, 70000)) * 2).astype(np.float32)   # ~10 distinct values
+    compare(M, s, 3000, 1, 69999, 11, "ties-3-slices")
+    compare(M, normal("tk.sl2", (1, 100000)), 1000, 1, 80000, 0, "cols-past-available")
+    # a short last slice: 32768 + 5 keys, top_k larger than that slice
+    compare(M, normal("tk.sl3", (1, 32773)), 2048, 1, 32772, 0, "short-last-slice")
+    z = np.zeros((1, 98304), np.float32)   # one value everywhere: the first keys win
+    compare(M, z, 4096, 1, 98303, 0, "all-equal-3-slices")
+
+
+def test_nan_in_a_late_slice_is_reported(M):
+    import torch
+
+    import minirun_hip as MH
+
+    s = normal("tk.nanl", (1, 140000))
+    s[0, 139999] = np.nan   # past the last ranked key of a 131072-key row
+    with pytest.raises(MH.MRError) as e:
+        M.lightning_select(dev(s), 256, 1, 131071, 0)
+    assert e.value.status == MH.NONFINITE
+    status = torch.full((1,), -1, dtype=torch.int32, device="cuda")
+    M.lightning_select(dev(normal("tk.nanok", (1, 140000))), 256, 1, 131071, 0, check=False, status=status)
+    assert int(status.item()) == 0
 
 
 def test_nan_is_reported(M):

@@ -115,7 +115,7 @@ def test_index_table_errors():
     (2, 4, 2, 0, 0, 0, "invalid lightning-index selection geometry"),
     (2, 4, 2, 1, 3, 0, "exactly one token"),
     (1, 2, 2, 1, 3, 0, "fewer compressed keys"),
-    (1, 70000, 8, 1, 69999, 0, "exceed the limit"),
+    (1, 8192, 5000, 1, 8191, 0, "exceed the limit"),
     (1, 8, 5000, 1, 7, 0, None),
     (1, 8, 4, 1, 7, 2147483645, "overflows"),
 ])
@@ -134,6 +134,7 @@ def test_topk_geometry_errors(rows, cols, top_k, ratio, start, offset, needle):
 
 def test_topk_geometry_counts():
     assert M.topk_geometry(1, 32768, 2048, 4, 131071, 0) == 2048
+    assert M.topk_geometry(1, 262144, 2048, 4, 1048575, 0) == 2048   # V4 at 1M positions: no key limit
     assert M.topk_geometry(300, 75, 16, 4, 0, 128) == 16
     assert M.topk_geometry(3, 4, 16, 4, 0, 0) == 0   # fewer than ratio tokens: empty rows
 
