@@ -48,9 +48,12 @@ def split_kernel_bytes():
 
 # HBM bytes one launch of the dense split kernel moves (H=128, N=32768):
 # FETCH_SIZE x 2.0 + WRITE_SIZE x 1.0 (factors from a streaming kernel of
-# known size), measured with rocprofv3 --pmc; profiles/mla_decode_hbm_counters.md
-# holds the passes.  Of it, 16,777,216 B are the bf16 split partials written.
+# known size), from two rocprofv3 --pmc passes over this bench command; the
+# passes and the commit they measured are in profiles/mla_decode_hbm_counters.md.
+# A recorded value, not measured by this run.  Of it, 16,777,216 B are the
+# bf16 split partials written.
 SPLIT_TRAFFIC_BYTES = 56488746
+SPLIT_TRAFFIC_SOURCE = "recorded: rocprofv3 FETCH_SIZE/WRITE_SIZE passes, profiles/mla_decode_hbm_counters.md"
 
 
 def sparse_bytes(B=4, K=2048):
@@ -517,17 +520,47 @@ def mfma_probe(torch, M):
     return {"tflops": round(flop / (ms * 1e-3) / 1e12, 1), "clock_ghz": round(clock_ghz, 3)}
 
 
-def cpu_baseline(budget_s=12.0):
+def torch_cpu_decode(torch, threads, budget_s=8.0):
+    """The same decode layer as fp32 BLAS products on the host (torch CPU):
+    S = (q_lat . c^T + q_rope . k^T) * scale, softmax, O = P . c; median of
+    whole layers within the time budget."""
+    torch.set_num_threads(threads)
+    g = torch.Generator().manual_seed(0x4D4C410002)
+    q_lat = torch.randn(H, R, generator=g)
+    q_rope = torch.randn(H, DR, generator=g)
+    cache = 0.5 * torch.randn(N, R + DR, generator=g)
+    lat, rk = cache[:, :R], cache[:, R:]
+
+    def layer():
+        s = (q_lat @ lat.T + q_rope @ rk.T) * SCALE
+        return torch.softmax(s, dim=-1) @ lat
+
+    layer()
+    times = []
+    t_start = time.perf_counter()
+    while len(times) < 3 or time.perf_counter() - t_start < budget_s:
+        t0 = time.perf_counter()
+        layer()
+        times.append(time.perf_counter() - t0)
+        if len(times) >= 200:
+            break
+    times.sort()
+    return times[len(times) // 2], len(times)
+
+
+def cpu_baseline(torch, budget_s=12.0):
     """The oracle (scalar C, OpenMP over heads) on the same workload, timed on
-    this host's cores; a bounded sample: whole config-2 decode calls until the
-    time budget is used (at least 2)."""
+    this host's cores; a bounded sample: whole decode layers (H=128,
+    N=32768) until the time budget is used (at least 2).  Threads: every
+    core of the process's CPU share (OMP_NUM_THREADS when set, else the
+    affinity mask).  Beside it, the same layer as torch-CPU fp32 BLAS."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import numpy as np
 
     import oracle as O
 
-    threads = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()
-    threads = max(1, min(threads, 16))
+    visible = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()
+    threads = max(1, min(visible, int(os.environ.get("OMP_NUM_THREADS", visible))))
     ql = O.normal_bf16("c2.q_lat", (H, R), threads=threads)
     qr = O.normal_bf16("c2.q_rope", (H, DR), threads=threads)
     cache = O.normal_bf16("c2.cache", (N, R + DR), std=0.5, threads=threads)
@@ -542,13 +575,17 @@ def cpu_baseline(budget_s=12.0):
             break
     times.sort()
     med = times[len(times) // 2]
+    t_blas, n_blas = torch_cpu_decode(torch, threads)
     try:
         model = [l.split(":", 1)[1].strip() for l in open("/proc/cpuinfo") if l.startswith("model name")][0]
     except Exception:
         model = platform.processor()
     return {"value": round(med * 1e6, 1), "unit": "us/layer", "cores": threads, "kind": "port",
-            "sample": f"{len(times)} full decode layers (H=128, N=32768) in fp32, oracle C port, "
-                      f"median; host: {model}"}
+            "sample": f"{len(times)} full decode layers (H=128, N=32768) in fp32, oracle C port (OpenMP over "
+                      f"heads), median; {threads} threads = the process's CPU share ({visible} cores visible); "
+                      f"host: {model}",
+            "torch_cpu_fp32": {"value": round(t_blas * 1e6, 1), "unit": "us/layer", "threads": threads,
+                               "sample": f"{n_blas} layers as torch CPU fp32 BLAS products, median"}}
 
 
 def main():
@@ -589,7 +626,7 @@ def main():
     d96 = time_decode_96(torch, M, args.steps, args.warmup)
     log(f"bench: decode 96 heads {d96}")
     log("bench: causal prefill T=4096 H=128")
-    pf = time_prefill(torch, M, max(args.steps // 20, 5), 3)
+    pf = time_prefill(torch, M, max(args.steps // 8, 50), 10)
     log(f"bench: prefill {pf}")
     tk_ms = time_topk(torch, M)
     log(f"bench: top-k 2048 of 32768 {tk_ms * 1e3:.2f} us")
@@ -648,7 +685,9 @@ def main():
         "mfma_probe_clock_ghz": mp["clock_ghz"],
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": SPLIT_TRAFFIC_BYTES,
-                     "kernel": "mla_decode_ws", "algorithmic_bytes": split_kernel_bytes()},
+                     "traffic_source": SPLIT_TRAFFIC_SOURCE,
+                     "kernel": "mla_decode_ws", "algorithmic_bytes": split_kernel_bytes(),
+                     "layer_frac": round(cache_bytes_per_layer() / (d["wall_ms"] * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)},
     }
     if args.copy_calibration:
         src = torch.randn(64 << 20, device="cuda")
@@ -659,7 +698,7 @@ def main():
         log("bench: copy calibration: 3 x neg over 268435456 B read + 268435456 B written")
     if not args.no_cpu_baseline:
         log("bench: cpu baseline (oracle port)")
-        result["cpu_baseline"] = cpu_baseline()
+        result["cpu_baseline"] = cpu_baseline(torch)
     print(json.dumps(result), flush=True)
 
 

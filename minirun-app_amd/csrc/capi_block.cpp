@@ -195,7 +195,7 @@ mr_status block_proj(const void* x, int64_t in, const mr_projection* w, void* y,
     g.y_f32 = 0;
     g.y_stride_row = 1;
     g.y_stride_token = w->dense.out_features;
-    const bool staged = in <= mr::DENSE_STAGE_FLOATS;
+    const bool staged = in * 2 <= mr::DENSE_STAGE_BYTES;  // one bf16 vector in LDS
     if (staged) {
         g.norm_w = norm_w;
         g.norm_w_f32 = norm_dtype == MR_F32;
@@ -356,7 +356,7 @@ mr_status mr_linear(const void* x, mr_dtype x_dtype, int32_t tokens, int64_t x_s
     g.y_f32 = y_dtype == MR_F32;
     g.y_stride_row = 1;
     g.y_stride_token = y_stride;
-    const bool staged = w->in_features <= mr::DENSE_STAGE_FLOATS;
+    const bool staged = w->in_features * (x_dtype == MR_F32 ? 4 : 2) <= mr::DENSE_STAGE_BYTES;
     const hipError_t e = mr::launch_dense_gemv(g, staged, mrc::cu_count(), (hipStream_t)stream);
     return e == hipSuccess ? MR_OK : hip_fail(e, "linear launch");
 }

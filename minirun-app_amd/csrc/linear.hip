@@ -33,34 +33,58 @@ namespace {
 
 constexpr int LT = 256;  // threads per workgroup
 
-__device__ __forceinline__ float bf16_round(float v) { return bf16_bits_to_f32(f32_to_bf16_bits(v)); }
-
 __device__ __forceinline__ float load_act(const void* p, int f32, int64_t i) {
     return f32 ? ((const float*)p)[i] : bf16_bits_to_f32(((const uint16_t*)p)[i]);
 }
 
-// fp32 dot of one 16-byte weight chunk (8 bf16 or 4 f32 values) with the
-// matching x values
-template <bool WF32>
-__device__ __forceinline__ float chunk_dot(const u32x4& w, const float* x) {
-    float a = 0.f;
+typedef __bf16 bf16x2v __attribute__((ext_vector_type(2)));
+
+// Dot of one 16-byte weight chunk with the matching activation values:
+// bf16 weights and bf16 activations as four v_dot2_f32_bf16 on the pairs;
+// otherwise fp32 multiply-adds (f32 weights: 4 values a chunk).
+template <bool WF32, bool XF32>
+__device__ __forceinline__ float chunk_dot(const u32x4& w, const void* x, float a) {
     if (WF32) {
+        if (XF32) {
+            const f32x4 xv = *(const f32x4*)x;
 #pragma unroll
-        for (int k = 0; k < 4; ++k) a = fmaf(__uint_as_float(w[k]), x[k], a);
-    } else {
+            for (int k = 0; k < 4; ++k) a = fmaf(__uint_as_float(w[k]), xv[k], a);
+        } else {
+            const u32x2 xv = *(const u32x2*)x;
+            a = fmaf(__uint_as_float(w[0]), __uint_as_float(xv[0] << 16), a);
+            a = fmaf(__uint_as_float(w[1]), __uint_as_float(xv[0] & 0xffff0000u), a);
+            a = fmaf(__uint_as_float(w[2]), __uint_as_float(xv[1] << 16), a);
+            a = fmaf(__uint_as_float(w[3]), __uint_as_float(xv[1] & 0xffff0000u), a);
+        }
+    } else if (!XF32) {
+        const u32x4 xv = *(const u32x4*)x;
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
-            a = fmaf(__uint_as_float(w[k] << 16), x[2 * k], a);
-            a = fmaf(__uint_as_float(w[k] & 0xffff0000u), x[2 * k + 1], a);
+            // bit_cast of a vector element reads element 0 with this compiler: copy to scalars first
+            const uint32_t wk = w[k], xk = xv[k];
+            a = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2v, wk), __builtin_bit_cast(bf16x2v, xk), a,
+                                                false);
+        }
+    } else {
+        const f32x4 x0 = *(const f32x4*)x, x1 = *((const f32x4*)x + 1);
+#pragma unroll
+        for (int k = 0; k < 2; ++k) {
+            a = fmaf(__uint_as_float(w[k] << 16), x0[2 * k], a);
+            a = fmaf(__uint_as_float(w[k] & 0xffff0000u), x0[2 * k + 1], a);
+            a = fmaf(__uint_as_float(w[k + 2] << 16), x1[2 * k], a);
+            a = fmaf(__uint_as_float(w[k + 2] & 0xffff0000u), x1[2 * k + 1], a);
         }
     }
     return a;
 }
 
-template <bool WF32, bool STAGED>
+constexpr int GEMV_UNROLL = 8;  // weight chunks in flight per lane
+
+template <bool WF32, bool XF32, bool STAGED>
 __global__ void __launch_bounds__(LT) dense_gemv_kernel(DenseGemvParams p) {
-    constexpr int VPC = WF32 ? 4 : 8;  // values per 16-byte chunk
-    extern __shared__ float xs[];       // staged: [mt][in]
+    constexpr int VPC = WF32 ? 4 : 8;  // values per 16-byte weight chunk
+    constexpr int XE = XF32 ? 4 : 2;   // bytes per activation value
+    extern __shared__ __attribute__((aligned(16))) char xs[];  // staged: [mt][in] activations
     __shared__ float red[LT / 64];
     const int tid = threadIdx.x;
     const int t0 = blockIdx.y * p.mt;
@@ -91,7 +115,10 @@ __global__ void __launch_bounds__(LT) dense_gemv_kernel(DenseGemvParams p) {
                     const float g = load_act(p.gate, p.gate_f32, (int64_t)(t0 + t) * p.gate_stride + i);
                     v = v * (1.f / (1.f + __builtin_amdgcn_exp2f(-g * 1.4426950408889634f)));
                 }
-                xs[t * p.in + i] = p.x_f32 ? v : bf16_round(v);
+                if (XF32)
+                    ((float*)xs)[t * p.in + i] = v;
+                else  // bf16 inputs stay bf16, as a separate norm or gate stage would store them
+                    ((uint16_t*)xs)[t * p.in + i] = f32_to_bf16_bits(v);
             }
         }
         __syncthreads();
@@ -111,45 +138,32 @@ __global__ void __launch_bounds__(LT) dense_gemv_kernel(DenseGemvParams p) {
         const int64_t g = jj / p.map_a;
         const int64_t wrow = g * p.map_b + p.map_c + (jj - g * p.map_a);
         const char* wr = (const char*)p.w + wrow * p.w_rs * (WF32 ? 4 : 2);
-        const int64_t xd = (int64_t)t0 * p.x_stride + g * p.x_vec_stride;  // direct mode: this row's x
+        // direct mode: this row's activation vector in global memory
+        const char* xd = (const char*)p.x + ((int64_t)t0 * p.x_stride + g * p.x_vec_stride) * XE;
         float acc[MAX_GEMV_TOKENS];
 #pragma unroll
         for (int t = 0; t < MAX_GEMV_TOKENS; ++t) acc[t] = 0.f;
-        int c = li;
-        // four chunks of the row in flight per lane, then the remainder
-        for (; c + 3 * tpr < chunks; c += 4 * tpr) {
-            u32x4 wv[4];
-#pragma unroll
-            for (int u = 0; u < 4; ++u) wv[u] = __builtin_nontemporal_load((const u32x4*)(wr + 16 * (int64_t)(c + u * tpr)));
-#pragma unroll
-            for (int u = 0; u < 4; ++u) {
-                const int i0 = (c + u * tpr) * VPC;
-                if (STAGED) {
-#pragma unroll
-                    for (int t = 0; t < MAX_GEMV_TOKENS; ++t)
-                        if (t < mt) acc[t] += chunk_dot<WF32>(wv[u], xs + t * p.in + i0);
-                } else {
-                    float xv[VPC];
-#pragma unroll
-                    for (int k = 0; k < VPC; ++k) xv[k] = load_act(p.x, p.x_f32, xd + i0 + k);
-                    acc[0] += chunk_dot<WF32>(wv[u], xv);
-                }
-            }
-        }
-        for (; c < chunks; c += tpr) {
-            const u32x4 wv = __builtin_nontemporal_load((const u32x4*)(wr + 16 * (int64_t)c));
+        auto use = [&](const u32x4& wv, int c) {
             const int i0 = c * VPC;
             if (STAGED) {
 #pragma unroll
                 for (int t = 0; t < MAX_GEMV_TOKENS; ++t)
-                    if (t < mt) acc[t] += chunk_dot<WF32>(wv, xs + t * p.in + i0);
+                    if (t < mt) acc[t] = chunk_dot<WF32, XF32>(wv, xs + ((int64_t)t * p.in + i0) * XE, acc[t]);
             } else {
-                float xv[VPC];
-#pragma unroll
-                for (int k = 0; k < VPC; ++k) xv[k] = load_act(p.x, p.x_f32, xd + i0 + k);
-                acc[0] += chunk_dot<WF32>(wv, xv);
+                acc[0] = chunk_dot<WF32, XF32>(wv, xd + (int64_t)i0 * XE, acc[0]);
             }
+        };
+        int c = li;
+        // GEMV_UNROLL chunks of the row in flight per lane, then the remainder
+        for (; c + (GEMV_UNROLL - 1) * tpr < chunks; c += GEMV_UNROLL * tpr) {
+            u32x4 wv[GEMV_UNROLL];
+#pragma unroll
+            for (int u = 0; u < GEMV_UNROLL; ++u)
+                wv[u] = __builtin_nontemporal_load((const u32x4*)(wr + 16 * (int64_t)(c + u * tpr)));
+#pragma unroll
+            for (int u = 0; u < GEMV_UNROLL; ++u) use(wv[u], c + u * tpr);
         }
+        for (; c < chunks; c += tpr) use(__builtin_nontemporal_load((const u32x4*)(wr + 16 * (int64_t)c)), c);
         const int nt = STAGED ? mt : 1;
 #pragma unroll
         for (int t = 0; t < MAX_GEMV_TOKENS; ++t) {
@@ -233,9 +247,24 @@ hipError_t launch_gate_mul(const uint16_t* x, const uint16_t* g, int64_t n, uint
     return hipGetLastError();
 }
 
-int dense_gemv_tokens_per_tile(int in, int m) {
-    const int by_lds = (DENSE_STAGE_FLOATS / in) > 0 ? DENSE_STAGE_FLOATS / in : 1;
-    return max(1, min(min(m, by_lds), MAX_GEMV_TOKENS));
+int dense_gemv_tokens_per_tile(int in, int m, bool x_f32) {
+    const int cap = DENSE_STAGE_BYTES / (in * (x_f32 ? 4 : 2));
+    return max(1, min(min(m, cap > 0 ? cap : 1), MAX_GEMV_TOKENS));
+}
+
+template <bool WF32, bool XF32>
+static hipError_t launch_gemv(const DenseGemvParams& p, bool staged, dim3 grid, size_t lds, hipStream_t st) {
+    if (staged) {
+        if (lds > 65536) {
+            const hipError_t e = hipFuncSetAttribute((const void*)dense_gemv_kernel<WF32, XF32, true>,
+                                                     hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+            if (e != hipSuccess) return e;
+        }
+        hipLaunchKernelGGL((dense_gemv_kernel<WF32, XF32, true>), grid, dim3(LT), lds, st, p);
+    } else {
+        hipLaunchKernelGGL((dense_gemv_kernel<WF32, XF32, false>), grid, dim3(LT), 0, st, p);
+    }
+    return hipGetLastError();
 }
 
 hipError_t launch_dense_gemv(DenseGemvParams p, bool staged, int cus, hipStream_t st) {
@@ -250,27 +279,13 @@ hipError_t launch_dense_gemv(DenseGemvParams p, bool staged, int cus, hipStream_
     const int64_t wg = steps < max_wg ? steps : max_wg;
     p.steps_per_wg = (int)((steps + wg - 1) / wg);
     const int64_t grid_x = (steps + p.steps_per_wg - 1) / p.steps_per_wg;
-    p.mt = staged ? dense_gemv_tokens_per_tile(p.in, p.m) : 1;
+    p.mt = staged ? dense_gemv_tokens_per_tile(p.in, p.m, p.x_f32) : 1;
     const int grid_y = (p.m + p.mt - 1) / p.mt;
-    const size_t lds = staged ? sizeof(float) * (size_t)p.mt * p.in : 0;
-    if (lds > 65536) {
-        const void* f = p.w_f32 ? (const void*)dense_gemv_kernel<true, true> : (const void*)dense_gemv_kernel<false, true>;
-        const hipError_t e = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-        if (e != hipSuccess) return e;
-    }
+    const size_t lds = staged ? (size_t)p.mt * p.in * (p.x_f32 ? 4 : 2) : 0;
     const dim3 grid((unsigned)grid_x, (unsigned)grid_y);
-    if (p.w_f32) {
-        if (staged)
-            hipLaunchKernelGGL((dense_gemv_kernel<true, true>), grid, dim3(LT), lds, st, p);
-        else
-            hipLaunchKernelGGL((dense_gemv_kernel<true, false>), grid, dim3(LT), 0, st, p);
-    } else {
-        if (staged)
-            hipLaunchKernelGGL((dense_gemv_kernel<false, true>), grid, dim3(LT), lds, st, p);
-        else
-            hipLaunchKernelGGL((dense_gemv_kernel<false, false>), grid, dim3(LT), 0, st, p);
-    }
-    return hipGetLastError();
+    if (p.w_f32)
+        return p.x_f32 ? launch_gemv<true, true>(p, staged, grid, lds, st) : launch_gemv<true, false>(p, staged, grid, lds, st);
+    return p.x_f32 ? launch_gemv<false, true>(p, staged, grid, lds, st) : launch_gemv<false, false>(p, staged, grid, lds, st);
 }
 
 hipError_t launch_dense_absorb(const DenseAbsorbParams& p, hipStream_t st) {

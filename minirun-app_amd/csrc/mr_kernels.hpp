@@ -196,8 +196,8 @@ hipError_t launch_indexer_scores(const IndexerParams& p, hipStream_t st);
 //   wrow(j) = (j / map_a) * map_b + map_c + j % map_a,  xvec(j) = j / map_a.
 // Staged launches (one activation vector per token: map_a == out_rows)
 // apply the optional RMSNorm or sigmoid gate to x once, in LDS.
-constexpr int MAX_GEMV_TOKENS = 8;         // tokens per launch tile
-constexpr int DENSE_STAGE_FLOATS = 16384;  // staged fp32 x values per workgroup (64 KB)
+constexpr int MAX_GEMV_TOKENS = 8;        // tokens per launch tile
+constexpr int DENSE_STAGE_BYTES = 65536;  // staged activations per workgroup (bf16 or fp32)
 struct DenseGemvParams {
     const void* x;
     int x_f32;
@@ -221,8 +221,8 @@ struct DenseGemvParams {
     int64_t gate_stride;
     int tpr, steps_per_wg, mt;  // set by the launcher
 };
-// staged: map_a == out_rows and tokens_per_tile(in) * in fits LDS
-int dense_gemv_tokens_per_tile(int in, int m);
+// staged: map_a == out_rows and one activation vector fits DENSE_STAGE_BYTES
+int dense_gemv_tokens_per_tile(int in, int m, bool x_f32);
 hipError_t launch_dense_gemv(DenseGemvParams p, bool staged, int cus, hipStream_t st);
 
 // q_lat[h][r] = sum_{d < nope} q[h][d] * W[h*(nope+v) + d][r], r < 512
