@@ -6,11 +6,22 @@
 //
 // dense_gemv_kernel (HBM-bound: every weight byte is read once per token
 // tile):
-//   - tpr lanes share an output row (a power of two, tpr * 4 >= the row's
-//     16-byte chunks when it can, so a lane holds up to four loads of one
-//     row); a wave covers 64 / tpr rows per step, a workgroup 4 waves.
-//   - "staged" mode: the activation vectors of the token tile go to LDS as
-//     fp32 once per workgroup, with the optional RMSNorm
+//   - tpr lanes share an output row (a power of two, tpr * 4 <= the row's
+//     16-byte chunks when it can); a wave covers 64 / tpr rows, a "unit".
+//   - Each wave walks a flat list of items (unit, batch of GEMV_BATCH chunks
+//     per lane) with two batches of loads in flight: batch k + 1 streams in
+//     while batch k is multiplied, and the next load is issued as soon as a
+//     batch's registers are free (past its last item a wave re-reads that
+//     item, so every load is unconditional).  A row's tail batch clamps its chunk index
+//     (re-reading the last chunk, a cache hit) and masks the product, so no
+//     lane runs a serial remainder loop.  The first two batches are issued
+//     before the activations are staged.
+//   - The grid holds up to GEMV_WG_PER_CU workgroups per CU and the waves
+//     stride over the units, which spreads the activation staging over many
+//     rows.
+//   - "staged" mode: the activation vectors of the token tile go to LDS
+//     once per workgroup (bf16 activations stay bf16 pairs for
+//     v_dot2_f32_bf16; 16-byte loads when aligned), with the optional RMSNorm
 //     (weight * (x * rsqrt(mean(x^2) + eps)), K3Norm.rms) or the optional
 //     sigmoid gate (x * sigmoid(g), MLA.swift:209-211) applied there; bf16
 //     inputs are rounded back to bf16 after that, as a separate norm or gate
@@ -78,105 +89,268 @@ __device__ __forceinline__ float chunk_dot(const u32x4& w, const void* x, float 
     return a;
 }
 
-constexpr int GEMV_UNROLL = 8;  // weight chunks in flight per lane
+// Eight consecutive activations at element offset o as floats; the address
+// is 16-byte aligned (bf16: one 16-byte load, f32: two).
+__device__ __forceinline__ void load8(const void* p, bool f32, int64_t o, float (&v)[8]) {
+    if (f32) {
+        const f32x4 a = *(const f32x4*)((const float*)p + o), b = *(const f32x4*)((const float*)p + o + 4);
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            v[k] = a[k];
+            v[k + 4] = b[k];
+        }
+    } else {
+        const u32x4 a = *(const u32x4*)((const uint16_t*)p + o);
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            v[2 * k] = __uint_as_float(a[k] << 16);
+            v[2 * k + 1] = __uint_as_float(a[k] & 0xffff0000u);
+        }
+    }
+}
 
-template <bool WF32, bool XF32, bool STAGED>
+__device__ __forceinline__ float sigmoid_gate(float e, float g) {
+    return e * (1.f / (1.f + __builtin_amdgcn_exp2f(-g * 1.4426950408889634f)));
+}
+
+// sum over the workgroup of one value per thread
+__device__ __forceinline__ float block_sum(float v, float* red) {
+    v = wave_sum(v);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+    __syncthreads();
+    float tot = 0.f;
+#pragma unroll
+    for (int w = 0; w < LT / 64; ++w) tot += red[w];
+    __syncthreads();
+    return tot;
+}
+
+// Stage token t's effective activations (optional RMSNorm or gate applied)
+// into xs[t][in], eight values per 16-byte load, SG groups of eight per
+// thread with all loads of a round issued before the first use.
+template <bool XF32>
+__device__ void stage_vec8(const DenseGemvParams& p, int t, char* xs, float* red) {
+    constexpr int SG = 2;
+    const int tid = threadIdx.x;
+    const int groups = p.in / 8;
+    const int tt = blockIdx.y * p.mt + t;
+    const int64_t xo = (int64_t)tt * p.x_stride, go = (int64_t)tt * p.gate_stride;
+    float r = 1.f;
+    if (p.norm_w) {
+        float ss = 0.f;
+        for (int base = 0; base < groups; base += LT * SG) {
+            float v[SG][8];
+#pragma unroll
+            for (int u = 0; u < SG; ++u) load8(p.x, XF32, xo + 8 * (int64_t)min(base + u * LT + tid, groups - 1), v[u]);
+#pragma unroll
+            for (int u = 0; u < SG; ++u) {
+                float s8 = 0.f;
+#pragma unroll
+                for (int k = 0; k < 8; ++k) s8 = fmaf(v[u][k], v[u][k], s8);
+                ss += base + u * LT + tid < groups ? s8 : 0.f;
+            }
+        }
+        r = rsqrtf(block_sum(ss, red) / (float)p.in + p.norm_eps);
+    }
+    for (int base = 0; base < groups; base += LT * SG) {
+        float v[SG][8], a[SG][8];
+#pragma unroll
+        for (int u = 0; u < SG; ++u) {
+            const int gi = min(base + u * LT + tid, groups - 1);
+            load8(p.x, XF32, xo + 8 * (int64_t)gi, v[u]);
+            if (p.norm_w)
+                load8(p.norm_w, p.norm_w_f32, 8 * (int64_t)gi, a[u]);
+            else if (p.gate)
+                load8(p.gate, p.gate_f32, go + 8 * (int64_t)gi, a[u]);
+        }
+#pragma unroll
+        for (int u = 0; u < SG; ++u) {
+            const int gi = base + u * LT + tid;
+            float e[8];
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+                e[k] = v[u][k];
+                if (p.norm_w) e[k] = a[u][k] * (e[k] * r);
+                else if (p.gate) e[k] = sigmoid_gate(e[k], a[u][k]);
+            }
+            if (gi < groups) {
+                if (XF32) {
+                    f32x4* d = (f32x4*)(xs + 4 * ((int64_t)t * p.in + 8 * gi));
+                    d[0] = f32x4{e[0], e[1], e[2], e[3]};
+                    d[1] = f32x4{e[4], e[5], e[6], e[7]};
+                } else {  // bf16 inputs stay bf16, as a separate norm or gate stage would store them
+                    u32x4 w;
+#pragma unroll
+                    for (int k = 0; k < 4; ++k) w[k] = f32_to_bf16_bits(e[2 * k]) | ((uint32_t)f32_to_bf16_bits(e[2 * k + 1]) << 16);
+                    *(u32x4*)(xs + 2 * ((int64_t)t * p.in + 8 * gi)) = w;
+                }
+            }
+        }
+    }
+}
+
+// The same for activations without 16-byte alignment: element loads, SR per
+// thread per round.
+template <bool XF32>
+__device__ void stage_scalar(const DenseGemvParams& p, int t, char* xs, float* red) {
+    constexpr int SR = 8;
+    const int tid = threadIdx.x;
+    const int tt = blockIdx.y * p.mt + t;
+    const int64_t xo = (int64_t)tt * p.x_stride, go = (int64_t)tt * p.gate_stride;
+    float r = 1.f;
+    if (p.norm_w) {
+        float ss = 0.f;
+        for (int base = 0; base < p.in; base += LT * SR) {
+            float v[SR];
+#pragma unroll
+            for (int u = 0; u < SR; ++u) v[u] = load_act(p.x, XF32, xo + min(base + u * LT + tid, p.in - 1));
+#pragma unroll
+            for (int u = 0; u < SR; ++u) ss = base + u * LT + tid < p.in ? fmaf(v[u], v[u], ss) : ss;
+        }
+        r = rsqrtf(block_sum(ss, red) / (float)p.in + p.norm_eps);
+    }
+    for (int base = 0; base < p.in; base += LT * SR) {
+        float v[SR], a[SR];
+#pragma unroll
+        for (int u = 0; u < SR; ++u) {
+            const int i = min(base + u * LT + tid, p.in - 1);
+            v[u] = load_act(p.x, XF32, xo + i);
+            if (p.norm_w)
+                a[u] = load_act(p.norm_w, p.norm_w_f32, i);
+            else if (p.gate)
+                a[u] = load_act(p.gate, p.gate_f32, go + i);
+        }
+#pragma unroll
+        for (int u = 0; u < SR; ++u) {
+            const int i = base + u * LT + tid;
+            float e = v[u];
+            if (p.norm_w) e = a[u] * (e * r);
+            else if (p.gate) e = sigmoid_gate(e, a[u]);
+            if (i < p.in) {
+                if (XF32)
+                    ((float*)xs)[t * p.in + i] = e;
+                else
+                    ((uint16_t*)xs)[t * p.in + i] = f32_to_bf16_bits(e);
+            }
+        }
+    }
+}
+
+constexpr int GEMV_BATCH = 8;      // 16-byte weight chunks per lane per batch
+constexpr int GEMV_WG_PER_CU = 4;  // resident workgroups per CU the grid aims for
+
+template <bool WF32, bool XF32, bool STAGED, int MT>
 __global__ void __launch_bounds__(LT) dense_gemv_kernel(DenseGemvParams p) {
     constexpr int VPC = WF32 ? 4 : 8;  // values per 16-byte weight chunk
     constexpr int XE = XF32 ? 4 : 2;   // bytes per activation value
+    constexpr int B = GEMV_BATCH;
     extern __shared__ __attribute__((aligned(16))) char xs[];  // staged: [mt][in] activations
     __shared__ float red[LT / 64];
     const int tid = threadIdx.x;
     const int t0 = blockIdx.y * p.mt;
     const int mt = min(p.mt, p.m - t0);
+    const int tpr = p.tpr;
+    const int lane = tid & 63;
+    const int sub = lane / tpr;       // row of this lane within its unit
+    const int li = lane - sub * tpr;  // lane within the row
+    const int rpw = 64 / tpr;
+    const int chunks = p.in / VPC;
+    const int nb = p.batches;  // batches per unit
+    const int64_t gw = (int64_t)blockIdx.x * (LT / 64) + (tid >> 6);
+    const int64_t tw = (int64_t)gridDim.x * (LT / 64);
+    const int64_t my_units = gw < p.units ? (p.units - 1 - gw) / tw + 1 : 0;
+    const int nitems = (int)my_units * nb;
+
+    // item k: unit gw + (k / nb) * tw, chunks li + (b * B + u) * tpr of its rows
+    auto row_of = [&](int ui) -> int64_t { return (gw + (int64_t)ui * tw) * rpw + sub; };
+    auto wrow_of = [&](int64_t j, int64_t& g) -> int64_t {
+        const int64_t jj = j < p.out_rows ? j : 0;
+        if (STAGED) {
+            g = 0;
+            return jj + p.map_c;
+        }
+        g = (int64_t)((uint32_t)jj / (uint32_t)p.map_a);
+        return g * p.map_b + p.map_c + (jj - g * p.map_a);
+    };
+    auto load = [&](int k, u32x4(&w)[B]) {
+        // past the end the wave re-reads its last item: unconditional loads
+        // keep the compiler's count of loads in flight exact across the loop
+        k = min(k, nitems - 1);
+        const int ui = k / nb, b = k - ui * nb;
+        int64_t g;
+        const char* wr = (const char*)p.w + wrow_of(row_of(ui), g) * p.w_rs * (WF32 ? 4 : 2);
+#pragma unroll
+        for (int u = 0; u < B; ++u) {
+            const int c = min(li + (b * B + u) * tpr, chunks - 1);
+            w[u] = __builtin_nontemporal_load((const u32x4*)(wr + 16 * (int64_t)c));
+        }
+    };
+    float acc[MT];
+#pragma unroll
+    for (int t = 0; t < MT; ++t) acc[t] = 0.f;
+    auto consume = [&](int k, const u32x4(&w)[B]) {
+        const int ui = k / nb, b = k - ui * nb;
+        const int64_t j = row_of(ui);
+        int64_t g;
+        (void)wrow_of(j, g);
+        const char* xd = (const char*)p.x + ((int64_t)t0 * p.x_stride + g * p.x_vec_stride) * XE;
+#pragma unroll
+        for (int u = 0; u < B; ++u) {
+            const int cr = li + (b * B + u) * tpr;
+            const bool ok = cr < chunks;
+            const int i0 = min(cr, chunks - 1) * VPC;
+            if (STAGED) {
+#pragma unroll
+                for (int t = 0; t < MT; ++t) {
+                    if (t < mt) {
+                        const float a = chunk_dot<WF32, XF32>(w[u], xs + ((int64_t)t * p.in + i0) * XE, acc[t]);
+                        acc[t] = ok ? a : acc[t];
+                    }
+                }
+            } else {
+                const float a = chunk_dot<WF32, XF32>(w[u], xd + (int64_t)i0 * XE, acc[0]);
+                acc[0] = ok ? a : acc[0];
+            }
+        }
+        if (b == nb - 1) {  // the unit's last batch: reduce its rows and store
+            const bool live = j < p.out_rows;
+            const int nt = STAGED ? mt : 1;
+#pragma unroll
+            for (int t = 0; t < MT; ++t) {
+                if (t >= nt) break;
+                const float v = group_sum(acc[t], tpr);
+                acc[t] = 0.f;
+                if (live && li == 0) {
+                    const int64_t yo = (int64_t)(t0 + t) * p.y_stride_token + j * p.y_stride_row;
+                    if (p.y_f32)
+                        ((float*)p.y)[yo] = v;
+                    else
+                        ((uint16_t*)p.y)[yo] = f32_to_bf16_bits(v);
+                }
+            }
+        }
+    };
+
+    u32x4 wa[B], wb[B];
+    if (nitems > 0) {
+        load(0, wa);
+        load(1, wb);
+    }
     if (STAGED) {
         for (int t = 0; t < mt; ++t) {
-            const int64_t xo = (int64_t)(t0 + t) * p.x_stride;
-            float r = 1.f;
-            if (p.norm_w) {  // sum of squares over the whole vector
-                float ss = 0.f;
-                for (int i = tid; i < p.in; i += LT) {
-                    const float v = load_act(p.x, p.x_f32, xo + i);
-                    ss = fmaf(v, v, ss);
-                }
-                ss = wave_sum(ss);
-                if ((tid & 63) == 0) red[tid >> 6] = ss;
-                __syncthreads();
-                float tot = 0.f;
-#pragma unroll
-                for (int w = 0; w < LT / 64; ++w) tot += red[w];
-                r = rsqrtf(tot / (float)p.in + p.norm_eps);
-                __syncthreads();
-            }
-            for (int i = tid; i < p.in; i += LT) {
-                float v = load_act(p.x, p.x_f32, xo + i);
-                if (p.norm_w) v = load_act(p.norm_w, p.norm_w_f32, i) * (v * r);
-                if (p.gate) {
-                    const float g = load_act(p.gate, p.gate_f32, (int64_t)(t0 + t) * p.gate_stride + i);
-                    v = v * (1.f / (1.f + __builtin_amdgcn_exp2f(-g * 1.4426950408889634f)));
-                }
-                if (XF32)
-                    ((float*)xs)[t * p.in + i] = v;
-                else  // bf16 inputs stay bf16, as a separate norm or gate stage would store them
-                    ((uint16_t*)xs)[t * p.in + i] = f32_to_bf16_bits(v);
-            }
+            if (p.stage_vec)
+                stage_vec8<XF32>(p, t, xs, red);
+            else
+                stage_scalar<XF32>(p, t, xs, red);
         }
         __syncthreads();
     }
-    const int tpr = p.tpr;
-    const int lane = tid & 63;
-    const int sub = lane / tpr;      // row of this lane within the wave's step
-    const int li = lane - sub * tpr;  // lane within the row
-    const int rows_per_wave = 64 / tpr;
-    const int chunks = p.in / VPC;
-    const int wave = tid >> 6;
-    const int64_t step0 = (int64_t)blockIdx.x * p.steps_per_wg;
-    for (int s = 0; s < p.steps_per_wg; ++s) {
-        const int64_t j = ((step0 + s) * (LT / 64) + wave) * rows_per_wave + sub;
-        const bool live = j < p.out_rows;
-        const int64_t jj = live ? j : 0;
-        const int64_t g = jj / p.map_a;
-        const int64_t wrow = g * p.map_b + p.map_c + (jj - g * p.map_a);
-        const char* wr = (const char*)p.w + wrow * p.w_rs * (WF32 ? 4 : 2);
-        // direct mode: this row's activation vector in global memory
-        const char* xd = (const char*)p.x + ((int64_t)t0 * p.x_stride + g * p.x_vec_stride) * XE;
-        float acc[MAX_GEMV_TOKENS];
-#pragma unroll
-        for (int t = 0; t < MAX_GEMV_TOKENS; ++t) acc[t] = 0.f;
-        auto use = [&](const u32x4& wv, int c) {
-            const int i0 = c * VPC;
-            if (STAGED) {
-#pragma unroll
-                for (int t = 0; t < MAX_GEMV_TOKENS; ++t)
-                    if (t < mt) acc[t] = chunk_dot<WF32, XF32>(wv, xs + ((int64_t)t * p.in + i0) * XE, acc[t]);
-            } else {
-                acc[0] = chunk_dot<WF32, XF32>(wv, xd + (int64_t)i0 * XE, acc[0]);
-            }
-        };
-        int c = li;
-        // GEMV_UNROLL chunks of the row in flight per lane, then the remainder
-        for (; c + (GEMV_UNROLL - 1) * tpr < chunks; c += GEMV_UNROLL * tpr) {
-            u32x4 wv[GEMV_UNROLL];
-#pragma unroll
-            for (int u = 0; u < GEMV_UNROLL; ++u)
-                wv[u] = __builtin_nontemporal_load((const u32x4*)(wr + 16 * (int64_t)(c + u * tpr)));
-#pragma unroll
-            for (int u = 0; u < GEMV_UNROLL; ++u) use(wv[u], c + u * tpr);
-        }
-        for (; c < chunks; c += tpr) use(__builtin_nontemporal_load((const u32x4*)(wr + 16 * (int64_t)c)), c);
-        const int nt = STAGED ? mt : 1;
-#pragma unroll
-        for (int t = 0; t < MAX_GEMV_TOKENS; ++t) {
-            if (t >= nt) break;
-            const float v = group_sum(acc[t], tpr);
-            if (live && li == 0) {
-                const int64_t yo = (int64_t)(t0 + t) * p.y_stride_token + j * p.y_stride_row;
-                if (p.y_f32)
-                    ((float*)p.y)[yo] = v;
-                else
-                    ((uint16_t*)p.y)[yo] = f32_to_bf16_bits(v);
-            }
-        }
+    for (int k = 0; k < nitems; k += 2) {
+        consume(k, wa);
+        load(k + 2, wa);
+        if (k + 1 >= nitems) break;
+        consume(k + 1, wb);
+        load(k + 3, wb);
     }
 }
 
@@ -252,19 +426,23 @@ int dense_gemv_tokens_per_tile(int in, int m, bool x_f32) {
     return max(1, min(min(m, cap > 0 ? cap : 1), MAX_GEMV_TOKENS));
 }
 
+template <bool WF32, bool XF32, bool STAGED, int MT>
+static hipError_t launch_gemv_mt(const DenseGemvParams& p, dim3 grid, size_t lds, hipStream_t st) {
+    if (lds > 65536) {
+        const hipError_t e = hipFuncSetAttribute((const void*)dense_gemv_kernel<WF32, XF32, STAGED, MT>,
+                                                 hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        if (e != hipSuccess) return e;
+    }
+    hipLaunchKernelGGL((dense_gemv_kernel<WF32, XF32, STAGED, MT>), grid, dim3(LT), lds, st, p);
+    return hipGetLastError();
+}
+
 template <bool WF32, bool XF32>
 static hipError_t launch_gemv(const DenseGemvParams& p, bool staged, dim3 grid, size_t lds, hipStream_t st) {
-    if (staged) {
-        if (lds > 65536) {
-            const hipError_t e = hipFuncSetAttribute((const void*)dense_gemv_kernel<WF32, XF32, true>,
-                                                     hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-            if (e != hipSuccess) return e;
-        }
-        hipLaunchKernelGGL((dense_gemv_kernel<WF32, XF32, true>), grid, dim3(LT), lds, st, p);
-    } else {
-        hipLaunchKernelGGL((dense_gemv_kernel<WF32, XF32, false>), grid, dim3(LT), 0, st, p);
-    }
-    return hipGetLastError();
+    if (!staged) return launch_gemv_mt<WF32, XF32, false, 1>(p, grid, 0, st);
+    if (p.mt == 1) return launch_gemv_mt<WF32, XF32, true, 1>(p, grid, lds, st);
+    if (p.mt <= 4) return launch_gemv_mt<WF32, XF32, true, 4>(p, grid, lds, st);
+    return launch_gemv_mt<WF32, XF32, true, MAX_GEMV_TOKENS>(p, grid, lds, st);
 }
 
 hipError_t launch_dense_gemv(DenseGemvParams p, bool staged, int cus, hipStream_t st) {
@@ -273,15 +451,19 @@ hipError_t launch_dense_gemv(DenseGemvParams p, bool staged, int cus, hipStream_
     int tpr = 64;
     while (tpr > 1 && tpr * 4 > chunks) tpr >>= 1;
     p.tpr = tpr;
-    const int rows_per_step = (LT / 64) * (64 / tpr);
-    const int64_t steps = (p.out_rows + rows_per_step - 1) / rows_per_step;
-    const int64_t max_wg = 2 * (int64_t)cus;
-    const int64_t wg = steps < max_wg ? steps : max_wg;
-    p.steps_per_wg = (int)((steps + wg - 1) / wg);
-    const int64_t grid_x = (steps + p.steps_per_wg - 1) / p.steps_per_wg;
+    const int rpw = 64 / tpr;
+    p.units = (p.out_rows + rpw - 1) / rpw;
+    const int per_lane = (chunks + tpr - 1) / tpr;
+    p.batches = (per_lane + GEMV_BATCH - 1) / GEMV_BATCH;
+    const int64_t waves = (int64_t)GEMV_WG_PER_CU * cus * (LT / 64);
+    const int64_t wave_need = p.units < waves ? p.units : waves;
+    const int64_t grid_x = (wave_need + LT / 64 - 1) / (LT / 64);
     p.mt = staged ? dense_gemv_tokens_per_tile(p.in, p.m, p.x_f32) : 1;
     const int grid_y = (p.m + p.mt - 1) / p.mt;
     const size_t lds = staged ? (size_t)p.mt * p.in * (p.x_f32 ? 4 : 2) : 0;
+    auto al16 = [](const void* q, int64_t stride_bytes) { return ((uintptr_t)q & 15) == 0 && stride_bytes % 16 == 0; };
+    p.stage_vec = staged && p.in % 8 == 0 && al16(p.x, p.x_stride * (p.x_f32 ? 4 : 2)) &&
+                  (!p.norm_w || al16(p.norm_w, 0)) && (!p.gate || al16(p.gate, p.gate_stride * (p.gate_f32 ? 4 : 2)));
     const dim3 grid((unsigned)grid_x, (unsigned)grid_y);
     if (p.w_f32)
         return p.x_f32 ? launch_gemv<true, true>(p, staged, grid, lds, st) : launch_gemv<true, false>(p, staged, grid, lds, st);

@@ -216,10 +216,11 @@ struct DenseGemvParams {
     const void* norm_w;  // optional: x_eff = norm_w * (x * rsqrt(mean(x^2) + eps))
     int norm_w_f32;
     float norm_eps;
-    const void* gate;    // optional: x_eff = x * sigmoid(gate[t * gate_stride + i])
+    const void* gate;    // optional (not with norm_w): x_eff = x * sigmoid(gate[t * gate_stride + i])
     int gate_f32;
     int64_t gate_stride;
-    int tpr, steps_per_wg, mt;  // set by the launcher
+    int tpr, batches, mt, stage_vec;  // set by the launcher
+    int64_t units;
 };
 // staged: map_a == out_rows and one activation vector fits DENSE_STAGE_BYTES
 int dense_gemv_tokens_per_tile(int in, int m, bool x_f32);
