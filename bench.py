@@ -134,7 +134,7 @@ def k3_block_bytes():
     return w + N * (R + DR) * 2 + act
 
 
-def time_k3_block(torch, M, steps, warmup, nset=2):
+def time_k3_block(torch, M, steps, warmup, nset=8):
     """The K3 flagship attention layer for one token at position 32767: dense
     bf16 projections (K3 keeps self_attn weights unquantized), NoPE, the
     sigmoid output gate, 96 heads; `nset` weight/cache sets of 502 MB rotate."""
@@ -196,7 +196,7 @@ def time_decode_96(torch, M, steps, warmup, nbuf=10):
     return {"wall_ms": (time.perf_counter() - t0) / steps * 1e3}
 
 
-def time_block(torch, M, steps, warmup, nset=4):
+def time_block(torch, M, steps, warmup, nset=8):
     """The decode block (affine 4-bit projections + absorbed attention over a
     32768-row cache) for one token at position 32767; `nset` weight/cache
     sets (143 MB each) rotate so the Infinity Cache cannot hold the operands."""
@@ -618,15 +618,15 @@ def main():
     su = time_sparse(torch, M, args.steps, args.warmup, checked=False)
     log(f"bench: sparse, no index checks {su}")
     log("bench: decode block, hidden 7168, affine 4-bit g64, ctx 32768")
-    blk = time_block(torch, M, max(args.steps // 4, 10), max(args.warmup // 4, 5))
+    blk = time_block(torch, M, args.steps, args.warmup)
     log(f"bench: block {blk}")
     log("bench: K3 attention block, dense bf16, 96 heads, NoPE, gated, ctx 32768")
-    k3 = time_k3_block(torch, M, max(args.steps // 4, 10), max(args.warmup // 4, 5))
+    k3 = time_k3_block(torch, M, args.steps, args.warmup)
     log(f"bench: k3 block {k3}")
     d96 = time_decode_96(torch, M, args.steps, args.warmup)
     log(f"bench: decode 96 heads {d96}")
     log("bench: causal prefill T=4096 H=128")
-    pf = time_prefill(torch, M, max(args.steps // 8, 50), 10)
+    pf = time_prefill(torch, M, max(args.steps // 2, 200), max(args.warmup // 2, 20))
     log(f"bench: prefill {pf}")
     tk_ms = time_topk(torch, M)
     log(f"bench: top-k 2048 of 32768 {tk_ms * 1e3:.2f} us")
@@ -670,6 +670,7 @@ def main():
         "block_hbm_fraction": round(block_bytes() / (blk["wall_ms"] * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
         "k3_block_us": round(k3["wall_ms"] * 1e3, 3),
         "k3_block_hbm_fraction": round(k3_block_bytes() / (k3["wall_ms"] * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+        "block_weight_cache_sets": 8,
         "decode_96_heads_us": round(d96["wall_ms"] * 1e3, 3),
         "prefill_us": round(pf["wall_ms"] * 1e3, 2),
         "prefill_mfma_fraction": round((UPPROJ_FLOP + ATTN_FLOP) / (pf["wall_ms"] * 1e-3) / 1e12 / MFMA_PEAK_TFLOPS, 4),

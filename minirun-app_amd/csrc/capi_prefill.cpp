@@ -74,7 +74,8 @@ mr_status mr_mla_prefill(const mr_mla_prefill_args* a, void* stream) {
     hipStream_t s = (hipStream_t)stream;
     hipEvent_t const* ev = (hipEvent_t const*)a->phase_events;
     uint16_t* kv = (uint16_t*)a->workspace;
-    const int64_t kv_rs = int64_t(a->heads) * 256;
+    // keys/values head-major: head h's [n_ctx][256] block is contiguous
+    const int64_t kv_hs = int64_t(a->n_ctx) * 256;
 
     mr::UpProjParams u{};
     u.a = (const uint16_t*)a->latent;
@@ -82,7 +83,8 @@ mr_status mr_mla_prefill(const mr_mla_prefill_args* a, void* stream) {
     u.b = (const uint16_t*)a->kv_b;
     u.ldb = a->kv_b_row_stride;
     u.c = kv;
-    u.ldc = kv_rs;
+    u.ldc = 256;
+    u.c_hs = kv_hs;
     u.M = a->n_ctx;
     u.N = a->heads * 256;
     u.K = 512;
@@ -92,7 +94,8 @@ mr_status mr_mla_prefill(const mr_mla_prefill_args* a, void* stream) {
     p.q_ts = a->q_token_stride;
     p.q_hs = a->q_head_stride;
     p.kv = kv;
-    p.kv_rs = kv_rs;
+    p.kv_rs = 256;
+    p.kv_hs = kv_hs;
     p.rope = (const uint16_t*)a->rope_keys;
     p.rope_rs = a->rope_row_stride;
     p.out = a->out;

@@ -62,6 +62,15 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
     return (uint32_t)f32_to_bf16_bits(lo) | ((uint32_t)f32_to_bf16_bits(hi) << 16);
 }
 
+// The same pair through gfx950's v_cvt_pk_bf16_f32 (round to nearest even,
+// one instruction for both values); NaNs stay NaNs, their payload bits may
+// differ from f32_to_bf16_bits'.
+__device__ __forceinline__ uint32_t pack_bf16x2_hw(float lo, float hi) {
+    typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+    const bf16x2_t v = {(__bf16)lo, (__bf16)hi};
+    return __builtin_bit_cast(uint32_t, v);
+}
+
 // One correctly rounded fp32 operation each, never fused into an FMA with a
 // neighbour (hipcc contracts a*b+c by default; these carry no contract flag).
 __device__ __forceinline__ float mul_rn(float a, float b) {

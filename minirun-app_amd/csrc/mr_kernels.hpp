@@ -70,19 +70,20 @@ struct UpProjParams {
     int64_t lda;
     const uint16_t* b;  // kv_b [N][K], row stride ldb
     int64_t ldb;
-    uint16_t* c;        // [M][N], row stride ldc
-    int64_t ldc;
+    uint16_t* c;        // column block n / 256 at c + (n / 256) * c_hs, rows of stride ldc
+    int64_t ldc, c_hs;
     int32_t M, N, K;
 };
 
-// Causal attention over the up-projected keys/values.  Head h of key p:
-// K = [kv[p][h*256 + 0..127] ++ rope[p][0..63]], V = kv[p][h*256 + 128..255].
+// Causal attention over the up-projected keys/values.  Head h of key p, with
+// r = kv + h * kv_hs + p * kv_rs: K = [r[0..127] ++ rope[p][0..63]],
+// V = r[128..255].
 // Query i (of T, at cache position P - T + i) attends keys 0 .. P - T + i.
 struct PrefillAttnParams {
     const uint16_t* q;  // [T][H][192] bf16 (nope 128 ++ rope 64)
     int64_t q_ts, q_hs;
-    const uint16_t* kv;  // [P][H*256]
-    int64_t kv_rs;
+    const uint16_t* kv;  // head h, key p: kv + h * kv_hs + p * kv_rs, 256 values
+    int64_t kv_rs, kv_hs;
     const uint16_t* rope;  // [P][64] rows, stride rope_rs
     int64_t rope_rs;
     void* out;  // [T][H][128]

@@ -2,10 +2,11 @@
 // 198-206; expand :231-245; causal mask :257-275).
 //
 // Two kernels:
-//   upproj_kernel       kv[p][h*256 + e] = latent[p] . kv_b[h*256 + e]: the
+//   upproj_kernel       kv[h][p][e] = latent[p] . kv_b[h*256 + e]: the
 //                       per-head keys (e < 128, W_UK rows) and values (e >= 128,
 //                       W_UV rows) of every cached position, one NT GEMM on
-//                       32x32x16 bf16 MFMA, fp32 accumulation, bf16 out.
+//                       32x32x16 bf16 MFMA (256 x 256 tiles, DMA-fed LDS
+//                       ring), fp32 accumulation, bf16 out.
 //   prefill_attn_kernel flash attention over those keys/values plus the
 //                       shared rotary key, fp32 online softmax, bf16 P.
 //
@@ -27,99 +28,205 @@ namespace mr {
 namespace {
 
 // ---------------------------------------------------------------- up-projection
-constexpr int UG_TILE = 128;  // M and N tile
-constexpr int UG_BK = 32;     // K per stage
+// C [M][N] = A [M][K] . B [N][K]^T, K = 512, with C stored in blocks of 256
+// columns (one head's keys and values): column n of row m at
+// c + (n / 256) * c_hs + m * ldc + n % 256, so a workgroup's 256 x 256 tile
+// is one contiguous 128 KB block when ldc = 256.
+//
+// A 256 x 256 tile per workgroup of 4 waves, each wave a 128 x 128 block of
+// 4 x 4 32x32x16 MFMA tiles (256 accumulators per lane, in AGPRs), so a
+// 16-deep k-step reads 8 KB of operands per wave for 16 MFMAs.  The wave
+// computes C^T blocks (B rows as the MFMA's first operand), so each lane
+// ends with four runs of four consecutive N columns of one C row.
+//
+// K streams through a ring of UG_STAGES LDS stages of UG_BK = 32 columns
+// (A 16 KB + B 16 KB each, 160 KB in all) filled by global -> LDS DMA four
+// stages ahead; a
+// stage is 64-byte rows of four 16-byte chunks, chunk c of row r in slot
+// c ^ ((r >> 2) & 3), so the 16 lanes of one ds_read_b128 phase (16
+// consecutive rows, one chunk) hit 16 distinct bank groups.  The DMA writes
+// slots in lane order, so lane l of a 1 KB instruction fetches the global
+// chunk that belongs in slot l.  The operand fragments are read one 16-deep
+// step ahead of the MFMAs that use them, and the one barrier per stage sits
+// after 16 MFMAs, by when the reads it waits for have landed.
+//
+// Epilogue: bf16 C tile through LDS (128 KB of the ring), 16-byte
+// chunk q of row r at q ^ (r & 31), then 16-byte row-contiguous stores.
+constexpr int UG_TM = 256, UG_TN = 256, UG_BK = 64, UG_STAGES = 2;
+constexpr int UG_THREADS = 256;
+constexpr int UG_GROUP_M = 4;  // M tiles that share an L2 walk
+constexpr int UG_STAGE_HALF = UG_TM * UG_BK;  // bf16 elements of A (or B) in one stage
+constexpr int UG_CPR = UG_BK / 8;             // 16-byte chunks per stage row
+constexpr int UG_KS = UG_BK / 16;             // 16-deep MFMA steps per stage
+constexpr int UG_DPW = 2 * UG_CPR;            // DMA instructions per wave per stage
+static_assert((UG_CPR == 4 || UG_CPR == 8) && UG_KS % 2 == 0, "stage shape");
 
-// 64-byte LDS rows of 4 x 16-byte chunks; chunk c of row r sits at
-// c ^ ((r >> 2) & 3): 16 consecutive rows read at one chunk hit 16
-// distinct bank groups.
-__device__ __forceinline__ int ug_off(int r, int c) { return r * UG_BK + ((c ^ ((r >> 2) & 3)) << 3); }
+// chunk c of stage row r: 16 consecutive rows read at one chunk land in 16
+// distinct 16-byte bank groups
+__device__ __forceinline__ int ug_slot(int r, int c) {
+    return UG_CPR == 4 ? r * 4 + (c ^ ((r >> 2) & 3)) : r * 8 + (c ^ ((r >> 1) & 7));
+}
 
-__global__ void __launch_bounds__(256, 2) upproj_kernel(UpProjParams p) {
-    __shared__ __attribute__((aligned(16))) uint16_t lds[4 * UG_TILE * UG_BK];  // 2 stages x (A, B): 32 KB
+// lds_barrier with its lgkmcnt(0) also issued as the builtin (gfx9 encoding:
+// vmcnt 63, expcnt 7, lgkmcnt 0), so the compiler knows every earlier LDS
+// read has landed and adds no waits for them after the barrier
+__device__ __forceinline__ void lds_barrier_seen() {
+    __builtin_amdgcn_s_waitcnt(0xC07F);
+    lds_barrier();
+}
+
+__global__ void __launch_bounds__(UG_THREADS, 1) upproj_kernel(UpProjParams p) {
+    extern __shared__ __attribute__((aligned(16))) uint16_t lds[];  // UG_STAGES x (A, B), 160 KB
     const int tid = threadIdx.x, w = tid >> 6, l = tid & 63;
-    const int m_tiles = (p.M + UG_TILE - 1) / UG_TILE;
-    const int total = m_tiles * (p.N / UG_TILE);
-    // XCD-aware order: the workgroups one XCD runs are consecutive tiles,
-    // which share an N tile (kv_b rows) across all M tiles
+    const int m_tiles = (p.M + UG_TM - 1) / UG_TM, n_tiles = p.N / UG_TN;
+    const int total = m_tiles * n_tiles;
+    // XCD-aware order: consecutive workgroups land on the 8 XCDs in turn, so
+    // each XCD gets a contiguous range of tile ids; ids run over groups of
+    // UG_GROUP_M M tiles, and within a group over the N tiles with the M
+    // tiles fastest.  One XCD's 32 resident workgroups then cover 4 M x 8 N
+    // tiles (1 MB of latent rows, 2 MB of kv_b rows), and its next rounds
+    // keep the same latent rows in its L2.
     int bid = blockIdx.x;
     if ((total & 7) == 0) bid = (bid & 7) * (total >> 3) + (bid >> 3);
-    const int mt = bid % m_tiles, nt = bid / m_tiles;
-    const int m0 = mt * UG_TILE, n0 = nt * UG_TILE;
+    const int group = bid / (UG_GROUP_M * n_tiles), first_m = group * UG_GROUP_M;
+    const int gsize = min(m_tiles - first_m, UG_GROUP_M);
+    const int mt = first_m + (bid % (UG_GROUP_M * n_tiles)) % gsize;
+    const int nt = (bid % (UG_GROUP_M * n_tiles)) / gsize;
+    const int m0 = mt * UG_TM, n0 = nt * UG_TN;
+    const int KT = p.K / UG_BK;
 
-    // stage s: A tile at lds + 2s * 4096, B tile right after it
-    auto sa = [&](int s) { return lds + (2 * s) * UG_TILE * UG_BK; };
-    auto sb = [&](int s) { return lds + (2 * s + 1) * UG_TILE * UG_BK; };
-    u32x4 ra[2], rb[2];
-    auto gload = [&](int k0) {
+    // DMA: a stage is 32 instructions of 64 lanes x 16 bytes (16 for A, 16
+    // for B); wave w issues A and B instructions 4w .. 4w + 3.  Lane l of
+    // instruction i fills slot 64 i + l: row 16 i + l / 4, slot chunk l % 4,
+    // which holds global chunk (l % 4) ^ ((row >> 2) & 3).  Offsets are
+    // bytes from the tile's first A (B) row; A rows past M repeat row M - 1.
+    const uint16_t* abase = p.a + (int64_t)m0 * p.lda;
+    const uint16_t* bbase = p.b + (int64_t)n0 * p.ldb;
+    // instruction i of an operand (UG_CPR per wave): rows (64 / UG_CPR) i ..,
+    // lane l fills slot 64 i + l = (row, slot chunk l % UG_CPR)
+    uint32_t voff[UG_DPW];
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
-            const int q = tid + 256 * i, row = q >> 2, ch = q & 3;
-            const int am = min(m0 + row, p.M - 1);
-            ra[i] = *(const u32x4*)(p.a + (int64_t)am * p.lda + k0 + ch * 8);
-            rb[i] = *(const u32x4*)(p.b + (int64_t)(n0 + row) * p.ldb + k0 + ch * 8);
-        }
-    };
-    auto sstore = [&](int buf) {
-#pragma unroll
-        for (int i = 0; i < 2; ++i) {
-            const int q = tid + 256 * i, row = q >> 2, ch = q & 3;
-            *(u32x4*)(sa(buf) + ug_off(row, ch)) = ra[i];
-            *(u32x4*)(sb(buf) + ug_off(row, ch)) = rb[i];
-        }
-    };
-
-    const int wm = w >> 1, wn = w & 1;  // this wave's 64 x 64 sub-tile
-    f32x16 acc[2][2];
-#pragma unroll
-    for (int i = 0; i < 2; ++i)
-#pragma unroll
-        for (int j = 0; j < 2; ++j) acc[i][j] = f32x16{};
-
-    const int ksteps = p.K / UG_BK;
-    gload(0);
-    sstore(0);
-    __syncthreads();
-    for (int kt = 0; kt < ksteps; ++kt) {
-        const int buf = kt & 1;
-        if (kt + 1 < ksteps) gload((kt + 1) * UG_BK);
-#pragma unroll
-        for (int ks = 0; ks < 2; ++ks) {
-            bf16x8 av[2], bv[2];
-            const int ch = 2 * ks + (l >> 5);
-#pragma unroll
-            for (int i = 0; i < 2; ++i) {
-                av[i] = *(const bf16x8*)(sa(buf) + ug_off(wm * 64 + i * 32 + (l & 31), ch));
-                bv[i] = *(const bf16x8*)(sb(buf) + ug_off(wn * 64 + i * 32 + (l & 31), ch));
-            }
-#pragma unroll
-            for (int i = 0; i < 2; ++i)
-#pragma unroll
-                for (int j = 0; j < 2; ++j) acc[i][j] = mfma32(av[i], bv[j], acc[i][j]);
-        }
-        if (kt + 1 < ksteps) sstore(buf ^ 1);
-        __syncthreads();
+    for (int q = 0; q < UG_DPW; ++q) {
+        const int i = UG_CPR * w + q % UG_CPR;
+        const int row = (64 / UG_CPR) * i + l / UG_CPR;
+        const int sc = l % UG_CPR;
+        const int c = UG_CPR == 4 ? sc ^ ((row >> 2) & 3) : sc ^ ((row >> 1) & 7);
+        voff[q] = q < UG_CPR ? (uint32_t)(((int64_t)min(row, p.M - 1 - m0) * p.lda + 8 * c) * 2)
+                             : (uint32_t)(((int64_t)row * p.ldb + 8 * c) * 2);
     }
+    const int wu = __builtin_amdgcn_readfirstlane(w);
+    auto issue = [&](int kt) {
+        uint16_t* st = lds + (kt % UG_STAGES) * 2 * UG_STAGE_HALF;
+        const uint32_t ko = (uint32_t)kt * UG_BK * 2;
+#pragma unroll
+        for (int q = 0; q < UG_CPR; ++q) dma16_off(abase, voff[q] + ko, st + 512 * (UG_CPR * wu + q));
+#pragma unroll
+        for (int q = 0; q < UG_CPR; ++q)
+            dma16_off(bbase, voff[UG_CPR + q] + ko, st + UG_STAGE_HALF + 512 * (UG_CPR * wu + q));
+    };
+    // this wave's part of stage kt + 1 has landed once only the stages after
+    // it that were issued (up to kt + UG_STAGES - 1) are pending
+    auto wait_next = [&](int kt) {
+        const int later = min(KT - 1, kt + UG_STAGES - 1) - (kt + 1);
+        static_assert(UG_STAGES <= 5, "wait ladder");
+        if (later >= 3)
+            wait_vmcnt<3 * UG_DPW>();
+        else if (later == 2)
+            wait_vmcnt<2 * UG_DPW>();
+        else if (later == 1)
+            wait_vmcnt<UG_DPW>();
+        else
+            wait_vmcnt<0>();
+    };
 
-    // epilogue: the 128 x 128 bf16 tile through LDS (32 KB), then 16-byte
-    // row-contiguous stores
-    uint16_t* tile = lds;  // [128][128]
+    const int wm = w >> 1, wn = w & 1;  // rows wm*128.., columns wn*128..
+    f32x16 acc[4][4];
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+    for (int i = 0; i < 4; ++i)
 #pragma unroll
-        for (int j = 0; j < 2; ++j)
+        for (int j = 0; j < 4; ++j) acc[i][j] = f32x16{};
+
+    auto read = [&](int kt, int ks, bf16x8(&a)[4], bf16x8(&b)[4]) {
+        const uint16_t* sa = lds + (kt % UG_STAGES) * 2 * UG_STAGE_HALF;
+        const uint16_t* sb = sa + UG_STAGE_HALF;
+        const int ch = 2 * ks + (l >> 5);
 #pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int row = wm * 64 + i * 32 + 8 * (r >> 2) + 4 * (l >> 5) + (r & 3);
-                const int col = wn * 64 + j * 32 + (l & 31);
-                tile[row * UG_TILE + col] = f32_to_bf16_bits(acc[i][j][r]);
+        for (int i = 0; i < 4; ++i) a[i] = *(const bf16x8*)(sa + 8 * ug_slot(wm * 128 + i * 32 + (l & 31), ch));
+#pragma unroll
+        for (int j = 0; j < 4; ++j) b[j] = *(const bf16x8*)(sb + 8 * ug_slot(wn * 128 + j * 32 + (l & 31), ch));
+    };
+    auto mma = [&](const bf16x8(&a)[4], const bf16x8(&b)[4]) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) acc[i][j] = mfma32(b[j], a[i], acc[i][j]);
+    };
+
+    // KT >= UG_STAGES (the launcher checks): stages 0 .. UG_STAGES - 1 in
+    // flight, UG_DPW DMA instructions per wave each
+#pragma unroll
+    for (int s = 0; s < UG_STAGES; ++s) issue(s);
+    wait_vmcnt<UG_DPW * (UG_STAGES - 1)>();
+    lds_barrier_seen();
+    bf16x8 fa[2][4], fb[2][4];  // fragments of two consecutive 16-deep steps
+    read(0, 0, fa[0], fb[0]);
+    // the last stage is peeled off so every path through the loop body is
+    // the same for the compiler's LDS wait counts
+    for (int kt = 0; kt + 1 < KT; ++kt) {
+#pragma unroll
+        for (int ks = 0; ks < UG_KS; ++ks) {
+            const int nx = (ks + 1) & 1;
+            if (ks + 1 < UG_KS) {
+                read(kt, ks + 1, fa[nx], fb[nx]);
+            } else {
+                wait_next(kt);
+                lds_barrier_seen();  // every wave's part landed; every wave is done with stage kt
+                if (kt + UG_STAGES < KT) issue(kt + UG_STAGES);
+                read(kt + 1, 0, fa[nx], fb[nx]);
             }
-    __syncthreads();
+            mma(fa[ks & 1], fb[ks & 1]);
+        }
+    }
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        const int q = tid + 256 * i, row = q >> 4, ch = q & 15;
-        if (m0 + row < p.M)
-            *(u32x4*)(p.c + (int64_t)(m0 + row) * p.ldc + n0 + ch * 8) = *(const u32x4*)(tile + row * UG_TILE + ch * 8);
+    for (int ks = 0; ks < UG_KS; ++ks) {
+        if (ks + 1 < UG_KS) read(KT - 1, ks + 1, fa[(ks + 1) & 1], fb[(ks + 1) & 1]);
+        mma(fa[ks & 1], fb[ks & 1]);
+    }
+    lds_barrier_seen();  // the ring is free
+
+    // acc[i][j][4g + e]: C row wm*128 + i*32 + l%32, column
+    // wn*128 + j*32 + 8g + 4(l/32) + e
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int row = wm * 128 + i * 32 + (l & 31);
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                const int col = wn * 128 + j * 32 + 8 * g + 4 * (l >> 5);
+                const int q = (col >> 3) ^ (row & 31);
+                u32x2 v;
+                v[0] = pack_bf16x2_hw(acc[i][j][4 * g], acc[i][j][4 * g + 1]);
+                v[1] = pack_bf16x2_hw(acc[i][j][4 * g + 2], acc[i][j][4 * g + 3]);
+                *(u32x2*)(lds + row * UG_TN + 8 * q + (col & 7)) = v;
+            }
+    }
+    __syncthreads();
+    uint16_t* cb = p.c + (int64_t)nt * p.c_hs + (int64_t)m0 * p.ldc;
+#pragma unroll
+    for (int half = 0; half < 2; ++half) {
+        constexpr int PER = (UG_TM * UG_TN / 8) / UG_THREADS / 2;
+        u32x4 v[PER];
+#pragma unroll
+        for (int it = 0; it < PER; ++it) {
+            const int idx = tid + UG_THREADS * (it + PER * half), row = idx >> 5, q = idx & 31;
+            v[it] = *(const u32x4*)(lds + row * UG_TN + 8 * (q ^ (row & 31)));
+        }
+#pragma unroll
+        for (int it = 0; it < PER; ++it) {
+            const int idx = tid + UG_THREADS * (it + PER * half), row = idx >> 5, q = idx & 31;
+            if (m0 + row < p.M) *(u32x4*)(cb + (int64_t)row * p.ldc + 8 * q) = v[it];
+        }
     }
 }
 
@@ -207,7 +314,7 @@ __global__ void __launch_bounds__(256, 2) prefill_attn_kernel(PrefillAttnParams 
         const int sl = 64 * (w + 4 * i) + l, r = sl >> 3, pc = sl & 7;
         vo_r[i] = r * rope_rb + ((pc ^ kr_swz(r)) << 4);
     }
-    const uint16_t* kv_h = p.kv + (int64_t)head * 256;
+    const uint16_t* kv_h = p.kv + (int64_t)head * p.kv_hs;
     const int wu = __builtin_amdgcn_readfirstlane(w);  // LDS destinations in SGPRs
     auto issue = [&](int kt, int buf) {
         const uint32_t rows = (uint32_t)min(p.P - kt * AT_K, AT_K);
@@ -389,9 +496,18 @@ __global__ void __launch_bounds__(256, 2) prefill_attn_kernel(PrefillAttnParams 
 }  // namespace
 
 hipError_t launch_upproj(const UpProjParams& p, hipStream_t st) {
-    const int m_tiles = (p.M + UG_TILE - 1) / UG_TILE;
-    const unsigned grid = (unsigned)(m_tiles * (p.N / UG_TILE));
-    hipLaunchKernelGGL(upproj_kernel, dim3(grid), dim3(256), 0, st, p);
+    // N a multiple of 256, K a multiple of 32 with at least UG_STAGES steps,
+    // rows 16-byte aligned, one tile's A / B rows within 32-bit byte offsets
+    if (p.N % UG_TN || p.K % UG_BK || p.K < UG_BK * UG_STAGES || (int64_t)UG_TM * p.lda * 2 >= (1ll << 32) ||
+        (int64_t)UG_TN * p.ldb * 2 >= (1ll << 32))
+        return hipErrorInvalidValue;
+    const int m_tiles = (p.M + UG_TM - 1) / UG_TM;
+    const unsigned grid = (unsigned)(m_tiles * (p.N / UG_TN));
+    const size_t lds = sizeof(uint16_t) * UG_STAGES * 2 * UG_STAGE_HALF;
+    const hipError_t attr =
+        hipFuncSetAttribute((const void*)upproj_kernel, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (attr != hipSuccess) return attr;
+    hipLaunchKernelGGL(upproj_kernel, dim3(grid), dim3(UG_THREADS), lds, st, p);
     return hipGetLastError();
 }
 
