@@ -214,6 +214,50 @@ mr_status block_proj(const void* x, int64_t in, const mr_projection* w, void* y,
     return e == hipSuccess ? MR_OK : hip_fail(e, "dense projection launch");
 }
 
+// Dense projections of one bf16 activation vector stacked into one staged
+// launch (x_eff = x or RMSNorm(x) staged once): true when every weight is
+// dense with the same dtype and width and the vector fits the staging.
+bool dense_stack_ok(const mr_projection* const* w, int n, int64_t in) {
+    if (n < 1 || n > 3 || in * 2 > mr::DENSE_STAGE_BYTES) return false;
+    int64_t rows = 0;
+    for (int i = 0; i < n; ++i) {
+        if (w[i]->kind != MR_PROJ_DENSE || w[i]->dense.dtype != w[0]->dense.dtype || w[i]->dense.in_features != in)
+            return false;
+        rows += w[i]->dense.out_features;
+    }
+    return rows <= INT32_MAX;
+}
+
+mr_status dense_stack(const void* x, int64_t in, const mr_projection* const* w, void* const* y, int n,
+                      const void* norm_w, mr_dtype norm_dtype, float eps, void* stream) {
+    mr::DenseGemvParams g = dense_params(&w[0]->dense);
+    g.x = x;
+    g.x_f32 = 0;
+    g.x_stride = in;
+    g.y = y[0];
+    g.y_f32 = 0;
+    g.y_stride_row = 1;
+    g.y_stride_token = w[0]->dense.out_features;
+    g.norm_w = norm_w;
+    g.norm_w_f32 = norm_dtype == MR_F32;
+    g.norm_eps = eps;
+    g.nseg = n;
+    int64_t end = 0;
+    for (int i = 0; i < n; ++i) {
+        end += w[i]->dense.out_features;
+        g.seg_end[i] = (int)end;
+        g.seg_w[i] = w[i]->dense.weight;
+        g.seg_w_rs[i] = w[i]->dense.row_stride;
+        g.seg_y[i] = y[i];
+        g.seg_y_ts[i] = w[i]->dense.out_features;
+    }
+    for (int i = n; i < 3; ++i) g.seg_end[i] = (int)end;
+    g.out_rows = (int)end;
+    g.map_a = (int)end;
+    const hipError_t e = mr::launch_dense_gemv(g, true, mrc::cu_count(), (hipStream_t)stream);
+    return e == hipSuccess ? MR_OK : hip_fail(e, "dense projection launch");
+}
+
 mr::AffineGemvParams gemv_params(const mr_affine_weight* w) {
     mr::AffineGemvParams g{};
     g.packed = w->packed;
@@ -546,9 +590,10 @@ mr_status mr_mla_cache_append(const void* kv, mr_dtype kv_dtype, int64_t kv_stri
     if (tokens <= 0 || kv_rank <= 0 || rope_dim < 0 || rope_dim % 2 || kv_stride < kv_rank + rope_dim ||
         latent_row_stride < kv_rank || (rope_dim && rope_row_stride < rope_dim) || start_row < 0 || tokens > INT32_MAX)
         return fail(MR_INVALID_SHAPE, "cache append: bad geometry");
-    mr::CacheAppendParams p{kv, kv_dtype == MR_F32, kv_stride, norm_w, w_dtype == MR_F32, eps, kv_rank, rope_dim,
-                            cos_t, sin_t, (uint16_t*)latent, latent_row_stride, (uint16_t*)rope, rope_row_stride,
-                            start_row, tokens};
+    const mr::CacheAppendParams p{kv,      kv_dtype == MR_F32, kv_stride,         norm_w,       w_dtype == MR_F32,
+                                  eps,     kv_rank,            rope_dim,          cos_t,        sin_t,
+                                  (uint16_t*)latent, latent_row_stride, (uint16_t*)rope, rope_row_stride, start_row,
+                                  tokens};
     const hipError_t e = mr::launch_cache_append(p, (hipStream_t)stream);
     return e == hipSuccess ? MR_OK : hip_fail(e, "cache append launch");
 }
@@ -571,10 +616,12 @@ static mr_status check_kv_b(const mr_projection* kv_b, int32_t heads, int32_t no
 }
 
 // q_lat[h] = q_nope[h] . W_UK[h], optionally rotating q's rope slice
-// (rope_cos non-null) in the same launch
+// (rope_cos non-null) and appending one cache row (app non-null) in the
+// same launch
 static mr_status absorb(const void* q, int64_t q_head_stride, int32_t heads, int32_t nope_dim, int32_t v_dim,
                         const mr_projection* kv_b, void* q_lat, int64_t q_lat_head_stride, const float* rope_cos,
-                        const float* rope_sin, int32_t rope_dim, void* stream) {
+                        const float* rope_sin, int32_t rope_dim, void* stream,
+                        const mr::CacheAppendParams* app = nullptr) {
     hipError_t e;
     if (kv_b->kind == MR_PROJ_AFFINE) {
         const mr_affine_weight* w = &kv_b->affine;
@@ -584,6 +631,10 @@ static mr_status absorb(const void* q, int64_t q_head_stride, int32_t heads, int
         p.rope_sin = rope_sin;
         p.rope_dim = rope_dim;
         p.rope_col0 = nope_dim;
+        if (app) {
+            p.app = *app;
+            p.app_on = 1;
+        }
         e = mr::launch_absorb_q(p, (hipStream_t)stream);
     } else {
         const mr_dense_weight* w = &kv_b->dense;
@@ -602,6 +653,10 @@ static mr_status absorb(const void* q, int64_t q_head_stride, int32_t heads, int
         p.rope_sin = rope_sin;
         p.rope_dim = rope_dim;
         p.rope_col0 = nope_dim;
+        if (app) {
+            p.app = *app;
+            p.app_on = 1;
+        }
         e = mr::launch_dense_absorb(p, (hipStream_t)stream);
     }
     return e == hipSuccess ? MR_OK : hip_fail(e, "absorb launch");
@@ -729,6 +784,9 @@ mr_status mr_mla_decode_block(const mr_mla_block_args* a, void* stream) {
         return fail(MR_INVALID_ARGUMENT, "mla block: NULL pointer");
     if (!a->rope_cos != !a->rope_sin)
         return fail(MR_INVALID_ARGUMENT, "mla block: give both rotary tables (rotated MLA) or neither (NoPE)");
+    if (a->latent_row_stride < a->kv_rank || a->rope_row_stride < a->qk_rope_dim)  // before any cache write
+        return fail(MR_INVALID_SHAPE, "mla block: cache row strides %lld / %lld are below %d / %d",
+                    (long long)a->latent_row_stride, (long long)a->rope_row_stride, a->kv_rank, a->qk_rope_dim);
     if (!act_dtype_ok(a->norm_w_dtype)) return fail(MR_INVALID_DTYPE, "mla block: norm weights must be bf16 or f32");
     const int dq = a->qk_nope_dim + a->qk_rope_dim;
     const bool gated = a->g_proj.kind != MR_PROJ_NONE;
@@ -772,6 +830,42 @@ mr_status mr_mla_decode_block(const mr_mla_block_args* a, void* stream) {
     void* gate = W + L.gate;
     void* stage = W + L.stage;
     const mr_dtype nd = a->norm_w_dtype;
+
+    // dense projections (K3): q_a, kv_a and g_proj all read the (normed)
+    // input, so they run as one launch, and the chain stays on one stream
+    const mr_projection* xw[3] = {&a->q_a, &a->kv_a, &a->g_proj};
+    void* xy[3] = {q_lora, kv, gate};
+    const int nx = gated ? 3 : 2;
+    if (dense_stack_ok(xw, nx, a->hidden)) {
+        if ((st = dense_stack(a->x, a->hidden, xw, xy, nx, a->input_norm_w, nd, a->eps, stream)) != MR_OK) return st;
+        if ((st = block_proj(q_lora, a->q_lora_rank, &a->q_b, q, a->q_a_norm_w, nd, a->eps, nullptr, q_lora_n,
+                             stream)) != MR_OK)
+            return st;
+        // the absorption carries the cache append (row `position`) as one
+        // more workgroup
+        const mr::CacheAppendParams app{kv,           0,           a->kv_rank + a->qk_rope_dim,
+                                        a->kv_a_norm_w, nd == MR_F32, a->eps,
+                                        a->kv_rank,   a->qk_rope_dim, a->rope_cos,
+                                        a->rope_sin,  (uint16_t*)a->cache_latent, a->latent_row_stride,
+                                        (uint16_t*)a->cache_rope, a->rope_row_stride, a->position,
+                                        1};
+        if ((st = absorb(q, dq, a->heads, a->qk_nope_dim, a->v_head_dim, &a->kv_b, q_lat, a->kv_rank, a->rope_cos,
+                         a->rope_sin, a->qk_rope_dim, stream, &app)) != MR_OK)
+            return st;
+        mr_mla_decode_args d = L.dec_args;
+        d.q_lat = q_lat;
+        d.q_rope = q + a->qk_nope_dim;
+        d.latent = a->cache_latent;
+        d.rope_keys = a->cache_rope;
+        d.out = ctx;
+        d.workspace = W + L.dec;
+        d.workspace_bytes = L.total - L.dec;
+        if ((st = mr_mla_decode(&d, stream)) != MR_OK) return st;
+        if ((st = mr_mla_unabsorb_values(ctx, a->kv_rank, a->heads, a->qk_nope_dim, a->v_head_dim, &a->kv_b, attn,
+                                         MR_BF16, stream)) != MR_OK)
+            return st;
+        return block_proj(attn, hv, &a->o_proj, a->out, nullptr, nd, a->eps, gated ? gate : nullptr, stage, stream);
+    }
 
     // side stream: [input norm] -> kv_a -> cache row `position` (norm +
     // rope), joined before the attention; then the gate projection, joined

@@ -28,14 +28,20 @@
 //     stage would store them.
 //   - "direct" mode (grouped rows, y[j] = x[j / map_a] . W[wrow(j)]): each
 //     lane reads its x chunk from global memory next to the weight chunk
-//     (the vectors are small and shared through L2).
+//     (the vectors are small and shared through L2); with bf16 weights and
+//     activations the x chunks are loaded with the weight batch.
 //   - The lanes of a row meet by DPP / permlane butterflies (group_sum).
+//   - A staged launch may stack up to three weights of the same width along
+//     its output rows (projections of one activation vector in one launch).
 //
 // dense_absorb_kernel: q_lat[h][:] = sum_d q[h][d] * W[h*(nope+v) + d][:]
 // (the transposed product: each weight row is scaled by one query value),
-// one workgroup per head, each lane owning 8 of the 512 columns, the four
-// waves taking every fourth row and meeting in LDS; the head's rotary
-// columns may be rotated in the same launch (one position, adjacent pairs).
+// four workgroups per head, each taking 128 of the 512 columns: a lane owns
+// one 16-byte chunk of the slice, the row groups step over the nope rows
+// with ABS_UNROLL rows in flight per lane and meet in LDS; the head's rotary
+// columns may be rotated in the same launch (one position, adjacent pairs),
+// and one extra workgroup may append the token's cache row.
+#include "cache_append.hpp"
 #include "mr_kernels.hpp"
 
 namespace mr {
@@ -272,23 +278,42 @@ __global__ void __launch_bounds__(LT) dense_gemv_kernel(DenseGemvParams p) {
         g = (int64_t)((uint32_t)jj / (uint32_t)p.map_a);
         return g * p.map_b + p.map_c + (jj - g * p.map_a);
     };
-    auto load = [&](int k, u32x4(&w)[B]) {
+    // stacked weights (staged only): segment of row j and its first row
+    auto seg_of = [&](int64_t j, int& sg, int64_t& first) {
+        sg = (j >= p.seg_end[0]) + (p.nseg > 2 && j >= p.seg_end[1]);
+        first = sg == 0 ? 0 : (sg == 1 ? p.seg_end[0] : p.seg_end[1]);
+    };
+    // direct mode with bf16 activations: the activation chunks ride with the
+    // weight chunks (same 8 values when the weights are bf16)
+    constexpr bool XPRE = !STAGED && !XF32 && !WF32;
+    auto load = [&](int k, u32x4(&w)[B], u32x4(&xv)[B]) {
         // past the end the wave re-reads its last item: unconditional loads
         // keep the compiler's count of loads in flight exact across the loop
         k = min(k, nitems - 1);
         const int ui = k / nb, b = k - ui * nb;
         int64_t g;
-        const char* wr = (const char*)p.w + wrow_of(row_of(ui), g) * p.w_rs * (WF32 ? 4 : 2);
+        const int64_t wrow = wrow_of(row_of(ui), g);
+        const char* wr = (const char*)p.w + wrow * p.w_rs * (WF32 ? 4 : 2);
+        if (STAGED && p.nseg) {
+            int sg;
+            int64_t first;
+            seg_of(wrow, sg, first);
+            const void* sw = sg == 0 ? p.seg_w[0] : (sg == 1 ? p.seg_w[1] : p.seg_w[2]);
+            const int64_t rs = sg == 0 ? p.seg_w_rs[0] : (sg == 1 ? p.seg_w_rs[1] : p.seg_w_rs[2]);
+            wr = (const char*)sw + (wrow - first) * rs * (WF32 ? 4 : 2);
+        }
+        const char* xd = (const char*)p.x + ((int64_t)t0 * p.x_stride + g * p.x_vec_stride) * XE;
 #pragma unroll
         for (int u = 0; u < B; ++u) {
             const int c = min(li + (b * B + u) * tpr, chunks - 1);
             w[u] = __builtin_nontemporal_load((const u32x4*)(wr + 16 * (int64_t)c));
+            if (XPRE) xv[u] = *(const u32x4*)(xd + 16 * (int64_t)c);
         }
     };
     float acc[MT];
 #pragma unroll
     for (int t = 0; t < MT; ++t) acc[t] = 0.f;
-    auto consume = [&](int k, const u32x4(&w)[B]) {
+    auto consume = [&](int k, const u32x4(&w)[B], const u32x4(&xv)[B]) {
         const int ui = k / nb, b = k - ui * nb;
         const int64_t j = row_of(ui);
         int64_t g;
@@ -307,6 +332,9 @@ __global__ void __launch_bounds__(LT) dense_gemv_kernel(DenseGemvParams p) {
                         acc[t] = ok ? a : acc[t];
                     }
                 }
+            } else if (XPRE) {
+                const float a = chunk_dot<WF32, XF32>(w[u], &xv[u], acc[0]);
+                acc[0] = ok ? a : acc[0];
             } else {
                 const float a = chunk_dot<WF32, XF32>(w[u], xd + (int64_t)i0 * XE, acc[0]);
                 acc[0] = ok ? a : acc[0];
@@ -321,20 +349,30 @@ __global__ void __launch_bounds__(LT) dense_gemv_kernel(DenseGemvParams p) {
                 const float v = group_sum(acc[t], tpr);
                 acc[t] = 0.f;
                 if (live && li == 0) {
-                    const int64_t yo = (int64_t)(t0 + t) * p.y_stride_token + j * p.y_stride_row;
+                    void* y = p.y;
+                    int64_t yo = (int64_t)(t0 + t) * p.y_stride_token + j * p.y_stride_row;
+                    if (STAGED && p.nseg) {
+                        int sg;
+                        int64_t first;
+                        seg_of(j, sg, first);
+                        y = sg == 0 ? p.seg_y[0] : (sg == 1 ? p.seg_y[1] : p.seg_y[2]);
+                        const int64_t ts = sg == 0 ? p.seg_y_ts[0] : (sg == 1 ? p.seg_y_ts[1] : p.seg_y_ts[2]);
+                        yo = (int64_t)(t0 + t) * ts + (j - first) * p.y_stride_row;
+                    }
                     if (p.y_f32)
-                        ((float*)p.y)[yo] = v;
+                        ((float*)y)[yo] = v;
                     else
-                        ((uint16_t*)p.y)[yo] = f32_to_bf16_bits(v);
+                        ((uint16_t*)y)[yo] = f32_to_bf16_bits(v);
                 }
             }
         }
     };
 
     u32x4 wa[B], wb[B];
+    u32x4 xa[B], xb[B];  // used only with XPRE
     if (nitems > 0) {
-        load(0, wa);
-        load(1, wb);
+        load(0, wa, xa);
+        load(1, wb, xb);
     }
     if (STAGED) {
         for (int t = 0; t < mt; ++t) {
@@ -346,25 +384,32 @@ __global__ void __launch_bounds__(LT) dense_gemv_kernel(DenseGemvParams p) {
         __syncthreads();
     }
     for (int k = 0; k < nitems; k += 2) {
-        consume(k, wa);
-        load(k + 2, wa);
+        consume(k, wa, xa);
+        load(k + 2, wa, xa);
         if (k + 1 >= nitems) break;
-        consume(k + 1, wb);
-        load(k + 3, wb);
+        consume(k + 1, wb, xb);
+        load(k + 3, wb, xb);
     }
 }
 
+constexpr int ABS_CW = 128;  // q_lat columns per absorb workgroup
+constexpr int ABS_UNROLL = 8;  // row steps in flight per lane
+
 template <bool WF32>
 __global__ void __launch_bounds__(LT) dense_absorb_kernel(DenseAbsorbParams p) {
-    constexpr int VPC = WF32 ? 4 : 8;
-    constexpr int CPL = 8 / VPC;  // 16-byte chunks per lane (a lane owns 8 columns)
-    __shared__ float qs[1024];
-    __shared__ __attribute__((aligned(16))) float part[LT / 64][512];
-    const int h = blockIdx.x;
+    constexpr int VPC = WF32 ? 4 : 8;      // columns per 16-byte chunk
+    constexpr int LPR = ABS_CW / VPC;      // lanes per weight row slice
+    constexpr int RPS = LT / LPR;          // rows per step
+    __shared__ __attribute__((aligned(16))) float part[RPS][ABS_CW];
+    if (p.app_on && blockIdx.x == gridDim.x - 1) {  // the extra workgroup: the cache append
+        cache_append_row(p.app, 0, &part[0][0]);
+        return;
+    }
+    const int h = blockIdx.x / (512 / ABS_CW);
+    const int cs = blockIdx.x - h * (512 / ABS_CW);
     const int tid = threadIdx.x;
     uint16_t* qh = (uint16_t*)p.q + (int64_t)h * p.q_head_stride;
-    for (int d = tid; d < p.nope_dim; d += LT) qs[d] = bf16_bits_to_f32(qh[d]);
-    if (p.rope_cos) {  // the head's rotary columns, in place (they are not read below)
+    if (cs == 0 && p.rope_cos) {  // the head's rotary columns, in place (they are not read below)
         for (int i = tid; i < p.rope_dim / 2; i += LT) {
             const float a = bf16_bits_to_f32(qh[p.rope_col0 + 2 * i]);
             const float b = bf16_bits_to_f32(qh[p.rope_col0 + 2 * i + 1]);
@@ -373,33 +418,40 @@ __global__ void __launch_bounds__(LT) dense_absorb_kernel(DenseAbsorbParams p) {
             qh[p.rope_col0 + 2 * i + 1] = f32_to_bf16_bits(add_rn(mul_rn(a, s), mul_rn(b, c)));
         }
     }
-    __syncthreads();
-    const int wave = tid >> 6, lane = tid & 63;
-    float acc[8];
-#pragma unroll
-    for (int k = 0; k < 8; ++k) acc[k] = 0.f;
+    const int rg = tid / LPR, li = tid - rg * LPR;  // row group, chunk of the slice
     const int64_t row0 = (int64_t)h * (p.nope_dim + p.v_dim);
     const int esz = WF32 ? 4 : 2;
-#pragma unroll 4
-    for (int d = wave; d < p.nope_dim; d += LT / 64) {
-        const char* wr = (const char*)p.w + (row0 + d) * p.w_rs * esz + 16 * lane * CPL;
-        const float qd = qs[d];
+    const char* wc = (const char*)p.w + (int64_t)(cs * ABS_CW + li * VPC) * esz;
+    float acc[VPC];
 #pragma unroll
-        for (int u = 0; u < CPL; ++u) {
-            const u32x4 wv = __builtin_nontemporal_load((const u32x4*)(wr + 16 * u));
+    for (int k = 0; k < VPC; ++k) acc[k] = 0.f;
+    for (int d0 = rg; d0 < p.nope_dim; d0 += RPS * ABS_UNROLL) {
+        u32x4 wv[ABS_UNROLL];
+        float qd[ABS_UNROLL];
+#pragma unroll
+        for (int u = 0; u < ABS_UNROLL; ++u) {  // rows past nope_dim re-read the last one, weighted 0
+            const int d = d0 + u * RPS;
+            const int dc = min(d, p.nope_dim - 1);
+            wv[u] = __builtin_nontemporal_load((const u32x4*)(wc + (row0 + dc) * p.w_rs * esz));
+            qd[u] = d < p.nope_dim ? bf16_bits_to_f32(qh[dc]) : 0.f;
+        }
+#pragma unroll
+        for (int u = 0; u < ABS_UNROLL; ++u)
 #pragma unroll
             for (int k = 0; k < VPC; ++k) {
-                const float wk = WF32 ? __uint_as_float(wv[k]) : __uint_as_float(k & 1 ? wv[k >> 1] & 0xffff0000u : wv[k >> 1] << 16);
-                acc[u * VPC + k] = fmaf(qd, wk, acc[u * VPC + k]);
+                const float wk =
+                    WF32 ? __uint_as_float(wv[u][k]) : __uint_as_float(k & 1 ? wv[u][k >> 1] & 0xffff0000u : wv[u][k >> 1] << 16);
+                acc[k] = fmaf(qd[u], wk, acc[k]);
             }
-        }
     }
 #pragma unroll
-    for (int k = 0; k < 8; ++k) part[wave][8 * lane + k] = acc[k];
+    for (int k = 0; k < VPC; ++k) part[rg][li * VPC + k] = acc[k];
     __syncthreads();
-    uint16_t* out = p.q_lat + (int64_t)h * p.q_lat_head_stride;
-    for (int c = tid; c < 512; c += LT) {
-        const float v = (part[0][c] + part[1][c]) + (part[2][c] + part[3][c]);
+    uint16_t* out = p.q_lat + (int64_t)h * p.q_lat_head_stride + cs * ABS_CW;
+    for (int c = tid; c < ABS_CW; c += LT) {
+        float v = 0.f;
+#pragma unroll
+        for (int g = 0; g < RPS; ++g) v += part[g][c];
         out[c] = f32_to_bf16_bits(v);
     }
 }
@@ -471,10 +523,11 @@ hipError_t launch_dense_gemv(DenseGemvParams p, bool staged, int cus, hipStream_
 }
 
 hipError_t launch_dense_absorb(const DenseAbsorbParams& p, hipStream_t st) {
+    const dim3 grid((unsigned)(p.heads * (512 / ABS_CW) + (p.app_on ? 1 : 0)));
     if (p.w_f32)
-        hipLaunchKernelGGL(dense_absorb_kernel<true>, dim3(p.heads), dim3(LT), 0, st, p);
+        hipLaunchKernelGGL(dense_absorb_kernel<true>, grid, dim3(LT), 0, st, p);
     else
-        hipLaunchKernelGGL(dense_absorb_kernel<false>, dim3(p.heads), dim3(LT), 0, st, p);
+        hipLaunchKernelGGL(dense_absorb_kernel<false>, grid, dim3(LT), 0, st, p);
     return hipGetLastError();
 }
 

@@ -3,6 +3,7 @@
 // absorption of the query.
 #include <algorithm>
 
+#include "cache_append.hpp"
 #include "mr_kernels.hpp"
 
 // Arithmetic rounds as written (no a*b+c contraction): the rotary and the
@@ -75,41 +76,10 @@ __global__ void __launch_bounds__(256) rope_kernel(RopeParams p) {
     }
 }
 
-// Latent-cache append (MLA.swift:142-157 with the rotary tail of
-// DeepSeekV4CompressedAttention.swift:676-694): for token t, the kv_a row
-// [kv_rank latent ++ rope_dim key] -> RMSNorm(latent) * w -> bf16 cache row
-// (start + t)[0:kv_rank]; the key tail rotated at its position -> bf16
-// [kv_rank : kv_rank + rope_dim].  One block per token.
+// Latent-cache append: one block per token (cache_append_row).
 __global__ void __launch_bounds__(256) cache_append_kernel(CacheAppendParams p) {
     __shared__ float sh[4];
-    const int64_t t = blockIdx.x;
-    float ss = 0.f;
-    for (int i = threadIdx.x; i < p.kv_rank; i += 256) {
-        const float v = ld(p.kv, p.kv_f32, t * p.kv_stride + i);
-        ss = fmaf(v, v, ss);
-    }
-    ss = block_sum_256(ss, sh);
-    const float inv = 1.f / sqrtf(ss / (float)p.kv_rank + p.eps);
-    uint16_t* lat = p.latent + (p.start_row + t) * p.latent_stride;
-    for (int i = threadIdx.x; i < p.kv_rank; i += 256) {
-        const float v = ld(p.kv, p.kv_f32, t * p.kv_stride + i);
-        lat[i] = f32_to_bf16_bits(ld(p.norm_w, p.w_f32, i) * (v * inv));
-    }
-    const int half = p.rope_dim / 2;
-    uint16_t* rk = p.rope + (p.start_row + t) * p.rope_stride;
-    for (int i = threadIdx.x; i < half; i += 256) {
-        const float e = ld(p.kv, p.kv_f32, t * p.kv_stride + p.kv_rank + 2 * i);
-        const float o = ld(p.kv, p.kv_f32, t * p.kv_stride + p.kv_rank + 2 * i + 1);
-        if (!p.cos_t) {  // NoPE (MLA.swift:5-13): the shared key slice is kept as it is
-            rk[2 * i] = f32_to_bf16_bits(e);
-            rk[2 * i + 1] = f32_to_bf16_bits(o);
-            continue;
-        }
-        const float c = p.cos_t[t * half + i];
-        const float s = p.sin_t[t * half + i];
-        rk[2 * i] = f32_to_bf16_bits(sub_rn(mul_rn(e, c), mul_rn(o, s)));
-        rk[2 * i + 1] = f32_to_bf16_bits(add_rn(mul_rn(e, s), mul_rn(o, c)));
-    }
+    cache_append_row(p, blockIdx.x, sh);
 }
 
 // Query absorption (MLA.swift:180-188): q_lat[h][r] = sum_{d<dn} q_nope[h][d]
@@ -118,6 +88,10 @@ __global__ void __launch_bounds__(256) cache_append_kernel(CacheAppendParams p) 
 // thread t owns packed word t%64 (8 columns) and rows d = t/64 (mod 4).
 __global__ void __launch_bounds__(256) absorb_q_kernel(AbsorbParams p) {
     __shared__ float part[4][512];
+    if (p.app_on && blockIdx.x == gridDim.x - 1) {  // the extra workgroup: the cache append
+        cache_append_row(p.app, 0, &part[0][0]);
+        return;
+    }
     const int h = blockIdx.x;
     const int c = threadIdx.x & 63;  // word (8 columns of 512)
     const int ds = threadIdx.x >> 6;
@@ -163,6 +137,10 @@ __global__ void __launch_bounds__(256) absorb_q_fast_kernel(AbsorbParams p) {
     __shared__ float qs[128];
     __shared__ float sc[128][8], bi[128][8];
     __shared__ __attribute__((aligned(16))) float part[4][256];
+    if (p.app_on && blockIdx.x == gridDim.x - 1) {  // the extra workgroup: the cache append
+        cache_append_row(p.app, 0, qs);
+        return;
+    }
     const int h = blockIdx.x >> 1;
     const int half = blockIdx.x & 1;
     const int t = threadIdx.x;
@@ -289,7 +267,7 @@ hipError_t launch_absorb_q(const AbsorbParams& p, hipStream_t st) {
         return launch_absorb_q(q, st);
     }
     if (fast) {
-        const dim3 grid((unsigned)p.heads * 2);
+        const dim3 grid((unsigned)p.heads * 2 + (p.app_on ? 1 : 0));
         if (p.scale_dtype == 0)
             hipLaunchKernelGGL(absorb_q_fast_kernel<0>, grid, dim3(256), 0, st, p);
         else if (p.scale_dtype == 1)
@@ -298,7 +276,7 @@ hipError_t launch_absorb_q(const AbsorbParams& p, hipStream_t st) {
             hipLaunchKernelGGL(absorb_q_fast_kernel<2>, grid, dim3(256), 0, st, p);
         return hipGetLastError();
     }
-    hipLaunchKernelGGL(absorb_q_kernel, dim3((unsigned)p.heads), dim3(256), 0, st, p);
+    hipLaunchKernelGGL(absorb_q_kernel, dim3((unsigned)p.heads + (p.app_on ? 1 : 0)), dim3(256), 0, st, p);
     return hipGetLastError();
 }
 

@@ -220,12 +220,40 @@ struct DenseGemvParams {
     const void* gate;    // optional (not with norm_w): x_eff = x * sigmoid(gate[t * gate_stride + i])
     int gate_f32;
     int64_t gate_stride;
+    // staged launches: up to 3 weights with the same in_features stacked
+    // along the output rows (rows [seg_end[s-1], seg_end[s]) read seg_w[s],
+    // row stride seg_w_rs[s], and write seg_y[s], token stride seg_y_ts[s]);
+    // nseg 0 = the single weight w / y above
+    int nseg;
+    int seg_end[3];
+    const void* seg_w[3];
+    int64_t seg_w_rs[3];
+    void* seg_y[3];
+    int64_t seg_y_ts[3];
     int tpr, batches, mt, stage_vec;  // set by the launcher
     int64_t units;
 };
 // staged: map_a == out_rows and one activation vector fits DENSE_STAGE_BYTES
 int dense_gemv_tokens_per_tile(int in, int m, bool x_f32);
 hipError_t launch_dense_gemv(DenseGemvParams p, bool staged, int cus, hipStream_t st);
+
+// Latent-cache append of one kv_a row per token (layout in cache_append_row).
+struct CacheAppendParams {
+    const void* kv;  // [tokens, kv_rank + rope_dim]
+    int kv_f32;
+    int64_t kv_stride;
+    const void* norm_w;
+    int w_f32;
+    float eps;
+    int kv_rank, rope_dim;
+    const float* cos_t;  // [tokens, rope_dim/2]; null: the key is stored unrotated (NoPE)
+    const float* sin_t;
+    uint16_t* latent;
+    int64_t latent_stride;
+    uint16_t* rope;
+    int64_t rope_stride;
+    int64_t start_row, tokens;
+};
 
 // q_lat[h][r] = sum_{d < nope} q[h][d] * W[h*(nope+v) + d][r], r < 512
 // (W_UK of a dense kv_b_proj); optional rotation of q's rotary columns.
@@ -242,6 +270,8 @@ struct DenseAbsorbParams {
     const float* rope_sin;
     int rope_dim;
     int64_t rope_col0;
+    CacheAppendParams app;  // app_on: one extra workgroup appends token 0's cache row in the same launch
+    int app_on;
 };
 hipError_t launch_dense_absorb(const DenseAbsorbParams& p, hipStream_t st);
 // out[i] = bf16(x[i] * sigmoid(g[i])), bf16 vectors of n elements
@@ -275,22 +305,6 @@ struct RopeParams {
     const float* sin_t;
 };
 
-struct CacheAppendParams {
-    const void* kv;  // [tokens, kv_rank + rope_dim]
-    int kv_f32;
-    int64_t kv_stride;
-    const void* norm_w;
-    int w_f32;
-    float eps;
-    int kv_rank, rope_dim;
-    const float* cos_t;  // [tokens, rope_dim/2]; null: the key is stored unrotated (NoPE)
-    const float* sin_t;
-    uint16_t* latent;
-    int64_t latent_stride;
-    uint16_t* rope;
-    int64_t rope_stride;
-    int64_t start_row, tokens;
-};
 
 struct AbsorbParams {
     const uint16_t* q;  // [heads, q_head_stride], nope part first
@@ -308,6 +322,8 @@ struct AbsorbParams {
     const float* rope_sin;
     int rope_dim;
     int64_t rope_col0;
+    CacheAppendParams app;  // app_on: one extra workgroup appends token 0's cache row in the same launch
+    int app_on;
 };
 
 hipError_t launch_rmsnorm(const RmsNormParams& p, hipStream_t st);
