@@ -425,8 +425,8 @@ hipError_t launch_affine_gemv(const AffineGemvParams& q, hipStream_t st) {
     if (affine_gemv_fast_ok(q)) {
         AffineGemvParams p = q;
         // threads per row: about G/4 groups each, more while the grid holds
-        // fewer row steps than the GPU has CUs; tiles of whole steps, about
-        // one per CU
+        // fewer row steps than the GPU has CUs; tiles of whole steps, at
+        // least one per CU
         const int G = p.in_features / 64;
         const int nvec = (p.out_rows + p.map_a - 1) / p.map_a;
         const int per_vec = std::min(p.map_a, p.out_rows);
@@ -436,7 +436,7 @@ hipError_t launch_affine_gemv(const AffineGemvParams& q, hipStream_t st) {
         while (tpr < 64 && steps(tpr) < 256) tpr <<= 1;
         const int rps = GEMV_THREADS / tpr;
         const int64_t total = steps(tpr);
-        const int64_t per_tile = std::max<int64_t>(1, (total + 255) / 256);
+        const int64_t per_tile = std::max<int64_t>(1, total / 256);  // at least one tile per CU
         p.tpr = tpr;
         p.tile_rows = (int)std::min<int64_t>(per_tile * rps, per_vec);
         p.tiles_per_vec = (per_vec + p.tile_rows - 1) / p.tile_rows;

@@ -11,8 +11,8 @@
 //   - Each wave walks a flat list of items (unit, batch of GEMV_BATCH chunks
 //     per lane) with two batches of loads in flight: batch k + 1 streams in
 //     while batch k is multiplied, and the next load is issued as soon as a
-//     batch's registers are free (past its last item a wave re-reads that
-//     item, so every load is unconditional).  A row's tail batch clamps its chunk index
+//     batch's registers are free (past its last item a wave loads from the
+//     activation vector instead, an L2 hit, so every load is unconditional).  A row's tail batch clamps its chunk index
 //     (re-reading the last chunk, a cache hit) and masks the product, so no
 //     lane runs a serial remainder loop.  The first two batches are issued
 //     before the activations are staged.
@@ -286,9 +286,12 @@ __global__ void __launch_bounds__(LT) dense_gemv_kernel(DenseGemvParams p) {
     // direct mode with bf16 activations: the activation chunks ride with the
     // weight chunks (same 8 values when the weights are bf16)
     constexpr bool XPRE = !STAGED && !XF32 && !WF32;
+    const int xch = max(1, p.in * XE / 16);  // 16-byte chunks of one activation vector
     auto load = [&](int k, u32x4(&w)[B], u32x4(&xv)[B]) {
-        // past the end the wave re-reads its last item: unconditional loads
-        // keep the compiler's count of loads in flight exact across the loop
+        // past its last item a wave still loads (unconditional loads keep the
+        // compiler's count of loads in flight exact across the loop), from
+        // the activation vector, which every workgroup has just read (L2)
+        const bool past = k >= nitems;
         k = min(k, nitems - 1);
         const int ui = k / nb, b = k - ui * nb;
         int64_t g;
@@ -303,9 +306,11 @@ __global__ void __launch_bounds__(LT) dense_gemv_kernel(DenseGemvParams p) {
             wr = (const char*)sw + (wrow - first) * rs * (WF32 ? 4 : 2);
         }
         const char* xd = (const char*)p.x + ((int64_t)t0 * p.x_stride + g * p.x_vec_stride) * XE;
+        if (past) wr = (const char*)p.x;
 #pragma unroll
         for (int u = 0; u < B; ++u) {
-            const int c = min(li + (b * B + u) * tpr, chunks - 1);
+            const int cl = li + (b * B + u) * tpr;
+            const int c = min(cl, past ? xch - 1 : chunks - 1);
             w[u] = __builtin_nontemporal_load((const u32x4*)(wr + 16 * (int64_t)c));
             if (XPRE) xv[u] = *(const u32x4*)(xd + 16 * (int64_t)c);
         }
