@@ -358,6 +358,9 @@ __global__ void __launch_bounds__(256, 2) prefill_attn_kernel(PrefillAttnParams 
         };
 #pragma unroll
         for (int e = 0; e < 4; ++e) ga[0][e] = qk_a(e >> 1, e & 1);
+        // the two waves sharing a SIMD (one from each workgroup) take turns:
+        // the wave in an MFMA phase issues first, the other's softmax fills in
+        __builtin_amdgcn_s_setprio(1);
 #pragma unroll
         for (int gq = 0; gq < 6; ++gq) {
             if (gq + 1 < 6) {
@@ -369,6 +372,7 @@ __global__ void __launch_bounds__(256, 2) prefill_attn_kernel(PrefillAttnParams 
             for (int e = 0; e < 4; ++e) s[e & 1] = mfma32(ga[gq & 1][e], qf[2 * gq + (e >> 1)], s[e & 1]);
             __builtin_amdgcn_sched_barrier(0);
         }
+        __builtin_amdgcn_s_setprio(0);
         // causal mask on raw scores, running max (lane = query, 32 of its keys)
         float mx = -INFINITY;
         const int lim = q_limit - k0 - 4 * hh;  // tile key index kb*32 + 8*(i>>2) + (i&3) visible iff <= lim
@@ -405,6 +409,7 @@ __global__ void __launch_bounds__(256, 2) prefill_attn_kernel(PrefillAttnParams 
         l_part += ls;
 
         // O^T += V^T . P^T: k-step t covers tile keys 16t .. 16t+15
+        __builtin_amdgcn_s_setprio(1);
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
             const int kb = t >> 1, base = 8 * (t & 1);
@@ -420,6 +425,7 @@ __global__ void __launch_bounds__(256, 2) prefill_attn_kernel(PrefillAttnParams 
                 o[db] = mfma32(a, pb, o[db]);
             }
         }
+        __builtin_amdgcn_s_setprio(0);
     };
 
     // tile 0 in flight, wait for it
