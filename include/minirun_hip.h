@@ -324,10 +324,8 @@ mr_status mr_mla_unabsorb_values(const void *ctx, int64_t ctx_head_stride, int32
  * MLA.swift:5-13: the slice is carried through unrotated).
  * Each projection is affine (MLX 4-bit) or dense (k3Linear); K3's attention
  * weights are dense bf16.  All activations between the projections are bf16.
- * The key path (kv_a, cache append) and the gate projection run on a
- * library-owned side stream of the current device, forked from `stream` and
- * joined back by events (before the attention and before o_proj); the call
- * stays ordered on `stream` as a whole.
+ * Every stage is enqueued on `stream`, in order (dense projections of the
+ * input run as one launch; the cache append rides in the absorption launch).
  * ------------------------------------------------------------------------ */
 typedef struct mr_mla_block_args {
     int32_t hidden, q_lora_rank, heads, qk_nope_dim, qk_rope_dim, v_head_dim, kv_rank;

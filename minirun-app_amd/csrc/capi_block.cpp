@@ -1,13 +1,11 @@
 // C-ABI: affine weights, RMSNorm, rotary, cache append, absorption, the
 // composed decode block, and the V4 index tables.  Validation first, with
-// the reference's messages where it has them; no device memory allocation
-// (the block creates one side stream and two events per device, once).
+// the reference's messages where it has them; no device memory allocation.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
 #include <cmath>
 #include <cstdio>
-#include <mutex>
 #include <string>
 
 #include "../../include/minirun_hip.h"
@@ -63,40 +61,6 @@ mr_status check_weight(const mr_affine_weight* w, const char* what) {
 bool act_dtype_ok(mr_dtype d) { return d == MR_BF16 || d == MR_F32; }
 
 mr::AffineGemvParams gemv_params(const mr_affine_weight* w);
-
-// The block's key path (kv_a projection, cache append) does not depend on
-// its query path until the attention: it runs on a side stream of the
-// device, forked from and joined back to the caller's stream by events.
-// One side stream per device for the process, with one fork and two join
-// events (the key path; the gate projection).  A call holds `mu` from its fork record to its wait on the join, so
-// calls from several host threads cannot pick up each other's fork point;
-// calls that share the stream are ordered on it.
-struct SideStream {
-    hipStream_t s = nullptr;
-    hipEvent_t fork = nullptr, join = nullptr, join_gate = nullptr;
-    std::mutex mu;
-};
-
-mr_status side_stream(SideStream** out) {
-    static std::mutex mu;
-    static SideStream per_dev[64];
-    int dev = 0;
-    hipError_t e = hipGetDevice(&dev);
-    if (e != hipSuccess) return hip_fail(e, "mla block: hipGetDevice");
-    if (dev < 0 || dev >= 64) return fail(MR_INVALID_ARGUMENT, "mla block: device %d out of range", dev);
-    std::lock_guard<std::mutex> lock(mu);
-    SideStream& ss = per_dev[dev];
-    if (!ss.s) {
-        if ((e = hipStreamCreateWithFlags(&ss.s, hipStreamNonBlocking)) != hipSuccess)
-            return hip_fail(e, "mla block: side stream");
-        if ((e = hipEventCreateWithFlags(&ss.fork, hipEventDisableTiming)) != hipSuccess ||
-            (e = hipEventCreateWithFlags(&ss.join, hipEventDisableTiming)) != hipSuccess ||
-            (e = hipEventCreateWithFlags(&ss.join_gate, hipEventDisableTiming)) != hipSuccess)
-            return hip_fail(e, "mla block: side stream events");
-    }
-    *out = &ss;
-    return MR_OK;
-}
 
 // y = W . RMSNorm(x) (norm_w non-null) or y = W . x for one bf16 token:
 // the norm rides in the GEMV's staging of x when the 4-bit fast path takes
@@ -733,7 +697,7 @@ bool block_layout(const mr_mla_block_args* a, BlockLayout* L) {
     const int dq = a->qk_nope_dim + a->qk_rope_dim;
     const size_t hv = size_t(a->heads) * a->v_head_dim;
     L->h = take(size_t(a->hidden) * 2);
-    L->h_kv = take(size_t(a->hidden) * 2);  // the key path's normed x (it runs beside the query path)
+    L->h_kv = take(size_t(a->hidden) * 2);  // the key path's (and the gate's) normed x
     L->q_lora = take(size_t(a->q_lora_rank) * 2);
     L->q_lora_n = take(size_t(a->q_lora_rank) * 2);
     L->q = take(size_t(a->heads) * dq * 2);
@@ -831,83 +795,46 @@ mr_status mr_mla_decode_block(const mr_mla_block_args* a, void* stream) {
     void* stage = W + L.stage;
     const mr_dtype nd = a->norm_w_dtype;
 
-    // dense projections (K3): q_a, kv_a and g_proj all read the (normed)
-    // input, so they run as one launch, and the chain stays on one stream
+    // One stream, in order: the projections of the block input (q_a, kv_a
+    // and, gated, g_proj; one stacked launch when they are dense), q_b with
+    // its RMSNorm, the absorption (query rotary and the cache append of row
+    // `position` ride in it), the decode, W_UV and o_proj (the gate rides in
+    // its staging).  A side stream for the key path and the gate cost more
+    // in cross-stream waits than it overlapped.
     const mr_projection* xw[3] = {&a->q_a, &a->kv_a, &a->g_proj};
     void* xy[3] = {q_lora, kv, gate};
+    void* xs[3] = {h, h_kv, h_kv};  // stage buffers for an input norm that no kernel fuses
     const int nx = gated ? 3 : 2;
     if (dense_stack_ok(xw, nx, a->hidden)) {
         if ((st = dense_stack(a->x, a->hidden, xw, xy, nx, a->input_norm_w, nd, a->eps, stream)) != MR_OK) return st;
-        if ((st = block_proj(q_lora, a->q_lora_rank, &a->q_b, q, a->q_a_norm_w, nd, a->eps, nullptr, q_lora_n,
-                             stream)) != MR_OK)
-            return st;
-        // the absorption carries the cache append (row `position`) as one
-        // more workgroup
-        const mr::CacheAppendParams app{kv,           0,           a->kv_rank + a->qk_rope_dim,
-                                        a->kv_a_norm_w, nd == MR_F32, a->eps,
-                                        a->kv_rank,   a->qk_rope_dim, a->rope_cos,
-                                        a->rope_sin,  (uint16_t*)a->cache_latent, a->latent_row_stride,
-                                        (uint16_t*)a->cache_rope, a->rope_row_stride, a->position,
-                                        1};
-        if ((st = absorb(q, dq, a->heads, a->qk_nope_dim, a->v_head_dim, &a->kv_b, q_lat, a->kv_rank, a->rope_cos,
-                         a->rope_sin, a->qk_rope_dim, stream, &app)) != MR_OK)
-            return st;
-        mr_mla_decode_args d = L.dec_args;
-        d.q_lat = q_lat;
-        d.q_rope = q + a->qk_nope_dim;
-        d.latent = a->cache_latent;
-        d.rope_keys = a->cache_rope;
-        d.out = ctx;
-        d.workspace = W + L.dec;
-        d.workspace_bytes = L.total - L.dec;
-        if ((st = mr_mla_decode(&d, stream)) != MR_OK) return st;
-        if ((st = mr_mla_unabsorb_values(ctx, a->kv_rank, a->heads, a->qk_nope_dim, a->v_head_dim, &a->kv_b, attn,
-                                         MR_BF16, stream)) != MR_OK)
-            return st;
-        return block_proj(attn, hv, &a->o_proj, a->out, nullptr, nd, a->eps, gated ? gate : nullptr, stage, stream);
+    } else {
+        for (int i = 0; i < nx; ++i)
+            if ((st = block_proj(a->x, a->hidden, xw[i], xy[i], a->input_norm_w, nd, a->eps, nullptr, xs[i], stream)) !=
+                MR_OK)
+                return st;
     }
-
-    // side stream: [input norm] -> kv_a -> cache row `position` (norm +
-    // rope), joined before the attention; then the gate projection, joined
-    // before o_proj
-    SideStream* side = nullptr;
-    if ((st = side_stream(&side)) != MR_OK) return st;
-    std::unique_lock<std::mutex> side_lock(side->mu);  // released after the joins are waited on
-    hipError_t he;
-    if ((he = hipEventRecord(side->fork, (hipStream_t)stream)) != hipSuccess ||
-        (he = hipStreamWaitEvent(side->s, side->fork, 0)) != hipSuccess)
-        return hip_fail(he, "mla block: fork");
-    if ((st = block_proj(a->x, a->hidden, &a->kv_a, kv, a->input_norm_w, nd, a->eps, nullptr, h_kv, side->s)) != MR_OK)
-        return st;
-    if ((st = mr_mla_cache_append(kv, MR_BF16, a->kv_rank + a->qk_rope_dim, 1, a->kv_a_norm_w, nd, a->eps, a->kv_rank,
-                                  a->qk_rope_dim, a->rope_cos, a->rope_sin, a->cache_latent, a->latent_row_stride,
-                                  a->cache_rope, a->rope_row_stride, a->position, side->s)) != MR_OK)
-        return st;
-    if ((he = hipEventRecord(side->join, side->s)) != hipSuccess) return hip_fail(he, "mla block: join record");
-    if (gated) {
-        if ((st = block_proj(a->x, a->hidden, &a->g_proj, gate, a->input_norm_w, nd, a->eps, nullptr, h_kv, side->s)) !=
-            MR_OK)
-            return st;
-        if ((he = hipEventRecord(side->join_gate, side->s)) != hipSuccess)
-            return hip_fail(he, "mla block: gate join record");
-    }
-    // query path: [input norm] -> q_a -> RMSNorm -> q_b -> rotate the rope
-    // part (unless NoPE) -> absorb W_UK (norms ride in the projections'
-    // staging of x where they can)
-    if ((st = block_proj(a->x, a->hidden, &a->q_a, q_lora, a->input_norm_w, nd, a->eps, nullptr, h, stream)) != MR_OK)
-        return st;
     if ((st = block_proj(q_lora, a->q_lora_rank, &a->q_b, q, a->q_a_norm_w, nd, a->eps, nullptr, q_lora_n, stream)) !=
         MR_OK)
         return st;
-    // query rotary + absorb W_UK in one launch (the rotation touches only
-    // the rope columns, the absorption reads only the nope columns)
+    const mr::CacheAppendParams app{kv,
+                                    0,
+                                    a->kv_rank + a->qk_rope_dim,
+                                    a->kv_a_norm_w,
+                                    nd == MR_F32,
+                                    a->eps,
+                                    a->kv_rank,
+                                    a->qk_rope_dim,
+                                    a->rope_cos,
+                                    a->rope_sin,
+                                    (uint16_t*)a->cache_latent,
+                                    a->latent_row_stride,
+                                    (uint16_t*)a->cache_rope,
+                                    a->rope_row_stride,
+                                    a->position,
+                                    1};
     if ((st = absorb(q, dq, a->heads, a->qk_nope_dim, a->v_head_dim, &a->kv_b, q_lat, a->kv_rank, a->rope_cos,
-                     a->rope_sin, a->qk_rope_dim, stream)) != MR_OK)
+                     a->rope_sin, a->qk_rope_dim, stream, &app)) != MR_OK)
         return st;
-    // attend once the key path has written the cache row
-    if ((he = hipStreamWaitEvent((hipStream_t)stream, side->join, 0)) != hipSuccess)
-        return hip_fail(he, "mla block: join");
-    if (!gated) side_lock.unlock();
     mr_mla_decode_args d = L.dec_args;
     d.q_lat = q_lat;
     d.q_rope = q + a->qk_nope_dim;
@@ -917,16 +844,9 @@ mr_status mr_mla_decode_block(const mr_mla_block_args* a, void* stream) {
     d.workspace = W + L.dec;
     d.workspace_bytes = L.total - L.dec;
     if ((st = mr_mla_decode(&d, stream)) != MR_OK) return st;
-    // values: un-absorb W_UV per head, then o_proj of merged (* gate)
     if ((st = mr_mla_unabsorb_values(ctx, a->kv_rank, a->heads, a->qk_nope_dim, a->v_head_dim, &a->kv_b, attn, MR_BF16,
                                      stream)) != MR_OK)
         return st;
-    // the gate projection ran beside the attention
-    if (gated) {
-        if ((he = hipStreamWaitEvent((hipStream_t)stream, side->join_gate, 0)) != hipSuccess)
-            return hip_fail(he, "mla block: gate join");
-        side_lock.unlock();
-    }
     return block_proj(attn, hv, &a->o_proj, a->out, nullptr, nd, a->eps, gated ? gate : nullptr, stage, stream);
 }
 

@@ -350,9 +350,9 @@ def test_block_small_context_and_first_token(M, monkeypatch):
 
 
 def test_block_two_host_threads(M):
-    # two host threads, two streams, one device: each call's key path (on the
-    # library's shared side stream) must wait for its own caller's stream, so
-    # every result equals the single-thread one bit for bit
+    # two host threads, two streams, one device: every stage of a call is
+    # ordered on its own caller's stream, so every result equals the
+    # single-thread one bit for bit
     print("block from two host threads at once", flush=True)
     import threading
 
