@@ -87,14 +87,21 @@ constexpr int GEMV_MAX_CH = GEMV_MAX_IN / 8 / GEMV_THREADS;
 constexpr int GEMV_NPT_MAX = 4;  // groups per thread and row: tpr * GEMV_NPT >= G
 
 template <int SDT, int GEMV_NPT>
-__global__ void __launch_bounds__(GEMV_THREADS) affine_gemv4_kernel(AffineGemvParams p, uint32_t wbytes, uint32_t sbytes) {
+__global__ void __launch_bounds__(GEMV_THREADS)
+    affine_gemv4_kernel(AffineGemvParams p0, uint32_t wbytes0, uint32_t sbytes0, AffineGemvParams p1, uint32_t wbytes1,
+                        uint32_t sbytes1, int tiles0) {
+    // two weights of one activation vector in one launch: workgroups from
+    // tiles0 on take the second parameter set (tiles0 = gridDim.x: one set)
+    const bool second = (int)blockIdx.x >= tiles0;
+    const AffineGemvParams& p = second ? p1 : p0;
+    const uint32_t wbytes = second ? wbytes1 : wbytes0, sbytes = second ? sbytes1 : sbytes0;
     // (x_j, x_j+4) pairs, 16 bytes per packed word; a group's 128 bytes are
     // followed by 16 bytes of padding, so lanes reading consecutive groups
     // start on different banks
     __shared__ __attribute__((aligned(16))) uint32_t xp[GEMV_MAX_IN / 2 + GEMV_MAX_IN / 16];
     __shared__ float xs[GEMV_MAX_IN / 64];                              // per-group sums of the staged x
     __shared__ float red[GEMV_THREADS / 64];
-    const int tile = blockIdx.x;
+    const int tile = (int)blockIdx.x - (second ? tiles0 : 0);
     const int xg = tile / p.tiles_per_vec;  // activation vector of this tile
     const int r0 = xg * p.map_a + (tile - xg * p.tiles_per_vec) * p.tile_rows;
     const int r_end = min(r0 + p.tile_rows, min((xg + 1) * p.map_a, p.out_rows));
@@ -421,52 +428,83 @@ bool affine_gemv_fast_ok(const AffineGemvParams& p) {
            gemv_weight_rows(p) * (p.in_features / 64) * (p.scale_dtype == 2 ? 4 : 2) < (int64_t(1) << 31);
 }
 
-hipError_t launch_affine_gemv(const AffineGemvParams& q, hipStream_t st) {
-    if (affine_gemv_fast_ok(q)) {
-        AffineGemvParams p = q;
-        // threads per row: about G/4 groups each, more while the grid holds
-        // fewer row steps than the GPU has CUs; tiles of whole steps, at
-        // least one per CU
-        const int G = p.in_features / 64;
-        const int nvec = (p.out_rows + p.map_a - 1) / p.map_a;
-        const int per_vec = std::min(p.map_a, p.out_rows);
-        int tpr = 1;
-        while (tpr < 64 && tpr * 4 < G) tpr <<= 1;
-        auto steps = [&](int t) { return (int64_t)nvec * ((per_vec + GEMV_THREADS / t - 1) / (GEMV_THREADS / t)); };
-        while (tpr < 64 && steps(tpr) < 256) tpr <<= 1;
-        const int rps = GEMV_THREADS / tpr;
-        const int64_t total = steps(tpr);
-        const int64_t per_tile = std::max<int64_t>(1, total / 256);  // at least one tile per CU
-        p.tpr = tpr;
-        p.tile_rows = (int)std::min<int64_t>(per_tile * rps, per_vec);
-        p.tiles_per_vec = (per_vec + p.tile_rows - 1) / p.tile_rows;
-        const unsigned grid = (unsigned)(nvec * p.tiles_per_vec);
-        const int npt = (G + tpr - 1) / tpr;  // 1 .. 4
-        const int64_t w_rows = gemv_weight_rows(p);
-        const uint32_t wbytes = (uint32_t)(w_rows * (p.in_features / 2));
-        const uint32_t sbytes = (uint32_t)(w_rows * G * (p.scale_dtype == 2 ? 4 : 2));
-#define MR_GEMV4(SDT, NPT) hipLaunchKernelGGL((affine_gemv4_kernel<SDT, NPT>), dim3(grid), dim3(GEMV_THREADS), 0, st, p, wbytes, sbytes)
-#define MR_GEMV4_NPT(SDT) \
-    do {                     \
-        if (npt == 1)        \
+// Launch geometry of the 4-bit fast path.
+struct FastPlan {
+    AffineGemvParams p;  // with tpr, tile_rows, tiles_per_vec set
+    unsigned grid;
+    int npt;
+    uint32_t wbytes, sbytes;
+};
+
+static FastPlan plan_fast(const AffineGemvParams& q) {
+    FastPlan f;
+    AffineGemvParams& p = f.p;
+    p = q;
+    // threads per row: about G/4 groups each, more while the grid holds
+    // fewer row steps than the GPU has CUs; tiles of whole steps, at least
+    // one per CU
+    const int G = p.in_features / 64;
+    const int nvec = (p.out_rows + p.map_a - 1) / p.map_a;
+    const int per_vec = std::min(p.map_a, p.out_rows);
+    int tpr = 1;
+    while (tpr < 64 && tpr * 4 < G) tpr <<= 1;
+    auto steps = [&](int t) { return (int64_t)nvec * ((per_vec + GEMV_THREADS / t - 1) / (GEMV_THREADS / t)); };
+    while (tpr < 64 && steps(tpr) < 256) tpr <<= 1;
+    const int rps = GEMV_THREADS / tpr;
+    const int64_t total = steps(tpr);
+    const int64_t per_tile = std::max<int64_t>(1, total / 256);  // at least one tile per CU
+    p.tpr = tpr;
+    p.tile_rows = (int)std::min<int64_t>(per_tile * rps, per_vec);
+    p.tiles_per_vec = (per_vec + p.tile_rows - 1) / p.tile_rows;
+    f.grid = (unsigned)(nvec * p.tiles_per_vec);
+    f.npt = (G + tpr - 1) / tpr;  // 1 .. 4
+    const int64_t w_rows = gemv_weight_rows(p);
+    f.wbytes = (uint32_t)(w_rows * (p.in_features / 2));
+    f.sbytes = (uint32_t)(w_rows * G * (p.scale_dtype == 2 ? 4 : 2));
+    return f;
+}
+
+// One launch of a (or of a and b, which share the template instance).
+static hipError_t launch_fast(const FastPlan& a, const FastPlan* b, hipStream_t st) {
+    const FastPlan& s = b ? *b : a;
+    const dim3 grid(a.grid + (b ? b->grid : 0));
+    const int tiles0 = (int)a.grid;
+#define MR_GEMV4(SDT, NPT)                                                                                              \
+    hipLaunchKernelGGL((affine_gemv4_kernel<SDT, NPT>), grid, dim3(GEMV_THREADS), 0, st, a.p, a.wbytes, a.sbytes, s.p, \
+                       s.wbytes, s.sbytes, tiles0)
+#define MR_GEMV4_NPT(SDT)     \
+    do {                      \
+        if (a.npt == 1)       \
             MR_GEMV4(SDT, 1); \
-        else if (npt == 2)   \
+        else if (a.npt == 2)  \
             MR_GEMV4(SDT, 2); \
-        else if (npt == 3)   \
+        else if (a.npt == 3)  \
             MR_GEMV4(SDT, 3); \
-        else                 \
+        else                  \
             MR_GEMV4(SDT, 4); \
     } while (0)
-        if (p.scale_dtype == 0)
-            MR_GEMV4_NPT(0);
-        else if (p.scale_dtype == 1)
-            MR_GEMV4_NPT(1);
-        else
-            MR_GEMV4_NPT(2);
+    if (a.p.scale_dtype == 0)
+        MR_GEMV4_NPT(0);
+    else if (a.p.scale_dtype == 1)
+        MR_GEMV4_NPT(1);
+    else
+        MR_GEMV4_NPT(2);
 #undef MR_GEMV4_NPT
 #undef MR_GEMV4
-        return hipGetLastError();
+    return hipGetLastError();
+}
+
+hipError_t launch_affine_gemv_pair(const AffineGemvParams& a, const AffineGemvParams& b, hipStream_t st) {
+    if (affine_gemv_fast_ok(a) && affine_gemv_fast_ok(b) && a.scale_dtype == b.scale_dtype) {
+        const FastPlan fa = plan_fast(a), fb = plan_fast(b);
+        if (fa.npt == fb.npt) return launch_fast(fa, &fb, st);
     }
+    const hipError_t e = launch_affine_gemv(a, st);
+    return e != hipSuccess ? e : launch_affine_gemv(b, st);
+}
+
+hipError_t launch_affine_gemv(const AffineGemvParams& q, hipStream_t st) {
+    if (affine_gemv_fast_ok(q)) return launch_fast(plan_fast(q), nullptr, st);
     const AffineGemvParams& p = q;
     const int64_t waves = (int64_t)p.m * p.out_rows;
     const unsigned grid = (unsigned)((waves + 3) / 4);

@@ -90,6 +90,40 @@ mr_status block_gemv(const void* x, int64_t in, const mr_affine_weight* w, void*
     return e == hipSuccess ? MR_OK : hip_fail(e, "affine matmul launch");
 }
 
+// The same for two weights of one activation vector (q_a and kv_a of the
+// block input) as one launch when both take the fast path, sharing the
+// norm: fused in both, or one stage into `norm_buf` for both.
+mr_status block_gemv_pair(const void* x, int64_t in, const mr_affine_weight* wa, void* ya, const mr_affine_weight* wb,
+                          void* yb, const void* norm_w, mr_dtype norm_dtype, float eps, void* norm_buf, void* stream) {
+    mr::AffineGemvParams g[2] = {gemv_params(wa), gemv_params(wb)};
+    const mr_affine_weight* w[2] = {wa, wb};
+    void* y[2] = {ya, yb};
+    for (int i = 0; i < 2; ++i) {
+        g[i].x = x;
+        g[i].x_f32 = 0;
+        g[i].x_stride = in;
+        g[i].m = 1;
+        g[i].y = y[i];
+        g[i].y_f32 = 0;
+        g[i].y_stride_row = 1;
+        g[i].y_stride_token = w[i]->out_features;
+        g[i].force_generic = !aligned16(w[i]->packed);
+        g[i].norm_w = norm_w;
+        g[i].norm_w_f32 = norm_dtype == MR_F32;
+        g[i].norm_eps = eps;
+    }
+    if (norm_w && !(mr::affine_gemv_fast_ok(g[0]) && mr::affine_gemv_fast_ok(g[1]))) {
+        mr_status st = mr_rmsnorm(x, MR_BF16, 1, (int32_t)in, in, norm_w, norm_dtype, eps, norm_buf, MR_BF16, in, stream);
+        if (st != MR_OK) return st;
+        for (auto& gi : g) {
+            gi.x = norm_buf;
+            gi.norm_w = nullptr;
+        }
+    }
+    const hipError_t e = mr::launch_affine_gemv_pair(g[0], g[1], (hipStream_t)stream);
+    return e == hipSuccess ? MR_OK : hip_fail(e, "affine matmul launch");
+}
+
 mr_status check_dense(const mr_dense_weight* w, const char* what) {
     if (!w) return fail(MR_INVALID_ARGUMENT, "%s: weight descriptor is NULL", what);
     if (!w->weight) return fail(MR_INVALID_ARGUMENT, "%s: weight is NULL", what);
@@ -796,7 +830,8 @@ mr_status mr_mla_decode_block(const mr_mla_block_args* a, void* stream) {
     const mr_dtype nd = a->norm_w_dtype;
 
     // One stream, in order: the projections of the block input (q_a, kv_a
-    // and, gated, g_proj; one stacked launch when they are dense), q_b with
+    // and, gated, g_proj; one stacked launch when they are dense, q_a and
+    // kv_a as one launch when they are 4-bit), q_b with
     // its RMSNorm, the absorption (query rotary and the cache append of row
     // `position` ride in it), the decode, W_UV and o_proj (the gate rides in
     // its staging).  A side stream for the key path and the gate cost more
@@ -807,6 +842,13 @@ mr_status mr_mla_decode_block(const mr_mla_block_args* a, void* stream) {
     const int nx = gated ? 3 : 2;
     if (dense_stack_ok(xw, nx, a->hidden)) {
         if ((st = dense_stack(a->x, a->hidden, xw, xy, nx, a->input_norm_w, nd, a->eps, stream)) != MR_OK) return st;
+    } else if (a->q_a.kind == MR_PROJ_AFFINE && a->kv_a.kind == MR_PROJ_AFFINE) {
+        if ((st = block_gemv_pair(a->x, a->hidden, &a->q_a.affine, q_lora, &a->kv_a.affine, kv, a->input_norm_w, nd,
+                                  a->eps, h, stream)) != MR_OK)
+            return st;
+        if (gated && (st = block_proj(a->x, a->hidden, &a->g_proj, gate, a->input_norm_w, nd, a->eps, nullptr, h_kv,
+                                      stream)) != MR_OK)
+            return st;
     } else {
         for (int i = 0; i < nx; ++i)
             if ((st = block_proj(a->x, a->hidden, xw[i], xy[i], a->input_norm_w, nd, a->eps, nullptr, xs[i], stream)) !=

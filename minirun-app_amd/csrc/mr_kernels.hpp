@@ -280,6 +280,9 @@ hipError_t launch_gate_mul(const uint16_t* x, const uint16_t* g, int64_t n, uint
 hipError_t launch_affine_dequant(const AffineDequantParams& p, hipStream_t st);
 bool affine_gemv_fast_ok(const AffineGemvParams& p);
 hipError_t launch_affine_gemv(const AffineGemvParams& p, hipStream_t st);
+// two GEMVs (of one activation vector) as one launch when both take the
+// 4-bit fast path with the same scale dtype and geometry class, else two
+hipError_t launch_affine_gemv_pair(const AffineGemvParams& a, const AffineGemvParams& b, hipStream_t st);
 
 // ---------------------------------------------------------------- block pieces
 struct RmsNormParams {
