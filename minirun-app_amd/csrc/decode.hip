@@ -141,7 +141,7 @@ __device__ void validate_token(const int32_t* __restrict__ ind, int32_t n_idx, i
 }
 
 // ---------------------------------------------------------------------------
-// Role-split variant for head groups of HGS heads (32 or 64).  HGS/32 QK
+// Role-split variant for head groups of HGS heads (32, 48 or 64).  HGS/32 QK
 // waves score 32 heads each over all 32 rows of a sub-chunk as
 // S^T = K . Q^T on 32x32x16 MFMA: a lane owns one head, so its running max
 // and sum stay in the lane (one exchange between the wave halves), and each
@@ -779,6 +779,9 @@ hipError_t launch_ws(const DecodeParams& p, int grid, hipStream_t st) {
     if (p.hg_size == 64)
         hipLaunchKernelGGL((mla_decode_ws<DR, GATHER, PACKED, 64, true>), dim3(grid), dim3(WsShape<64, true>::THREADS), 0,
                            st, p);
+    else if (p.hg_size == 48)
+        hipLaunchKernelGGL((mla_decode_ws<DR, GATHER, PACKED, 48, true>), dim3(grid), dim3(WsShape<48, true>::THREADS), 0,
+                           st, p);
     else
         hipLaunchKernelGGL((mla_decode_ws<DR, GATHER, PACKED, 32, false>), dim3(grid), dim3(WsShape<32, false>::THREADS),
                            0, st, p);
@@ -815,7 +818,14 @@ hipError_t launch_validate_indices(const int32_t* indices, int32_t batch, int32_
 
 int validate_max_indices() { return VALIDATE_MAX_IDX; }
 
-int decode_head_group_size(int heads) { return heads > 32 ? 64 : 32; }
+// 32 heads for small layers, else 64, or 48 where that splits the heads
+// exactly and 64 would not (96 heads: two groups of 48 instead of two of 64
+// with a quarter of the MFMA work and partial records spent on padding)
+int decode_head_group_size(int heads) {
+    if (heads <= 32) return 32;
+    if (heads % 64 != 0 && heads % 48 == 0) return 48;
+    return 64;
+}
 
 hipError_t launch_mla_decode(const DecodeParams& p, const CombineParams& cp, bool split_only,
                              hipEvent_t const* events, hipStream_t st) {

@@ -103,7 +103,9 @@ def test_split_count_invariance(M, splits):
     check(host_f32(out)[0], ref, f"splits={splits}", scale_bar=2e-3)
 
 
-@pytest.mark.parametrize("H,N", [(1, 1), (5, 63), (33, 65), (128, 1000), (64, 64)])
+# 48, 96 and 144 heads run in head groups of 48 (no padding heads)
+@pytest.mark.parametrize("H,N", [(1, 1), (5, 63), (33, 65), (128, 1000), (64, 64), (48, 129), (96, 3000),
+                                 (144, 700)])
 def test_ragged_shapes(M, H, N):
     print(f"decode ragged H={H} N={N}", flush=True)
     import torch
@@ -149,6 +151,18 @@ def test_sparse_top2048_128k(M):
     check(host_f32(out), ref, "sparse-4x2048")
 
 
+def test_sparse_96_heads(M):
+    # the K3 layer's head count: two head groups of 48
+    print("sparse B=3 H=96 N=9000 K=1024", flush=True)
+    ql, qr, cache, idx = MI.sparse_inputs(3, 96, 9000, 1024, tag="s96")
+    idx = idx.copy()
+    idx[1, 5::11] = -1
+    st, ref = O.sparse_attention(ql, qr, cache, idx)
+    assert st == O.OK
+    out = run_sparse(M, ql, qr, cache, idx)
+    check(host_f32(out), ref, "sparse-96")
+
+
 def test_sparse_sentinels_sinks_and_empty(M):
     print("sparse sentinels/sinks/empty", flush=True)
     import torch
@@ -182,11 +196,12 @@ def test_sparse_all_indices_equals_dense(M):
     assert d < 4e-3, d
 
 
-def test_sparse_v4_form_no_rope(M):
-    print("sparse V4 form (512-wide rows, sinks)", flush=True)
+@pytest.mark.parametrize("H", [64, 96])
+def test_sparse_v4_form_no_rope(M, H):
+    print(f"sparse V4 form (512-wide rows, sinks) H={H}", flush=True)
     import torch
 
-    B, H, N, K = 2, 64, 3000, 640
+    B, N, K = 2, 3000, 640
     q = O.normal_bf16("v4.q", (B, H, 512))
     rows = O.normal_bf16("v4.rows", (N, 512), std=0.5)   # one cache shared by all tokens
     idx = np.stack([O.sparse_topk_indices(f"v4.i{b}", N, K, 128) for b in range(B)])
