@@ -117,6 +117,9 @@ struct TopkParams {
     int32_t slices;
     unsigned long long* cand;
     int32_t* slice_nan;
+    // one row: the kernel that writes the row's NaN flag also writes the
+    // device status (MR_NONFINITE or 0) here, with no status launch; else null
+    int32_t* status_direct;
 };
 
 // Workspace of a selection: per-row NaN flags, and for rows of more than

@@ -371,7 +371,10 @@ __global__ void __launch_bounds__(NT) topk_select_kernel(TopkParams p) {
             orow[i] = key >= visible ? -1 : p.offset + key;
         }
     }
-    if (tid == 0) p.nan_flags[row] = nan_seen;
+    if (tid == 0) {
+        p.nan_flags[row] = nan_seen;
+        if (p.status_direct) *p.status_direct = nan_seen ? 5 /* MR_NONFINITE */ : 0;
+    }
 }
 
 // One merge round over rows of sorted composite lists: list pair q of a row
@@ -421,6 +424,7 @@ __global__ void __launch_bounds__(256) topk_merge_kernel(TopkParams p, const uns
         int f = 0;
         for (int sl = 0; sl < p.slices; ++sl) f |= p.slice_nan[row * p.slices + sl];
         p.nan_flags[row] = f;
+        if (p.status_direct) *p.status_direct = f ? 5 /* MR_NONFINITE */ : 0;
     }
 }
 
@@ -452,6 +456,9 @@ size_t topk_workspace_bytes(int32_t rows, int32_t cols, int32_t selected) {
 hipError_t launch_topk_select(const TopkParams& p0, void* workspace, int32_t* status, hipStream_t st) {
     TopkParams p = p0;
     p.slices = 1;
+    // a single row's status comes from the kernel that flags its NaN (the
+    // selection, or the last merge round), not from a launch of its own
+    p.status_direct = p.rows == 1 ? status : nullptr;
     // keys per thread: the row's ranked keys in registers
     if (p.available <= 256 * 4) {
         hipLaunchKernelGGL((topk_select_kernel<256, 4>), dim3((unsigned)p.rows), dim3(256), 0, st, p);
@@ -485,7 +492,7 @@ hipError_t launch_topk_select(const TopkParams& p0, void* workspace, int32_t* st
         }
     }
     hipError_t e = hipGetLastError();
-    if (e == hipSuccess && status) {
+    if (e == hipSuccess && status && !p.status_direct) {
         hipLaunchKernelGGL(topk_status_kernel, dim3(1), dim3(256), 0, st, p.nan_flags, p.rows, status);
         e = hipGetLastError();
     }
