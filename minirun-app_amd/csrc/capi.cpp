@@ -125,6 +125,15 @@ DecodePlan plan_decode(const mr_mla_decode_args* a) {
     return pl;
 }
 
+}  // namespace
+
+mrc::DecodePartials mrc::decode_partials(const mr_mla_decode_args* a) {
+    const DecodePlan pl = plan_decode(a);
+    return DecodePartials{pl.splits, pl.h_pad, pl.ws_f32, pl.o_bytes};
+}
+
+namespace {
+
 mr_status check_decode(const mr_mla_decode_args* a) {
     if (!a) return fail(MR_INVALID_ARGUMENT, "mr_mla_decode: args is NULL");
     if (a->batch <= 0 || a->heads <= 0)

@@ -716,6 +716,21 @@ mr_status mr_mla_unabsorb_values(const void* ctx, int64_t ctx_head_stride, int32
 // ---------------------------------------------------------------- decode block
 namespace {
 
+// The split merge and W_UV run as one launch (mla_combine_unabsorb) for a
+// 4-bit group-64 affine kv_b with bf16 scales and biases, or a dense bf16
+// one, 16-byte aligned, with at most 128 value rows per head (a multiple of
+// 64); other weights take the decode's own combine and the grouped GEMV.
+bool unabsorb_fuses(const mr_projection* kv_b, int32_t v_dim) {
+    if (v_dim % 64 != 0 || v_dim > mr::UNABSORB_MAX_V) return false;
+    if (kv_b->kind == MR_PROJ_AFFINE) {
+        const mr_affine_weight* w = &kv_b->affine;
+        return w->bits == 4 && w->group == 64 && w->scale_dtype == MR_BF16 && aligned16(w->packed) &&
+               aligned16(w->scales) && aligned16(w->biases);
+    }
+    const mr_dense_weight* w = &kv_b->dense;
+    return kv_b->kind == MR_PROJ_DENSE && w->dtype == MR_BF16 && aligned16(w->weight) && w->row_stride % 8 == 0;
+}
+
 struct BlockLayout {
     size_t h, h_kv, q_lora, q_lora_n, q, q_lat, kv, ctx, attn, gate, stage, dec, total;
     mr_mla_decode_args dec_args;
@@ -885,10 +900,40 @@ mr_status mr_mla_decode_block(const mr_mla_block_args* a, void* stream) {
     d.out = ctx;
     d.workspace = W + L.dec;
     d.workspace_bytes = L.total - L.dec;
-    if ((st = mr_mla_decode(&d, stream)) != MR_OK) return st;
-    if ((st = mr_mla_unabsorb_values(ctx, a->kv_rank, a->heads, a->qk_nope_dim, a->v_head_dim, &a->kv_b, attn, MR_BF16,
-                                     stream)) != MR_OK)
-        return st;
+    if (unabsorb_fuses(&a->kv_b, a->v_head_dim)) {
+        // the split kernel alone, then one launch that merges the splits of
+        // each head and un-absorbs them (W_UV) into the o_proj input
+        d.flags |= MR_DECODE_SPLIT_ONLY;
+        if ((st = mr_mla_decode(&d, stream)) != MR_OK) return st;
+        const mrc::DecodePartials dp = mrc::decode_partials(&d);
+        mr::CombineUnabsorbParams u{};
+        u.ws_o = d.workspace;
+        u.ws_f32 = dp.ws_f32;
+        u.ws_ml = (const float*)((const char*)d.workspace + dp.ml_offset);
+        u.splits = dp.splits;
+        u.h_pad = dp.h_pad;
+        u.heads = a->heads;
+        u.affine = a->kv_b.kind == MR_PROJ_AFFINE;
+        if (u.affine) {
+            u.packed = a->kv_b.affine.packed;
+            u.scales = (const uint16_t*)a->kv_b.affine.scales;
+            u.biases = (const uint16_t*)a->kv_b.affine.biases;
+        } else {
+            u.w = (const uint16_t*)a->kv_b.dense.weight;
+            u.w_rs = a->kv_b.dense.row_stride;
+        }
+        u.row_step = a->qk_nope_dim + a->v_head_dim;
+        u.row0 = a->qk_nope_dim;
+        u.v_dim = a->v_head_dim;
+        u.out = (uint16_t*)attn;
+        const hipError_t e = mr::launch_combine_unabsorb(u, (hipStream_t)stream);
+        if (e != hipSuccess) return hip_fail(e, "mla block: merge + W_UV launch");
+    } else {
+        if ((st = mr_mla_decode(&d, stream)) != MR_OK) return st;
+        if ((st = mr_mla_unabsorb_values(ctx, a->kv_rank, a->heads, a->qk_nope_dim, a->v_head_dim, &a->kv_b, attn,
+                                         MR_BF16, stream)) != MR_OK)
+            return st;
+    }
     return block_proj(attn, hv, &a->o_proj, a->out, nullptr, nd, a->eps, gated ? gate : nullptr, stage, stream);
 }
 

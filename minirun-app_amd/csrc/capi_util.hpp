@@ -17,4 +17,14 @@ inline size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 const char* dtype_name(mr_dtype d);
 int cu_count();  // compute units of the current device (cached per device)
 
+// Where mr_mla_decode leaves its split partials in the workspace (the layout
+// its combine reads): records [batch][h_pad][splits][512] at offset 0, bf16
+// (f32 when ws_f32), then (m, l) pairs at ml_offset.
+struct DecodePartials {
+    int32_t splits, h_pad;
+    bool ws_f32;
+    size_t ml_offset;
+};
+DecodePartials decode_partials(const mr_mla_decode_args* a);
+
 }  // namespace mrc

@@ -774,6 +774,196 @@ __global__ void __launch_bounds__(COMBINE_THREADS) mla_combine(CombineParams p) 
     }
 }
 
+// The split merge of one head fused with its value un-absorption (the decode
+// block's W_UV stage).  512 threads per head: waves 0-3 merge the splits as
+// mla_combine does (lane l of wave w takes 16-byte chunk l of the records of
+// splits w, w+4, ..., all in flight at once) while waves 4-7 copy the head's
+// W_UV rows into LDS by DMA (a dense bf16 row is one 1 KB load; the 4-bit
+// rows, scales and biases are contiguous KB blocks) once the records have
+// been requested (a CU keeps a bounded number of requests in flight, and the
+// records are needed first).  The context, rounded to bf16 as mla_combine's
+// output is, goes to LDS, and all eight waves then form the head's v_dim
+// outputs from LDS, 8 lanes per row.  (Spreading a head over its column
+// blocks, with a second launch adding the blocks' partial sums, measured
+// slower: that launch alone took 4.3 us.)
+constexpr int CU_PF = 32;  // split records in flight per lane (bf16 records)
+
+template <bool F32, bool AFF>
+__global__ void __launch_bounds__(512) mla_combine_unabsorb(CombineUnabsorbParams p) {
+    extern __shared__ __attribute__((aligned(1024))) char wlds[];  // the head's W_UV rows
+    __shared__ float wgt[MAX_COMBINE_SPLITS];
+    __shared__ float red_m[4], red_l[4];
+    __shared__ __attribute__((aligned(16))) float ctx_part[4][R];
+    __shared__ __attribute__((aligned(16))) float ctx_s[R];
+    __shared__ float gsum[8];
+    const int h = blockIdx.x;
+    const int tid = threadIdx.x, w = tid >> 6, l = tid & 63;
+    const int V = p.v_dim;
+    const int64_t row_base = (int64_t)h * p.row_step + p.row0;
+    const int64_t rec0 = (int64_t)h * p.splits;  // batch 1: the splits of head h are contiguous
+    constexpr int RB = R * (F32 ? 4 : 2);        // bytes per record
+    constexpr int PF = F32 ? CU_PF / 2 : CU_PF;  // splits per batch (F32: two loads per split)
+
+    if (w >= 4) {
+        // ------------------------------------------------ DMA waves
+        lds_barrier();  // 1: max
+        lds_barrier();  // 2: sum
+        const int dw = w - 4;
+        if (AFF) {
+            // V rows of 256 packed bytes, then V x 16 bytes of scales and of
+            // biases (8 groups of 64 inputs per row), all contiguous
+            const char* pk = (const char*)(p.packed + row_base * (R / 8));
+            const char* sc = (const char*)(p.scales + row_base * (R / 64));
+            const char* bi = (const char*)(p.biases + row_base * (R / 64));
+            const int npk = V / 4, nsb = V / 64;  // KB blocks
+            for (int k = dw; k < npk + 2 * nsb; k += 4) {
+                const char* src = k < npk ? pk + 1024 * k : (k < npk + nsb ? sc + 1024 * (k - npk) : bi + 1024 * (k - npk - nsb));
+                dma16(src + 16 * l, wlds + 1024 * k);
+            }
+        } else {
+            for (int j = dw; j < V; j += 4) dma16(p.w + (row_base + j) * p.w_rs + 8 * l, wlds + 1024 * j);
+        }
+        lds_barrier();  // 3: per-wave context
+        wait_vmcnt<0>();
+        lds_barrier();  // 4: context and weights in LDS
+    } else {
+        // ------------------------------------------------ merge waves
+        constexpr int MLK = MAX_COMBINE_SPLITS / 256;
+        float ml_m[MLK], ml_l[MLK];
+        float M = NEG_INF;
+        // every load is issued unconditionally (indices clamped to the last
+        // split, the extra values weighted out), so the compiler's waits
+        // count exactly and the (m, l) loads do not wait for the records
+#pragma unroll
+        for (int k = 0; k < MLK; ++k) {
+            const int s = tid + 256 * k;
+            const f32x2 ml = *(const f32x2*)(p.ws_ml + (rec0 + min(s, p.splits - 1)) * 2);
+            ml_m[k] = s < p.splits ? ml[0] : NEG_INF;
+            ml_l[k] = s < p.splits ? ml[1] : 0.f;
+        }
+        const char* base = (const char*)p.ws_o + rec0 * RB + 16 * l;
+        u32x4 x[PF][F32 ? 2 : 1];
+        auto fetch = [&](int s0) {
+#pragma unroll
+            for (int k = 0; k < PF; ++k) {
+                const int s = min(s0 + 4 * k, p.splits - 1);
+#pragma unroll
+                for (int c = 0; c < (F32 ? 2 : 1); ++c) x[k][c] = *(const u32x4*)(base + (int64_t)s * RB + 1024 * c);
+            }
+        };
+        fetch(w);
+#pragma unroll
+        for (int k = 0; k < MLK; ++k)
+            if (ml_l[k] > 0.f) M = fmaxf(M, ml_m[k]);
+        M = wave_max(M);
+        if (l == 0) red_m[w] = M;
+        lds_barrier();  // 1
+        M = fmaxf(fmaxf(red_m[0], red_m[1]), fmaxf(red_m[2], red_m[3]));
+        float L = 0.f;
+#pragma unroll
+        for (int k = 0; k < MLK; ++k) {
+            const int s = tid + 256 * k;
+            if (s < p.splits) {
+                const float wv = ml_l[k] > 0.f ? ml_l[k] * exp2f(ml_m[k] - M) : 0.f;
+                wgt[s] = wv;
+                L += wv;
+            }
+        }
+        L = wave_sum(L);
+        if (l == 0) red_l[w] = L;
+        lds_barrier();  // 2
+        L = (red_l[0] + red_l[1]) + (red_l[2] + red_l[3]);
+        constexpr int VPL = 8;  // values per lane: 8 bf16, or 2 x 4 f32
+        float acc[VPL];
+#pragma unroll
+        for (int v = 0; v < VPL; ++v) acc[v] = 0.f;
+        for (int s0 = w;; s0 += 4 * PF) {
+#pragma unroll
+            for (int k = 0; k < PF; ++k) {
+                const int s = s0 + 4 * k;
+                const float wv = s < p.splits ? wgt[s] : 0.f;
+                if (wv == 0.f) continue;  // an empty split is selected out, never multiplied in
+#pragma unroll
+                for (int v = 0; v < VPL; ++v) {
+                    float xv;
+                    if (F32)
+                        xv = __uint_as_float(x[k][v >> 2][v & 3]);
+                    else
+                        xv = __uint_as_float(v & 1 ? x[k][0][v >> 1] & 0xffff0000u : x[k][0][v >> 1] << 16);
+                    acc[v] += wv * xv;
+                }
+            }
+            if (s0 + 4 * PF >= p.splits) break;
+            fetch(s0 + 4 * PF);
+        }
+        // columns of the lane: bf16 8l .. 8l+7; f32 4l .. 4l+3 and 256+4l .. +3
+        if (F32) {
+            *(f32x4*)(&ctx_part[w][4 * l]) = f32x4{acc[0], acc[1], acc[2], acc[3]};
+            *(f32x4*)(&ctx_part[w][256 + 4 * l]) = f32x4{acc[4], acc[5], acc[6], acc[7]};
+        } else {
+            *(f32x4*)(&ctx_part[w][8 * l]) = f32x4{acc[0], acc[1], acc[2], acc[3]};
+            *(f32x4*)(&ctx_part[w][8 * l + 4]) = f32x4{acc[4], acc[5], acc[6], acc[7]};
+        }
+        lds_barrier();  // 3
+        // the context, bf16-rounded as mla_combine writes it: thread t holds
+        // columns 2t, 2t+1; the 4-bit path also needs each group's sum
+        const float sc = M != NEG_INF ? 1.f / L : 0.f;
+        float cv[2];
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+            const int c = 2 * tid + e;
+            const float o = ((ctx_part[0][c] + ctx_part[1][c]) + (ctx_part[2][c] + ctx_part[3][c])) * sc;
+            cv[e] = bf16_bits_to_f32(f32_to_bf16_bits(o));
+            ctx_s[c] = cv[e];
+        }
+        if (AFF) {
+            const float gs = group_sum(cv[0] + cv[1], 32);  // 32 threads = one group of 64 columns
+            if ((tid & 31) == 0) gsum[tid >> 5] = gs;
+        }
+        lds_barrier();  // 4
+    }
+
+    // ---------------------------------------------------- W_UV rows, 8 lanes per row
+    const int i = l & 7;
+    for (int r = 8 * w + (l >> 3); r < V; r += 64) {
+        float y = 0.f;
+        if (AFF) {
+            // lane i takes group i of row r: 8 packed words, its scale and bias
+            const u32x4 q0 = *(const u32x4*)(wlds + r * 256 + 32 * i);
+            const u32x4 q1 = *(const u32x4*)(wlds + r * 256 + 32 * i + 16);
+            const uint16_t* sc = (const uint16_t*)(wlds + V * 256);
+            const uint16_t* bi = (const uint16_t*)(wlds + V * 256 + V * 16);
+            const float s = bf16_bits_to_f32(sc[8 * r + i]), b = bf16_bits_to_f32(bi[8 * r + i]);
+            const uint32_t wd[8] = {q0[0], q0[1], q0[2], q0[3], q1[0], q1[1], q1[2], q1[3]};
+            float dot = 0.f;
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+                const f32x4 c0 = *(const f32x4*)(&ctx_s[64 * i + 8 * k]);
+                const f32x4 c1 = *(const f32x4*)(&ctx_s[64 * i + 8 * k + 4]);
+#pragma unroll
+                for (int n = 0; n < 8; ++n) dot += (float)((wd[k] >> (4 * n)) & 15u) * (n < 4 ? c0[n] : c1[n - 4]);
+            }
+            y = s * dot + b * gsum[i];
+        } else {
+            // lane i takes 16-byte chunks 8c + i of row r
+#pragma unroll
+            for (int c = 0; c < 8; ++c) {
+                const int k = 8 * c + i;
+                const u32x4 wv = *(const u32x4*)(wlds + r * 1024 + 16 * k);
+                const f32x4 c0 = *(const f32x4*)(&ctx_s[8 * k]);
+                const f32x4 c1 = *(const f32x4*)(&ctx_s[8 * k + 4]);
+#pragma unroll
+                for (int n = 0; n < 4; ++n) {
+                    y += __uint_as_float(wv[n] << 16) * (n < 2 ? c0[2 * n] : c1[2 * n - 4]);
+                    y += __uint_as_float(wv[n] & 0xffff0000u) * (n < 2 ? c0[2 * n + 1] : c1[2 * n - 3]);
+                }
+            }
+        }
+        y = group_sum(y, 8);
+        if (i == 0) p.out[(int64_t)h * V + r] = f32_to_bf16_bits(y);
+    }
+}
+
 template <int DR, bool GATHER, bool PACKED>
 hipError_t launch_ws(const DecodeParams& p, int grid, hipStream_t st) {
     if (p.hg_size == 64)
@@ -825,6 +1015,31 @@ int decode_head_group_size(int heads) {
     if (heads <= 32) return 32;
     if (heads % 64 != 0 && heads % 48 == 0) return 48;
     return 64;
+}
+
+hipError_t launch_combine_unabsorb(const CombineUnabsorbParams& p, hipStream_t st) {
+    const size_t lds = p.affine ? size_t(p.v_dim) * (256 + 2 * 16) : size_t(p.v_dim) * 1024;
+    auto go = [&](const void* kern, auto launch) {
+        if (lds > 65536) {
+            const hipError_t e = hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+            if (e != hipSuccess) return e;
+        }
+        launch();
+        return hipGetLastError();
+    };
+    const dim3 grid((unsigned)p.heads), block(512);
+    if (p.affine) {
+        if (p.ws_f32)
+            return go((const void*)mla_combine_unabsorb<true, true>,
+                      [&] { hipLaunchKernelGGL((mla_combine_unabsorb<true, true>), grid, block, lds, st, p); });
+        return go((const void*)mla_combine_unabsorb<false, true>,
+                  [&] { hipLaunchKernelGGL((mla_combine_unabsorb<false, true>), grid, block, lds, st, p); });
+    }
+    if (p.ws_f32)
+        return go((const void*)mla_combine_unabsorb<true, false>,
+                  [&] { hipLaunchKernelGGL((mla_combine_unabsorb<true, false>), grid, block, lds, st, p); });
+    return go((const void*)mla_combine_unabsorb<false, false>,
+              [&] { hipLaunchKernelGGL((mla_combine_unabsorb<false, false>), grid, block, lds, st, p); });
 }
 
 hipError_t launch_mla_decode(const DecodeParams& p, const CombineParams& cp, bool split_only,

@@ -50,6 +50,30 @@ struct CombineParams {
     int32_t out_f32;
 };
 
+// The split merge fused with the value un-absorption of the decode block
+// (MLA.swift:198-206): per head h, ctx = bf16(sum_s w_s O_s / sum_s w_s)
+// as mla_combine forms it (no sinks), then out[h][j] = bf16(W_UV[h][j] . ctx)
+// for j < v_dim, where W_UV[h][j] is row h * row_step + row0 + j of kv_b.
+// The weight is a 4-bit group-64 affine one with bf16 scales and biases
+// (rows of 512 inputs contiguous, as MLX stores them) or a dense bf16 one
+// (rows 16-byte aligned at stride w_rs).  Batch 1, one workgroup per head.
+struct CombineUnabsorbParams {
+    const void* ws_o;  // split partials, bf16 (or f32 when ws_f32)
+    int32_t ws_f32;
+    const float* ws_ml;
+    int32_t splits, h_pad, heads;
+    int32_t affine;  // 1: 4-bit affine, 0: dense bf16
+    const uint32_t* packed;
+    const uint16_t* scales;
+    const uint16_t* biases;
+    const uint16_t* w;
+    int64_t w_rs;
+    int32_t row_step, row0, v_dim;
+    uint16_t* out;  // [heads][v_dim] bf16
+};
+constexpr int UNABSORB_MAX_V = 128;  // value rows of one head the fused kernel stages
+hipError_t launch_combine_unabsorb(const CombineUnabsorbParams& p, hipStream_t st);
+
 // Heads per decode workgroup: 64 when there are more than 32 heads, else 32.
 int decode_head_group_size(int heads);
 // Index checks (DeepSeekV4Attention.swift:884-895), one workgroup per token:
