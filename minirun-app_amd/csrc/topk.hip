@@ -73,6 +73,10 @@ __device__ __forceinline__ uint32_t block_scan_incl(uint32_t v, uint32_t* sh) {
 
 constexpr int TK_BINS = 2048;
 constexpr unsigned long long TK_NONE = ~0ull;  // padding: past every composite
+// Rows ranked by 1024 threads take the compacted path when the first digit's
+// cut bin holds at most TK_CAND keys: the keys above the cut go straight to
+// the selected list and only the cut bin's keys take the remaining digits.
+constexpr int TK_CAND = 4096;
 
 template <int NT, int KPT>
 __global__ void __launch_bounds__(NT) topk_select_kernel(TopkParams p) {
@@ -82,6 +86,9 @@ __global__ void __launch_bounds__(NT) topk_select_kernel(TopkParams p) {
     __shared__ uint32_t scan_sh[NT / 64];
     __shared__ uint32_t pick[3];  // bin, count before it, count in it
     __shared__ unsigned long long comp[TOPK_MAX];
+    constexpr bool FAST = NT == 1024;  // the compacted path (four candidates per thread)
+    constexpr int CPT = FAST ? TK_CAND / NT : 1;
+    __shared__ unsigned long long cand[FAST ? TK_CAND : 1];
     __shared__ int nan_seen;
 
     const int row = blockIdx.x;
@@ -120,6 +127,8 @@ __global__ void __launch_bounds__(NT) topk_select_kernel(TopkParams p) {
     // 15..8, 7..0 (all in 32-bit arithmetic)
     uint32_t dimg = 0, dkey = 0;
     uint32_t remaining = (uint32_t)k;  // rank of D among the still-matching composites
+    uint32_t cut_count = 0;            // keys in the first digit's cut bin
+    bool fast = false;
     for (int i = tid; i < TK_BINS; i += NT) hist[0][i] = 0;
     __syncthreads();
 #pragma unroll 1
@@ -188,6 +197,12 @@ __global__ void __launch_bounds__(NT) topk_select_kernel(TopkParams p) {
             dkey |= pick[0] << sh;
         remaining -= pick[1];
         const uint32_t in_bin = pick[2];
+        // few keys share the cut bin: rank them apart from the rest
+        if (FAST && pass == 0 && in_bin <= (uint32_t)TK_CAND) {
+            cut_count = in_bin;
+            fast = true;
+            break;
+        }
         // image complete and every key with that image is taken: D's key
         // part is past them all (ties need the key digits)
         if (pass == 2 && remaining == in_bin) {
@@ -197,179 +212,261 @@ __global__ void __launch_bounds__(NT) topk_select_kernel(TopkParams p) {
     }
     // exactly k composites are <= D
 
-    // 2. collection: each thread's composites <= D at offsets from one scan
-    auto le_d = [&](int j) {
-        const uint32_t key = (uint32_t)(NT * j + tid);
-        return valid(j) && (img[j] < dimg || (img[j] == dimg && key <= dkey));
-    };
-    uint32_t cnt = 0;
+    auto composite = [&](int j) { return ((unsigned long long)img[j] << 16) | (uint32_t)(NT * j + tid); };
+    if (FAST && fast) {
+        // 2a. keys of bins above the cut bin are all taken: to comp; keys of
+        // the cut bin to cand.  One scan places both (counts packed 16:16).
+        const uint32_t top = dimg >> 21;
+        uint32_t ns = 0, nc = 0;
 #pragma unroll
-    for (int j = 0; j < KPT; ++j) cnt += le_d(j);
-    uint32_t pos = block_scan_incl<NT>(cnt, scan_sh) - cnt;
-#pragma unroll
-    for (int j = 0; j < KPT; ++j)
-        if (le_d(j)) {
-            if (pos < TOPK_MAX) comp[pos] = ((unsigned long long)img[j] << 16) | (uint32_t)(NT * j + tid);
-            ++pos;
+        for (int j = 0; j < KPT; ++j) {
+            const uint32_t b = img[j] >> 21;
+            ns += valid(j) && b < top;
+            nc += valid(j) && b == top;
         }
+        const uint32_t pk = (ns << 16) | nc;
+        const uint32_t ex = block_scan_incl<NT>(pk, scan_sh) - pk;
+        uint32_t ps = ex >> 16, pc = ex & 0xffffu;
+#pragma unroll
+        for (int j = 0; j < KPT; ++j) {
+            const uint32_t b = img[j] >> 21;
+            if (valid(j) && b < top) comp[ps++] = composite(j);
+            if (valid(j) && b == top) cand[pc++] = composite(j);
+        }
+        __syncthreads();
+        const uint32_t before = (uint32_t)k - remaining;
+        // 2b. the remaining-th smallest candidate: 8-bit digits of composite
+        // bits 36..0 (image bits 20..0, then the key), 256-bin histograms
+        unsigned long long cv[CPT];
+#pragma unroll
+        for (int i = 0; i < CPT; ++i) {
+            const int idx = tid + NT * i;
+            cv[i] = idx < (int)cut_count ? cand[idx] : TK_NONE;
+        }
+        unsigned long long dacc = (unsigned long long)top << 37;
+        unsigned long long dsel = dacc | ((1ull << 37) - 1ull);  // the whole bin, unless a digit cuts it
+        if (remaining != cut_count) {
+#pragma unroll 1
+            for (int q = 0; q < 5; ++q) {
+                const int sh = q == 0 ? 29 : q == 1 ? 21 : q == 2 ? 16 : q == 3 ? 8 : 0;
+                const int wd = q == 2 ? 5 : 8;
+                uint32_t* hc = hist[(q + 1) & 1];  // hist[1] was cleared during the first pass
+                if (tid < 256) hist[q & 1][tid] = 0;  // the next digit's
+#pragma unroll
+                for (int i = 0; i < CPT; ++i)
+                    if (cv[i] != TK_NONE && ((cv[i] ^ dacc) >> (sh + wd)) == 0ull)
+                        atomicAdd(&hc[(uint32_t)(cv[i] >> sh) & ((1u << wd) - 1u)], 1u);
+                __syncthreads();
+                if (tid < 64) {  // lane l sums bins 4l .. 4l+3; the crossing lane walks them
+                    const u32x4 h4 = *(const u32x4*)(hc + 4 * tid);
+                    const uint32_t tot = (h4[0] + h4[1]) + (h4[2] + h4[3]);
+                    const uint32_t incl = wave_scan_incl(tot);
+                    uint32_t bef = incl - tot;
+                    if (bef < remaining && remaining <= incl) {
+                        int b = 0;
+                        uint32_t cb = h4[0];
+                        if (bef + cb < remaining) { bef += cb; b = 1; cb = h4[1]; }
+                        if (b == 1 && bef + cb < remaining) { bef += cb; b = 2; cb = h4[2]; }
+                        if (b == 2 && bef + cb < remaining) { bef += cb; b = 3; cb = h4[3]; }
+                        pick[0] = (uint32_t)(4 * tid + b);
+                        pick[1] = bef;
+                        pick[2] = cb;
+                    }
+                }
+                __syncthreads();
+                dacc |= (unsigned long long)pick[0] << sh;
+                remaining -= pick[1];
+                if (remaining == pick[2]) {  // every candidate with this prefix is taken
+                    dsel = dacc | ((1ull << sh) - 1ull);
+                    break;
+                }
+            }
+        }
+        // 2c. the candidates <= dsel (exactly the remaining ones) after the taken keys
+        uint32_t cnt = 0;
+#pragma unroll
+        for (int i = 0; i < CPT; ++i) cnt += cv[i] <= dsel;
+        uint32_t pos = before + block_scan_incl<NT>(cnt, scan_sh) - cnt;
+#pragma unroll
+        for (int i = 0; i < CPT; ++i)
+            if (cv[i] <= dsel) comp[pos++] = cv[i];
+    } else {
+        // 2. collection: each thread's composites <= D at offsets from one scan
+        auto le_d = [&](int j) {
+            const uint32_t key = (uint32_t)(NT * j + tid);
+            return valid(j) && (img[j] < dimg || (img[j] == dimg && key <= dkey));
+        };
+        uint32_t cnt = 0;
+#pragma unroll
+        for (int j = 0; j < KPT; ++j) cnt += le_d(j);
+        uint32_t pos = block_scan_incl<NT>(cnt, scan_sh) - cnt;
+#pragma unroll
+        for (int j = 0; j < KPT; ++j)
+            if (le_d(j)) {
+                if (pos < TOPK_MAX) comp[pos] = composite(j);
+                ++pos;
+            }
+    }
     // pad to a power of two (at least 4) for the sort
     int npow = 4;
     while (npow < k) npow <<= 1;
     for (int i = k + tid; i < npow; i += NT) comp[i] = TK_NONE;
     __syncthreads();
 
-    // 3. sort, ascending.  Thread t holds elements 4t .. 4t+3 in registers.
-    // Each wave sorts its 256 elements (a bitonic network whose lane
-    // exchanges have constant distances), then runs of 256, 512, ... merge
-    // pairwise through LDS: each output position finds its split by a
-    // merge-path binary search (the composites are distinct).
-    constexpr int EPT = 4;
-    const bool act = EPT * tid < npow;
+    // 3. sort, ascending.  Thread t holds elements EPT t .. EPT t + EPT-1 in
+    // registers (EPT = 2 when the padded count fits 2 per thread, so every
+    // wave works; else 4).  Each wave sorts its 64 EPT elements (a bitonic
+    // network whose lane exchanges have constant distances), then runs of
+    // 64 EPT, 128 EPT, ... merge pairwise through LDS: each output position
+    // finds its split by a merge-path binary search (the composites are
+    // distinct).  The sorted keys go out as offsets (or, per slice, as 64-bit
+    // composites for the merge rounds).
     const int lane = tid & 63;
-    unsigned long long x[EPT];
+    auto sort_and_emit = [&](auto ept_tag) {
+        constexpr int EPT = decltype(ept_tag)::value;
+        const bool act = EPT * tid < npow;
+        unsigned long long x[EPT];
 #pragma unroll
-    for (int e = 0; e < EPT; ++e) x[e] = act ? comp[EPT * tid + e] : TK_NONE;
-    auto cswap = [&](unsigned long long& lo, unsigned long long& hi, bool up) {
-        // lo sits at the lower index: ascending blocks keep the smaller there
-        if ((lo > hi) == up) {
-            const unsigned long long t = lo;
-            lo = hi;
-            hi = t;
-        }
-    };
-    auto xchg = [&](unsigned long long v, auto ld_tag) -> unsigned long long {
-        constexpr int LD = decltype(ld_tag)::value;
-        const uint32_t lo = (uint32_t)v, hi = (uint32_t)(v >> 32);
-        uint32_t rlo, rhi;
-        if constexpr (LD == 32) {
-            const auto a = __builtin_amdgcn_permlane32_swap(lo, lo, false, false);
-            const auto c = __builtin_amdgcn_permlane32_swap(hi, hi, false, false);
-            rlo = (lane & 32) ? a[0] : a[1];
-            rhi = (lane & 32) ? c[0] : c[1];
-        } else if constexpr (LD == 16) {
-            const auto a = __builtin_amdgcn_permlane16_swap(lo, lo, false, false);
-            const auto c = __builtin_amdgcn_permlane16_swap(hi, hi, false, false);
-            rlo = (lane & 16) ? a[0] : a[1];
-            rhi = (lane & 16) ? c[0] : c[1];
-        } else {
-            rlo = __shfl_xor(lo, LD);
-            rhi = __shfl_xor(hi, LD);
-        }
-        return ((unsigned long long)rhi << 32) | rlo;
-    };
-    // one bitonic stage with lane distance LD (element stride 4 LD); blocks
-    // of `size` elements, ascending unless the block index bit says
-    // otherwise (the last size of the wave sort is all ascending)
-    auto lane_stage = [&](auto ld_tag, int size, bool all_up) {
-        constexpr int LD = decltype(ld_tag)::value;
-        const bool lower = (lane & LD) == 0;
-#pragma unroll
-        for (int e = 0; e < EPT; ++e) {
-            const unsigned long long y = xchg(x[e], ld_tag);
+        for (int e = 0; e < EPT; ++e) x[e] = act ? comp[EPT * tid + e] : TK_NONE;
+        auto cswap = [&](unsigned long long& lo, unsigned long long& hi, bool up) {
+            // lo sits at the lower index: ascending blocks keep the smaller there
+            if ((lo > hi) == up) {
+                const unsigned long long t = lo;
+                lo = hi;
+                hi = t;
+            }
+        };
+        auto xchg = [&](unsigned long long v, auto ld_tag) -> unsigned long long {
+            constexpr int LD = decltype(ld_tag)::value;
+            const uint32_t lo = (uint32_t)v, hi = (uint32_t)(v >> 32);
+            uint32_t rlo, rhi;
+            if constexpr (LD == 32) {
+                const auto a = __builtin_amdgcn_permlane32_swap(lo, lo, false, false);
+                const auto c = __builtin_amdgcn_permlane32_swap(hi, hi, false, false);
+                rlo = (lane & 32) ? a[0] : a[1];
+                rhi = (lane & 32) ? c[0] : c[1];
+            } else if constexpr (LD == 16) {
+                const auto a = __builtin_amdgcn_permlane16_swap(lo, lo, false, false);
+                const auto c = __builtin_amdgcn_permlane16_swap(hi, hi, false, false);
+                rlo = (lane & 16) ? a[0] : a[1];
+                rhi = (lane & 16) ? c[0] : c[1];
+            } else {
+                rlo = __shfl_xor(lo, LD);
+                rhi = __shfl_xor(hi, LD);
+            }
+            return ((unsigned long long)rhi << 32) | rlo;
+        };
+        // one bitonic stage with lane distance LD (element stride EPT LD);
+        // blocks of `size` elements, ascending unless the block index bit
+        // says otherwise (the last size of the wave sort is all ascending)
+        auto lane_stage = [&](auto ld_tag, int size, bool all_up) {
+            constexpr int LD = decltype(ld_tag)::value;
+            const bool lower = (lane & LD) == 0;
             const bool up = all_up || ((EPT * tid) & size) == 0;
             const bool take_min = lower == up;
-            x[e] = take_min ? (x[e] < y ? x[e] : y) : (x[e] > y ? x[e] : y);
-        }
-    };
-    auto thread_stages = [&](int size, bool all_up) {  // element strides 2 and 1
-        const bool up0 = all_up || ((EPT * tid) & size) == 0;
-        const bool up2 = all_up || ((EPT * tid + 2) & size) == 0;
-        if (size >= 4) {
-            cswap(x[0], x[2], up0);
-            cswap(x[1], x[3], up0);
-        }
-        cswap(x[0], x[1], up0);
-        cswap(x[2], x[3], up2);
-    };
-    using L1 = std::integral_constant<int, 1>;
-    using L2 = std::integral_constant<int, 2>;
-    using L4 = std::integral_constant<int, 4>;
-    using L8 = std::integral_constant<int, 8>;
-    using L16 = std::integral_constant<int, 16>;
-    using L32 = std::integral_constant<int, 32>;
-    {
-        const int wsize = min(npow, 256);  // elements each wave sorts
-        // size 2, 4
-        thread_stages(2, wsize == 2);
-        if (wsize >= 4) thread_stages(4, wsize == 4);
-        if (wsize >= 8) { lane_stage(L1{}, 8, wsize == 8); thread_stages(8, wsize == 8); }
-        if (wsize >= 16) {
-            lane_stage(L2{}, 16, wsize == 16); lane_stage(L1{}, 16, wsize == 16); thread_stages(16, wsize == 16);
-        }
-        if (wsize >= 32) {
-            lane_stage(L4{}, 32, wsize == 32); lane_stage(L2{}, 32, wsize == 32); lane_stage(L1{}, 32, wsize == 32);
-            thread_stages(32, wsize == 32);
-        }
-        if (wsize >= 64) {
-            lane_stage(L8{}, 64, wsize == 64); lane_stage(L4{}, 64, wsize == 64); lane_stage(L2{}, 64, wsize == 64);
-            lane_stage(L1{}, 64, wsize == 64); thread_stages(64, wsize == 64);
-        }
-        if (wsize >= 128) {
-            lane_stage(L16{}, 128, wsize == 128); lane_stage(L8{}, 128, wsize == 128);
-            lane_stage(L4{}, 128, wsize == 128); lane_stage(L2{}, 128, wsize == 128);
-            lane_stage(L1{}, 128, wsize == 128); thread_stages(128, wsize == 128);
-        }
-        if (wsize >= 256) {
-            lane_stage(L32{}, 256, true); lane_stage(L16{}, 256, true); lane_stage(L8{}, 256, true);
-            lane_stage(L4{}, 256, true); lane_stage(L2{}, 256, true); lane_stage(L1{}, 256, true);
-            thread_stages(256, true);
-        }
-    }
-    // merge sorted runs of `run` elements pairwise, in place in LDS
-    for (int run = 256; run < npow; run <<= 1) {
-        __syncthreads();  // readers of the last round are done
-        if (act) {
-#pragma unroll
-            for (int e = 0; e < EPT; ++e) comp[EPT * tid + e] = x[e];
-        }
-        __syncthreads();
-        if (act) {
-            const int q0 = EPT * tid;
-            const int base = q0 & ~(2 * run - 1);  // pair start
-            const unsigned long long* A = comp + base;
-            const unsigned long long* B = A + run;
-            const int q = q0 - base;  // output position within the pair
-            // i = number of the first q outputs taken from A
-            int lo = max(0, q - run), hi = min(q, run);
-            while (lo < hi) {
-                const int mid = (lo + hi) >> 1;
-                if (A[mid] < B[q - mid - 1])
-                    lo = mid + 1;
-                else
-                    hi = mid;
-            }
-            int ia = lo, ib = q - lo;
 #pragma unroll
             for (int e = 0; e < EPT; ++e) {
-                const unsigned long long va = ia < run ? A[ia] : TK_NONE;
-                const unsigned long long vb = ib < run ? B[ib] : TK_NONE;
-                const bool ta = va < vb;
-                x[e] = ta ? va : vb;
-                ia += ta;
-                ib += !ta;
+                const unsigned long long y = xchg(x[e], ld_tag);
+                x[e] = take_min ? (x[e] < y ? x[e] : y) : (x[e] > y ? x[e] : y);
+            }
+        };
+        auto lane_stage_d = [&](int ld, int size, bool all_up) {  // ld wave-uniform
+            switch (ld) {
+                case 1: lane_stage(std::integral_constant<int, 1>{}, size, all_up); break;
+                case 2: lane_stage(std::integral_constant<int, 2>{}, size, all_up); break;
+                case 4: lane_stage(std::integral_constant<int, 4>{}, size, all_up); break;
+                case 8: lane_stage(std::integral_constant<int, 8>{}, size, all_up); break;
+                case 16: lane_stage(std::integral_constant<int, 16>{}, size, all_up); break;
+                default: lane_stage(std::integral_constant<int, 32>{}, size, all_up); break;
+            }
+        };
+        // element distances below EPT, inside the thread
+        auto thread_stages = [&](int size, bool all_up) {
+            if constexpr (EPT == 4) {
+                const bool up0 = all_up || ((EPT * tid) & size) == 0;
+                const bool up2 = all_up || ((EPT * tid + 2) & size) == 0;
+                if (size >= 4) {
+                    cswap(x[0], x[2], up0);
+                    cswap(x[1], x[3], up0);
+                }
+                cswap(x[0], x[1], up0);
+                cswap(x[2], x[3], up2);
+            } else {
+                cswap(x[0], x[1], all_up || ((EPT * tid) & size) == 0);
+            }
+        };
+        const int wsize = min(npow, 64 * EPT);  // elements each wave sorts
+#pragma unroll 1
+        for (int size = 2; size <= wsize; size <<= 1) {
+            const bool all_up = size == wsize;
+#pragma unroll 1
+            for (int d = size >> 1; d >= EPT; d >>= 1) lane_stage_d(d / EPT, size, all_up);
+            thread_stages(size, all_up);
+        }
+        // merge sorted runs of `run` elements pairwise, in place in LDS
+#pragma unroll 1
+        for (int run = 64 * EPT; run < npow; run <<= 1) {
+            __syncthreads();  // readers of the last round are done
+            if (act) {
+#pragma unroll
+                for (int e = 0; e < EPT; ++e) comp[EPT * tid + e] = x[e];
+            }
+            __syncthreads();
+            if (act) {
+                const int q0 = EPT * tid;
+                const int base = q0 & ~(2 * run - 1);  // pair start
+                const unsigned long long* A = comp + base;
+                const unsigned long long* B = A + run;
+                const int q = q0 - base;  // output position within the pair
+                // i = number of the first q outputs taken from A
+                int lo = max(0, q - run), hi = min(q, run);
+                while (lo < hi) {
+                    const int mid = (lo + hi) >> 1;
+                    if (A[mid] < B[q - mid - 1])
+                        lo = mid + 1;
+                    else
+                        hi = mid;
+                }
+                int ia = lo, ib = q - lo;
+#pragma unroll
+                for (int e = 0; e < EPT; ++e) {
+                    const unsigned long long va = ia < run ? A[ia] : TK_NONE;
+                    const unsigned long long vb = ib < run ? B[ib] : TK_NONE;
+                    const bool ta = va < vb;
+                    x[e] = ta ? va : vb;
+                    ia += ta;
+                    ib += !ta;
+                }
             }
         }
-    }
 
-    if (p.slices > 1) {  // this slice's sorted composites, ~0 past its keys
-        unsigned long long* crow = p.cand + ((int64_t)row * p.slices + slice) * p.selected;
+        if (p.slices > 1) {  // this slice's sorted composites, ~0 past its keys
+            unsigned long long* crow = p.cand + ((int64_t)row * p.slices + slice) * p.selected;
+#pragma unroll
+            for (int e = 0; e < EPT; ++e) {
+                const int i = EPT * tid + e;
+                if (i < p.selected)
+                    crow[i] = i < k ? ((x[e] >> 16) << 32) | (uint32_t)(key0 + (int)(uint32_t)(x[e] & 0xffffull)) : TK_NONE;
+            }
+            return;
+        }
+        int32_t* orow = p.out + (int64_t)row * p.out_stride;
 #pragma unroll
         for (int e = 0; e < EPT; ++e) {
             const int i = EPT * tid + e;
-            if (i < p.selected)
-                crow[i] = i < k ? ((x[e] >> 16) << 32) | (uint32_t)(key0 + (int)(uint32_t)(x[e] & 0xffffull)) : TK_NONE;
+            if (i < k) {
+                const int key = (int)(uint32_t)(x[e] & 0xffffull);
+                orow[i] = key >= visible ? -1 : p.offset + key;
+            }
         }
+    };
+    if (npow <= 2 * NT)
+        sort_and_emit(std::integral_constant<int, 2>{});
+    else
+        sort_and_emit(std::integral_constant<int, 4>{});
+    if (p.slices > 1) {
         if (tid == 0) p.slice_nan[row * p.slices + slice] = nan_seen;
         return;
-    }
-    int32_t* orow = p.out + (int64_t)row * p.out_stride;
-#pragma unroll
-    for (int e = 0; e < EPT; ++e) {
-        const int i = EPT * tid + e;
-        if (i < k) {
-            const int key = (int)(uint32_t)(x[e] & 0xffffull);
-            orow[i] = key >= visible ? -1 : p.offset + key;
-        }
     }
     if (tid == 0) {
         p.nan_flags[row] = nan_seen;
