@@ -77,6 +77,10 @@ constexpr unsigned long long TK_NONE = ~0ull;  // padding: past every composite
 // cut bin holds at most TK_CAND keys: the keys above the cut go straight to
 // the selected list and only the cut bin's keys take the remaining digits.
 constexpr int TK_CAND = 4096;
+// Bucket order of the selected keys: buckets over the span of their score
+// images; a bucket of more than TK_BUCKET_MAX keys (ties, a few distinct
+// scores) sends the row to the bitonic sort instead.
+constexpr int TK_BUCKET_MAX = 32;
 
 template <int NT, int KPT>
 __global__ void __launch_bounds__(NT) topk_select_kernel(TopkParams p) {
@@ -213,6 +217,7 @@ __global__ void __launch_bounds__(NT) topk_select_kernel(TopkParams p) {
     // exactly k composites are <= D
 
     auto composite = [&](int j) { return ((unsigned long long)img[j] << 16) | (uint32_t)(NT * j + tid); };
+    static_assert(TK_BINS % 1024 == 0 && TK_CAND >= TOPK_MAX, "bucket arrays");
     if (FAST && fast) {
         // 2a. keys of bins above the cut bin are all taken: to comp; keys of
         // the cut bin to cand.  One scan places both (counts packed 16:16).
@@ -460,10 +465,101 @@ __global__ void __launch_bounds__(NT) topk_select_kernel(TopkParams p) {
             }
         }
     };
-    if (npow <= 2 * NT)
+    // 3a. bucket order: bucket = (image - smallest image) >> shift, with
+    // shift the least that fits the span into TK_BINS buckets; counts, one
+    // scan and a scatter place the buckets, and a key's place inside its
+    // bucket is the number of its bucket's keys below it
+    bool bucketed = false;
+    if (FAST && k > 1) {  // cand holds the scattered keys (1024-thread rows)
+        uint32_t* cnt_b = hist[0];
+        uint32_t* cur_b = hist[1];
+        uint32_t mn = 0xffffffffu, mx = 0u;
+        for (int i = tid; i < k; i += NT) {
+            const uint32_t im = (uint32_t)(comp[i] >> 16);
+            mn = min(mn, im);
+            mx = max(mx, im);
+        }
+#pragma unroll
+        for (int o = 32; o >= 1; o >>= 1) {
+            mn = min(mn, (uint32_t)__shfl_xor((int)mn, o));
+            mx = max(mx, (uint32_t)__shfl_xor((int)mx, o));
+        }
+        if ((tid & 63) == 0) {
+            cur_b[tid >> 6] = mn;
+            cur_b[32 + (tid >> 6)] = mx;
+        }
+        __syncthreads();
+        mn = cur_b[0];
+        mx = cur_b[32];
+        for (int w = 1; w < NT / 64; ++w) {
+            mn = min(mn, cur_b[w]);
+            mx = max(mx, cur_b[32 + w]);
+        }
+        const uint32_t span = mx - mn;
+        const int bits = span ? 32 - __builtin_clz(span) : 0;
+        const int shift = max(0, bits - 11);  // span >> shift < 2048 = TK_BINS
+        auto bucket = [&](unsigned long long c) { return ((uint32_t)(c >> 16) - mn) >> shift; };
+        __syncthreads();  // the reduction's words are read
+        for (int i = tid; i < TK_BINS; i += NT) {
+            cnt_b[i] = 0;
+            cur_b[i] = 0;
+        }
+        __syncthreads();
+        for (int i = tid; i < k; i += NT) atomicAdd(&cnt_b[bucket(comp[i])], 1u);
+        __syncthreads();
+        // the fullest bucket decides; then start offsets by one scan
+        constexpr int BPT = TK_BINS / NT;  // buckets per thread (2 or 8)
+        uint32_t bc[BPT], tot = 0, big = 0;
+#pragma unroll
+        for (int e = 0; e < BPT; ++e) {
+            bc[e] = cnt_b[BPT * tid + e];
+            tot += bc[e];
+            big = max(big, bc[e]);
+        }
+        const bool any_big = __syncthreads_or(big > (uint32_t)TK_BUCKET_MAX);
+        if (!any_big) {
+            uint32_t st = block_scan_incl<NT>(tot, scan_sh) - tot;
+#pragma unroll
+            for (int e = 0; e < BPT; ++e) {
+                cur_b[BPT * tid + e] = st;
+                st += bc[e];
+            }
+            __syncthreads();
+            for (int i = tid; i < k; i += NT) {
+                const unsigned long long c = comp[i];
+                cand[atomicAdd(&cur_b[bucket(c)], 1u)] = c;
+            }
+            __syncthreads();
+            // cur_b[b] is now the end of bucket b
+            for (int i = tid; i < k; i += NT) {
+                const unsigned long long c = cand[i];
+                const uint32_t b = bucket(c);
+                const uint32_t end = cur_b[b], start = end - cnt_b[b];
+                uint32_t r = 0;
+                for (uint32_t j = start; j < end; ++j) r += cand[j] < c;
+                comp[start + r] = c;
+            }
+            __syncthreads();
+            bucketed = true;
+        }
+    }
+    if (bucketed || k <= 1) {
+        if (p.slices > 1) {  // this slice's sorted composites, ~0 past its keys
+            unsigned long long* crow = p.cand + ((int64_t)row * p.slices + slice) * p.selected;
+            for (int i = tid; i < p.selected; i += NT)
+                crow[i] = i < k ? ((comp[i] >> 16) << 32) | (uint32_t)(key0 + (int)(uint32_t)(comp[i] & 0xffffull)) : TK_NONE;
+        } else {
+            int32_t* orow = p.out + (int64_t)row * p.out_stride;
+            for (int i = tid; i < k; i += NT) {
+                const int key = (int)(uint32_t)(comp[i] & 0xffffull);
+                orow[i] = key >= visible ? -1 : p.offset + key;
+            }
+        }
+    } else if (npow <= 2 * NT) {
         sort_and_emit(std::integral_constant<int, 2>{});
-    else
+    } else {
         sort_and_emit(std::integral_constant<int, 4>{});
+    }
     if (p.slices > 1) {
         if (tid == 0) p.slice_nan[row * p.slices + slice] = nan_seen;
         return;

@@ -123,3 +123,19 @@ def test_nan_is_reported(M):
     assert int(status.item()) == MH.NONFINITE
     M.lightning_select(dev(normal("tk.ok", (3, 64))), 8, 1, 0, 0, check=False, status=status)
     assert int(status.item()) == 0
+
+
+@pytest.mark.parametrize("kind", ["uniform", "quantized", "heavy-tail"])
+def test_decode_row_score_distributions(M, kind):
+    # 2048 of 32768 keys for score distributions whose selected keys fill
+    # the order buckets differently: spread evenly (uniform), many keys per
+    # bucket and exact ties (values on a 1/512 grid), and a long tail
+    # (exponential magnitudes) where a few buckets hold most keys
+    u = O.bf16_to_f32(O.normal_bf16(f"tk.dist.{kind}", (1, 32768))).astype(np.float64)
+    if kind == "uniform":
+        s = (0.5 * (1.0 + np.tanh(u))).astype(np.float32)
+    elif kind == "quantized":
+        s = (np.round(u * 512.0) / 512.0).astype(np.float32)
+    else:
+        s = np.exp(np.abs(u) * 3.0).astype(np.float32)
+    compare(M, s, 2048, 4, 131071, 0, f"dist-{kind}")
