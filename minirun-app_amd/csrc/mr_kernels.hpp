@@ -144,10 +144,27 @@ struct TopkParams {
     // one row: the kernel that writes the row's NaN flag also writes the
     // device status (MR_NONFINITE or 0) here, with no status launch; else null
     int32_t* status_direct;
+    // spread selection (a row over many workgroups, set by the launcher):
+    // per (row, slice of TOPK_SPREAD_SLICE keys) the slice's keys ordered by
+    // their first digit, the digit's start offsets and a coarse copy of them
+    int32_t sp_slices;
+    unsigned short* sp_coarse;        // [rows][sp_slices][TOPK_SPREAD_CO] (8-byte records)
+    unsigned short* sp_off;           // [rows][sp_slices][TOPK_SPREAD_OFF]
+    unsigned long long* sp_sorted;    // [rows][sp_slices][TOPK_SPREAD_SLICE]
 };
+constexpr int TOPK_SPREAD_SLICE = 2048;                  // keys per slice workgroup
+constexpr int TOPK_SPREAD_BITS = 12;                     // first digit: the score image's top bits
+constexpr int TOPK_SPREAD_BINS = 1 << TOPK_SPREAD_BITS;
+constexpr int TOPK_SPREAD_OFF = TOPK_SPREAD_BINS + 8;    // u16 per slice: BINS + 1 offsets, 16-byte rows
+constexpr int TOPK_SPREAD_COARSE = 64;                   // coarse bins (of BINS / 64 digit values)
+constexpr int TOPK_SPREAD_CO = TOPK_SPREAD_COARSE + 8;   // u16 per slice: 65 coarse offsets, the NaN flag,
+                                                         // the smallest composite (u64 at u16 68)
+constexpr int TOPK_SPREAD_MAX_SLICES = 128;              // rows of up to 262144 keys
+constexpr int TOPK_SPREAD_MAX_ROWS = 8;
 
-// Workspace of a selection: per-row NaN flags, and for rows of more than
-// TOPK_SLICE keys the slice flags and two candidate buffers.
+// Workspace of a selection: per-row NaN flags; for few rows the spread
+// selection's per-slice arrays; for rows of more than TOPK_SLICE keys the
+// slice flags and two candidate buffers.
 size_t topk_workspace_bytes(int32_t rows, int32_t cols, int32_t selected);
 hipError_t launch_topk_select(const TopkParams& p, void* workspace, int32_t* status, hipStream_t st);
 

@@ -20,7 +20,10 @@
 //   3. a bitonic sort of those composites in LDS gives the final order.
 // The row's NaN flag (any NaN among all `cols` scores) goes to nan_flags.
 //
-// Rows of more than 32768 keys split into slices of 32768, one workgroup
+// A few rows of more than 4096 keys (a decode token's row) spread over many
+// workgroups instead: see topk_spread_slice / topk_spread_finish.
+//
+// Other rows of more than 32768 keys split into slices of 32768, one workgroup
 // each (the same kernel, in parallel), which emit their own first
 // `selected` keys as sorted 64-bit composites (image << 32 | key); merge
 // rounds (topk_merge_kernel) then take the first `selected` of the merge of
@@ -29,6 +32,7 @@
 // The order is the same total order, so the result is the same.
 #include <math.h>
 
+#include <algorithm>
 #include <type_traits>
 
 #include "mr_kernels.hpp"
@@ -81,6 +85,142 @@ constexpr int TK_CAND = 4096;
 // images; a bucket of more than TK_BUCKET_MAX keys (ties, a few distinct
 // scores) sends the row to the bitonic sort instead.
 constexpr int TK_BUCKET_MAX = 32;
+
+// Bitonic sort of the 64 EPT composites one wave holds in registers (lane l:
+// elements EPT l .. EPT l + EPT-1), ascending within every run of wsize
+// elements (wsize a power of two, 2 <= wsize <= 64 EPT).  The lane exchanges
+// have constant distances (DPP / permlane swaps, shuffles below 16).
+template <int EPT>
+__device__ void wave_sort(unsigned long long (&x)[EPT], int wsize) {
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    auto cswap = [&](unsigned long long& lo, unsigned long long& hi, bool up) {
+        // lo sits at the lower index: ascending blocks keep the smaller there
+        if ((lo > hi) == up) {
+            const unsigned long long t = lo;
+            lo = hi;
+            hi = t;
+        }
+    };
+    auto xchg = [&](unsigned long long v, auto ld_tag) -> unsigned long long {
+        constexpr int LD = decltype(ld_tag)::value;
+        const uint32_t lo = (uint32_t)v, hi = (uint32_t)(v >> 32);
+        uint32_t rlo, rhi;
+        if constexpr (LD == 32) {
+            const auto a = __builtin_amdgcn_permlane32_swap(lo, lo, false, false);
+            const auto c = __builtin_amdgcn_permlane32_swap(hi, hi, false, false);
+            rlo = (lane & 32) ? a[0] : a[1];
+            rhi = (lane & 32) ? c[0] : c[1];
+        } else if constexpr (LD == 16) {
+            const auto a = __builtin_amdgcn_permlane16_swap(lo, lo, false, false);
+            const auto c = __builtin_amdgcn_permlane16_swap(hi, hi, false, false);
+            rlo = (lane & 16) ? a[0] : a[1];
+            rhi = (lane & 16) ? c[0] : c[1];
+        } else {
+            rlo = __shfl_xor(lo, LD);
+            rhi = __shfl_xor(hi, LD);
+        }
+        return ((unsigned long long)rhi << 32) | rlo;
+    };
+    // one bitonic stage with lane distance LD (element stride EPT LD);
+    // blocks of `size` elements, ascending unless the block index bit
+    // says otherwise (the last size of the wave sort is all ascending)
+    auto lane_stage = [&](auto ld_tag, int size, bool all_up) {
+        constexpr int LD = decltype(ld_tag)::value;
+        const bool lower = (lane & LD) == 0;
+        const bool up = all_up || ((EPT * tid) & size) == 0;
+        const bool take_min = lower == up;
+#pragma unroll
+        for (int e = 0; e < EPT; ++e) {
+            const unsigned long long y = xchg(x[e], ld_tag);
+            x[e] = take_min ? (x[e] < y ? x[e] : y) : (x[e] > y ? x[e] : y);
+        }
+    };
+    auto lane_stage_d = [&](int ld, int size, bool all_up) {  // ld wave-uniform
+        switch (ld) {
+            case 1: lane_stage(std::integral_constant<int, 1>{}, size, all_up); break;
+            case 2: lane_stage(std::integral_constant<int, 2>{}, size, all_up); break;
+            case 4: lane_stage(std::integral_constant<int, 4>{}, size, all_up); break;
+            case 8: lane_stage(std::integral_constant<int, 8>{}, size, all_up); break;
+            case 16: lane_stage(std::integral_constant<int, 16>{}, size, all_up); break;
+            default: lane_stage(std::integral_constant<int, 32>{}, size, all_up); break;
+        }
+    };
+    // element distances below EPT, inside the thread
+    auto thread_stages = [&](int size, bool all_up) {
+        if constexpr (EPT == 4) {
+            const bool up0 = all_up || ((EPT * tid) & size) == 0;
+            const bool up2 = all_up || ((EPT * tid + 2) & size) == 0;
+            if (size >= 4) {
+                cswap(x[0], x[2], up0);
+                cswap(x[1], x[3], up0);
+            }
+            cswap(x[0], x[1], up0);
+            cswap(x[2], x[3], up2);
+        } else {
+            cswap(x[0], x[1], all_up || ((EPT * tid) & size) == 0);
+        }
+    };
+#pragma unroll 1
+    for (int size = 2; size <= wsize; size <<= 1) {
+        const bool all_up = size == wsize;
+#pragma unroll 1
+        for (int d = size >> 1; d >= EPT; d >>= 1) lane_stage_d(d / EPT, size, all_up);
+        thread_stages(size, all_up);
+    }
+}
+
+// Ascending sort of comp[0 .. npow) in LDS (npow a power of two, 4 <= npow
+// <= EPT NT, padded with TK_NONE; the composites distinct).  Thread t holds
+// elements EPT t .. EPT t + EPT-1 in registers.  Each wave sorts its 64 EPT
+// elements (wave_sort), then runs of 64 EPT, 128 EPT, ... merge pairwise
+// through LDS: each output position finds its split by a merge-path binary
+// search.  On return x[e] is element EPT t + e of the sorted order; comp
+// holds the last merge's input.
+template <int NT, int EPT>
+__device__ void sort_lds(unsigned long long* comp, int npow, unsigned long long (&x)[EPT]) {
+    const int tid = threadIdx.x;
+    const bool act = EPT * tid < npow;
+#pragma unroll
+    for (int e = 0; e < EPT; ++e) x[e] = act ? comp[EPT * tid + e] : TK_NONE;
+    wave_sort<EPT>(x, min(npow, 64 * EPT));
+    // merge sorted runs of `run` elements pairwise, in place in LDS
+#pragma unroll 1
+    for (int run = 64 * EPT; run < npow; run <<= 1) {
+        __syncthreads();  // readers of the last round are done
+        if (act) {
+#pragma unroll
+            for (int e = 0; e < EPT; ++e) comp[EPT * tid + e] = x[e];
+        }
+        __syncthreads();
+        if (act) {
+            const int q0 = EPT * tid;
+            const int base = q0 & ~(2 * run - 1);  // pair start
+            const unsigned long long* A = comp + base;
+            const unsigned long long* B = A + run;
+            const int q = q0 - base;  // output position within the pair
+            // i = number of the first q outputs taken from A
+            int lo = max(0, q - run), hi = min(q, run);
+            while (lo < hi) {
+                const int mid = (lo + hi) >> 1;
+                if (A[mid] < B[q - mid - 1])
+                    lo = mid + 1;
+                else
+                    hi = mid;
+            }
+            int ia = lo, ib = q - lo;
+#pragma unroll
+            for (int e = 0; e < EPT; ++e) {
+                const unsigned long long va = ia < run ? A[ia] : TK_NONE;
+                const unsigned long long vb = ib < run ? B[ib] : TK_NONE;
+                const bool ta = va < vb;
+                x[e] = ta ? va : vb;
+                ia += ta;
+                ib += !ta;
+            }
+        }
+    }
+}
 
 template <int NT, int KPT>
 __global__ void __launch_bounds__(NT) topk_select_kernel(TopkParams p) {
@@ -318,133 +458,13 @@ __global__ void __launch_bounds__(NT) topk_select_kernel(TopkParams p) {
     for (int i = k + tid; i < npow; i += NT) comp[i] = TK_NONE;
     __syncthreads();
 
-    // 3. sort, ascending.  Thread t holds elements EPT t .. EPT t + EPT-1 in
-    // registers (EPT = 2 when the padded count fits 2 per thread, so every
-    // wave works; else 4).  Each wave sorts its 64 EPT elements (a bitonic
-    // network whose lane exchanges have constant distances), then runs of
-    // 64 EPT, 128 EPT, ... merge pairwise through LDS: each output position
-    // finds its split by a merge-path binary search (the composites are
-    // distinct).  The sorted keys go out as offsets (or, per slice, as 64-bit
-    // composites for the merge rounds).
-    const int lane = tid & 63;
+    // 3. sort, ascending (sort_lds, EPT = 2 when the padded count fits 2 per
+    // thread, so every wave works; else 4).  The sorted keys go out as
+    // offsets (or, per slice, as 64-bit composites for the merge rounds).
     auto sort_and_emit = [&](auto ept_tag) {
         constexpr int EPT = decltype(ept_tag)::value;
-        const bool act = EPT * tid < npow;
         unsigned long long x[EPT];
-#pragma unroll
-        for (int e = 0; e < EPT; ++e) x[e] = act ? comp[EPT * tid + e] : TK_NONE;
-        auto cswap = [&](unsigned long long& lo, unsigned long long& hi, bool up) {
-            // lo sits at the lower index: ascending blocks keep the smaller there
-            if ((lo > hi) == up) {
-                const unsigned long long t = lo;
-                lo = hi;
-                hi = t;
-            }
-        };
-        auto xchg = [&](unsigned long long v, auto ld_tag) -> unsigned long long {
-            constexpr int LD = decltype(ld_tag)::value;
-            const uint32_t lo = (uint32_t)v, hi = (uint32_t)(v >> 32);
-            uint32_t rlo, rhi;
-            if constexpr (LD == 32) {
-                const auto a = __builtin_amdgcn_permlane32_swap(lo, lo, false, false);
-                const auto c = __builtin_amdgcn_permlane32_swap(hi, hi, false, false);
-                rlo = (lane & 32) ? a[0] : a[1];
-                rhi = (lane & 32) ? c[0] : c[1];
-            } else if constexpr (LD == 16) {
-                const auto a = __builtin_amdgcn_permlane16_swap(lo, lo, false, false);
-                const auto c = __builtin_amdgcn_permlane16_swap(hi, hi, false, false);
-                rlo = (lane & 16) ? a[0] : a[1];
-                rhi = (lane & 16) ? c[0] : c[1];
-            } else {
-                rlo = __shfl_xor(lo, LD);
-                rhi = __shfl_xor(hi, LD);
-            }
-            return ((unsigned long long)rhi << 32) | rlo;
-        };
-        // one bitonic stage with lane distance LD (element stride EPT LD);
-        // blocks of `size` elements, ascending unless the block index bit
-        // says otherwise (the last size of the wave sort is all ascending)
-        auto lane_stage = [&](auto ld_tag, int size, bool all_up) {
-            constexpr int LD = decltype(ld_tag)::value;
-            const bool lower = (lane & LD) == 0;
-            const bool up = all_up || ((EPT * tid) & size) == 0;
-            const bool take_min = lower == up;
-#pragma unroll
-            for (int e = 0; e < EPT; ++e) {
-                const unsigned long long y = xchg(x[e], ld_tag);
-                x[e] = take_min ? (x[e] < y ? x[e] : y) : (x[e] > y ? x[e] : y);
-            }
-        };
-        auto lane_stage_d = [&](int ld, int size, bool all_up) {  // ld wave-uniform
-            switch (ld) {
-                case 1: lane_stage(std::integral_constant<int, 1>{}, size, all_up); break;
-                case 2: lane_stage(std::integral_constant<int, 2>{}, size, all_up); break;
-                case 4: lane_stage(std::integral_constant<int, 4>{}, size, all_up); break;
-                case 8: lane_stage(std::integral_constant<int, 8>{}, size, all_up); break;
-                case 16: lane_stage(std::integral_constant<int, 16>{}, size, all_up); break;
-                default: lane_stage(std::integral_constant<int, 32>{}, size, all_up); break;
-            }
-        };
-        // element distances below EPT, inside the thread
-        auto thread_stages = [&](int size, bool all_up) {
-            if constexpr (EPT == 4) {
-                const bool up0 = all_up || ((EPT * tid) & size) == 0;
-                const bool up2 = all_up || ((EPT * tid + 2) & size) == 0;
-                if (size >= 4) {
-                    cswap(x[0], x[2], up0);
-                    cswap(x[1], x[3], up0);
-                }
-                cswap(x[0], x[1], up0);
-                cswap(x[2], x[3], up2);
-            } else {
-                cswap(x[0], x[1], all_up || ((EPT * tid) & size) == 0);
-            }
-        };
-        const int wsize = min(npow, 64 * EPT);  // elements each wave sorts
-#pragma unroll 1
-        for (int size = 2; size <= wsize; size <<= 1) {
-            const bool all_up = size == wsize;
-#pragma unroll 1
-            for (int d = size >> 1; d >= EPT; d >>= 1) lane_stage_d(d / EPT, size, all_up);
-            thread_stages(size, all_up);
-        }
-        // merge sorted runs of `run` elements pairwise, in place in LDS
-#pragma unroll 1
-        for (int run = 64 * EPT; run < npow; run <<= 1) {
-            __syncthreads();  // readers of the last round are done
-            if (act) {
-#pragma unroll
-                for (int e = 0; e < EPT; ++e) comp[EPT * tid + e] = x[e];
-            }
-            __syncthreads();
-            if (act) {
-                const int q0 = EPT * tid;
-                const int base = q0 & ~(2 * run - 1);  // pair start
-                const unsigned long long* A = comp + base;
-                const unsigned long long* B = A + run;
-                const int q = q0 - base;  // output position within the pair
-                // i = number of the first q outputs taken from A
-                int lo = max(0, q - run), hi = min(q, run);
-                while (lo < hi) {
-                    const int mid = (lo + hi) >> 1;
-                    if (A[mid] < B[q - mid - 1])
-                        lo = mid + 1;
-                    else
-                        hi = mid;
-                }
-                int ia = lo, ib = q - lo;
-#pragma unroll
-                for (int e = 0; e < EPT; ++e) {
-                    const unsigned long long va = ia < run ? A[ia] : TK_NONE;
-                    const unsigned long long vb = ib < run ? B[ib] : TK_NONE;
-                    const bool ta = va < vb;
-                    x[e] = ta ? va : vb;
-                    ia += ta;
-                    ib += !ta;
-                }
-            }
-        }
-
+        sort_lds<NT, EPT>(comp, npow, x);
         if (p.slices > 1) {  // this slice's sorted composites, ~0 past its keys
             unsigned long long* crow = p.cand + ((int64_t)row * p.slices + slice) * p.selected;
 #pragma unroll
@@ -570,6 +590,500 @@ __global__ void __launch_bounds__(NT) topk_select_kernel(TopkParams p) {
     }
 }
 
+// ---------------------------------------------------------------------------
+// Spread selection: one row over many workgroups (a decode token's row of
+// many keys).  Two launches, the kernel boundary between them the only
+// hand-off:
+//   1. topk_spread_slice, one workgroup per TOPK_SPREAD_SLICE keys: the keys'
+//      composites (image << 32 | key id, 64-bit) ordered by their first digit
+//      (the image's top TOPK_SPREAD_BITS bits) by a counting sort (LDS
+//      histogram, one scan, a scatter by LDS cursors), written out with the
+//      digit's start offsets, every 64th offset (coarse) and the NaN flag;
+//   2. topk_spread_finish, one workgroup per row: the coarse offsets summed
+//      over the slices give the coarse bin that holds the selected-th key,
+//      the fine offsets inside it the cut digit value.  Keys of smaller
+//      digits are all taken (each slice's are a prefix of its ordered keys);
+//      the cut value's keys (the next run of each slice) are candidates, and
+//      a radix select over the rest of their composite (8-bit digits) finds
+//      the last one taken.  The selected keys are then ordered: buckets over
+//      the span of their composites (counts, one scan, a scatter, the rank
+//      inside the bucket), or the bitonic sort when a bucket holds more than
+//      TK_BUCKET_MAX keys.
+// The order is the same total order as the one-workgroup kernel's.
+
+// 64-bit min / max over the wave (DPP within rows of 16 lanes, then
+// permlane swaps across rows); every lane ends with the result.
+template <int CTRL>
+__device__ __forceinline__ unsigned long long dpp_u64(unsigned long long v) {
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)v, CTRL, 0xf, 0xf, false);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)(v >> 32), CTRL, 0xf, 0xf, false);
+    return ((unsigned long long)hi << 32) | lo;
+}
+template <bool MAX>
+__device__ __forceinline__ unsigned long long wave_ext_u64(unsigned long long v) {
+    auto f = [](unsigned long long a, unsigned long long b) { return MAX ? (a > b ? a : b) : (a < b ? a : b); };
+    v = f(v, dpp_u64<0xB1>(v));   // quad_perm 1,0,3,2
+    v = f(v, dpp_u64<0x4E>(v));   // quad_perm 2,3,0,1
+    v = f(v, dpp_u64<0x141>(v));  // row_half_mirror
+    v = f(v, dpp_u64<0x140>(v));  // row_mirror
+    {
+        // one element of each pair is this lane's own value, the other its partner's
+        const auto a = __builtin_amdgcn_permlane16_swap((uint32_t)v, (uint32_t)v, false, false);
+        const auto b = __builtin_amdgcn_permlane16_swap((uint32_t)(v >> 32), (uint32_t)(v >> 32), false, false);
+        v = f(((unsigned long long)b[0] << 32) | a[0], ((unsigned long long)b[1] << 32) | a[1]);
+    }
+    {
+        const auto a = __builtin_amdgcn_permlane32_swap((uint32_t)v, (uint32_t)v, false, false);
+        const auto b = __builtin_amdgcn_permlane32_swap((uint32_t)(v >> 32), (uint32_t)(v >> 32), false, false);
+        v = f(((unsigned long long)b[0] << 32) | a[0], ((unsigned long long)b[1] << 32) | a[1]);
+    }
+    return v;
+}
+
+// Called by wave 0: the bin of a 256-bin histogram at which the running
+// count reaches `rank` (1 <= rank <= total); pick = {bin, count before it,
+// count in it}.  Lane l sums bins 4l .. 4l+3, a wave scan places the lanes
+// and the lane whose range crosses the rank walks its four bins.
+__device__ __forceinline__ void rank_bin256(const uint32_t* h, uint32_t rank, uint32_t* pick) {
+    const int lane = threadIdx.x & 63;
+    const u32x4 h4 = *(const u32x4*)(h + 4 * lane);
+    const uint32_t tot = (h4[0] + h4[1]) + (h4[2] + h4[3]);
+    const uint32_t incl = wave_scan_incl(tot);
+    uint32_t bef = incl - tot;
+    if (bef < rank && rank <= incl) {
+        int b = 0;
+        uint32_t cb = h4[0];
+        if (bef + cb < rank) { bef += cb; b = 1; cb = h4[1]; }
+        if (b == 1 && bef + cb < rank) { bef += cb; b = 2; cb = h4[2]; }
+        if (b == 2 && bef + cb < rank) { bef += cb; b = 3; cb = h4[3]; }
+        pick[0] = (uint32_t)(4 * lane + b);
+        pick[1] = bef;
+        pick[2] = cb;
+    }
+}
+
+constexpr int TK_SLICE_NT = 512;  // threads of a slice workgroup
+
+__global__ void __launch_bounds__(TK_SLICE_NT) topk_spread_slice(TopkParams p) {
+    constexpr int NT = TK_SLICE_NT, KPT = TOPK_SPREAD_SLICE / NT, BINS = TOPK_SPREAD_BINS;
+    constexpr int SH = 32 - TOPK_SPREAD_BITS;           // image >> SH = first digit
+    constexpr int BPT = BINS / NT;                        // digit values per thread
+    constexpr int CSTEP = BINS / TOPK_SPREAD_COARSE;      // digit values per coarse bin
+    static_assert(BPT % 8 == 0 && CSTEP % BPT == 0 && TOPK_SPREAD_SLICE <= 65535, "offset rows");
+    __shared__ __attribute__((aligned(16))) uint32_t hist[BINS];
+    __shared__ unsigned long long srt[TOPK_SPREAD_SLICE];
+    __shared__ uint32_t scan_sh[NT / 64];
+    __shared__ unsigned long long wmin[NT / 64];
+    __shared__ int nan_sh;
+    static_assert(TOPK_SPREAD_CO % 4 == 0 && TOPK_SPREAD_CO >= TOPK_SPREAD_COARSE + 8, "coarse records");
+
+    const int s = blockIdx.x, row = blockIdx.y, tid = threadIdx.x;
+    const int S = p.sp_slices;
+    const int key0 = s * TOPK_SPREAD_SLICE;
+    const float* sr = p.scores + (int64_t)row * p.row_stride;
+    const int visible = p.start_pos == 0 ? (row + 1) / p.ratio : p.available;
+    const int n = min(p.available - key0, TOPK_SPREAD_SLICE);  // >= 1
+    const int64_t slot = (int64_t)row * S + s;
+
+    for (int i = tid; i < BINS / 4; i += NT) ((u32x4*)hist)[i] = u32x4{0u, 0u, 0u, 0u};
+    if (tid == 0) nan_sh = 0;
+    // key NT j + tid of the slice (coalesced loads) as its 32-bit image
+    uint32_t img[KPT];
+    bool nan_here = false;
+#pragma unroll
+    for (int j = 0; j < KPT; ++j) {
+        const int i = NT * j + tid;
+        const float f = i < n ? sr[key0 + i] : 0.f;
+        nan_here |= isnan(f);
+        img[j] = ~ordered_bits(key0 + i < visible ? f : -INFINITY);
+    }
+    // NaN anywhere in the row: the columns past the ranked keys, split over the slices
+    const int extra = p.cols - p.available;
+    if (extra > 0) {
+        const int per = (extra + S - 1) / S;
+        const int a = p.available + s * per, b = min(a + per, p.cols);
+        for (int c = a + tid; c < b; c += NT) nan_here |= isnan(sr[c]);
+    }
+    __syncthreads();
+    if (nan_here) nan_sh = 1;
+#pragma unroll
+    for (int j = 0; j < KPT; ++j)
+        if (NT * j + tid < n) atomicAdd(&hist[img[j] >> SH], 1u);
+    __syncthreads();
+
+    // start offset of every digit value (thread t: values BPT t .. BPT t + BPT-1);
+    // the counts become the scatter cursors in place
+    uint32_t c[BPT], tot = 0;
+#pragma unroll
+    for (int q = 0; q < BPT / 4; ++q) {
+        const u32x4 v = ((const u32x4*)hist)[BPT / 4 * tid + q];
+        c[4 * q] = v[0];
+        c[4 * q + 1] = v[1];
+        c[4 * q + 2] = v[2];
+        c[4 * q + 3] = v[3];
+        tot += (v[0] + v[1]) + (v[2] + v[3]);
+    }
+    uint32_t o = block_scan_incl<NT>(tot, scan_sh) - tot;
+    uint32_t ov[BPT / 2];
+#pragma unroll
+    for (int e = 0; e < BPT; ++e) {
+        hist[BPT * tid + e] = o;
+        if (e & 1)
+            ov[e / 2] |= o << 16;
+        else
+            ov[e / 2] = o;
+        o += c[e];
+    }
+    __syncthreads();
+    unsigned long long mn = ~0ull;
+#pragma unroll
+    for (int j = 0; j < KPT; ++j)
+        if (NT * j + tid < n) {
+            const uint32_t pos = atomicAdd(&hist[img[j] >> SH], 1u);
+            const unsigned long long v = ((unsigned long long)img[j] << 32) | (uint32_t)(key0 + NT * j + tid);
+            srt[pos] = v;
+            mn = v < mn ? v : mn;
+        }
+    mn = wave_ext_u64<false>(mn);
+    if ((tid & 63) == 0) wmin[tid >> 6] = mn;
+    __syncthreads();
+    // global stores after the last barrier (a barrier waits for them)
+    unsigned short* orow = p.sp_off + slot * TOPK_SPREAD_OFF;
+    unsigned short* crow = p.sp_coarse + slot * TOPK_SPREAD_CO;
+#pragma unroll
+    for (int q = 0; q < BPT / 8; ++q)
+        ((u32x4*)orow)[BPT / 8 * tid + q] = u32x4{ov[4 * q], ov[4 * q + 1], ov[4 * q + 2], ov[4 * q + 3]};
+    if ((BPT * tid) % CSTEP == 0) crow[BPT * tid / CSTEP] = (unsigned short)(ov[0] & 0xffffu);
+    unsigned long long* drow = p.sp_sorted + slot * TOPK_SPREAD_SLICE;
+    for (int i = tid; i < n; i += NT) drow[i] = srt[i];
+    if (tid == 0) {
+        orow[BINS] = (unsigned short)n;
+        crow[TOPK_SPREAD_COARSE] = (unsigned short)n;
+        crow[TOPK_SPREAD_COARSE + 1] = (unsigned short)nan_sh;
+#pragma unroll
+        for (int i = 1; i < NT / 64; ++i) mn = wmin[i] < mn ? wmin[i] : mn;
+        *(unsigned long long*)(crow + TOPK_SPREAD_COARSE + 4) = mn;  // the slice's smallest composite
+    }
+}
+
+__global__ void __launch_bounds__(1024) topk_spread_finish(TopkParams p) {
+    constexpr int NT = 1024, NW = NT / 64;
+    constexpr int CO = TOPK_SPREAD_COARSE;
+    constexpr int CSTEP = TOPK_SPREAD_BINS / CO;
+    constexpr int FW = CSTEP + 1;        // fine offsets read per slice
+    constexpr int CAND = 4096;           // candidates held in LDS
+    constexpr int MS = TOPK_SPREAD_MAX_SLICES;
+    static_assert(MS <= 128 && CO <= 64 && CSTEP <= 64, "one wave scans the slices and the bins");
+    static_assert(TK_BINS == 2 * NT, "two buckets per thread");
+    __shared__ uint32_t gco[CO + 1], gfi[FW];
+    __shared__ unsigned short fine[MS * FW];
+    __shared__ uint32_t pick[3];
+    __shared__ __attribute__((aligned(16))) unsigned long long comp[TOPK_MAX];
+    __shared__ __attribute__((aligned(16))) unsigned long long aux[CAND];
+    __shared__ __attribute__((aligned(16))) uint32_t cnt[TK_BINS], cur[TK_BINS];
+    __shared__ __attribute__((aligned(16))) uint32_t dh[2][256];
+    __shared__ uint32_t scan_sh[NW];
+    __shared__ unsigned long long mn_sh;
+    __shared__ uint16_t big[128];  // buckets of TK_BUCKET_MAX+1 .. WAVE_MAX keys
+    __shared__ uint32_t nbig;
+    __shared__ int nan_sh;
+    __shared__ uint32_t ctr;
+
+    const int row = blockIdx.x, tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int S = p.sp_slices;
+    const uint32_t k = (uint32_t)p.selected;  // 1 <= k <= available
+    const int visible = p.start_pos == 0 ? (row + 1) / p.ratio : p.available;
+    const int64_t slot0 = (int64_t)row * S;
+
+    if (tid <= CO) gco[tid] = 0;
+    if (tid < FW) gfi[tid] = 0;
+    if (tid < 256) dh[0][tid] = 0;
+    cnt[2 * tid] = 0;
+    cnt[2 * tid + 1] = 0;
+    if (tid == 0) {
+        nan_sh = 0;
+        ctr = 0;
+        nbig = 0;
+        mn_sh = ~0ull;
+    }
+    // 1. coarse offsets summed over the slices: the coarse bin holding the
+    // k-th key; the row's NaN flag and its smallest composite (each record's
+    // first 33 words: 65 offsets and the flag; and its minimum).
+    constexpr int CW = (CO + 2) / 2;                  // words of offsets and flag per record
+    constexpr int CPT = (MS * CW + NT - 1) / NT;      // of them per thread
+    static_assert(TOPK_SPREAD_CO % 4 == 0 && CW * 2 == CO + 2, "coarse records");
+    const uint32_t* co32 = (const uint32_t*)(p.sp_coarse + slot0 * TOPK_SPREAD_CO);
+    uint32_t cw[CPT];
+#pragma unroll
+    for (int e = 0; e < CPT; ++e) {
+        const int i = tid + NT * e, s = i / CW;
+        cw[e] = co32[i < S * CW ? s * (TOPK_SPREAD_CO / 2) + (i - s * CW) : 0];
+    }
+    const unsigned long long smin =
+        *(const unsigned long long*)(p.sp_coarse + (slot0 + (tid < S ? tid : 0)) * TOPK_SPREAD_CO + CO + 4);
+    __syncthreads();
+#pragma unroll
+    for (int e = 0; e < CPT; ++e) {
+        const int i = tid + NT * e, s = i / CW, c = 2 * (i - s * CW);  // u16 c and c + 1
+        if (i < S * CW) {
+            atomicAdd(&gco[c], cw[e] & 0xffffu);
+            if (c + 1 <= CO)
+                atomicAdd(&gco[c + 1], cw[e] >> 16);
+            else if (cw[e] >> 16)
+                nan_sh = 1;
+        }
+    }
+    if (tid < S) atomicMin(&mn_sh, smin);
+    __syncthreads();
+    // every wave finds the coarse bin itself (gco is read-only from here)
+    const int c0 = __ffsll((long long)__ballot(lane < CO && gco[lane] < k && k <= gco[lane + 1])) - 1;
+    // 2. fine offsets inside it: the cut digit value
+    for (int i = tid; i < S * FW; i += NT) {
+        const int s = i / FW, j = i - s * FW;
+        const uint32_t v = p.sp_off[(slot0 + s) * TOPK_SPREAD_OFF + CSTEP * c0 + j];
+        fine[i] = (unsigned short)v;
+        atomicAdd(&gfi[j], v);
+    }
+    __syncthreads();
+    const int cb = __ffsll((long long)__ballot(lane < CSTEP && gfi[lane] < k && k <= gfi[lane + 1])) - 1;
+    const uint32_t P = gfi[cb], C = gfi[cb + 1] - P;  // keys below the cut value, keys at it
+    const uint32_t cut = (uint32_t)(CSTEP * c0 + cb);
+    // Usually every key through the cut value fits: all of them are ordered
+    // and the first k emitted.  Otherwise the keys below it are gathered and
+    // a radix select picks the cut value's taken keys.
+    const bool all = P + C <= (uint32_t)TOPK_MAX;
+    const bool cand_lds = !all && C <= (uint32_t)CAND;
+    // where each slice's keys go: every wave scans the slices itself (slices
+    // 2l, 2l+1 on lane l) and reads its own slices' places by readlane
+    uint32_t ps0, cs0, pe, ce;
+    {
+        uint32_t ps[2], cs[2];
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+            const int s = 2 * lane + e;
+            const uint32_t lo = s < S ? fine[s * FW + cb] : 0u, hi = s < S ? fine[s * FW + cb + 1] : 0u;
+            ps[e] = all ? hi : lo;
+            cs[e] = hi - lo;
+        }
+        const uint32_t pt = ps[0] + ps[1], ct = cs[0] + cs[1];
+        pe = wave_scan_incl(pt) - pt;
+        ce = wave_scan_incl(ct) - ct;
+        ps0 = ps[0];
+        cs0 = cs[0];
+    }
+    auto place = [&](int s, bool cand) {  // s wave-uniform
+        const int l = s >> 1;
+        uint32_t v = (uint32_t)__builtin_amdgcn_readlane((int)(cand ? ce : pe), l);
+        if (s & 1) v += (uint32_t)__builtin_amdgcn_readlane((int)(cand ? cs0 : ps0), l);
+        return v;
+    };
+    // bucket of a key for the final order: (composite - smallest) >> shift,
+    // shift the least that fits every key through the cut value into
+    // TK_BINS buckets
+    const unsigned long long mn = mn_sh;
+    const unsigned long long mx = (((unsigned long long)cut + 1ull) << (64 - TOPK_SPREAD_BITS)) - 1ull;
+    const unsigned long long span = mx - mn;
+    const int shift = max(0, (span ? 64 - __clzll((long long)span) : 0) - 11);  // span >> shift < TK_BINS
+    auto bucket = [&](unsigned long long v) { return (uint32_t)((v - mn) >> shift); };
+    // 3. gather (wave w: slices w, w + NW, ...; four keys per lane a batch),
+    // counting the buckets
+    auto gather = [&](int s) {
+        const uint32_t ps = fine[s * FW + cb], es = fine[s * FW + cb + 1];
+        const uint32_t g = (all || cand_lds) ? es : ps;
+        const uint32_t dst = place(s, false), dcand = place(s, true);
+        const unsigned long long* src = p.sp_sorted + (slot0 + s) * TOPK_SPREAD_SLICE;
+        for (uint32_t i0 = 0; i0 < g; i0 += 256) {
+            unsigned long long v[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const uint32_t i = i0 + lane + 64 * e;
+                v[e] = src[i < g ? i : 0];
+            }
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const uint32_t i = i0 + lane + 64 * e;
+                if (i < g) {
+                    if (all || i < ps) {
+                        comp[dst + i] = v[e];
+                        atomicAdd(&cnt[bucket(v[e])], 1u);
+                    } else {
+                        aux[dcand + (i - ps)] = v[e];
+                    }
+                }
+            }
+        }
+    };
+    for (int s = w; s < S; s += NW) gather(s);
+    uint32_t nsort = P + C;
+    if (!all) {
+        // 4. the (k - P)-th smallest candidate: 8-bit digits of composite
+        // bits 51..0 (image bits 19..0, then the key id); all candidates
+        // share the top TOPK_SPREAD_BITS bits.  Candidates come from LDS or
+        // (too many for it) from the slices' rows.
+        auto for_each_cand = [&](auto&& f) {
+            if (cand_lds) {
+                for (uint32_t i = tid; i < C; i += NT) f(aux[i]);
+            } else {
+                for (int s = w; s < S; s += NW) {
+                    const uint32_t ps = fine[s * FW + cb], es = fine[s * FW + cb + 1];
+                    const unsigned long long* src = p.sp_sorted + (slot0 + s) * TOPK_SPREAD_SLICE;
+                    for (uint32_t i = ps + lane; i < es; i += 64) f(src[i]);
+                }
+            }
+        };
+        __syncthreads();
+        const uint32_t need = k - P;  // >= 1, < C
+        unsigned long long dsel = ~0ull;
+        unsigned long long dacc = (unsigned long long)cut << (64 - TOPK_SPREAD_BITS);
+        uint32_t remaining = need;
+#pragma unroll 1
+        for (int q = 0; q < 7; ++q) {
+            const int sh = q == 0 ? 44 : q == 1 ? 36 : q == 2 ? 32 : 8 * (6 - q);
+            const int wd = q == 2 ? 4 : 8;
+            uint32_t* h = dh[q & 1];
+            if (tid < 256) dh[(q & 1) ^ 1][tid] = 0;  // the next digit's
+            for_each_cand([&](unsigned long long v) {
+                if (((v ^ dacc) >> (sh + wd)) == 0ull) atomicAdd(&h[(uint32_t)(v >> sh) & ((1u << wd) - 1u)], 1u);
+            });
+            __syncthreads();
+            if (tid < 64) rank_bin256(h, remaining, pick);
+            __syncthreads();
+            dacc |= (unsigned long long)pick[0] << sh;
+            remaining -= pick[1];
+            if (remaining == pick[2]) {  // every candidate with this prefix is taken
+                dsel = dacc | ((1ull << sh) - 1ull);
+                break;
+            }
+        }
+        // the candidates <= dsel (exactly `need` of them) after the taken keys;
+        // their order here is arbitrary, the sort below fixes it
+        for_each_cand([&](unsigned long long v) {
+            if (v <= dsel) {
+                const uint32_t pos = P + atomicAdd(&ctr, 1u);
+                if (pos < k) {
+                    comp[pos] = v;
+                    atomicAdd(&cnt[bucket(v)], 1u);
+                }
+            }
+        });
+        nsort = k;
+    }
+
+    // 5. order the nsort keys by their buckets (counted above: one scan, a
+    // scatter, the rank inside the bucket); the first k go out
+    int32_t* orow = p.out + (int64_t)row * p.out_stride;
+    auto emit = [&](uint32_t i, unsigned long long v) {
+        const int key = (int)(uint32_t)v;
+        orow[i] = key >= visible ? -1 : p.offset + key;
+    };
+    __syncthreads();
+    // one scan places the buckets and counts those too full for a wave's
+    // sort (bit 16 up); buckets of more than TK_BUCKET_MAX keys are listed,
+    // a wave sorts each in registers
+    constexpr uint32_t WAVE_MAX = 256;  // 64 lanes x 4
+    static_assert((TOPK_MAX + TK_BUCKET_MAX) / (TK_BUCKET_MAX + 1) <= 128, "listed buckets");
+    const uint32_t b0 = cnt[2 * tid], b1 = cnt[2 * tid + 1];
+    const uint32_t full = (b0 > WAVE_MAX) + (b1 > WAVE_MAX);
+    if (b0 > (uint32_t)TK_BUCKET_MAX && b0 <= WAVE_MAX) big[atomicAdd(&nbig, 1u)] = (uint16_t)(2 * tid);
+    if (b1 > (uint32_t)TK_BUCKET_MAX && b1 <= WAVE_MAX) big[atomicAdd(&nbig, 1u)] = (uint16_t)(2 * tid + 1);
+    const uint32_t sv = (b0 + b1) | (full << 16);
+    uint32_t incl = wave_scan_incl(sv);
+    if (lane == 63) scan_sh[w] = incl;
+    __syncthreads();
+    uint32_t before = 0, total = 0;
+#pragma unroll
+    for (int i = 0; i < NW; ++i) {
+        const uint32_t t = scan_sh[i];
+        before += i < w ? t : 0u;
+        total += t;
+    }
+    if ((total >> 16) == 0u) {
+        const uint32_t st = before + incl - sv;
+        cur[2 * tid] = st;
+        cur[2 * tid + 1] = st + b0;
+        __syncthreads();
+        static_assert(TOPK_MAX <= 4 * NT, "four keys per thread");
+        unsigned long long kv[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) kv[e] = comp[min(tid + NT * e, TOPK_MAX - 1)];
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+            if (tid + NT * e < (int)nsort) aux[atomicAdd(&cur[bucket(kv[e])], 1u)] = kv[e];
+        __syncthreads();
+        // cur[b] is now the end of bucket b; a key's place is its bucket's
+        // start plus the number of its bucket's keys below it (small
+        // buckets), or its place in its bucket's wave sort (listed ones)
+        uint32_t kend[4], kstart[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            kv[e] = aux[min(tid + NT * e, TOPK_MAX - 1)];
+            const uint32_t b = bucket(kv[e]) & (TK_BINS - 1);
+            kend[e] = cur[b];
+            kstart[e] = kend[e] - cnt[b];
+        }
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            if (tid + NT * e >= (int)nsort || kend[e] - kstart[e] > (uint32_t)TK_BUCKET_MAX) continue;
+            const unsigned long long v = kv[e];
+            uint32_t r = kstart[e];
+            for (uint32_t j0 = kstart[e]; j0 < kend[e]; j0 += 4) {
+                unsigned long long u[4];
+#pragma unroll
+                for (int q = 0; q < 4; ++q) u[q] = j0 + q < kend[e] ? aux[j0 + q] : ~0ull;
+#pragma unroll
+                for (int q = 0; q < 4; ++q) r += u[q] < v;
+            }
+            if (r < k) emit(r, v);
+        }
+        auto sort_bucket = [&](uint32_t b, auto ept_tag) {  // 64 EPT >= the bucket's keys
+            constexpr int EPT = decltype(ept_tag)::value;
+            const uint32_t end = cur[b], nb = cnt[b], start = end - nb;
+            unsigned long long x[EPT];
+#pragma unroll
+            for (int e = 0; e < EPT; ++e) {
+                const uint32_t j = EPT * lane + e;
+                x[e] = j < nb ? aux[start + j] : TK_NONE;
+            }
+            wave_sort<EPT>(x, 64 * EPT);
+#pragma unroll
+            for (int e = 0; e < EPT; ++e) {
+                const uint32_t j = EPT * lane + e;
+                if (j < nb && start + j < k) emit(start + j, x[e]);
+            }
+        };
+        for (uint32_t i = w; i < nbig; i += NW) {
+            const uint32_t b = big[i], nb = cnt[b];
+            if (nb <= 128)
+                sort_bucket(b, std::integral_constant<int, 2>{});
+            else
+                sort_bucket(b, std::integral_constant<int, 4>{});
+        }
+    } else {
+        // a bucket too full for a wave (ties, few distinct scores): the
+        // bitonic sort of all keys
+        int npow = 4;
+        while (npow < (int)nsort) npow <<= 1;
+        for (int i = (int)nsort + tid; i < npow; i += NT) comp[i] = TK_NONE;
+        __syncthreads();
+        auto sort_emit = [&](auto ept_tag) {
+            constexpr int EPT = decltype(ept_tag)::value;
+            unsigned long long x[EPT];
+            sort_lds<NT, EPT>(comp, npow, x);
+#pragma unroll
+            for (int e = 0; e < EPT; ++e)
+                if (EPT * tid + e < (int)k) emit((uint32_t)(EPT * tid + e), x[e]);
+        };
+        if (npow <= 2 * NT)
+            sort_emit(std::integral_constant<int, 2>{});
+        else
+            sort_emit(std::integral_constant<int, 4>{});
+    }
+    if (tid == 0) {
+        p.nan_flags[row] = nan_sh;
+        if (p.status_direct) *p.status_direct = nan_sh ? 5 /* MR_NONFINITE */ : 0;
+    }
+}
+
 // One merge round over rows of sorted composite lists: list pair q of a row
 // (lists 2q and 2q+1 of `lists`, each `len` long; an odd last list passes
 // through) -> the first `len` of their merge.  Output position i takes its
@@ -635,15 +1149,49 @@ __global__ void __launch_bounds__(256) topk_status_kernel(const int32_t* flags, 
 
 }  // namespace
 
+namespace {
+
+size_t a256(size_t x) { return (x + 255) & ~size_t(255); }
+
+// Rows of more keys than this (and few rows) take the spread selection.
+constexpr int TOPK_SPREAD_MIN_KEYS = 4096;
+
+bool spread_applies(int32_t rows, int32_t keys) {
+    return rows <= TOPK_SPREAD_MAX_ROWS && keys > TOPK_SPREAD_MIN_KEYS &&
+           keys <= TOPK_SPREAD_MAX_SLICES * TOPK_SPREAD_SLICE;
+}
+
+// Byte offsets of the spread selection's arrays, after the per-row flags.
+struct SpreadLayout {
+    size_t coarse, off, sorted, end;
+};
+SpreadLayout spread_layout(int32_t rows, int slices) {
+    const size_t rs = size_t(rows) * size_t(slices);
+    SpreadLayout L;
+    L.coarse = 0;
+    L.off = L.coarse + a256(rs * TOPK_SPREAD_CO * 2);
+    L.sorted = L.off + a256(rs * TOPK_SPREAD_OFF * 2);
+    L.end = L.sorted + a256(rs * TOPK_SPREAD_SLICE * 8);
+    return L;
+}
+
+}  // namespace
+
 size_t topk_workspace_bytes(int32_t rows, int32_t cols, int32_t selected) {
-    auto a256 = [](size_t x) { return (x + 255) & ~size_t(255); };
     size_t bytes = a256(size_t(rows) * 4);
+    size_t extra = 0;
     if (cols > TOPK_SLICE) {
         const size_t slices = (size_t(cols) + TOPK_SLICE - 1) / TOPK_SLICE;
-        bytes += a256(size_t(rows) * slices * 4);
-        bytes += 2 * a256(size_t(rows) * slices * size_t(selected) * 8);
+        extra = a256(size_t(rows) * slices * 4);
+        extra += 2 * a256(size_t(rows) * slices * size_t(selected) * 8);
     }
-    return bytes;
+    if (rows <= TOPK_SPREAD_MAX_ROWS && cols > TOPK_SPREAD_MIN_KEYS) {
+        // the ranked keys never exceed the columns
+        const int slices = (int)std::min<int64_t>((int64_t(cols) + TOPK_SPREAD_SLICE - 1) / TOPK_SPREAD_SLICE,
+                                                  TOPK_SPREAD_MAX_SLICES);
+        extra = std::max(extra, spread_layout(rows, slices).end);
+    }
+    return bytes + extra;
 }
 
 hipError_t launch_topk_select(const TopkParams& p0, void* workspace, int32_t* status, hipStream_t st) {
@@ -652,8 +1200,21 @@ hipError_t launch_topk_select(const TopkParams& p0, void* workspace, int32_t* st
     // a single row's status comes from the kernel that flags its NaN (the
     // selection, or the last merge round), not from a launch of its own
     p.status_direct = p.rows == 1 ? status : nullptr;
-    // keys per thread: the row's ranked keys in registers
-    if (p.available <= 256 * 4) {
+    if (spread_applies(p.rows, p.available)) {
+        // a few rows of many keys: each row over many workgroups
+        const int slices = (p.available + TOPK_SPREAD_SLICE - 1) / TOPK_SPREAD_SLICE;
+        char* ws = (char*)workspace + a256(size_t(p.rows) * 4);
+        const SpreadLayout L = spread_layout(p.rows, slices);
+        p.sp_slices = slices;
+        p.sp_coarse = (unsigned short*)(ws + L.coarse);
+        p.sp_off = (unsigned short*)(ws + L.off);
+        p.sp_sorted = (unsigned long long*)(ws + L.sorted);
+        hipLaunchKernelGGL(topk_spread_slice, dim3((unsigned)slices, (unsigned)p.rows), dim3(TK_SLICE_NT), 0, st, p);
+        hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+        hipLaunchKernelGGL(topk_spread_finish, dim3((unsigned)p.rows), dim3(1024), 0, st, p);
+    } else if (p.available <= 256 * 4) {
+        // keys per thread: the row's ranked keys in registers
         hipLaunchKernelGGL((topk_select_kernel<256, 4>), dim3((unsigned)p.rows), dim3(256), 0, st, p);
     } else if (p.available <= 1024 * 16) {
         hipLaunchKernelGGL((topk_select_kernel<1024, 16>), dim3((unsigned)p.rows), dim3(1024), 0, st, p);
@@ -661,7 +1222,6 @@ hipError_t launch_topk_select(const TopkParams& p0, void* workspace, int32_t* st
         hipLaunchKernelGGL((topk_select_kernel<1024, 32>), dim3((unsigned)p.rows), dim3(1024), 0, st, p);
     } else {
         // slices of 32768 keys in parallel, then pairwise merge rounds
-        auto a256 = [](size_t x) { return (x + 255) & ~size_t(255); };
         char* ws = (char*)workspace + a256(size_t(p.rows) * 4);
         const int slices = (p.available + TOPK_SLICE - 1) / TOPK_SLICE;
         const int max_slices = (p.cols + TOPK_SLICE - 1) / TOPK_SLICE;

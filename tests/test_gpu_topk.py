@@ -139,3 +139,31 @@ def test_decode_row_score_distributions(M, kind):
     else:
         s = np.exp(np.abs(u) * 3.0).astype(np.float32)
     compare(M, s, 2048, 4, 131071, 0, f"dist-{kind}")
+
+
+def test_spread_selection_branches(M):
+    # one decode row over many workgroups, through each ordering branch:
+    # half of the keys taken with the cut below zero (the taken composites
+    # span both signs, buckets fill up and each full one is sorted by a
+    # wave), a row whose keys through the cut value exceed the sort buffer
+    # (a radix select among the cut value's keys first), and a short last
+    # slice
+    compare(M, normal("tk.half", (1, 8192)) - np.float32(0.25), 4096, 1, 8191, 0, "half-8192")
+    compare(M, normal("tk.half2", (1, 4097)) - np.float32(0.25), 2048, 1, 4096, 3, "half-4097")
+    compare(M, normal("tk.sel", (1, 65536)), 4096, 1, 65535, 0, "select-65536-k4096")
+    compare(M, normal("tk.short", (1, 6145)), 1000, 1, 6144, 0, "short-last-slice-6145")
+
+
+def test_spread_nan_among_ranked_keys(M):
+    import torch
+
+    import minirun_hip as MH
+
+    s = normal("tk.nanmid", (1, 32768))
+    s[0, 12345] = np.nan
+    with pytest.raises(MH.MRError) as e:
+        M.lightning_select(dev(s), 2048, 4, 131071, 0)
+    assert e.value.status == MH.NONFINITE
+    status = torch.full((1,), -1, dtype=torch.int32, device="cuda")
+    M.lightning_select(dev(s), 2048, 4, 131071, 0, check=False, status=status)
+    assert int(status.item()) == MH.NONFINITE
