@@ -81,13 +81,13 @@ __global__ void __launch_bounds__(256) affine_dequant_kernel(AffineDequantParams
 // dotted the next two steps' weights are in flight.  Every load goes through
 // a buffer descriptor, so rows past the tile and groups past the row take an
 // out-of-buffer offset: they read zeros without a memory request or a branch.
-constexpr int GEMV_THREADS = 256;
+// NT threads (256, or 1024 so that each SIMD runs four waves on one staged
+// vector); a row of more than 64 threads sums its waves' parts through LDS.
 constexpr int GEMV_MAX_IN = 16384;  // activation length staged per vector
-constexpr int GEMV_MAX_CH = GEMV_MAX_IN / 8 / GEMV_THREADS;
 constexpr int GEMV_NPT_MAX = 4;  // groups per thread and row: tpr * GEMV_NPT >= G
 
-template <int SDT, int GEMV_NPT>
-__global__ void __launch_bounds__(GEMV_THREADS)
+template <int SDT, int GEMV_NPT, int NT>
+__global__ void __launch_bounds__(NT)
     affine_gemv4_kernel(AffineGemvParams p0, uint32_t wbytes0, uint32_t sbytes0, AffineGemvParams p1, uint32_t wbytes1,
                         uint32_t sbytes1, int tiles0) {
     // two weights of one activation vector in one launch: workgroups from
@@ -100,7 +100,10 @@ __global__ void __launch_bounds__(GEMV_THREADS)
     // start on different banks
     __shared__ __attribute__((aligned(16))) uint32_t xp[GEMV_MAX_IN / 2 + GEMV_MAX_IN / 16];
     __shared__ float xs[GEMV_MAX_IN / 64];                              // per-group sums of the staged x
-    __shared__ float red[GEMV_THREADS / 64];
+    constexpr int GEMV_THREADS = NT;
+    constexpr int GEMV_MAX_CH = GEMV_MAX_IN / 8 / NT;
+    __shared__ float red[NT / 64];
+    __shared__ float part[2][NT / 64];  // rows of more than one wave: the waves' sums, by step parity
     const int tile = (int)blockIdx.x - (second ? tiles0 : 0);
     const int xg = tile / p.tiles_per_vec;  // activation vector of this tile
     const int r0 = xg * p.map_a + (tile - xg * p.tiles_per_vec) * p.tile_rows;
@@ -232,7 +235,16 @@ __global__ void __launch_bounds__(GEMV_THREADS)
         ss = wave_sum(ss);
         if ((t & 63) == 0) red[t >> 6] = ss;
         __syncthreads();
-        ss = (red[0] + red[1]) + (red[2] + red[3]);
+        if (NT == 256) {
+            ss = (red[0] + red[1]) + (red[2] + red[3]);
+        } else {
+            float r4[NT / 256];
+#pragma unroll
+            for (int i = 0; i < NT / 256; ++i) r4[i] = (red[4 * i] + red[4 * i + 1]) + (red[4 * i + 2] + red[4 * i + 3]);
+            ss = 0.f;
+#pragma unroll
+            for (int i = 0; i < NT / 256; ++i) ss += r4[i];
+        }
         inv = 1.f / sqrtf(ss / (float)in + p.norm_eps);
     }
 #pragma unroll
@@ -314,8 +326,22 @@ __global__ void __launch_bounds__(GEMV_THREADS)
         }
         return acc;
     };
+    int fstep = 0;
     auto finish = [&](int j, float acc) {
-        acc = group_sum(acc, tpr);
+        if (tpr <= 64) {
+            acc = group_sum(acc, tpr);
+        } else {
+            // the row's waves: sums through LDS behind an LDS-only barrier
+            // (the weights in flight are not waited for)
+            acc = group_sum(acc, 64);
+            float* pp = part[fstep & 1];
+            if ((t & 63) == 0) pp[t >> 6] = acc;
+            lds_barrier();
+            const int w0 = (t - tl) >> 6;  // the row's first wave
+            acc = 0.f;
+            for (int i = 0; i < tpr / 64; ++i) acc += pp[w0 + i];
+            ++fstep;
+        }
         if (tl == 0 && j < r_end) {
             const int64_t o = (int64_t)j * p.y_stride_row;
             if (p.y_f32)
@@ -408,6 +434,13 @@ hipError_t launch_affine_dequant(const AffineDequantParams& p, hipStream_t st) {
     return hipGetLastError();
 }
 
+// Threads per workgroup of the 4-bit fast path: 1024 (one group per thread
+// and row, four waves per SIMD on one staged vector) for rows of at least
+// 128 groups, where the 256-thread form leaves one wave per SIMD with four
+// groups each and the dot latency exposed; 256 for shorter rows, whose
+// grid has too few row steps per CU for the larger workgroup.
+static int gemv_threads(int groups) { return groups >= 128 ? 1024 : 256; }
+
 // Weight rows the fast path addresses: the last activation vector's rows end
 // at (nvec - 1) * map_b + map_c + (its row count).
 static int64_t gemv_weight_rows(const AffineGemvParams& p) {
@@ -433,6 +466,7 @@ struct FastPlan {
     AffineGemvParams p;  // with tpr, tile_rows, tiles_per_vec set
     unsigned grid;
     int npt;
+    int nt;  // threads per workgroup
     uint32_t wbytes, sbytes;
 };
 
@@ -440,24 +474,31 @@ static FastPlan plan_fast(const AffineGemvParams& q) {
     FastPlan f;
     AffineGemvParams& p = f.p;
     p = q;
-    // threads per row: about G/4 groups each, more while the grid holds
-    // fewer row steps than the GPU has CUs; tiles of whole steps, at least
-    // one per CU
     const int G = p.in_features / 64;
     const int nvec = (p.out_rows + p.map_a - 1) / p.map_a;
     const int per_vec = std::min(p.map_a, p.out_rows);
+    const int nt = gemv_threads(G);
+    f.nt = nt;
+    auto steps = [&](int t) { return (int64_t)nvec * ((per_vec + nt / t - 1) / (nt / t)); };
     int tpr = 1;
-    while (tpr < 64 && tpr * 4 < G) tpr <<= 1;
-    auto steps = [&](int t) { return (int64_t)nvec * ((per_vec + GEMV_THREADS / t - 1) / (GEMV_THREADS / t)); };
-    while (tpr < 64 && steps(tpr) < 256) tpr <<= 1;
-    const int rps = GEMV_THREADS / tpr;
+    if (nt == 256) {
+        // about G/4 groups each, more while the grid holds fewer row steps
+        // than the GPU has CUs; tiles of whole steps, at least one per CU
+        while (tpr < 64 && tpr * 4 < G) tpr <<= 1;
+        while (tpr < 64 && steps(tpr) < 256) tpr <<= 1;
+    } else {
+        // one group each (three row sets fit the 128 registers of a
+        // 1024-thread workgroup only so)
+        while (tpr < G) tpr <<= 1;
+    }
+    const int rps = nt / tpr;
     const int64_t total = steps(tpr);
     const int64_t per_tile = std::max<int64_t>(1, total / 256);  // at least one tile per CU
     p.tpr = tpr;
     p.tile_rows = (int)std::min<int64_t>(per_tile * rps, per_vec);
     p.tiles_per_vec = (per_vec + p.tile_rows - 1) / p.tile_rows;
     f.grid = (unsigned)(nvec * p.tiles_per_vec);
-    f.npt = (G + tpr - 1) / tpr;  // 1 .. 4
+    f.npt = (G + tpr - 1) / tpr;  // 1 .. 4 (1 at 1024 threads)
     const int64_t w_rows = gemv_weight_rows(p);
     f.wbytes = (uint32_t)(w_rows * (p.in_features / 2));
     f.sbytes = (uint32_t)(w_rows * G * (p.scale_dtype == 2 ? 4 : 2));
@@ -469,9 +510,15 @@ static hipError_t launch_fast(const FastPlan& a, const FastPlan* b, hipStream_t 
     const FastPlan& s = b ? *b : a;
     const dim3 grid(a.grid + (b ? b->grid : 0));
     const int tiles0 = (int)a.grid;
-#define MR_GEMV4(SDT, NPT)                                                                                              \
-    hipLaunchKernelGGL((affine_gemv4_kernel<SDT, NPT>), grid, dim3(GEMV_THREADS), 0, st, a.p, a.wbytes, a.sbytes, s.p, \
-                       s.wbytes, s.sbytes, tiles0)
+#define MR_GEMV4(SDT, NPT)                                                                                   \
+    do {                                                                                                     \
+        if (a.nt == 1024)                                                                                    \
+            hipLaunchKernelGGL((affine_gemv4_kernel<SDT, 1, 1024>), grid, dim3(1024), 0, st, a.p,                 \
+                               a.wbytes, a.sbytes, s.p, s.wbytes, s.sbytes, tiles0);                         \
+        else                                                                                                 \
+            hipLaunchKernelGGL((affine_gemv4_kernel<SDT, NPT, 256>), grid, dim3(256), 0, st, a.p, a.wbytes,  \
+                               a.sbytes, s.p, s.wbytes, s.sbytes, tiles0);                                   \
+    } while (0)
 #define MR_GEMV4_NPT(SDT)     \
     do {                      \
         if (a.npt == 1)       \
@@ -497,7 +544,7 @@ static hipError_t launch_fast(const FastPlan& a, const FastPlan* b, hipStream_t 
 hipError_t launch_affine_gemv_pair(const AffineGemvParams& a, const AffineGemvParams& b, hipStream_t st) {
     if (affine_gemv_fast_ok(a) && affine_gemv_fast_ok(b) && a.scale_dtype == b.scale_dtype) {
         const FastPlan fa = plan_fast(a), fb = plan_fast(b);
-        if (fa.npt == fb.npt) return launch_fast(fa, &fb, st);
+        if (fa.npt == fb.npt && fa.nt == fb.nt) return launch_fast(fa, &fb, st);
     }
     const hipError_t e = launch_affine_gemv(a, st);
     return e != hipSuccess ? e : launch_affine_gemv(b, st);
