@@ -189,6 +189,38 @@ mr_status mr_affine_validate(mr_dtype packed_dtype, int32_t packed_rank, const i
                              int32_t group, int32_t bits, int64_t *experts, int64_t *out_features,
                              int64_t *in_features);
 
+/* AffineWeights.adopting (AffineWeights.swift:159-198): ownership of three
+ * caller buffers (packed uint32, scales, biases: device memory, or pinned
+ * host memory the device reads, such as the sub-regions of one StorageCore
+ * slot) passes to an adopted weight, each buffer with its own finalizer.
+ * Shapes follow the reference: packed [experts?, out, in * bits / 32],
+ * scales and biases [experts?, out, in / group] (experts 0: no expert axis),
+ * checked as mr_affine_validate checks them.
+ * As in the reference, the finalizers own the buffers from the call on:
+ * each runs exactly once, when the last reference to the weight is dropped
+ * and the GPU work that reads it has completed.  A failing call drops the
+ * weight at once, so all three have run when it returns its error.  They run
+ * on a HIP runtime thread or on the releasing thread and must not call HIP
+ * (the reference's release a buffer-pool lease, BufferPool.swift:45-90). */
+typedef void (*mr_finalizer)(void *context);
+typedef struct mr_adopted_affine mr_adopted_affine; /* opaque */
+mr_status mr_affine_adopt(void *packed, void *scales, void *biases, mr_dtype scale_dtype, int64_t experts,
+                          int64_t out_features, int64_t in_features, int32_t group, int32_t bits,
+                          mr_finalizer packed_finalizer, void *packed_context, mr_finalizer scales_finalizer,
+                          void *scales_context, mr_finalizer biases_finalizer, void *biases_context,
+                          mr_adopted_affine **out);
+/* The adopted weight as a descriptor for mr_affine_matmul and the others (a
+ * view: valid while a reference is held). */
+mr_status mr_adopted_affine_weight(const mr_adopted_affine *a, mr_affine_weight *out);
+/* One more reference (another holder of the AffineWeights value), from any thread. */
+mr_status mr_adopted_affine_retain(mr_adopted_affine *a);
+/* Drops one reference, from any thread.  Dropping the last one enqueues the
+ * finalizers on `stream` behind the work already there, which must include
+ * every read of the weight (order reads on other streams before it with an
+ * event); with stream NULL they run before the call returns (no GPU work
+ * reads the weight any more).  The handle is invalid after its last release. */
+mr_status mr_adopted_affine_release(mr_adopted_affine *a, void *stream);
+
 /* affineDequantize (AffineWeights.swift:328-342): dense [out, in] in f32
  * (default, bit-exact: the bf16/f16-scale product is exact in fp32) or
  * bf16 (round-to-nearest-even of the f32 value). */

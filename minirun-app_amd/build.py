@@ -31,7 +31,7 @@ FLAGS = [
     "-I", CSRC,
 ]
 
-LIB_SOURCES = ["capi.cpp", "capi_block.cpp", "capi_prefill.cpp", "capi_topk.cpp", "decode.hip", "affine.hip",
+LIB_SOURCES = ["capi.cpp", "capi_adopt.cpp", "capi_block.cpp", "capi_prefill.cpp", "capi_topk.cpp", "decode.hip", "affine.hip",
                "mla_block.hip", "prefill.hip", "topk.hip", "indexer.hip", "linear.hip"]
 # Per-source flags.  The decode kernel keeps its MFMA accumulators in VGPRs
 # (VGPR-form MFMA): with the AGPR form the compiler shuttles all 64 of them

@@ -143,6 +143,11 @@ SIGNATURES = {
     "mr_affine_tile_view": (C.c_int, [_P, C.c_int64, C.c_int64, C.c_int32, C.c_int32, C.c_int,
                                       C.POINTER(AffineWeightDesc), C.POINTER(C.c_int64)]),
     "mr_tile_upload": (C.c_int, [_P, _P, C.c_int64, _P]),
+    "mr_affine_adopt": (C.c_int, [_P, _P, _P, C.c_int, C.c_int64, C.c_int64, C.c_int64, C.c_int32, C.c_int32,
+                                  _P, _P, _P, _P, _P, _P, C.POINTER(_P)]),
+    "mr_adopted_affine_weight": (C.c_int, [_P, C.POINTER(AffineWeightDesc)]),
+    "mr_adopted_affine_retain": (C.c_int, [_P]),
+    "mr_adopted_affine_release": (C.c_int, [_P, _P]),
     "mr_affine_gather_matmul": (C.c_int, [_P, C.c_int, C.c_int32, C.c_int64, C.POINTER(AffineWeightDesc), C.c_int64,
                                           _P, C.c_int32, _P, C.c_int, _P]),
     "mr_rmsnorm": (C.c_int, [_P, C.c_int, C.c_int64, C.c_int32, C.c_int64, _P, C.c_int, C.c_float, _P, C.c_int,
@@ -380,6 +385,44 @@ class AffineWeights:
     def desc(self):
         return AffineWeightDesc(self.packed.data_ptr(), self.scales.data_ptr(), self.biases.data_ptr(),
                                 self.scale_dtype, self.out_features, self.in_features, self.group_size, self.bits)
+
+
+FINALIZER = C.CFUNCTYPE(None, C.c_void_p)
+
+
+class AdoptedAffineWeights:
+    """AffineWeights.adopting (AffineWeights.swift:159-198): the three buffers
+    (device pointers, or pinned host memory the device reads) pass to the
+    library with a finalizer each (Python callables of one argument, the
+    context pointer).  Each finalizer runs exactly once, when the last
+    reference is released and the named stream has passed every read; a
+    failed adoption runs them before raising.  Shapes: packed [experts?, out,
+    in*bits/32], scales/biases [experts?, out, in/group]."""
+
+    def __init__(self, packed_ptr, scales_ptr, biases_ptr, scale_dtype, out_features, in_features, *,
+                 experts=0, group_size=64, bits=4, finalizers=(None, None, None), contexts=(None, None, None)):
+        # the ctypes callbacks must outlive the weight: the library calls them last
+        self._cbs = [FINALIZER(f) if f is not None else None for f in finalizers]
+        cb = [C.cast(c, _P) if c is not None else None for c in self._cbs]
+        h = _P()
+        _check(load().mr_affine_adopt(packed_ptr, scales_ptr, biases_ptr, scale_dtype, experts, out_features,
+                                      in_features, group_size, bits, cb[0], contexts[0], cb[1], contexts[1], cb[2],
+                                      contexts[2], C.byref(h)))
+        self.handle = h.value
+        self.out_features, self.in_features = out_features, in_features
+
+    def desc(self):
+        d = AffineWeightDesc()
+        _check(load().mr_adopted_affine_weight(self.handle, C.byref(d)))
+        return d
+
+    def retain(self):
+        _check(load().mr_adopted_affine_retain(self.handle))
+
+    def release(self, stream=None):
+        """Drop one reference; the last one runs the finalizers behind the
+        work on `stream` (a torch stream or a raw handle), or now when None."""
+        _check(load().mr_adopted_affine_release(self.handle, _stream(stream) if stream is not None else None))
 
 
 class DenseWeights:

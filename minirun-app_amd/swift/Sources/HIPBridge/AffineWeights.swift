@@ -79,3 +79,60 @@ public struct HIPAffineTile {
         try HIPError.check(mr_tile_upload(device, pinned, Int64(bytes), stream))
     }
 }
+
+/// A finalizer handed to the library: the Swift closure boxed as the C
+/// callback's context, freed once the callback has run it.
+private final class HIPFinalizerBox {
+    let run: () -> Void
+    init(_ run: @escaping () -> Void) { self.run = run }
+}
+
+private let hipRunFinalizer: mr_finalizer = { context in
+    guard let context else { return }
+    let box = Unmanaged<HIPFinalizerBox>.fromOpaque(context).takeRetainedValue()
+    box.run()
+}
+
+/// AffineWeights.adopting(packedPointer:scalesPointer:biasesPointer:scaleDType:experts:outFeatures:
+/// inFeatures:groupSize:bits:packedFinalizer:scalesFinalizer:biasesFinalizer:)
+/// (MLXBridge/AffineWeights.swift:159-198): ownership of the three buffers
+/// passes to the weight.  Each finalizer runs exactly once, after the last
+/// reference is released and the named stream has passed every read, on a
+/// HIP runtime thread or the releasing one (BufferPool.swift:45-90 releases
+/// leases from such callbacks); a failed adoption runs them before throwing,
+/// as the reference's arrays own the pointers before its validation.
+public final class HIPAdoptedAffineWeights {
+    public let handle: OpaquePointer
+    public let weights: HIPAffineWeights
+
+    public init(packedPointer: UnsafeMutableRawPointer, scalesPointer: UnsafeMutableRawPointer,
+                biasesPointer: UnsafeMutableRawPointer, scaleDType: mr_dtype, experts: Int? = nil,
+                outFeatures: Int, inFeatures: Int, groupSize: Int, bits: Int,
+                packedFinalizer: @escaping () -> Void, scalesFinalizer: @escaping () -> Void,
+                biasesFinalizer: @escaping () -> Void) throws {
+        let ctx = [packedFinalizer, scalesFinalizer, biasesFinalizer].map {
+            Unmanaged.passRetained(HIPFinalizerBox($0)).toOpaque()
+        }
+        var h: OpaquePointer?
+        try HIPError.check(mr_affine_adopt(packedPointer, scalesPointer, biasesPointer, scaleDType,
+                                           Int64(experts ?? 0), Int64(outFeatures), Int64(inFeatures),
+                                           Int32(groupSize), Int32(bits), hipRunFinalizer, ctx[0],
+                                           hipRunFinalizer, ctx[1], hipRunFinalizer, ctx[2], &h))
+        handle = h!
+        var d = mr_affine_weight()
+        try HIPError.check(mr_adopted_affine_weight(handle, &d))
+        weights = HIPAffineWeights(desc: d)
+    }
+
+    /// Another holder of the weight (a copy of the AffineWeights value in
+    /// the reference, AffineWeights.swift:171-198).
+    public func retain() throws {
+        try HIPError.check(mr_adopted_affine_retain(handle))
+    }
+
+    /// Drops one holder; the last one runs the finalizers behind the work
+    /// already enqueued on `stream` (nil: now, no GPU work reads the weight).
+    public func release(after stream: HIPStream = nil) throws {
+        try HIPError.check(mr_adopted_affine_release(handle, stream))
+    }
+}
