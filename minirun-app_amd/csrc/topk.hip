@@ -20,7 +20,7 @@
 //   3. a bitonic sort of those composites in LDS gives the final order.
 // The row's NaN flag (any NaN among all `cols` scores) goes to nan_flags.
 //
-// A few rows of more than 4096 keys (a decode token's row) spread over many
+// A few rows of more than 1024 keys (a decode token's row) spread over many
 // workgroups instead: see topk_spread_slice / topk_spread_finish.
 //
 // Other rows of more than 32768 keys split into slices of 32768, one workgroup
@@ -1154,7 +1154,7 @@ namespace {
 size_t a256(size_t x) { return (x + 255) & ~size_t(255); }
 
 // Rows of more keys than this (and few rows) take the spread selection.
-constexpr int TOPK_SPREAD_MIN_KEYS = 4096;
+constexpr int TOPK_SPREAD_MIN_KEYS = 1024;
 
 bool spread_applies(int32_t rows, int32_t keys) {
     return rows <= TOPK_SPREAD_MAX_ROWS && keys > TOPK_SPREAD_MIN_KEYS &&
