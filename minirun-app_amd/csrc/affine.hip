@@ -81,10 +81,12 @@ __global__ void __launch_bounds__(256) affine_dequant_kernel(AffineDequantParams
 // dotted the next two steps' weights are in flight.  Every load goes through
 // a buffer descriptor, so rows past the tile and groups past the row take an
 // out-of-buffer offset: they read zeros without a memory request or a branch.
-// NT threads (256, or 1024 so that each SIMD runs four waves on one staged
-// vector); a row of more than 64 threads sums its waves' parts through LDS.
+// NT = 512 threads (two waves per SIMD on one staged vector, each thread
+// dotting at most two groups of a row); a row of more than 64 threads sums
+// its waves' parts through LDS.
+constexpr int GEMV_NT = 512;
 constexpr int GEMV_MAX_IN = 16384;  // activation length staged per vector
-constexpr int GEMV_NPT_MAX = 4;  // groups per thread and row: tpr * GEMV_NPT >= G
+constexpr int GEMV_NPT_MAX = 2;  // groups per thread and row: tpr * GEMV_NPT >= G
 
 template <int SDT, int GEMV_NPT, int NT>
 __global__ void __launch_bounds__(NT)
@@ -434,13 +436,6 @@ hipError_t launch_affine_dequant(const AffineDequantParams& p, hipStream_t st) {
     return hipGetLastError();
 }
 
-// Threads per workgroup of the 4-bit fast path: 1024 (one group per thread
-// and row, four waves per SIMD on one staged vector) for rows of at least
-// 128 groups, where the 256-thread form leaves one wave per SIMD with four
-// groups each and the dot latency exposed; 256 for shorter rows, whose
-// grid has too few row steps per CU for the larger workgroup.
-static int gemv_threads(int groups) { return groups >= 128 ? 1024 : 256; }
-
 // Weight rows the fast path addresses: the last activation vector's rows end
 // at (nvec - 1) * map_b + map_c + (its row count).
 static int64_t gemv_weight_rows(const AffineGemvParams& p) {
@@ -453,7 +448,7 @@ static int64_t gemv_weight_rows(const AffineGemvParams& p) {
 bool affine_gemv_fast_ok(const AffineGemvParams& p) {
     return !p.force_generic && p.bits == 4 && p.group == 64 && !p.x_f32 && p.m == 1 && p.in_features <= GEMV_MAX_IN &&
            p.in_features % 64 == 0 && ((uintptr_t)p.x & 15) == 0 && p.x_stride % 8 == 0 &&
-           p.in_features <= 64 * GEMV_NPT_MAX * 64 && (!p.norm_w || ((uintptr_t)p.norm_w & 15) == 0) &&
+           p.in_features <= 64 * GEMV_NPT_MAX * GEMV_NT && (!p.norm_w || ((uintptr_t)p.norm_w & 15) == 0) &&
            // 32-bit buffer offsets (24-bit row numbers) reach every weight and
            // scale byte, with 2^31 free above them for the out-of-buffer offset
            gemv_weight_rows(p) < (int64_t(1) << 24) &&
@@ -477,28 +472,24 @@ static FastPlan plan_fast(const AffineGemvParams& q) {
     const int G = p.in_features / 64;
     const int nvec = (p.out_rows + p.map_a - 1) / p.map_a;
     const int per_vec = std::min(p.map_a, p.out_rows);
-    const int nt = gemv_threads(G);
+    const int nt = GEMV_NT;
     f.nt = nt;
     auto steps = [&](int t) { return (int64_t)nvec * ((per_vec + nt / t - 1) / (nt / t)); };
+    // threads per row: at most two groups each (two waves per SIMD; a row of
+    // more than 64 threads sums its waves through LDS), more while the grid
+    // holds fewer row steps than the GPU has CUs; tiles of whole steps, at
+    // least one per CU
     int tpr = 1;
-    if (nt == 256) {
-        // about G/4 groups each, more while the grid holds fewer row steps
-        // than the GPU has CUs; tiles of whole steps, at least one per CU
-        while (tpr < 64 && tpr * 4 < G) tpr <<= 1;
-        while (tpr < 64 && steps(tpr) < 256) tpr <<= 1;
-    } else {
-        // one group each (three row sets fit the 128 registers of a
-        // 1024-thread workgroup only so)
-        while (tpr < G) tpr <<= 1;
-    }
+    while (tpr < nt && tpr * 2 < G) tpr <<= 1;
+    while (tpr < 64 && steps(tpr) < 256) tpr <<= 1;
     const int rps = nt / tpr;
     const int64_t total = steps(tpr);
-    const int64_t per_tile = std::max<int64_t>(1, total / 256);  // at least one tile per CU
+    const int64_t per_tile = std::max<int64_t>(1, total / 256);
     p.tpr = tpr;
     p.tile_rows = (int)std::min<int64_t>(per_tile * rps, per_vec);
     p.tiles_per_vec = (per_vec + p.tile_rows - 1) / p.tile_rows;
     f.grid = (unsigned)(nvec * p.tiles_per_vec);
-    f.npt = (G + tpr - 1) / tpr;  // 1 .. 4 (1 at 1024 threads)
+    f.npt = (G + tpr - 1) / tpr;  // 1 or 2
     const int64_t w_rows = gemv_weight_rows(p);
     f.wbytes = (uint32_t)(w_rows * (p.in_features / 2));
     f.sbytes = (uint32_t)(w_rows * G * (p.scale_dtype == 2 ? 4 : 2));
@@ -508,27 +499,18 @@ static FastPlan plan_fast(const AffineGemvParams& q) {
 // One launch of a (or of a and b, which share the template instance).
 static hipError_t launch_fast(const FastPlan& a, const FastPlan* b, hipStream_t st) {
     const FastPlan& s = b ? *b : a;
+    if (a.npt > 2 || (b && b->npt != a.npt)) return hipErrorInvalidValue;  // the instances hold 1 or 2 groups
     const dim3 grid(a.grid + (b ? b->grid : 0));
     const int tiles0 = (int)a.grid;
-#define MR_GEMV4(SDT, NPT)                                                                                   \
-    do {                                                                                                     \
-        if (a.nt == 1024)                                                                                    \
-            hipLaunchKernelGGL((affine_gemv4_kernel<SDT, 1, 1024>), grid, dim3(1024), 0, st, a.p,                 \
-                               a.wbytes, a.sbytes, s.p, s.wbytes, s.sbytes, tiles0);                         \
-        else                                                                                                 \
-            hipLaunchKernelGGL((affine_gemv4_kernel<SDT, NPT, 256>), grid, dim3(256), 0, st, a.p, a.wbytes,  \
-                               a.sbytes, s.p, s.wbytes, s.sbytes, tiles0);                                   \
-    } while (0)
+#define MR_GEMV4(SDT, NPT)                                                                                         \
+    hipLaunchKernelGGL((affine_gemv4_kernel<SDT, NPT, GEMV_NT>), grid, dim3(GEMV_NT), 0, st, a.p, a.wbytes, a.sbytes, \
+                       s.p, s.wbytes, s.sbytes, tiles0)
 #define MR_GEMV4_NPT(SDT)     \
     do {                      \
         if (a.npt == 1)       \
             MR_GEMV4(SDT, 1); \
-        else if (a.npt == 2)  \
-            MR_GEMV4(SDT, 2); \
-        else if (a.npt == 3)  \
-            MR_GEMV4(SDT, 3); \
         else                  \
-            MR_GEMV4(SDT, 4); \
+            MR_GEMV4(SDT, 2); \
     } while (0)
     if (a.p.scale_dtype == 0)
         MR_GEMV4_NPT(0);
