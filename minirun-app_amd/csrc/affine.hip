@@ -15,6 +15,7 @@
 #include <algorithm>
 #include <type_traits>
 
+#include "capi_util.hpp"
 #include "mr_kernels.hpp"
 
 // Products and sums below round exactly as written: hipcc contracts a*b+c
@@ -462,10 +463,18 @@ struct FastPlan {
     unsigned grid;
     int npt;
     int nt;  // threads per workgroup
+    int64_t steps;  // row steps of the whole launch
     uint32_t wbytes, sbytes;
 };
 
-static FastPlan plan_fast(const AffineGemvParams& q) {
+// Workgroups of the fast path one CU holds at once: the two-group instance
+// takes 193 registers per lane (one 512-thread workgroup per CU), the
+// one-group instance 95 (two).
+static int64_t gemv_slots(int npt) { return (int64_t)mrc::cu_count() * (npt == 1 ? 2 : 1); }
+
+// per_tile 0: tiles of ceil(steps / slots) row steps, so the launch runs in
+// one round of workgroups (a second round repeats the whole staging chain)
+static FastPlan plan_fast(const AffineGemvParams& q, int64_t per_tile_req = 0) {
     FastPlan f;
     AffineGemvParams& p = f.p;
     p = q;
@@ -484,12 +493,15 @@ static FastPlan plan_fast(const AffineGemvParams& q) {
     while (tpr < 64 && steps(tpr) < 256) tpr <<= 1;
     const int rps = nt / tpr;
     const int64_t total = steps(tpr);
-    const int64_t per_tile = std::max<int64_t>(1, total / 256);
+    const int npt = (G + tpr - 1) / tpr;
+    const int64_t slots = gemv_slots(npt);
+    const int64_t per_tile = per_tile_req > 0 ? per_tile_req : std::max<int64_t>(1, (total + slots - 1) / slots);
+    f.steps = total;
     p.tpr = tpr;
     p.tile_rows = (int)std::min<int64_t>(per_tile * rps, per_vec);
     p.tiles_per_vec = (per_vec + p.tile_rows - 1) / p.tile_rows;
     f.grid = (unsigned)(nvec * p.tiles_per_vec);
-    f.npt = (G + tpr - 1) / tpr;  // 1 or 2
+    f.npt = npt;  // 1 or 2
     const int64_t w_rows = gemv_weight_rows(p);
     f.wbytes = (uint32_t)(w_rows * (p.in_features / 2));
     f.sbytes = (uint32_t)(w_rows * G * (p.scale_dtype == 2 ? 4 : 2));
@@ -525,8 +537,17 @@ static hipError_t launch_fast(const FastPlan& a, const FastPlan* b, hipStream_t 
 
 hipError_t launch_affine_gemv_pair(const AffineGemvParams& a, const AffineGemvParams& b, hipStream_t st) {
     if (affine_gemv_fast_ok(a) && affine_gemv_fast_ok(b) && a.scale_dtype == b.scale_dtype) {
-        const FastPlan fa = plan_fast(a), fb = plan_fast(b);
-        if (fa.npt == fb.npt && fa.nt == fb.nt) return launch_fast(fa, &fb, st);
+        FastPlan fa = plan_fast(a), fb = plan_fast(b);
+        if (fa.npt == fb.npt && fa.nt == fb.nt) {
+            // one round of workgroups for the two together
+            const int64_t slots = gemv_slots(fa.npt);
+            if ((int64_t)fa.grid + fb.grid > slots) {
+                const int64_t per_tile = (fa.steps + fb.steps + slots - 1) / slots;
+                fa = plan_fast(a, per_tile);
+                fb = plan_fast(b, per_tile);
+            }
+            return launch_fast(fa, &fb, st);
+        }
     }
     const hipError_t e = launch_affine_gemv(a, st);
     return e != hipSuccess ? e : launch_affine_gemv(b, st);
