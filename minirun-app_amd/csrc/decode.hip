@@ -23,6 +23,8 @@
 //   index check = with a device status buffer, `batch` extra workgroups at the
 //                 front of the gathered launch check each token's list
 //                 (validate_token) while the others attend
+#include <type_traits>
+
 #include "mr_kernels.hpp"
 
 namespace mr {
@@ -659,14 +661,17 @@ __global__ void __launch_bounds__((WsShape<HGS, QK16>::THREADS), 1) mla_decode_w
 // a wave reads four whole 256-byte pieces, and the first COMBINE_PF loads of
 // every lane are in flight before the weights are computed.
 constexpr int COMBINE_THREADS = 256;
-constexpr int COMBINE_PF = 8;  // 128 splits in flight per block
 
-template <bool F32>
+// PF record loads per lane in flight (16 PF splits) and MLK (m, l) loads per
+// thread (256 MLK splits), both at least the launch's split count needs, so
+// the unconditional loads below are not mostly duplicates of the last split.
+template <bool F32, int PF, int MLK>
 __global__ void __launch_bounds__(COMBINE_THREADS) mla_combine(CombineParams p) {
     constexpr int VPL = F32 ? 4 : 8;  // values per lane (16 bytes)
     constexpr int CB = 16 * VPL;      // columns per block
     constexpr int NCB = R / CB;
-    constexpr int MLK = MAX_COMBINE_SPLITS / COMBINE_THREADS;
+    constexpr int COMBINE_PF = PF;
+    static_assert(MLK * COMBINE_THREADS <= MAX_COMBINE_SPLITS, "split weights");
     __shared__ float wgt[MAX_COMBINE_SPLITS];
     __shared__ float red_m[4], red_l[4];
     __shared__ __attribute__((aligned(16))) float part[4][16][VPL];
@@ -683,24 +688,23 @@ __global__ void __launch_bounds__(COMBINE_THREADS) mla_combine(CombineParams p) 
     constexpr int RB = R * (F32 ? 4 : 2);  // bytes per record
     const char* base = (const char*)p.ws_o + rec0 * RB + 256 * cb + 16 * ch;
 
-    // (m, l) of every split first: the weights wait only on these
+    // (m, l) of every split first: the weights wait only on these.  Every
+    // load is issued unconditionally (indices clamped to the last split, the
+    // extra values weighted out), so the compiler's waits count exactly and
+    // the max and the sum run while the records are still in flight.
     float ml_m[MLK], ml_l[MLK];
 #pragma unroll
     for (int k = 0; k < MLK; ++k) {
         const int s = tid + COMBINE_THREADS * k;
-        ml_m[k] = NEG_INF;
-        ml_l[k] = 0.f;
-        if (s < p.splits) {
-            const f32x2 ml = *(const f32x2*)(p.ws_ml + (rec0 + s) * 2);
-            ml_m[k] = ml[0];
-            ml_l[k] = ml[1];
-        }
+        const f32x2 ml = *(const f32x2*)(p.ws_ml + (rec0 + min(s, p.splits - 1)) * 2);
+        ml_m[k] = s < p.splits ? ml[0] : NEG_INF;
+        ml_l[k] = s < p.splits ? ml[1] : 0.f;
     }
     u32x4 x[COMBINE_PF];
 #pragma unroll
     for (int k = 0; k < COMBINE_PF; ++k) {
         const int s = 16 * k + 4 * w + sg;
-        x[k] = s < p.splits ? *(const u32x4*)(base + (int64_t)s * RB) : u32x4{0u, 0u, 0u, 0u};
+        x[k] = *(const u32x4*)(base + (int64_t)min(s, p.splits - 1) * RB);
     }
     float M = NEG_INF;
 #pragma unroll
@@ -1056,10 +1060,35 @@ hipError_t launch_mla_decode(const DecodeParams& p, const CombineParams& cp, boo
     if (e != hipSuccess) return e;
     if (events && (e = hipEventRecord(events[1], st)) != hipSuccess) return e;
     if (split_only) return events ? hipEventRecord(events[2], st) : hipSuccess;
+    // loads in flight for the split count: 16 PF splits of records (at most
+    // 128; more are read by the tail loop) and 256 MLK of (m, l) pairs
+    const int pf = cp.splits <= 16 ? 1 : cp.splits <= 32 ? 2 : cp.splits <= 64 ? 4 : 8;
+    const bool mlk4 = cp.splits > COMBINE_THREADS;
+    auto combine = [&](auto f32_tag, auto pf_tag, auto mlk_tag) {
+        constexpr bool F = decltype(f32_tag)::value;
+        hipLaunchKernelGGL((mla_combine<F, decltype(pf_tag)::value, decltype(mlk_tag)::value>),
+                           dim3(p.batch * p.heads * (R / (F ? 64 : 128))), dim3(COMBINE_THREADS), 0, st, cp);
+    };
+    auto by_pf = [&](auto f32_tag, auto mlk_tag) {
+        if (pf == 1)
+            combine(f32_tag, std::integral_constant<int, 1>{}, mlk_tag);
+        else if (pf == 2)
+            combine(f32_tag, std::integral_constant<int, 2>{}, mlk_tag);
+        else if (pf == 4)
+            combine(f32_tag, std::integral_constant<int, 4>{}, mlk_tag);
+        else
+            combine(f32_tag, std::integral_constant<int, 8>{}, mlk_tag);
+    };
+    auto by_mlk = [&](auto f32_tag) {
+        if (mlk4)
+            by_pf(f32_tag, std::integral_constant<int, MAX_COMBINE_SPLITS / COMBINE_THREADS>{});
+        else
+            by_pf(f32_tag, std::integral_constant<int, 1>{});
+    };
     if (cp.ws_f32)
-        hipLaunchKernelGGL(mla_combine<true>, dim3(p.batch * p.heads * (R / 64)), dim3(COMBINE_THREADS), 0, st, cp);
+        by_mlk(std::true_type{});
     else
-        hipLaunchKernelGGL(mla_combine<false>, dim3(p.batch * p.heads * (R / 128)), dim3(COMBINE_THREADS), 0, st, cp);
+        by_mlk(std::false_type{});
     if ((e = hipGetLastError()) != hipSuccess) return e;
     if (events && (e = hipEventRecord(events[2], st)) != hipSuccess) return e;
     return hipSuccess;
