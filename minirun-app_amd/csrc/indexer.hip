@@ -38,23 +38,33 @@ constexpr int IX_KS = 4;      // 32-dim MFMA steps: D = 128
 
 template <int HT>
 __global__ void __launch_bounds__(256) indexer_scores_mfma(IndexerParams p) {
+    // the token's queries (16 HT rows of 128 dims, rows padded by 16 bytes so
+    // the fragment reads spread over the banks) and head weights, staged
+    // once per workgroup: every wave needs all of them
+    __shared__ __attribute__((aligned(16))) uint16_t qs[16 * HT][128 + 8];
+    __shared__ float hw[16 * HT];
     const int s = blockIdx.y;
-    const int l = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int t = threadIdx.x, l = t & 63, w = t >> 6;
     const int key0 = blockIdx.x * IX_KEYS + 32 * w;
-    // Q rows of this token: A operands for every (head tile, k step)
+    // queries first, then the keys: the staging waits for the queries only
+    // (loads complete in order), the keys stay in flight across the barrier
     const uint16_t* q = (const uint16_t*)p.q + (int64_t)s * p.q_ss;
-    bf16x8 qa[HT][IX_KS];
+    static_assert(16 * HT * 16 <= 4 * 256, "query chunks per thread");
+    bf16x8 qc[HT];
 #pragma unroll
-    for (int ht = 0; ht < HT; ++ht)
-#pragma unroll
-        for (int ks = 0; ks < IX_KS; ++ks)
-            qa[ht][ks] = *(const bf16x8*)(q + (int64_t)(16 * ht + (l & 15)) * p.q_hs + 32 * ks + 8 * (l >> 4));
-    // head weights of the D rows this lane holds: head 16ht + 4(l/16) + i
-    float wv[HT][4];
-#pragma unroll
-    for (int ht = 0; ht < HT; ++ht)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) wv[ht][i] = ix_ld(p.w, p.w_f32, (int64_t)s * p.w_ss + 16 * ht + 4 * (l >> 4) + i);
+    for (int i = 0; i < HT; ++i) {
+        const int c = t + 256 * i, r = c >> 4, k = c & 15;  // 16-byte chunk k of query row r
+        qc[i] = *(const bf16x8*)(q + (int64_t)r * p.q_hs + 8 * k);
+    }
+    // the head weight of thread t < 16 HT: one unconditional dword load (the
+    // dword holding a bf16 weight, through a descriptor that bounds the row
+    // set), its half picked once the keys are issued
+    const uint32_t esz = p.w_f32 ? 4u : 2u;
+    const __amdgpu_buffer_rsrc_t wres = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)p.w, 0, (int)(((int64_t)(p.S - 1) * p.w_ss + p.H) * esz), 0x00020000);
+    const uint32_t wa = (uint32_t)(((int64_t)s * p.w_ss + min(t, 16 * HT - 1)) * esz);
+    const uint32_t wraw = __builtin_amdgcn_raw_buffer_load_b32(wres, wa & ~3u, 0, 0);
+    asm volatile("" ::: "memory");  // the key loads issue after the query and weight loads
     // keys: B operands of both 16-key tiles
     const __amdgpu_buffer_rsrc_t kres = __builtin_amdgcn_make_buffer_rsrc((void*)p.k, 0, (int)p.k_bytes, 0x00020000);
     bf16x8 kb[2][IX_KS];
@@ -65,6 +75,25 @@ __global__ void __launch_bounds__(256) indexer_scores_mfma(IndexerParams p) {
 #pragma unroll
         for (int ks = 0; ks < IX_KS; ++ks)
             kb[kt][ks] = __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(kres, base + 64u * ks, 0, 0));
+    }
+#pragma unroll
+    for (int i = 0; i < HT; ++i) {
+        const int c = t + 256 * i;
+        *(bf16x8*)&qs[c >> 4][8 * (c & 15)] = qc[i];
+    }
+    if (t < 16 * HT)
+        hw[t] = p.w_f32 ? __uint_as_float(wraw) : __uint_as_float((wa & 2u) ? wraw & 0xffff0000u : wraw << 16);
+    lds_barrier();
+    // A operands for every (head tile, k step), and the head weights of the
+    // D rows this lane holds: head 16ht + 4(l/16) + i
+    bf16x8 qa[HT][IX_KS];
+    float wv[HT][4];
+#pragma unroll
+    for (int ht = 0; ht < HT; ++ht) {
+#pragma unroll
+        for (int ks = 0; ks < IX_KS; ++ks) qa[ht][ks] = *(const bf16x8*)&qs[16 * ht + (l & 15)][32 * ks + 8 * (l >> 4)];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) wv[ht][i] = hw[16 * ht + 4 * (l >> 4) + i];
     }
     f32x4 acc[2][HT];
 #pragma unroll
