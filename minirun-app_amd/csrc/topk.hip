@@ -89,7 +89,8 @@ constexpr int TK_BUCKET_MAX = 32;
 // Bitonic sort of the 64 EPT composites one wave holds in registers (lane l:
 // elements EPT l .. EPT l + EPT-1), ascending within every run of wsize
 // elements (wsize a power of two, 2 <= wsize <= 64 EPT).  The lane exchanges
-// have constant distances (DPP / permlane swaps, shuffles below 16).
+// have constant distances: DPP moves inside rows of 16 lanes, permlane swaps
+// across them (no LDS round trips).
 template <int EPT>
 __device__ void wave_sort(unsigned long long (&x)[EPT], int wsize) {
     const int tid = threadIdx.x;
@@ -116,9 +117,21 @@ __device__ void wave_sort(unsigned long long (&x)[EPT], int wsize) {
             const auto c = __builtin_amdgcn_permlane16_swap(hi, hi, false, false);
             rlo = (lane & 16) ? a[0] : a[1];
             rhi = (lane & 16) ? c[0] : c[1];
+        } else if constexpr (LD <= 2) {
+            // quad_perm 1,0,3,2 / 2,3,0,1
+            constexpr int Q = LD == 1 ? 0xB1 : 0x4E;
+            rlo = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)lo, Q, 0xf, 0xf, false);
+            rhi = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)hi, Q, 0xf, 0xf, false);
         } else {
-            rlo = __shfl_xor(lo, LD);
-            rhi = __shfl_xor(hi, LD);
+            // row_shl:LD for the lower lane of a pair (partner LD up, in
+            // the same row of 16), row_shr:LD for the upper one
+            constexpr int SHL = 0x100 + LD, SHR = 0x110 + LD;
+            const uint32_t ulo = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)lo, SHL, 0xf, 0xf, false);
+            const uint32_t uhi = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)hi, SHL, 0xf, 0xf, false);
+            const uint32_t dlo = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)lo, SHR, 0xf, 0xf, false);
+            const uint32_t dhi = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)hi, SHR, 0xf, 0xf, false);
+            rlo = (lane & LD) ? dlo : ulo;
+            rhi = (lane & LD) ? dhi : uhi;
         }
         return ((unsigned long long)rhi << 32) | rlo;
     };
@@ -664,6 +677,24 @@ __device__ __forceinline__ void rank_bin256(const uint32_t* h, uint32_t rank, ui
 
 constexpr int TK_SLICE_NT = 512;  // threads of a slice workgroup
 
+// atomicAdd(&a[i], 1) for the lanes with `on`, returning each its slot (the
+// old value plus its rank): the lanes that share the wave's first active
+// index add once, so keys of one score (ties, a dominant value) do not
+// serialise on one LDS address.  Lanes outside the branch take no part.
+__device__ __forceinline__ uint32_t agg_inc(uint32_t* a, uint32_t i, bool on) {
+    const unsigned long long act = __ballot(on);
+    if (act == 0ull) return 0u;
+    const int lead = __ffsll((long long)act) - 1;
+    const uint32_t i0 = (uint32_t)__builtin_amdgcn_readlane((int)i, lead);
+    const bool mine = on && i == i0;
+    const unsigned long long same = __ballot(mine);
+    uint32_t base = 0u;
+    if ((int)(threadIdx.x & 63) == lead) base = atomicAdd(&a[i0], (uint32_t)__popcll(same));
+    base = (uint32_t)__builtin_amdgcn_readlane((int)base, lead);
+    if (mine) return base + __builtin_amdgcn_mbcnt_hi((uint32_t)(same >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)same, 0u));
+    return on ? atomicAdd(&a[i], 1u) : 0u;
+}
+
 __global__ void __launch_bounds__(TK_SLICE_NT) topk_spread_slice(TopkParams p) {
     constexpr int NT = TK_SLICE_NT, KPT = TOPK_SPREAD_SLICE / NT, BINS = TOPK_SPREAD_BINS;
     constexpr int SH = 32 - TOPK_SPREAD_BITS;           // image >> SH = first digit
@@ -786,6 +817,11 @@ __global__ void __launch_bounds__(1024) topk_spread_finish(TopkParams p) {
     __shared__ unsigned long long mn_sh;
     __shared__ uint16_t big[128];  // buckets of TK_BUCKET_MAX+1 .. WAVE_MAX keys
     __shared__ uint32_t nbig;
+    __shared__ uint32_t hs[16], hn[16], nhuge;  // fuller buckets: start, keys
+    __shared__ uint32_t cpre[MS + 1];
+    __shared__ unsigned long long clo_sh, chi_sh;  // smallest and largest candidate
+    __shared__ unsigned long long wlo[NW], whi[NW];
+    __shared__ int deep;
     __shared__ int nan_sh;
     __shared__ uint32_t ctr;
 
@@ -804,7 +840,10 @@ __global__ void __launch_bounds__(1024) topk_spread_finish(TopkParams p) {
         nan_sh = 0;
         ctr = 0;
         nbig = 0;
+        nhuge = 0;
         mn_sh = ~0ull;
+        clo_sh = ~0ull;
+        chi_sh = 0ull;
     }
     // 1. coarse offsets summed over the slices: the coarse bin holding the
     // k-th key; the row's NaN flag and its smallest composite (each record's
@@ -871,6 +910,13 @@ __global__ void __launch_bounds__(1024) topk_spread_finish(TopkParams p) {
         ps0 = ps[0];
         cs0 = cs[0];
     }
+    // the candidates' flat positions: slice s holds cpre[s] .. cpre[s+1]-1
+    // (slices past S hold none, so cpre[S] = C)
+    if (w == 0) {
+        cpre[2 * lane] = ce;
+        cpre[2 * lane + 1] = ce + cs0;
+        if (lane == 0) cpre[MS] = C;
+    }
     auto place = [&](int s, bool cand) {  // s wave-uniform
         const int l = s >> 1;
         uint32_t v = (uint32_t)__builtin_amdgcn_readlane((int)(cand ? ce : pe), l);
@@ -886,7 +932,8 @@ __global__ void __launch_bounds__(1024) topk_spread_finish(TopkParams p) {
     const int shift = max(0, (span ? 64 - __clzll((long long)span) : 0) - 11);  // span >> shift < TK_BINS
     auto bucket = [&](unsigned long long v) { return (uint32_t)((v - mn) >> shift); };
     // 3. gather (wave w: slices w, w + NW, ...; four keys per lane a batch),
-    // counting the buckets
+    // counting the buckets; the smallest and largest candidate held in LDS
+    unsigned long long clo = ~0ull, chi = 0ull;
     auto gather = [&](int s) {
         const uint32_t ps = fine[s * FW + cb], es = fine[s * FW + cb + 1];
         const uint32_t g = (all || cand_lds) ? es : ps;
@@ -908,6 +955,8 @@ __global__ void __launch_bounds__(1024) topk_spread_finish(TopkParams p) {
                         atomicAdd(&cnt[bucket(v[e])], 1u);
                     } else {
                         aux[dcand + (i - ps)] = v[e];
+                        clo = v[e] < clo ? v[e] : clo;
+                        chi = v[e] > chi ? v[e] : chi;
                     }
                 }
             }
@@ -916,34 +965,85 @@ __global__ void __launch_bounds__(1024) topk_spread_finish(TopkParams p) {
     for (int s = w; s < S; s += NW) gather(s);
     uint32_t nsort = P + C;
     if (!all) {
-        // 4. the (k - P)-th smallest candidate: 8-bit digits of composite
-        // bits 51..0 (image bits 19..0, then the key id); all candidates
-        // share the top TOPK_SPREAD_BITS bits.  Candidates come from LDS or
-        // (too many for it) from the slices' rows.
+        // 4. the (k - P)-th smallest candidate: a radix select, 8-bit digits
+        // from the highest bit in which the candidates differ (all share the
+        // top TOPK_SPREAD_BITS bits; ties differ only in key id bits).
+        // Candidates come from LDS or (too many for it) from the slices'
+        // rows, each wave an equal share of the flat candidate range.
+        const uint32_t f0 = (uint32_t)((uint64_t)C * w / NW), f1 = (uint32_t)((uint64_t)C * (w + 1) / NW);
+        if (cand_lds) {
+            clo = wave_ext_u64<false>(clo);
+            chi = wave_ext_u64<true>(chi);
+            if (lane == 0) {
+                atomicMin(&clo_sh, clo);
+                atomicMax(&chi_sh, chi);
+            }
+        }
+        __syncthreads();
+        int s_first = 0;  // the slice holding flat position f0: the last s with cpre[s] <= f0
+        if (!cand_lds) {
+            int lo = 0, hi = S - 1;
+            while (lo < hi) {
+                const int mid = (lo + hi + 1) >> 1;
+                if (cpre[mid] <= f0)
+                    lo = mid;
+                else
+                    hi = mid - 1;
+            }
+            s_first = lo;
+        }
         auto for_each_cand = [&](auto&& f) {
             if (cand_lds) {
                 for (uint32_t i = tid; i < C; i += NT) f(aux[i]);
             } else {
-                for (int s = w; s < S; s += NW) {
-                    const uint32_t ps = fine[s * FW + cb], es = fine[s * FW + cb + 1];
+                uint32_t fp = f0;
+                for (int s = s_first; fp < f1; ++s) {  // s < S while fp < f1 <= cpre[S]
+                    const uint32_t fe = min(cpre[s + 1], f1);
+                    const int64_t adj = (int64_t)fine[s * FW + cb] - (int64_t)cpre[s];  // flat -> row index
                     const unsigned long long* src = p.sp_sorted + (slot0 + s) * TOPK_SPREAD_SLICE;
-                    for (uint32_t i = ps + lane; i < es; i += 64) f(src[i]);
+                    for (uint32_t i0 = fp; i0 < fe; i0 += 512) {  // eight loads in flight per lane
+                        unsigned long long v[8];
+#pragma unroll
+                        for (int e = 0; e < 8; ++e) {
+                            const uint32_t i = i0 + lane + 64 * e;
+                            v[e] = src[(int64_t)(i < fe ? i : fp) + adj];
+                        }
+#pragma unroll
+                        for (int e = 0; e < 8; ++e)
+                            if (i0 + lane + 64 * e < fe) f(v[e]);
+                    }
+                    fp = max(fp, fe);
                 }
             }
         };
-        __syncthreads();
+        if (!cand_lds) {
+            for_each_cand([&](unsigned long long v) {
+                clo = v < clo ? v : clo;
+                chi = v > chi ? v : chi;
+            });
+            clo = wave_ext_u64<false>(clo);
+            chi = wave_ext_u64<true>(chi);
+            if (lane == 0) {
+                atomicMin(&clo_sh, clo);
+                atomicMax(&chi_sh, chi);
+            }
+            __syncthreads();
+        }
+        clo = clo_sh;
+        chi = chi_sh;
         const uint32_t need = k - P;  // >= 1, < C
+        // C >= 2 distinct composites: 1 <= hib <= 64 - TOPK_SPREAD_BITS
+        int hib = 64 - __clzll((long long)(clo ^ chi));
         unsigned long long dsel = ~0ull;
-        unsigned long long dacc = (unsigned long long)cut << (64 - TOPK_SPREAD_BITS);
+        unsigned long long dacc = clo & ~((1ull << hib) - 1ull);
         uint32_t remaining = need;
 #pragma unroll 1
-        for (int q = 0; q < 7; ++q) {
-            const int sh = q == 0 ? 44 : q == 1 ? 36 : q == 2 ? 32 : 8 * (6 - q);
-            const int wd = q == 2 ? 4 : 8;
+        for (int q = 0; q < 8; ++q) {  // each pass fixes up to 8 bits; the last leaves one candidate
+            const int sh = max(0, hib - 8), wd = hib - sh;
             uint32_t* h = dh[q & 1];
             if (tid < 256) dh[(q & 1) ^ 1][tid] = 0;  // the next digit's
             for_each_cand([&](unsigned long long v) {
-                if (((v ^ dacc) >> (sh + wd)) == 0ull) atomicAdd(&h[(uint32_t)(v >> sh) & ((1u << wd) - 1u)], 1u);
+                agg_inc(h, (uint32_t)(v >> sh) & ((1u << wd) - 1u), ((v ^ dacc) >> hib) == 0ull);
             });
             __syncthreads();
             if (tid < 64) rank_bin256(h, remaining, pick);
@@ -954,17 +1054,15 @@ __global__ void __launch_bounds__(1024) topk_spread_finish(TopkParams p) {
                 dsel = dacc | ((1ull << sh) - 1ull);
                 break;
             }
+            hib = sh;
         }
         // the candidates <= dsel (exactly `need` of them) after the taken keys;
         // their order here is arbitrary, the sort below fixes it
         for_each_cand([&](unsigned long long v) {
-            if (v <= dsel) {
-                const uint32_t pos = P + atomicAdd(&ctr, 1u);
-                if (pos < k) {
-                    comp[pos] = v;
-                    atomicAdd(&cnt[bucket(v)], 1u);
-                }
-            }
+            const uint32_t pos = P + agg_inc(&ctr, 0u, v <= dsel);
+            const bool take = v <= dsel && pos < k;
+            agg_inc(cnt, take ? bucket(v) : 0u, take);
+            if (take) comp[pos] = v;
         });
         nsort = k;
     }
@@ -977,59 +1075,63 @@ __global__ void __launch_bounds__(1024) topk_spread_finish(TopkParams p) {
         orow[i] = key >= visible ? -1 : p.offset + key;
     };
     __syncthreads();
-    // one scan places the buckets and counts those too full for a wave's
-    // sort (bit 16 up); buckets of more than TK_BUCKET_MAX keys are listed,
-    // a wave sorts each in registers
+    // one scan places the buckets; buckets of TK_BUCKET_MAX+1 .. WAVE_MAX
+    // keys are listed for a wave's register sort, fuller ones (a value many
+    // keys share, few distinct scores) for a second bucket pass over their
+    // own span
     constexpr uint32_t WAVE_MAX = 256;  // 64 lanes x 4
+    constexpr int HUGE_MAX = TOPK_MAX / (WAVE_MAX + 1);
     static_assert((TOPK_MAX + TK_BUCKET_MAX) / (TK_BUCKET_MAX + 1) <= 128, "listed buckets");
-    const uint32_t b0 = cnt[2 * tid], b1 = cnt[2 * tid + 1];
-    const uint32_t full = (b0 > WAVE_MAX) + (b1 > WAVE_MAX);
-    if (b0 > (uint32_t)TK_BUCKET_MAX && b0 <= WAVE_MAX) big[atomicAdd(&nbig, 1u)] = (uint16_t)(2 * tid);
-    if (b1 > (uint32_t)TK_BUCKET_MAX && b1 <= WAVE_MAX) big[atomicAdd(&nbig, 1u)] = (uint16_t)(2 * tid + 1);
-    const uint32_t sv = (b0 + b1) | (full << 16);
-    uint32_t incl = wave_scan_incl(sv);
-    if (lane == 63) scan_sh[w] = incl;
-    __syncthreads();
-    uint32_t before = 0, total = 0;
+    static_assert(HUGE_MAX <= 16, "full buckets");
+    // bucket counts (two per thread) -> their starts in cur, the listings
+    // (full buckets only at the first level)
+    auto place_buckets = [&](uint32_t b0, uint32_t b1, bool list_full) {
+        if (b0 > (uint32_t)TK_BUCKET_MAX && b0 <= WAVE_MAX) big[atomicAdd(&nbig, 1u)] = (uint16_t)(2 * tid);
+        if (b1 > (uint32_t)TK_BUCKET_MAX && b1 <= WAVE_MAX) big[atomicAdd(&nbig, 1u)] = (uint16_t)(2 * tid + 1);
+        const uint32_t sv = b0 + b1;
+        const uint32_t incl = wave_scan_incl(sv);
+        if (lane == 63) scan_sh[w] = incl;
+        __syncthreads();
+        uint32_t before = 0;
 #pragma unroll
-    for (int i = 0; i < NW; ++i) {
-        const uint32_t t = scan_sh[i];
-        before += i < w ? t : 0u;
-        total += t;
-    }
-    if ((total >> 16) == 0u) {
+        for (int i = 0; i < NW; ++i) before += i < w ? scan_sh[i] : 0u;
         const uint32_t st = before + incl - sv;
         cur[2 * tid] = st;
         cur[2 * tid + 1] = st + b0;
+        if (list_full && b0 > WAVE_MAX) {
+            const uint32_t h = atomicAdd(&nhuge, 1u);
+            hs[h] = st;
+            hn[h] = b0;
+        }
+        if (list_full && b1 > WAVE_MAX) {
+            const uint32_t h = atomicAdd(&nhuge, 1u);
+            hs[h] = st + b0;
+            hn[h] = b1;
+        }
         __syncthreads();
-        static_assert(TOPK_MAX <= 4 * NT, "four keys per thread");
+    };
+    // rank of every key of a bucket of at most TK_BUCKET_MAX keys (the keys
+    // of its bucket below it), then a wave's sort of each listed bucket; the
+    // keys were scattered into buf, bucket by bucket, position off onwards
+    auto order_buckets = [&](unsigned long long* buf, uint32_t n, uint32_t off, auto&& bkt) {
         unsigned long long kv[4];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) kv[e] = comp[min(tid + NT * e, TOPK_MAX - 1)];
-#pragma unroll
-        for (int e = 0; e < 4; ++e)
-            if (tid + NT * e < (int)nsort) aux[atomicAdd(&cur[bucket(kv[e])], 1u)] = kv[e];
-        __syncthreads();
-        // cur[b] is now the end of bucket b; a key's place is its bucket's
-        // start plus the number of its bucket's keys below it (small
-        // buckets), or its place in its bucket's wave sort (listed ones)
         uint32_t kend[4], kstart[4];
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-            kv[e] = aux[min(tid + NT * e, TOPK_MAX - 1)];
-            const uint32_t b = bucket(kv[e]) & (TK_BINS - 1);
+            kv[e] = buf[min(tid + NT * e, TOPK_MAX - 1)];
+            const uint32_t b = bkt(kv[e]) & (TK_BINS - 1);
             kend[e] = cur[b];
             kstart[e] = kend[e] - cnt[b];
         }
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-            if (tid + NT * e >= (int)nsort || kend[e] - kstart[e] > (uint32_t)TK_BUCKET_MAX) continue;
+            if (tid + NT * e >= (int)n || kend[e] - kstart[e] > (uint32_t)TK_BUCKET_MAX) continue;
             const unsigned long long v = kv[e];
-            uint32_t r = kstart[e];
+            uint32_t r = off + kstart[e];
             for (uint32_t j0 = kstart[e]; j0 < kend[e]; j0 += 4) {
                 unsigned long long u[4];
 #pragma unroll
-                for (int q = 0; q < 4; ++q) u[q] = j0 + q < kend[e] ? aux[j0 + q] : ~0ull;
+                for (int q = 0; q < 4; ++q) u[q] = j0 + q < kend[e] ? buf[j0 + q] : ~0ull;
 #pragma unroll
                 for (int q = 0; q < 4; ++q) r += u[q] < v;
             }
@@ -1037,18 +1139,18 @@ __global__ void __launch_bounds__(1024) topk_spread_finish(TopkParams p) {
         }
         auto sort_bucket = [&](uint32_t b, auto ept_tag) {  // 64 EPT >= the bucket's keys
             constexpr int EPT = decltype(ept_tag)::value;
-            const uint32_t end = cur[b], nb = cnt[b], start = end - nb;
+            const uint32_t bend = cur[b], nb = cnt[b], bstart = bend - nb;
             unsigned long long x[EPT];
 #pragma unroll
             for (int e = 0; e < EPT; ++e) {
                 const uint32_t j = EPT * lane + e;
-                x[e] = j < nb ? aux[start + j] : TK_NONE;
+                x[e] = j < nb ? buf[bstart + j] : TK_NONE;
             }
             wave_sort<EPT>(x, 64 * EPT);
 #pragma unroll
             for (int e = 0; e < EPT; ++e) {
                 const uint32_t j = EPT * lane + e;
-                if (j < nb && start + j < k) emit(start + j, x[e]);
+                if (j < nb && off + bstart + j < k) emit(off + bstart + j, x[e]);
             }
         };
         for (uint32_t i = w; i < nbig; i += NW) {
@@ -1058,25 +1160,97 @@ __global__ void __launch_bounds__(1024) topk_spread_finish(TopkParams p) {
             else
                 sort_bucket(b, std::integral_constant<int, 4>{});
         }
-    } else {
-        // a bucket too full for a wave (ties, few distinct scores): the
-        // bitonic sort of all keys
-        int npow = 4;
-        while (npow < (int)nsort) npow <<= 1;
-        for (int i = (int)nsort + tid; i < npow; i += NT) comp[i] = TK_NONE;
-        __syncthreads();
-        auto sort_emit = [&](auto ept_tag) {
-            constexpr int EPT = decltype(ept_tag)::value;
-            unsigned long long x[EPT];
-            sort_lds<NT, EPT>(comp, npow, x);
+    };
+    __syncthreads();
+    place_buckets(cnt[2 * tid], cnt[2 * tid + 1], true);
+    static_assert(TOPK_MAX <= 4 * NT, "four keys per thread");
+    {
+        unsigned long long kv[4];
 #pragma unroll
-            for (int e = 0; e < EPT; ++e)
-                if (EPT * tid + e < (int)k) emit((uint32_t)(EPT * tid + e), x[e]);
-        };
-        if (npow <= 2 * NT)
-            sort_emit(std::integral_constant<int, 2>{});
-        else
-            sort_emit(std::integral_constant<int, 4>{});
+        for (int e = 0; e < 4; ++e) kv[e] = comp[min(tid + NT * e, TOPK_MAX - 1)];
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+            if (tid + NT * e < (int)nsort) aux[atomicAdd(&cur[bucket(kv[e])], 1u)] = kv[e];
+    }
+    __syncthreads();
+    // cur[b] is now the end of bucket b
+    order_buckets(aux, nsort, 0u, bucket);
+    // each full bucket in turn, by the whole workgroup: its keys bucketed
+    // again over the span from its smallest to its largest composite (keys
+    // of one score differ in the key id only, so they spread)
+    const uint32_t nh = nhuge;
+    for (uint32_t h = 0; h < nh; ++h) {
+        const uint32_t hst = hs[h], hnb = hn[h];
+        if (hst >= k) continue;  // nothing of it is emitted
+        __syncthreads();  // the last pass's readers of cnt, cur, comp, big are done
+        unsigned long long x[4], lo = ~0ull, hi = 0ull;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const uint32_t i = tid + NT * e;
+            x[e] = i < hnb ? aux[hst + i] : TK_NONE;
+            if (i < hnb) {
+                lo = x[e] < lo ? x[e] : lo;
+                hi = x[e] > hi ? x[e] : hi;
+            }
+        }
+        lo = wave_ext_u64<false>(lo);
+        hi = wave_ext_u64<true>(hi);
+        if (lane == 0) {
+            wlo[w] = lo;
+            whi[w] = hi;
+        }
+        cnt[2 * tid] = 0;
+        cnt[2 * tid + 1] = 0;
+        if (tid == 0) {
+            nbig = 0;
+            deep = 0;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int i = 0; i < NW; ++i) {
+            lo = wlo[i] < lo ? wlo[i] : lo;
+            hi = whi[i] > hi ? whi[i] : hi;
+        }
+        const unsigned long long hspan = hi - lo;
+        const int hshift = max(0, (hspan ? 64 - __clzll((long long)hspan) : 0) - 11);
+        auto sub = [&](unsigned long long v) { return (uint32_t)((v - lo) >> hshift); };
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+            if (tid + NT * e < (int)hnb) atomicAdd(&cnt[sub(x[e])], 1u);
+        __syncthreads();
+        const uint32_t c0 = cnt[2 * tid], c1 = cnt[2 * tid + 1];
+        if (c0 > WAVE_MAX || c1 > WAVE_MAX) deep = 1;
+        place_buckets(c0, c1, false);
+        if (!deep) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                if (tid + NT * e < (int)hnb) comp[atomicAdd(&cur[sub(x[e])], 1u)] = x[e];
+            __syncthreads();
+            order_buckets(comp, hnb, hst, sub);
+        } else {
+            // a sub-bucket still too full (several shared scores in one
+            // bucket): the bitonic sort of this bucket's keys
+            int npow = 4;
+            while (npow < (int)hnb) npow <<= 1;
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                if (tid + NT * e < npow) comp[tid + NT * e] = x[e];
+            __syncthreads();
+            auto sort_emit = [&](auto ept_tag) {
+                constexpr int EPT = decltype(ept_tag)::value;
+                unsigned long long y[EPT];
+                sort_lds<NT, EPT>(comp, npow, y);
+#pragma unroll
+                for (int e = 0; e < EPT; ++e) {
+                    const uint32_t j = EPT * tid + e;
+                    if (j < hnb && hst + j < k) emit(hst + j, y[e]);
+                }
+            };
+            if (npow <= 2 * NT)
+                sort_emit(std::integral_constant<int, 2>{});
+            else
+                sort_emit(std::integral_constant<int, 4>{});
+        }
     }
     if (tid == 0) {
         p.nan_flags[row] = nan_sh;

@@ -167,3 +167,21 @@ def test_spread_nan_among_ranked_keys(M):
     status = torch.full((1,), -1, dtype=torch.int32, device="cuda")
     M.lightning_select(dev(s), 2048, 4, 131071, 0, check=False, status=status)
     assert int(status.item()) == MH.NONFINITE
+
+
+@pytest.mark.parametrize("cols,top_k", [(8192, 4096), (32768, 2048), (16384, 4096)])
+def test_spread_heavy_ties(M, cols, top_k):
+    # rows where one value holds a large share of the keys: rectified scores
+    # (about half the keys exactly 0, and the cut falls among them when half
+    # are taken) and a row of one value everywhere (every key ties, so the
+    # selection is the first top_k key ids)
+    s = np.maximum(normal(f"tk.relu.{cols}", (1, cols)), np.float32(0.0))
+    compare(M, s, top_k, 1, cols - 1, 0, f"relu-{cols}-k{top_k}")
+    compare(M, np.zeros((1, cols), np.float32), top_k, 1, cols - 1, 0, f"zeros-{cols}-k{top_k}")
+    compare(M, np.full((1, cols), np.float32(-2.5)), top_k, 1, cols - 1, 5, f"equal-{cols}-k{top_k}")
+    # two adjacent values share the leading keys (one order bucket, and one
+    # bucket again over its own span) above a spread tail
+    two = normal(f"tk.two.{cols}", (1, cols)) * np.float32(0.1)
+    lead = O.bf16_to_f32(O.normal_bf16(f"tk.twosel.{cols}", (1, cols))) > 0.3
+    two[lead] = np.where(np.arange(cols)[lead[0]] % 3 == 0, np.float32(1.0), np.nextafter(np.float32(1.0), np.float32(0)))
+    compare(M, two, top_k, 1, cols - 1, 0, f"two-values-{cols}-k{top_k}")
