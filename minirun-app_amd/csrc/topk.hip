@@ -813,6 +813,7 @@ __global__ void __launch_bounds__(1024) topk_spread_finish(TopkParams p) {
     __shared__ __attribute__((aligned(16))) unsigned long long aux[CAND];
     __shared__ __attribute__((aligned(16))) uint32_t cnt[TK_BINS], cur[TK_BINS];
     __shared__ __attribute__((aligned(16))) uint32_t dh[2][256];
+    __shared__ __attribute__((aligned(16))) uint32_t whist[NW][256];  // a wave's sub-buckets
     __shared__ uint32_t scan_sh[NW];
     __shared__ unsigned long long mn_sh;
     __shared__ uint16_t big[128];  // buckets of TK_BUCKET_MAX+1 .. WAVE_MAX keys
@@ -1113,7 +1114,62 @@ __global__ void __launch_bounds__(1024) topk_spread_finish(TopkParams p) {
     // rank of every key of a bucket of at most TK_BUCKET_MAX keys (the keys
     // of its bucket below it), then a wave's sort of each listed bucket; the
     // keys were scattered into buf, bucket by bucket, position off onwards
-    auto order_buckets = [&](unsigned long long* buf, uint32_t n, uint32_t off, auto&& bkt) {
+    // A listed bucket (TK_BUCKET_MAX+1 .. WAVE_MAX keys at buf[bstart..]) by
+    // one wave: its keys bucketed again into 256 sub-buckets over their own
+    // span (a wave's histogram, scanned, the keys scattered to dst at the
+    // same positions), each key ranked inside its sub-bucket.  Returns false,
+    // with nothing emitted, when a sub-bucket holds more than TK_BUCKET_MAX
+    // keys (shared scores); the wave sorts the bucket instead.
+    auto sub_sort = [&](const unsigned long long* buf, unsigned long long* dst, uint32_t bstart, uint32_t nb,
+                        uint32_t off) -> bool {
+        uint32_t* hw = whist[w];
+        unsigned long long x[4], lo = ~0ull, hi = 0ull;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const uint32_t j = lane + 64 * e;
+            x[e] = buf[bstart + (j < nb ? j : 0u)];
+            if (j < nb) {
+                lo = x[e] < lo ? x[e] : lo;
+                hi = x[e] > hi ? x[e] : hi;
+            }
+        }
+        lo = wave_ext_u64<false>(lo);
+        hi = wave_ext_u64<true>(hi);
+        const unsigned long long span = hi - lo;
+        const int sh = max(0, (span ? 64 - __clzll((long long)span) : 0) - 8);
+        uint32_t sb[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) sb[e] = (uint32_t)((x[e] - lo) >> sh) & 255u;
+        *(u32x4*)(hw + 4 * lane) = u32x4{0u, 0u, 0u, 0u};
+        __builtin_amdgcn_wave_barrier();
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+            if (lane + 64 * e < (int)nb) atomicAdd(&hw[sb[e]], 1u);
+        __builtin_amdgcn_wave_barrier();
+        const u32x4 c4 = *(const u32x4*)(hw + 4 * lane);
+        const uint32_t tot = (c4[0] + c4[1]) + (c4[2] + c4[3]);
+        const uint32_t cmax = max(max(c4[0], c4[1]), max(c4[2], c4[3]));
+        if (__ballot(cmax > (uint32_t)TK_BUCKET_MAX) != 0ull) return false;
+        const uint32_t ex = wave_scan_incl(tot) - tot;
+        // sub-bucket starts, which the scatter advances to their ends
+        *(u32x4*)(hw + 4 * lane) = u32x4{ex, ex + c4[0], ex + c4[0] + c4[1], ex + c4[0] + c4[1] + c4[2]};
+        __builtin_amdgcn_wave_barrier();
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+            if (lane + 64 * e < (int)nb) dst[bstart + atomicAdd(&hw[sb[e]], 1u)] = x[e];
+        __builtin_amdgcn_wave_barrier();
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            if (lane + 64 * e >= (int)nb) continue;
+            const uint32_t se = hw[sb[e]], ss = sb[e] ? hw[sb[e] - 1] : 0u;  // [start, end) of its sub-bucket
+            uint32_t r = ss;
+            for (uint32_t j = ss; j < se; ++j) r += dst[bstart + j] < x[e];
+            if (off + bstart + r < k) emit(off + bstart + r, x[e]);
+        }
+        return true;
+    };
+    auto order_buckets = [&](unsigned long long* buf, unsigned long long* dst, uint32_t n, uint32_t off,
+                             auto&& bkt) {
         unsigned long long kv[4];
         uint32_t kend[4], kstart[4];
 #pragma unroll
@@ -1155,6 +1211,7 @@ __global__ void __launch_bounds__(1024) topk_spread_finish(TopkParams p) {
         };
         for (uint32_t i = w; i < nbig; i += NW) {
             const uint32_t b = big[i], nb = cnt[b];
+            if (sub_sort(buf, dst, cur[b] - nb, nb, off)) continue;
             if (nb <= 128)
                 sort_bucket(b, std::integral_constant<int, 2>{});
             else
@@ -1174,7 +1231,7 @@ __global__ void __launch_bounds__(1024) topk_spread_finish(TopkParams p) {
     }
     __syncthreads();
     // cur[b] is now the end of bucket b
-    order_buckets(aux, nsort, 0u, bucket);
+    order_buckets(aux, comp, nsort, 0u, bucket);
     // each full bucket in turn, by the whole workgroup: its keys bucketed
     // again over the span from its smallest to its largest composite (keys
     // of one score differ in the key id only, so they spread)
@@ -1226,7 +1283,7 @@ __global__ void __launch_bounds__(1024) topk_spread_finish(TopkParams p) {
             for (int e = 0; e < 4; ++e)
                 if (tid + NT * e < (int)hnb) comp[atomicAdd(&cur[sub(x[e])], 1u)] = x[e];
             __syncthreads();
-            order_buckets(comp, hnb, hst, sub);
+            order_buckets(comp, aux + hst, hnb, hst, sub);
         } else {
             // a sub-bucket still too full (several shared scores in one
             // bucket): the bitonic sort of this bucket's keys
