@@ -185,3 +185,15 @@ def test_spread_heavy_ties(M, cols, top_k):
     lead = O.bf16_to_f32(O.normal_bf16(f"tk.twosel.{cols}", (1, cols))) > 0.3
     two[lead] = np.where(np.arange(cols)[lead[0]] % 3 == 0, np.float32(1.0), np.nextafter(np.float32(1.0), np.float32(0)))
     compare(M, two, top_k, 1, cols - 1, 0, f"two-values-{cols}-k{top_k}")
+
+
+def test_spread_ties_full_size(M):
+    # rows of the largest spread size (128 slices): rectified scores with
+    # the cut among the positives, then with about 500 positive keys, so
+    # the cut falls among 260,000 zeros (candidates streamed from the
+    # slices, selected by key id)
+    big = np.maximum(normal("tk.relu.262144", (1, 262144)), np.float32(0.0))
+    compare(M, big, 2048, 1, 262143, 0, "relu-262144")
+    big[0, :261000] = 0.0
+    compare(M, big, 2048, 1, 262143, 0, "relu-262144-mostly-zero")
+    compare(M, np.zeros((1, 262144), np.float32), 4096, 1, 262143, 0, "zeros-262144-k4096")
