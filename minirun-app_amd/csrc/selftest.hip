@@ -76,6 +76,16 @@ __global__ void __launch_bounds__(64) k_permlane16(const uint32_t* in, uint32_t*
 }
 
 
+// v_permlane16_swap of two different values a = in[l], b = in[64 + l]:
+// out[2l] = r[0], out[2l+1] = r[1] (the decode reduces two head tiles'
+// values at once this way).
+__global__ void __launch_bounds__(64) k_permlane16_pair(const uint32_t* in, uint32_t* out) {
+    const int l = threadIdx.x;
+    const auto r = __builtin_amdgcn_permlane16_swap(in[l], in[64 + l], false, false);
+    out[2 * l] = r[0];
+    out[2 * l + 1] = r[1];
+}
+
 // MFMA rate probe: every wave runs `iters` rounds of 8 independent 32x32x16
 // bf16 MFMA chains (no memory traffic in the loop).  Thread 0 of each
 // workgroup writes the loop's shader cycles (s_memtime) and 100 MHz wall
@@ -126,6 +136,11 @@ int mr_selftest_permlane32(const void* d_in, void* d_out, void* stream) {
 }
 int mr_selftest_permlane16(const void* d_in, void* d_out, void* stream) {
     hipLaunchKernelGGL(k_permlane16, dim3(1), dim3(64), 0, (hipStream_t)stream, (const uint32_t*)d_in,
+                       (uint32_t*)d_out);
+    return hipGetLastError() == hipSuccess ? 0 : 6;
+}
+int mr_selftest_permlane16_pair(const void* d_in, void* d_out, void* stream) {
+    hipLaunchKernelGGL(k_permlane16_pair, dim3(1), dim3(64), 0, (hipStream_t)stream, (const uint32_t*)d_in,
                        (uint32_t*)d_out);
     return hipGetLastError() == hipSuccess ? 0 : 6;
 }

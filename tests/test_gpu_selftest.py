@@ -138,3 +138,31 @@ def test_mfma_rate_probe_runs():
     print(r, flush=True)
     assert 100.0 < r["tflops"] < 5000.0, r
     assert 0.5 < r["clock_ghz"] < 3.5, r
+
+
+def test_permlane16_swap_two_values(st):
+    """v_permlane16_swap of two different values a (first operand) and b:
+    with rows of 16 lanes, r[0] = (a.row0, b.row0, a.row2, b.row2) and
+    r[1] = (a.row1, b.row1, a.row3, b.row3), so max(r[0], r[1]) leaves a's
+    pairwise reduction in rows 0 and 2 and b's in rows 1 and 3: the decode
+    reduces its two head tiles' maxima and sums in one swap this way."""
+    import torch
+
+    print("selftest permlane16 pair", flush=True)
+    st.mr_selftest_permlane16_pair.argtypes = [C.c_void_p] * 3
+    a = np.arange(64, dtype=np.int32) * 3 + 7
+    b = np.arange(64, dtype=np.int32) * 5 + 1000
+    d_in = torch.tensor(np.concatenate([a, b]), device="cuda")
+    out = torch.zeros(128, dtype=torch.int32, device="cuda")
+    assert st.mr_selftest_permlane16_pair(d_in.data_ptr(), out.data_ptr(), None) == 0
+    torch.cuda.synchronize()
+    r = out.cpu().numpy().reshape(64, 2)
+    exp0 = np.empty(64, np.int32)
+    exp1 = np.empty(64, np.int32)
+    for lane in range(64):
+        row, col = lane // 16, lane % 16
+        even = 16 * (row & ~1) + col  # the same lane in the pair's even row
+        exp0[lane] = a[even] if row % 2 == 0 else b[even]
+        exp1[lane] = a[even + 16] if row % 2 == 0 else b[even + 16]
+    np.testing.assert_array_equal(r[:, 0], exp0)
+    np.testing.assert_array_equal(r[:, 1], exp1)
