@@ -84,7 +84,9 @@ const char *mr_get_last_error(void);
  *    when index_status is given.
  *  - MR_DECODE_UNCHECKED: no check; a bad entry is skipped like -1 and a
  *    repeated one counts once per occurrence.
- * Checked lists hold at most 8192 entries; n_idx is at most 524288.
+ * Any list the call takes can be checked (n_idx is at most 524288): a list
+ * of up to 10176 entries is checked in LDS, a longer one in a hash table in
+ * the workspace (mr_mla_decode_workspace_size includes it).
  *
  * Layout: the cache is one bf16 row per position; the latent part and the
  * shared rope key are given as two (pointer, row stride) pairs so that both
@@ -152,7 +154,8 @@ mr_status mr_mla_decode_noalloc(const mr_mla_decode_args *args, void *stream);
  * order, -1 skips, an entry outside [0, n_rows) is INDEX_OUT_OF_RANGE, a
  * repeat of an earlier entry is DUPLICATE_INDEX.  Synchronises `stream`.
  * bad_token / bad_position (optional host pointers) receive the location.
- * Needs n_idx <= 8192 and a workspace of mr_validate_indices_workspace_size. */
+ * Needs n_idx <= 4194304 and a workspace of mr_validate_indices_workspace_size
+ * (lists of more than 10176 entries keep their hash tables there). */
 size_t mr_validate_indices_workspace_size(int32_t batch, int32_t n_idx);
 mr_status mr_validate_indices(const int32_t *indices, int32_t batch, int32_t n_idx,
                               int32_t n_rows, void *workspace, size_t workspace_bytes,
@@ -215,11 +218,17 @@ mr_status mr_adopted_affine_weight(const mr_adopted_affine *a, mr_affine_weight 
 /* One more reference (another holder of the AffineWeights value), from any thread. */
 mr_status mr_adopted_affine_retain(mr_adopted_affine *a);
 /* Drops one reference, from any thread.  Dropping the last one enqueues the
- * finalizers on `stream` behind the work already there, which must include
- * every read of the weight (order reads on other streams before it with an
- * event); with stream NULL they run before the call returns (no GPU work
- * reads the weight any more).  The handle is invalid after its last release. */
+ * finalizers on `stream` (NULL: the default stream, as in every other entry
+ * point) behind the work already there, which must include every read of
+ * the weight (order reads on other streams before it with an event).  The
+ * handle is invalid after its last release: later calls with it return
+ * MR_INVALID_ARGUMENT (unless a later adoption happens to reuse its address). */
 mr_status mr_adopted_affine_release(mr_adopted_affine *a, void *stream);
+/* Drops one reference; the last one runs the finalizers before the call
+ * returns, on the calling thread.  For a weight no GPU work reads any more
+ * (no counterpart in the reference, where the last holder's deinit decides;
+ * here the caller states that no stream still reads the buffers). */
+mr_status mr_adopted_affine_release_now(mr_adopted_affine *a);
 
 /* affineDequantize (AffineWeights.swift:328-342): dense [out, in] in f32
  * (default, bit-exact: the bf16/f16-scale product is exact in fp32) or

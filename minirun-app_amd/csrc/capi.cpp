@@ -79,8 +79,14 @@ using mrc::cu_count;
 struct DecodePlan {
     int n_rows, hg_size, head_groups, h_pad, splits, rows_per_split;
     bool ws_f32;
-    size_t o_bytes, ml_bytes, total;
+    bool checked, sync_check;  // index checks, and whether they run before the launch
+    size_t o_bytes, ml_bytes, table_bytes, total;
 };
+
+size_t validate_ws_bytes(int32_t batch, int32_t n_idx) {
+    return align256(size_t(std::max(batch, 0)) * 3 * sizeof(int32_t)) +
+           align256(mr::validate_table_bytes(std::max(batch, 0), std::max(n_idx, 0)));
+}
 
 DecodePlan plan_decode(const mr_mla_decode_args* a) {
     DecodePlan pl{};
@@ -121,7 +127,13 @@ DecodePlan plan_decode(const mr_mla_decode_args* a) {
     pl.ws_f32 = a->out_dtype == MR_F32 || recs <= 4096;
     pl.o_bytes = align256(recs * 512 * (pl.ws_f32 ? sizeof(float) : sizeof(uint16_t)));
     pl.ml_bytes = align256(recs * 2 * sizeof(float));
-    pl.total = pl.o_bytes + pl.ml_bytes;
+    // index checks in the split launch keep long lists' tables after the
+    // partials; a check before the launch uses the workspace first
+    pl.checked = a->indices && !(a->flags & MR_DECODE_UNCHECKED);
+    pl.sync_check = pl.checked && (!a->index_status || (a->flags & MR_DECODE_VALIDATE_INDICES));
+    pl.table_bytes = (pl.checked && !pl.sync_check) ? align256(mr::validate_table_bytes(a->batch, a->n_idx)) : 0;
+    pl.total = pl.o_bytes + pl.ml_bytes + pl.table_bytes;
+    if (pl.sync_check) pl.total = std::max(pl.total, validate_ws_bytes(a->batch, a->n_idx));
     return pl;
 }
 
@@ -205,10 +217,7 @@ size_t mr_mla_decode_workspace_size(const mr_mla_decode_args* args) {
     return plan_decode(args).total;
 }
 
-size_t mr_validate_indices_workspace_size(int32_t batch, int32_t n_idx) {
-    (void)n_idx;
-    return align256(size_t(std::max(batch, 0)) * 3 * sizeof(int32_t));
-}
+size_t mr_validate_indices_workspace_size(int32_t batch, int32_t n_idx) { return validate_ws_bytes(batch, n_idx); }
 
 mr_status mr_validate_indices(const int32_t* indices, int32_t batch, int32_t n_idx, int32_t n_rows,
                               void* workspace, size_t workspace_bytes, int32_t* bad_token,
@@ -226,7 +235,8 @@ mr_status mr_validate_indices(const int32_t* indices, int32_t batch, int32_t n_i
                     mr_validate_indices_workspace_size(batch, n_idx));
     hipStream_t st = (hipStream_t)stream;
     int32_t* res = (int32_t*)workspace;
-    hipError_t e = mr::launch_validate_indices(indices, batch, n_idx, n_rows, res, st);
+    int32_t* tables = (int32_t*)((char*)workspace + align256(size_t(batch) * 3 * sizeof(int32_t)));
+    hipError_t e = mr::launch_validate_indices(indices, batch, n_idx, n_rows, tables, res, st);
     if (e != hipSuccess) return hip_fail(e, "index validation launch");
     std::vector<int32_t> host(size_t(batch) * 3);
     e = hipMemcpyAsync(host.data(), res, host.size() * sizeof(int32_t), hipMemcpyDeviceToHost, st);
@@ -254,8 +264,8 @@ mr_status mr_mla_decode(const mr_mla_decode_args* a, void* stream) {
     if (!aligned16(a->workspace)) return fail(MR_INVALID_ARGUMENT, "mla decode: workspace must be 16-byte aligned");
     // index checks: on the device in the split launch when the caller gives
     // a status buffer, else synchronously before it (the reference throws)
-    const bool checked = a->indices && !(a->flags & MR_DECODE_UNCHECKED);
-    const bool sync_check = checked && (!a->index_status || (a->flags & MR_DECODE_VALIDATE_INDICES));
+    const bool checked = pl.checked;
+    const bool sync_check = pl.sync_check;
     if (sync_check && a->n_idx > 0) {
         st = mr_validate_indices(a->indices, a->batch, a->n_idx, a->n_ctx, a->workspace, a->workspace_bytes, nullptr,
                                  nullptr, stream);
@@ -296,6 +306,8 @@ mr_status mr_mla_decode(const mr_mla_decode_args* a, void* stream) {
     // attention workgroups keep their XCD placement (blockIdx % 8)
     p.check_blocks = (checked && !sync_check) ? (a->batch + 7) / 8 * 8 : 0;
     p.index_status = p.check_blocks ? a->index_status : nullptr;
+    p.check_table = (p.check_blocks && pl.table_bytes) ? (int32_t*)((char*)a->workspace + pl.o_bytes + pl.ml_bytes)
+                                                       : nullptr;
 
     mr::CombineParams cp{};
     cp.ws_o = p.ws_o;

@@ -3,19 +3,23 @@
 // reference count shared by the holders of the weight (copies of the Swift
 // value); releases may come from any thread (BufferPool.swift:45-90).  The
 // last release runs every finalizer exactly once: behind the GPU work of the
-// stream it names (a host function on that stream), or on the releasing
-// thread when no stream is named.
+// stream it names (a host function on that stream; NULL is the default
+// stream, as everywhere in the ABI), or on the releasing thread through
+// mr_adopted_affine_release_now when no GPU work reads the weight any more.
+// Live handles are kept in a registry, so a call with a released handle is
+// rejected without touching freed memory.
 #include <hip/hip_runtime.h>
 
 #include <atomic>
+#include <mutex>
 #include <new>
+#include <unordered_set>
 
 #include "../../include/minirun_hip.h"
 #include "capi_util.hpp"
 
 struct mr_adopted_affine {
-    std::atomic<int32_t> refs;
-    std::atomic<uint32_t> live;  // kAlive from adoption until the last release
+    int32_t refs;  // guarded by the registry lock
     mr_affine_weight w;
     mr_finalizer fin[3];
     void* ctx[3];
@@ -26,7 +30,11 @@ namespace {
 using mrc::fail;
 using mrc::hip_fail;
 
-constexpr uint32_t kAlive = 0x41444f50u;
+std::mutex g_mu;
+std::unordered_set<const mr_adopted_affine*>& registry() {
+    static std::unordered_set<const mr_adopted_affine*> live;  // never destroyed before late releases
+    return live;
+}
 
 void run_finalizers(mr_finalizer const* fin, void* const* ctx) {
     for (int i = 0; i < 3; ++i)
@@ -40,7 +48,15 @@ void finish(void* p) {
     delete a;
 }
 
-bool live(const mr_adopted_affine* a) { return a && a->live.load(std::memory_order_acquire) == kAlive; }
+// Drops one reference under the registry lock.  Returns MR_OK and sets
+// *last when this was the last one (the handle has then left the registry).
+mr_status drop_ref(mr_adopted_affine* a, const char* who, bool* last) {
+    std::lock_guard<std::mutex> lock(g_mu);
+    if (!a || !registry().count(a)) return fail(MR_INVALID_ARGUMENT, "%s: not a live adopted weight", who);
+    *last = --a->refs == 0;
+    if (*last) registry().erase(a);
+    return MR_OK;
+}
 
 }  // namespace
 
@@ -78,7 +94,7 @@ mr_status mr_affine_adopt(void* packed, void* scales, void* biases, mr_dtype sca
         return drop(fail(MR_INVALID_ARGUMENT, "mr_affine_adopt: packed, scales and biases must be non-NULL"));
     mr_adopted_affine* a = new (std::nothrow) mr_adopted_affine;
     if (!a) return drop(fail(MR_INVALID_ARGUMENT, "mr_affine_adopt: out of host memory"));
-    a->refs.store(1);
+    a->refs = 1;
     a->w.packed = static_cast<const uint32_t*>(packed);
     a->w.scales = scales;
     a->w.biases = biases;
@@ -91,27 +107,32 @@ mr_status mr_affine_adopt(void* packed, void* scales, void* biases, mr_dtype sca
         a->fin[i] = fin[i];
         a->ctx[i] = ctx[i];
     }
-    a->live.store(kAlive, std::memory_order_release);
+    {
+        std::lock_guard<std::mutex> lock(g_mu);
+        registry().insert(a);
+    }
     *out = a;
     return MR_OK;
 }
 
 mr_status mr_adopted_affine_weight(const mr_adopted_affine* a, mr_affine_weight* out) {
-    if (!live(a) || !out) return fail(MR_INVALID_ARGUMENT, "mr_adopted_affine_weight: not a live adopted weight");
+    std::lock_guard<std::mutex> lock(g_mu);
+    if (!a || !out || !registry().count(a))
+        return fail(MR_INVALID_ARGUMENT, "mr_adopted_affine_weight: not a live adopted weight");
     *out = a->w;
     return MR_OK;
 }
 
 mr_status mr_adopted_affine_retain(mr_adopted_affine* a) {
-    if (!live(a)) return fail(MR_INVALID_ARGUMENT, "mr_adopted_affine_retain: not a live adopted weight");
-    a->refs.fetch_add(1, std::memory_order_relaxed);
+    std::lock_guard<std::mutex> lock(g_mu);
+    if (!a || !registry().count(a)) return fail(MR_INVALID_ARGUMENT, "mr_adopted_affine_retain: not a live adopted weight");
+    ++a->refs;
     return MR_OK;
 }
 
 mr_status mr_adopted_affine_release(mr_adopted_affine* a, void* stream) {
-    if (!live(a)) return fail(MR_INVALID_ARGUMENT, "mr_adopted_affine_release: not a live adopted weight");
-    hipStream_t s = static_cast<hipStream_t>(stream);
-    if (s) {
+    hipStream_t s = static_cast<hipStream_t>(stream);  // NULL: the default stream
+    {
         // a host function recorded into a graph would run on every replay
         hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
         const hipError_t e = hipStreamIsCapturing(s, &cap);
@@ -121,18 +142,22 @@ mr_status mr_adopted_affine_release(mr_adopted_affine* a, void* stream) {
                         "mr_adopted_affine_release: the stream is capturing a graph; release on a stream that runs "
                         "the work directly");
     }
-    if (a->refs.fetch_sub(1, std::memory_order_acq_rel) != 1) return MR_OK;
-    a->live.store(0, std::memory_order_relaxed);
-    if (!s) {
-        finish(a);
-        return MR_OK;
-    }
+    bool last = false;
+    mr_status st = drop_ref(a, "mr_adopted_affine_release", &last);
+    if (st != MR_OK || !last) return st;
     if (hipLaunchHostFunc(s, finish, a) == hipSuccess) return MR_OK;
     (void)hipGetLastError();
     // the stream takes no host function: wait for its reads, then release here
     const hipError_t e = hipStreamSynchronize(s);
     finish(a);
     return e == hipSuccess ? MR_OK : hip_fail(e, "adopted weight release");
+}
+
+mr_status mr_adopted_affine_release_now(mr_adopted_affine* a) {
+    bool last = false;
+    mr_status st = drop_ref(a, "mr_adopted_affine_release_now", &last);
+    if (st == MR_OK && last) finish(a);
+    return st;
 }
 
 }  // extern "C"

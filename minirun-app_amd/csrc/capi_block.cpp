@@ -389,6 +389,11 @@ mr_status mr_linear(const void* x, mr_dtype x_dtype, int32_t tokens, int64_t x_s
     if (x_stride < w->in_features || y_stride < w->out_features)
         return fail(MR_INVALID_SHAPE, "linear: x rows need %lld features, y rows %lld", (long long)w->in_features,
                     (long long)w->out_features);
+    // the GEMV reads activation vectors in 16-byte chunks (past its last row
+    // a wave still loads one chunk of the vector): at least one whole chunk
+    if (w->in_features * (x_dtype == MR_F32 ? 4 : 2) < 16)
+        return fail(MR_INVALID_SHAPE, "linear: an activation row of %lld %s values is under 16 bytes",
+                    (long long)w->in_features, dtype_name(x_dtype));
     mr::DenseGemvParams g = dense_params(w);
     g.x = x;
     g.x_f32 = x_dtype == MR_F32;

@@ -68,39 +68,42 @@ __device__ __forceinline__ int64_t part_rec(const DecodeParams& p, int b, int he
 // Index checks of one token's list, DeepSeekV4SparseAttention
 // (DeepSeekV4Attention.swift:884-895): the reference walks the entries in
 // order, skips -1, and stops at the first entry outside [0, n_rows) or equal
-// to an earlier entry.  One workgroup does it in LDS with no sort: every
-// in-range value goes into an open-addressing table (linear probing,
-// Fibonacci hash, at least twice as many slots as entries) that keeps the
-// smallest position holding the value; an entry is a repeat exactly when its
-// position is not its value's smallest.  The first error is the smallest
-// position that is out of range or a repeat.  res = (status, position, value),
-// (MR_OK, -1, -1) for a valid list.  `lds` holds 2 * slots int32.
-constexpr int VALIDATE_MAX_IDX = 8192;
+// to an earlier entry.  One workgroup does it with no sort: every in-range
+// value goes into an open-addressing table (linear probing, Fibonacci hash
+// mapped onto `slots` by a multiply-high, at least 1.6 slots per entry) that
+// keeps the smallest position holding the value; an entry is a repeat
+// exactly when its position is not its value's smallest.  The first error is
+// the smallest position that is out of range or a repeat.  res = (status,
+// position, value), (MR_OK, -1, -1) for a valid list.  `table` holds
+// 2 * validate_slots(n_idx) int32: in LDS for lists of up to
+// VALIDATE_LDS_MAX_IDX entries, else in global memory (the workspace), where
+// every access is a workgroup-scope atomic so the workgroup's own updates
+// are what it reads.
+__host__ __device__ constexpr int validate_slots(int n_idx) { return ((n_idx * 8 + 4) / 5 + 1 + 63) / 64 * 64; }
+constexpr int VALIDATE_LDS_BYTES = 131072;  // a check workgroup's LDS table (the smallest decode row ring)
+constexpr int VALIDATE_LDS_MAX_IDX = 10176;
+static_assert(validate_slots(VALIDATE_LDS_MAX_IDX) * 8 <= VALIDATE_LDS_BYTES, "LDS index table");
+constexpr int VALIDATE_MAX_IDX = 1 << 22;  // longest list the checks take (table in the workspace)
 
-__host__ __device__ inline int validate_slots_log2(int n_idx) {
-    int lg = 6;
-    while ((1 << lg) < 2 * n_idx) ++lg;
-    return lg;
-}
-
-__device__ void validate_token(const int32_t* __restrict__ ind, int32_t n_idx, int32_t n_rows, int32_t* lds, int nt,
+__device__ void validate_token(const int32_t* __restrict__ ind, int32_t n_idx, int32_t n_rows, int32_t* table, int nt,
                                int tid, int32_t* res) {
     __shared__ int32_t first_range, first_dup;
-    const int lg = validate_slots_log2(n_idx);
-    const int slots = 1 << lg;
-    const uint32_t mask = (uint32_t)slots - 1;
-    int32_t* key = lds;
-    int32_t* minpos = lds + slots;
-    for (int i = tid; i < slots; i += nt) {
-        key[i] = -1;
-        minpos[i] = 0x7fffffff;
+    const uint32_t slots = (uint32_t)validate_slots(n_idx);
+    int32_t* key = table;
+    int32_t* minpos = table + slots;
+    auto ld = [](int32_t* a) { return __hip_atomic_load(a, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP); };
+    auto st = [](int32_t* a, int32_t v) { __hip_atomic_store(a, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP); };
+    for (uint32_t i = tid; i < slots; i += nt) {
+        st(key + i, -1);
+        st(minpos + i, 0x7fffffff);
     }
     if (tid == 0) {
         first_range = 0x7fffffff;
         first_dup = 0x7fffffff;
     }
     __syncthreads();
-    auto home = [&](int32_t v) { return ((uint32_t)v * 2654435761u) >> (32 - lg); };
+    auto home = [&](int32_t v) { return (uint32_t)(((uint64_t)((uint32_t)v * 2654435761u) * slots) >> 32); };
+    auto next = [&](uint32_t h) { return h + 1 == slots ? 0u : h + 1; };
     for (int i = tid; i < n_idx; i += nt) {
         const int32_t v = ind[i];
         if (v == -1) continue;
@@ -109,13 +112,15 @@ __device__ void validate_token(const int32_t* __restrict__ ind, int32_t n_idx, i
             continue;
         }
         uint32_t h = home(v);
-        for (int t = 0; t < slots; ++t) {  // the table is never full: ends within `slots` probes
-            const int32_t prev = atomicCAS(&key[h], -1, v);
+        for (uint32_t t = 0; t < slots; ++t) {  // the table is never full: ends within `slots` probes
+            int32_t prev = -1;
+            __hip_atomic_compare_exchange_strong(key + h, &prev, v, __ATOMIC_RELAXED, __ATOMIC_RELAXED,
+                                                 __HIP_MEMORY_SCOPE_WORKGROUP);
             if (prev == -1 || prev == v) {
-                atomicMin(&minpos[h], i);
+                __hip_atomic_fetch_min(minpos + h, i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
                 break;
             }
-            h = (h + 1) & mask;
+            h = next(h);
         }
     }
     __syncthreads();
@@ -123,8 +128,8 @@ __device__ void validate_token(const int32_t* __restrict__ ind, int32_t n_idx, i
         const int32_t v = ind[i];
         if (v < 0 || v >= n_rows) continue;
         uint32_t h = home(v);
-        for (int t = 0; t < slots && key[h] != v; ++t) h = (h + 1) & mask;
-        if (minpos[h] != i) atomicMin(&first_dup, i);
+        for (uint32_t t = 0; t < slots && ld(key + h) != v; ++t) h = next(h);
+        if (ld(minpos + h) != i) atomicMin(&first_dup, i);
     }
     __syncthreads();
     if (tid == 0) {
@@ -187,8 +192,10 @@ __global__ void __launch_bounds__((WsShape<HGS, QK16>::THREADS), 1) mla_decode_w
 
     if (GATHER && (int)blockIdx.x < p.check_blocks) {  // index-check workgroups
         if ((int)blockIdx.x < p.batch)
-            validate_token(p.indices + (int64_t)blockIdx.x * p.n_idx, p.n_idx, p.n_ctx, (int32_t*)cbuf, NT,
-                           threadIdx.x, p.index_status + 3 * blockIdx.x);
+            validate_token(p.indices + (int64_t)blockIdx.x * p.n_idx, p.n_idx, p.n_ctx,
+                           p.check_table ? p.check_table + (int64_t)blockIdx.x * 2 * validate_slots(p.n_idx)
+                                         : (int32_t*)cbuf,
+                           NT, threadIdx.x, p.index_status + 3 * blockIdx.x);
         return;
     }
     const int bid = blockIdx.x - (GATHER ? p.check_blocks : 0);
@@ -988,25 +995,35 @@ hipError_t launch_split(const DecodeParams& p, int grid, hipStream_t st) {
     return packed ? launch_ws<DR, GATHER, true>(p, grid, st) : launch_ws<DR, GATHER, false>(p, grid, st);
 }
 
-// The same check as a launch of its own: one workgroup per token.
-__global__ void __launch_bounds__(256) validate_indices_kernel(const int32_t* indices, int32_t n_idx,
-                                                               int32_t n_rows, int32_t* result) {
+// The same check as a launch of its own: one workgroup per token, the table
+// in LDS (dynamic) or, for long lists, at `tables` (2 * slots int32 a token).
+__global__ void __launch_bounds__(1024) validate_indices_kernel(const int32_t* indices, int32_t n_idx, int32_t n_rows,
+                                                                int32_t* tables, int32_t* result) {
     extern __shared__ int32_t table[];
-    validate_token(indices + (int64_t)blockIdx.x * n_idx, n_idx, n_rows, table, 256, threadIdx.x,
-                   result + 3 * blockIdx.x);
+    int32_t* t = tables ? tables + (int64_t)blockIdx.x * 2 * validate_slots(n_idx) : table;
+    validate_token(indices + (int64_t)blockIdx.x * n_idx, n_idx, n_rows, t, 1024, threadIdx.x, result + 3 * blockIdx.x);
 }
 
 }  // namespace
 
+size_t validate_table_bytes(int32_t batch, int32_t n_idx) {
+    if (n_idx <= VALIDATE_LDS_MAX_IDX) return 0;
+    return size_t(batch) * 2 * sizeof(int32_t) * size_t(validate_slots(n_idx));
+}
+
 hipError_t launch_validate_indices(const int32_t* indices, int32_t batch, int32_t n_idx, int32_t n_rows,
-                                   int32_t* result, hipStream_t st) {
-    const size_t lds = sizeof(int32_t) * 2 * (size_t(1) << validate_slots_log2(n_idx));
-    if (lds > 65536) {  // tables past 64 KB (lists of more than 4096 entries)
-        const hipError_t e = hipFuncSetAttribute((const void*)validate_indices_kernel,
-                                                 hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-        if (e != hipSuccess) return e;
+                                   int32_t* tables, int32_t* result, hipStream_t st) {
+    size_t lds = 0;
+    if (n_idx <= VALIDATE_LDS_MAX_IDX) {
+        tables = nullptr;
+        lds = sizeof(int32_t) * 2 * size_t(validate_slots(n_idx));
+        if (lds > 65536) {
+            const hipError_t e = hipFuncSetAttribute((const void*)validate_indices_kernel,
+                                                     hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+            if (e != hipSuccess) return e;
+        }
     }
-    hipLaunchKernelGGL(validate_indices_kernel, dim3(batch), dim3(256), lds, st, indices, n_idx, n_rows, result);
+    hipLaunchKernelGGL(validate_indices_kernel, dim3(batch), dim3(1024), lds, st, indices, n_idx, n_rows, tables, result);
     return hipGetLastError();
 }
 

@@ -37,6 +37,9 @@ struct DecodeParams {
     // index_status[3 * token]; 0 = no check
     int32_t check_blocks;
     int32_t* index_status;
+    // the check workgroups' hash tables (2 * slots int32 per token) for lists
+    // too long for LDS; null: in LDS
+    int32_t* check_table;
 };
 
 struct CombineParams {
@@ -78,10 +81,13 @@ hipError_t launch_combine_unabsorb(const CombineUnabsorbParams& p, hipStream_t s
 int decode_head_group_size(int heads);
 // Index checks (DeepSeekV4Attention.swift:884-895), one workgroup per token:
 // result[3 * b] = (status, position, value); lists of at most
-// validate_max_indices() entries.
+// validate_max_indices() entries.  Lists too long for a workgroup's LDS keep
+// their hash tables in global memory: validate_table_bytes(batch, n_idx)
+// bytes at `tables` (0 bytes, and `tables` unused, for short lists).
 int validate_max_indices();
+size_t validate_table_bytes(int32_t batch, int32_t n_idx);
 hipError_t launch_validate_indices(const int32_t* indices, int32_t batch, int32_t n_idx, int32_t n_rows,
-                                   int32_t* result, hipStream_t st);
+                                   int32_t* tables, int32_t* result, hipStream_t st);
 hipError_t launch_mla_decode(const DecodeParams& p, const CombineParams& cp, bool split_only,
                              hipEvent_t const* events, hipStream_t st);
 

@@ -39,12 +39,11 @@ namespace {
 // computes C^T blocks (B rows as the MFMA's first operand), so each lane
 // ends with four runs of four consecutive N columns of one C row.
 //
-// K streams through a ring of UG_STAGES LDS stages of UG_BK = 32 columns
-// (A 16 KB + B 16 KB each, 160 KB in all) filled by global -> LDS DMA four
-// stages ahead; a
-// stage is 64-byte rows of four 16-byte chunks, chunk c of row r in slot
-// c ^ ((r >> 2) & 3), so the 16 lanes of one ds_read_b128 phase (16
-// consecutive rows, one chunk) hit 16 distinct bank groups.  The DMA writes
+// K streams through two LDS stages (UG_STAGES) of UG_BK = 64 columns (A 32 KB
+// + B 32 KB each, 128 KB in all) filled by global -> LDS DMA one stage
+// ahead; a stage is 128-byte rows of eight 16-byte chunks, chunk c of row r
+// in slot c ^ ((r >> 1) & 7) (ug_slot), so the 16 lanes of one ds_read_b128
+// phase (16 consecutive rows, one chunk) hit 16 distinct bank groups.  The DMA writes
 // slots in lane order, so lane l of a 1 KB instruction fetches the global
 // chunk that belongs in slot l.  The operand fragments are read one 16-deep
 // step ahead of the MFMAs that use them, and the one barrier per stage sits

@@ -12,6 +12,7 @@ Names follow the reference operators they stand in for:
 from __future__ import annotations
 
 import ctypes as C
+import threading
 import os
 
 HERE = os.path.dirname(os.path.abspath(__file__))
@@ -148,6 +149,7 @@ SIGNATURES = {
     "mr_adopted_affine_weight": (C.c_int, [_P, C.POINTER(AffineWeightDesc)]),
     "mr_adopted_affine_retain": (C.c_int, [_P]),
     "mr_adopted_affine_release": (C.c_int, [_P, _P]),
+    "mr_adopted_affine_release_now": (C.c_int, [_P]),
     "mr_affine_gather_matmul": (C.c_int, [_P, C.c_int, C.c_int32, C.c_int64, C.POINTER(AffineWeightDesc), C.c_int64,
                                           _P, C.c_int32, _P, C.c_int, _P]),
     "mr_rmsnorm": (C.c_int, [_P, C.c_int, C.c_int64, C.c_int32, C.c_int64, _P, C.c_int, C.c_float, _P, C.c_int,
@@ -216,6 +218,12 @@ def _torch():
 
 
 def _stream(stream):
+    """A stream argument as the C-ABI takes it: a torch stream, a raw handle
+    (int or c_void_p), or None for torch's current stream."""
+    if isinstance(stream, C.c_void_p):
+        return stream
+    if isinstance(stream, int):
+        return C.c_void_p(stream)
     torch = _torch()
     if stream is None:
         stream = torch.cuda.current_stream()
@@ -389,25 +397,54 @@ class AffineWeights:
 
 FINALIZER = C.CFUNCTYPE(None, C.c_void_p)
 
+# One C callback for every adopted weight's finalizers, alive as long as the
+# module: the library calls it with a context id, which names the Python
+# finalizer and its argument in _FINALIZERS.  The library may call it on a
+# HIP runtime thread after the AdoptedAffineWeights object is gone, so no
+# per-object ctypes thunk is ever handed to it.
+_FINALIZERS = {}
+_FIN_LOCK = threading.Lock()
+_FIN_NEXT = [1]
+
+
+@FINALIZER
+def _finalizer_trampoline(ctx):
+    with _FIN_LOCK:
+        fn, arg = _FINALIZERS.pop(ctx)
+    fn(arg)
+
+
+def _register_finalizer(fn, arg):
+    with _FIN_LOCK:
+        key = _FIN_NEXT[0]
+        _FIN_NEXT[0] += 1
+        _FINALIZERS[key] = (fn, arg)
+    return key
+
 
 class AdoptedAffineWeights:
     """AffineWeights.adopting (AffineWeights.swift:159-198): the three buffers
     (device pointers, or pinned host memory the device reads) pass to the
     library with a finalizer each (Python callables of one argument, the
-    context pointer).  Each finalizer runs exactly once, when the last
+    context value).  Each finalizer runs exactly once, when the last
     reference is released and the named stream has passed every read; a
     failed adoption runs them before raising.  Shapes: packed [experts?, out,
     in*bits/32], scales/biases [experts?, out, in/group]."""
 
     def __init__(self, packed_ptr, scales_ptr, biases_ptr, scale_dtype, out_features, in_features, *,
                  experts=0, group_size=64, bits=4, finalizers=(None, None, None), contexts=(None, None, None)):
-        # the ctypes callbacks must outlive the weight: the library calls them last
-        self._cbs = [FINALIZER(f) if f is not None else None for f in finalizers]
-        cb = [C.cast(c, _P) if c is not None else None for c in self._cbs]
+        cb, ctx = [], []
+        for f, c in zip(finalizers, contexts):
+            if f is None:
+                cb.append(None)
+                ctx.append(None)
+            else:
+                cb.append(C.cast(_finalizer_trampoline, _P))
+                ctx.append(_register_finalizer(f, c))
         h = _P()
         _check(load().mr_affine_adopt(packed_ptr, scales_ptr, biases_ptr, scale_dtype, experts, out_features,
-                                      in_features, group_size, bits, cb[0], contexts[0], cb[1], contexts[1], cb[2],
-                                      contexts[2], C.byref(h)))
+                                      in_features, group_size, bits, cb[0], ctx[0], cb[1], ctx[1], cb[2], ctx[2],
+                                      C.byref(h)))
         self.handle = h.value
         self.out_features, self.in_features = out_features, in_features
 
@@ -421,8 +458,14 @@ class AdoptedAffineWeights:
 
     def release(self, stream=None):
         """Drop one reference; the last one runs the finalizers behind the
-        work on `stream` (a torch stream or a raw handle), or now when None."""
-        _check(load().mr_adopted_affine_release(self.handle, _stream(stream) if stream is not None else None))
+        work on `stream` (a torch stream or a raw handle; None: torch's
+        current stream, as for every other call here)."""
+        _check(load().mr_adopted_affine_release(self.handle, _stream(stream)))
+
+    def release_now(self):
+        """Drop one reference; the last one runs the finalizers before this
+        returns (for a weight no GPU work reads any more)."""
+        _check(load().mr_adopted_affine_release_now(self.handle))
 
 
 class DenseWeights:

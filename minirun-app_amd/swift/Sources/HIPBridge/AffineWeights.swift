@@ -131,8 +131,15 @@ public final class HIPAdoptedAffineWeights {
     }
 
     /// Drops one holder; the last one runs the finalizers behind the work
-    /// already enqueued on `stream` (nil: now, no GPU work reads the weight).
-    public func release(after stream: HIPStream = nil) throws {
+    /// already enqueued on `stream` (nil is the default stream, as in every
+    /// other call; the stream must carry every read of the weight).
+    public func release(after stream: HIPStream) throws {
         try HIPError.check(mr_adopted_affine_release(handle, stream))
+    }
+
+    /// Drops one holder; the last one runs the finalizers before this
+    /// returns.  For a weight no GPU work reads any more.
+    public func releaseNow() throws {
+        try HIPError.check(mr_adopted_affine_release_now(handle))
     }
 }

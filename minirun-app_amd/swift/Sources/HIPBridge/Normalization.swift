@@ -7,7 +7,10 @@ public func hipRMSNorm(_ x: HIPTensor, weight: HIPTensor, eps: Float, into out: 
                        stream: HIPStream = nil) throws {
     let dim = x.shape[x.shape.count - 1]
     let rows = x.shape.dropLast().reduce(1, *)
-    try HIPError.check(mr_rmsnorm(x.raw, x.dtype, Int64(rows), Int32(dim), Int64(x.strides[x.strides.count - 2]),
+    // a 1-D tensor is one row: its row stride is never used, take the width
+    let xRowStride = x.strides.count > 1 ? x.strides[x.strides.count - 2] : dim
+    let outRowStride = out.strides.count > 1 ? out.strides[out.strides.count - 2] : dim
+    try HIPError.check(mr_rmsnorm(x.raw, x.dtype, Int64(rows), Int32(dim), Int64(xRowStride),
                                   weight.raw, weight.dtype, eps, out.pointer, out.dtype,
-                                  Int64(out.strides[out.strides.count - 2]), stream))
+                                  Int64(outRowStride), stream))
 }

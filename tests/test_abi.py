@@ -63,15 +63,26 @@ def test_workspace_size_is_deterministic_and_covers_partials():
 
 def test_validate_indices_rejects_oversize_without_gpu():
     lib = M.load()
-    st = lib.mr_validate_indices(None, 1, 8193, 10, None, 0, None, None, None)
+    st = lib.mr_validate_indices(None, 1, (1 << 22) + 1, 10, None, 0, None, None, None)
     assert st == M.INVALID_SHAPE
-    assert lib.mr_validate_indices(None, 1, 8192, 10, None, 0, None, None, None) == M.INVALID_ARGUMENT
+    assert lib.mr_validate_indices(None, 1, 1 << 22, 10, None, 0, None, None, None) == M.INVALID_ARGUMENT
+
+
+def test_validate_workspace_holds_long_list_tables():
+    # lists of up to 10176 entries are checked in LDS (the workspace holds
+    # the results only); longer ones keep one hash table per token there,
+    # at least 1.6 slots of 8 bytes per entry
+    lib = M.load()
+    small = lib.mr_validate_indices_workspace_size(4, 10176)
+    assert small == 256
+    big = lib.mr_validate_indices_workspace_size(4, 10177)
+    assert big >= 256 + 4 * 8 * int(1.6 * 10177)
+    assert lib.mr_validate_indices_workspace_size(2, 300000) >= 2 * 8 * int(1.6 * 300000)
 
 
 def test_sparse_decode_bounds_the_index_count_without_gpu():
     # a gathered split stages at most 512 indices and the combine merges at
-    # most 1024 splits: longer lists are refused before any launch; checked
-    # lists hold at most 8192 entries unless the caller opts out of checks
+    # most 1024 splits: longer lists are refused before any launch
     lib = M.load()
     a = M.DecodeArgs()
     a.batch, a.heads, a.n_ctx, a.kv_rank, a.rope_dim, a.scale = 1, 128, 1 << 20, 512, 64, 0.07
@@ -82,8 +93,18 @@ def test_sparse_decode_bounds_the_index_count_without_gpu():
     assert lib.mr_mla_decode(C.byref(a), None) == M.INVALID_SHAPE
     a.n_idx = 9000
     assert lib.mr_mla_decode(C.byref(a), None) == M.INVALID_ARGUMENT  # past the shape checks: NULL q
+    # checked lists of any length the call takes: the checks add their
+    # tables to the workspace once a list is too long for LDS
     a.flags = 0
-    assert lib.mr_mla_decode(C.byref(a), None) == M.INVALID_SHAPE and "8192" in M.last_error()
+    assert lib.mr_mla_decode(C.byref(a), None) == M.INVALID_ARGUMENT
+    a.n_idx = 512 * 1024
+    assert lib.mr_mla_decode(C.byref(a), None) == M.INVALID_ARGUMENT
+    a.index_status = 4096  # never dereferenced: the workspace size only
+    a.n_idx = 8320
+    w_lds = lib.mr_mla_decode_workspace_size(C.byref(a))
+    a.n_idx = 20000
+    w_tab = lib.mr_mla_decode_workspace_size(C.byref(a))
+    assert w_tab - w_lds >= 8 * int(1.6 * 20000)
 
 
 def test_prefill_rejects_bad_arguments_before_any_gpu_call():

@@ -306,10 +306,13 @@ def test_sparse_default_call_rejects_bad_lists(M):
     assert st == M.OK
 
 
-@pytest.mark.parametrize("n_ctx,n_idx,where", [(1 << 20, 8192, 8191), (1 << 20, 8192, None), (262144, 2176, 2000)])
+@pytest.mark.parametrize("n_ctx,n_idx,where", [(1 << 20, 8192, 8191), (1 << 20, 8192, None), (262144, 2176, 2000),
+                                              (1 << 20, 10176, 10175), (1 << 20, 10177, 10176),
+                                              (1 << 22, 300000, 299999), (1 << 22, 300000, None)])
 def test_device_index_check_long_lists(M, n_ctx, n_idx, where):
-    # V4-sized caches (up to 2^20 positions) and the longest checked list;
-    # a repeat at the very end, or none
+    # V4-sized caches (up to 2^22 positions); the longest list checked in LDS
+    # (10176) and the first one past it, and lists far longer, whose hash
+    # tables live in the workspace; a repeat at the very end, or none
     print(f"device index check n_ctx={n_ctx} n_idx={n_idx} repeat at {where}", flush=True)
     import ctypes as C
 
@@ -320,7 +323,8 @@ def test_device_index_check_long_lists(M, n_ctx, n_idx, where):
     idx = np.stack([rng.choice(n_ctx, n_idx, replace=False) for _ in range(B)]).astype(np.int32)
     if where is not None:
         idx[1, where] = idx[1, 0]
-    ws = torch.zeros(4096, dtype=torch.uint8, device="cuda")
+    lib = M.load()
+    ws = torch.zeros(lib.mr_validate_indices_workspace_size(B, n_idx), dtype=torch.uint8, device="cuda")
     bt, bp = C.c_int32(-9), C.c_int32(-9)
     st = M.load().mr_validate_indices(M._ptr(dev(idx)), B, n_idx, n_ctx, M._ptr(ws), ws.numel(), C.byref(bt),
                                       C.byref(bp), M._stream(None))
@@ -341,3 +345,84 @@ def test_sparse_validation_flag_rejects_before_compute(M):
     with pytest.raises(M.MRError) as e:
         run_sparse(M, ql, qr, cache, idx)
     assert e.value.status == M.DUPLICATE_INDEX and "token 1" in e.value.message
+
+
+def v4_ratio128_lists(B, start_pos=1048575, window=128, ratio=128):
+    """The index list DeepSeekV4CompressedAttention builds for one decode
+    token at start_pos with a ratio-128 compressed cache
+    (DeepSeekV4CompressedAttention.swift:1156-1166): the window positions,
+    then the compressed positions offset by the window, over keys/values
+    that are the window cache followed by the compressed cache.  Returns
+    (indices [B, 128 + (start_pos + 1) / 128], rows)."""
+    st, w = O.window_indices(window, 1, start_pos)
+    assert st == O.OK
+    st, c = O.compressed_indices(ratio, 1, start_pos, window)
+    assert st == O.OK
+    row = np.concatenate([w[0], c[0]]).astype(np.int32)
+    n_rows = window + (start_pos + 1) // ratio
+    return np.repeat(row[None], B, axis=0), n_rows
+
+
+def test_v4_ratio128_list_at_1m_positions_checked(M):
+    # the reference's longest causal sparse list at the V4 context limit
+    # (max_position_embeddings 1048576, current-official-config.json:22):
+    # 128 + 8192 = 8320 entries, checked on the device by the default call
+    # with a status buffer; a planted repeat and a planted out-of-range entry
+    # give the oracle's (status, position, value), the valid token's output
+    # matches the oracle
+    print("v4 ratio-128 list at position 1048575", flush=True)
+    import torch
+
+    B, H = 3, 16
+    idx, n_rows = v4_ratio128_lists(B)
+    K = idx.shape[1]
+    assert K == 8320 and n_rows == 8320
+    assert sorted(idx[0].tolist()) == list(range(n_rows))
+    idx[1, 7000] = idx[1, 300]                  # a repeat
+    idx[2, 5000] = n_rows                       # out of range, before
+    idx[2, 8000] = idx[2, 10]                   # a later repeat
+    ql = O.normal_bf16("v4l.q_lat", (B, H, 512))
+    qr = O.normal_bf16("v4l.q_rope", (B, H, 64))
+    cache = O.normal_bf16("v4l.cache", (1, n_rows, 576), std=0.5)
+    cache_b = np.ascontiguousarray(np.broadcast_to(cache, (B, n_rows, 576)))
+    status = torch.full((B, 3), 77, dtype=torch.int32, device="cuda")
+    st, out, _, _ = raw_sparse(M, ql, qr, cache_b, idx, index_status=status)
+    assert st == M.OK, M.last_error()
+    got = status.cpu().numpy()
+    for b in range(B):
+        ost, opos = O.validate_indices(idx[b], n_rows)
+        want = (ost, opos, idx[b, opos] if opos >= 0 else -1)
+        print(f"token {b}: device {tuple(got[b])} oracle {want}", flush=True)
+        assert tuple(got[b]) == want
+    assert [g[0] for g in got] == [M.OK, M.DUPLICATE_INDEX, M.INDEX_OUT_OF_RANGE]
+    assert got[1][1] == 7000 and got[2][1] == 5000
+    st0, ref0 = O.sparse_attention(ql[:1], qr[:1], cache, idx[:1])
+    assert st0 == O.OK
+    check(host_f32(out)[:1], ref0, "v4-8320", scale_bar=2e-3)
+    # the default call with no status buffer returns the first bad token's error
+    st, _, _, _ = raw_sparse(M, ql, qr, cache_b, idx)
+    assert st == M.DUPLICATE_INDEX
+    assert M.last_error() == f"token 1 names KV row {idx[1, 300]} more than once"
+
+
+def test_sparse_checked_list_past_lds_capacity(M):
+    # a list longer than an LDS table holds: the launch's check workgroups
+    # keep their tables in the workspace, the synchronous check too
+    print("sparse checked list of 12000 entries", flush=True)
+    import torch
+
+    B, H, N, K = 2, 16, 40000, 12000
+    ql, qr, cache, idx = MI.sparse_inputs(B, H, N, K, window=64, tag="lc")
+    idx = idx.copy()
+    idx[1, 11990] = idx[1, 7]
+    status = torch.full((B, 3), 77, dtype=torch.int32, device="cuda")
+    st, out, _, _ = raw_sparse(M, ql, qr, cache, idx, index_status=status)
+    assert st == M.OK, M.last_error()
+    got = status.cpu().numpy()
+    assert tuple(got[0]) == (M.OK, -1, -1)
+    assert tuple(got[1]) == (M.DUPLICATE_INDEX, 11990, idx[1, 7])
+    assert O.validate_indices(idx[1], N) == (O.DUPLICATE_INDEX, 11990)
+    st0, ref0 = O.sparse_attention(ql[:1], qr[:1], cache[:1], idx[:1])
+    check(host_f32(out)[:1], ref0, "sparse-12000", scale_bar=2e-3)
+    st, _, _, _ = raw_sparse(M, ql, qr, cache, idx)
+    assert st == M.DUPLICATE_INDEX
