@@ -70,7 +70,8 @@ __device__ __forceinline__ int64_t part_rec(const DecodeParams& p, int b, int he
 // order, skips -1, and stops at the first entry outside [0, n_rows) or equal
 // to an earlier entry.  One workgroup does it with no sort: every in-range
 // value goes into an open-addressing table (linear probing, Fibonacci hash
-// mapped onto `slots` by a multiply-high, at least 1.6 slots per entry) that
+// mapped onto `slots` by a multiply-high; a power of two with at least two
+// slots per entry for lists of up to 8192, else at least 1.6 per entry) that
 // keeps the smallest position holding the value; an entry is a repeat
 // exactly when its position is not its value's smallest.  The first error is
 // the smallest position that is out of range or a repeat.  res = (status,
@@ -79,20 +80,35 @@ __device__ __forceinline__ int64_t part_rec(const DecodeParams& p, int b, int he
 // VALIDATE_LDS_MAX_IDX entries, else in global memory (the workspace), where
 // every access is a workgroup-scope atomic so the workgroup's own updates
 // are what it reads.
-__host__ __device__ constexpr int validate_slots(int n_idx) { return ((n_idx * 8 + 4) / 5 + 1 + 63) / 64 * 64; }
+__host__ __device__ constexpr int validate_slots(int n_idx) {
+    if (n_idx <= 8192) {  // a power of two, at least twice the entries (the multiply-high below is then a shift)
+        int slots = 64;
+        while (slots < 2 * n_idx) slots *= 2;
+        return slots;
+    }
+    return ((n_idx * 8 + 4) / 5 + 1 + 63) / 64 * 64;  // at least 1.6 slots per entry
+}
 constexpr int VALIDATE_LDS_BYTES = 131072;  // a check workgroup's LDS table (the smallest decode row ring)
 constexpr int VALIDATE_LDS_MAX_IDX = 10176;
 static_assert(validate_slots(VALIDATE_LDS_MAX_IDX) * 8 <= VALIDATE_LDS_BYTES, "LDS index table");
 constexpr int VALIDATE_MAX_IDX = 1 << 22;  // longest list the checks take (table in the workspace)
 
+template <bool GLOBAL_TABLE>
 __device__ void validate_token(const int32_t* __restrict__ ind, int32_t n_idx, int32_t n_rows, int32_t* table, int nt,
                                int tid, int32_t* res) {
     __shared__ int32_t first_range, first_dup;
     const uint32_t slots = (uint32_t)validate_slots(n_idx);
     int32_t* key = table;
     int32_t* minpos = table + slots;
-    auto ld = [](int32_t* a) { return __hip_atomic_load(a, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP); };
-    auto st = [](int32_t* a, int32_t v) { __hip_atomic_store(a, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP); };
+    // LDS: plain ds operations; global memory: workgroup-scope atomics
+    auto ld = [](int32_t* a) {
+        if constexpr (GLOBAL_TABLE) return __hip_atomic_load(a, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        else return *a;
+    };
+    auto st = [](int32_t* a, int32_t v) {
+        if constexpr (GLOBAL_TABLE) __hip_atomic_store(a, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        else *a = v;
+    };
     for (uint32_t i = tid; i < slots; i += nt) {
         st(key + i, -1);
         st(minpos + i, 0x7fffffff);
@@ -113,11 +129,19 @@ __device__ void validate_token(const int32_t* __restrict__ ind, int32_t n_idx, i
         }
         uint32_t h = home(v);
         for (uint32_t t = 0; t < slots; ++t) {  // the table is never full: ends within `slots` probes
-            int32_t prev = -1;
-            __hip_atomic_compare_exchange_strong(key + h, &prev, v, __ATOMIC_RELAXED, __ATOMIC_RELAXED,
-                                                 __HIP_MEMORY_SCOPE_WORKGROUP);
+            int32_t prev;
+            if constexpr (GLOBAL_TABLE) {
+                prev = -1;
+                __hip_atomic_compare_exchange_strong(key + h, &prev, v, __ATOMIC_RELAXED, __ATOMIC_RELAXED,
+                                                     __HIP_MEMORY_SCOPE_WORKGROUP);
+            } else {
+                prev = atomicCAS(key + h, -1, v);
+            }
             if (prev == -1 || prev == v) {
-                __hip_atomic_fetch_min(minpos + h, i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+                if constexpr (GLOBAL_TABLE)
+                    __hip_atomic_fetch_min(minpos + h, i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+                else
+                    atomicMin(minpos + h, i);
                 break;
             }
             h = next(h);
@@ -192,10 +216,15 @@ __global__ void __launch_bounds__((WsShape<HGS, QK16>::THREADS), 1) mla_decode_w
 
     if (GATHER && (int)blockIdx.x < p.check_blocks) {  // index-check workgroups
         if ((int)blockIdx.x < p.batch)
-            validate_token(p.indices + (int64_t)blockIdx.x * p.n_idx, p.n_idx, p.n_ctx,
-                           p.check_table ? p.check_table + (int64_t)blockIdx.x * 2 * validate_slots(p.n_idx)
-                                         : (int32_t*)cbuf,
-                           NT, threadIdx.x, p.index_status + 3 * blockIdx.x);
+        {
+            const int32_t* ind = p.indices + (int64_t)blockIdx.x * p.n_idx;
+            int32_t* res = p.index_status + 3 * blockIdx.x;
+            if (p.check_table)
+                validate_token<true>(ind, p.n_idx, p.n_ctx, p.check_table + (int64_t)blockIdx.x * 2 * validate_slots(p.n_idx),
+                                     NT, threadIdx.x, res);
+            else
+                validate_token<false>(ind, p.n_idx, p.n_ctx, (int32_t*)cbuf, NT, threadIdx.x, res);
+        }
         return;
     }
     const int bid = blockIdx.x - (GATHER ? p.check_blocks : 0);
@@ -1000,8 +1029,12 @@ hipError_t launch_split(const DecodeParams& p, int grid, hipStream_t st) {
 __global__ void __launch_bounds__(1024) validate_indices_kernel(const int32_t* indices, int32_t n_idx, int32_t n_rows,
                                                                 int32_t* tables, int32_t* result) {
     extern __shared__ int32_t table[];
-    int32_t* t = tables ? tables + (int64_t)blockIdx.x * 2 * validate_slots(n_idx) : table;
-    validate_token(indices + (int64_t)blockIdx.x * n_idx, n_idx, n_rows, t, 1024, threadIdx.x, result + 3 * blockIdx.x);
+    const int32_t* ind = indices + (int64_t)blockIdx.x * n_idx;
+    if (tables)
+        validate_token<true>(ind, n_idx, n_rows, tables + (int64_t)blockIdx.x * 2 * validate_slots(n_idx), 1024,
+                             threadIdx.x, result + 3 * blockIdx.x);
+    else
+        validate_token<false>(ind, n_idx, n_rows, table, 1024, threadIdx.x, result + 3 * blockIdx.x);
 }
 
 }  // namespace
