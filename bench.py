@@ -548,6 +548,53 @@ def torch_cpu_decode(torch, threads, budget_s=8.0):
     return times[len(times) // 2], len(times)
 
 
+PROJ_T = 4096
+# prefill-sized projections (T = 4096 tokens): the 4-bit affine block shapes
+# (group 64, bf16 scales) and the K3 dense bf16 ones, [out, in]
+PROJ_AFFINE = [("q_a", 1536, 7168), ("q_b", 24576, 1536), ("kv_a", 576, 7168), ("o_proj", 7168, 16384)]
+PROJ_DENSE = [("q_a", 1536, 7168), ("q_b", 18432, 1536), ("kv_a", 576, 7168), ("o_proj", 7168, 12288)]
+
+
+def time_projections(torch, M, reps=20):
+    """mr_affine_matmul / mr_linear at T = 4096 on each shape (bf16 x and y,
+    random weights): the average duration of `reps` back-to-back launches
+    between two events, and the aggregate algorithmic TFLOP/s (2 T out in
+    per projection)."""
+    g = torch.Generator(device="cuda")
+    g.manual_seed(0x50524F4A)
+    out = {}
+    for kind, shapes in (("affine_4bit", PROJ_AFFINE), ("dense_bf16", PROJ_DENSE)):
+        res, flop_total, us_total = {}, 0.0, 0.0
+        for name, n, k in shapes:
+            x = torch.randn(PROJ_T, k, generator=g, device="cuda").to(torch.bfloat16)
+            if kind == "affine_4bit":
+                packed = torch.randint(-2 ** 31, 2 ** 31 - 1, (n, k // 8), generator=g, device="cuda", dtype=torch.int32)
+                sc = (torch.rand(n, k // 64, generator=g, device="cuda") * 0.01).to(torch.bfloat16)
+                bi = (torch.randn(n, k // 64, generator=g, device="cuda") * 0.01).to(torch.bfloat16)
+                w = M.AffineWeights(packed, sc, bi)
+                call = lambda: M.affine_mm(x, w)  # noqa: E731
+            else:
+                w = M.DenseWeights((torch.randn(n, k, generator=g, device="cuda") * k ** -0.5).to(torch.bfloat16))
+                call = lambda: M.linear(x, w)  # noqa: E731
+            for _ in range(3):
+                call()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            for _ in range(reps):
+                call()
+            e1.record()
+            torch.cuda.synchronize()
+            us = e0.elapsed_time(e1) / reps * 1e3
+            flop = 2.0 * PROJ_T * n * k
+            res[f"{name}_us"] = round(us, 1)
+            flop_total += flop
+            us_total += us
+        res["tflops"] = round(flop_total / (us_total * 1e-6) / 1e12, 1)
+        res["mfma_fraction"] = round(flop_total / (us_total * 1e-6) / 1e12 / MFMA_PEAK_TFLOPS, 4)
+        out[kind] = res
+    return out
+
+
 def cpu_baseline(torch, budget_s=4.0):
     """The decode layer (H=128, N=32768) on this host's cores.  The value is
     the layer as torch-CPU fp32 BLAS products (the fastest CPU form of the
@@ -640,6 +687,9 @@ def main():
     log("bench: routed-expert GEMV, 8 of 128 experts of [768, 2048] 4-bit")
     gx_ms = time_gather(torch, M)
     log(f"bench: gather {gx_ms * 1e3:.2f} us")
+    log(f"bench: projections at T={PROJ_T} (4-bit affine and dense bf16, MFMA)")
+    pj = time_projections(torch, M)
+    log(f"bench: projections {pj}")
     mp = mfma_probe(torch, M)
     log(f"bench: mfma probe {mp}")
 
@@ -686,6 +736,7 @@ def main():
         "indexer_hbm_fraction": round(32768 * 128 * 2 / (ix_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
         "gather_8x768x2048_us": round(gx_ms * 1e3, 2),
         "gather_hbm_fraction": round(8 * 768 * (2048 // 2 + 4 * 2048 // 64) / (gx_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+        "projections_t4096": pj,
         "mfma_probe_tflops": mp["tflops"],
         "mfma_probe_clock_ghz": mp["clock_ghz"],
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",

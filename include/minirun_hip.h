@@ -239,7 +239,12 @@ mr_status mr_affine_dequantize(const mr_affine_weight *w, void *out, mr_dtype ou
  * transpose fixed (W is [out, in]).  x: [tokens, in] bf16 or f32 with row
  * stride x_stride; y: [tokens, out] bf16 or f32 with row stride y_stride;
  * fp32 accumulation.  4-bit / group-64 / bf16 x / one token runs the fused
- * dequant-GEMV; other shapes run a generic kernel. */
+ * dequant-GEMV; 64 or more bf16 tokens of a 4-bit weight whose group is a
+ * multiple of 32 (in_features a multiple of 32, out_features of 8, 16-byte
+ * aligned x and y rows) run on MFMA: each k-tile dequantized into LDS and
+ * split into two bf16 operands (hi = bf16(w), lo = bf16(w - hi)), so each
+ * product misses x * w by at most 2^-18 |w|; other shapes run a generic
+ * kernel. */
 mr_status mr_affine_matmul(const void *x, mr_dtype x_dtype, int32_t tokens, int64_t x_stride,
                            const mr_affine_weight *w, void *y, mr_dtype y_dtype, int64_t y_stride,
                            void *stream);
@@ -285,7 +290,10 @@ typedef struct mr_dense_weight {
 
 /* y[t, :] = x[t, :] . W^T for `tokens` rows of x (bf16 or f32, row stride
  * x_stride) into y (bf16 or f32, row stride y_stride), fp32 accumulation.
- * Every weight byte is read once per tile of up to 8 tokens. */
+ * 64 or more bf16 tokens with a bf16 weight (in_features a multiple of 64,
+ * out_features of 8, 16-byte aligned rows) run as an MFMA GEMM in tiles of
+ * 256 (or 128) tokens x 256 outputs; otherwise every weight byte is read
+ * once per tile of up to 8 tokens. */
 mr_status mr_linear(const void *x, mr_dtype x_dtype, int32_t tokens, int64_t x_stride, const mr_dense_weight *w,
                     void *y, mr_dtype y_dtype, int64_t y_stride, void *stream);
 

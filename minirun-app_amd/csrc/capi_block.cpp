@@ -374,6 +374,28 @@ mr_status mr_affine_matmul(const void* x, mr_dtype x_dtype, int32_t tokens, int6
     g.y_stride_row = 1;
     g.y_stride_token = y_stride;
     g.force_generic = !aligned16(w->packed);  // the fused kernel loads 16-byte row chunks
+    if (tokens >= mr::PROJ_GEMM_MIN_TOKENS && x_dtype == MR_BF16) {
+        // many tokens: dequantized k-tiles into LDS and MFMA
+        mr::ProjGemmParams q{};
+        q.x = (const uint16_t*)x;
+        q.ldx = x_stride;
+        q.packed = w->packed;
+        q.scales = w->scales;
+        q.biases = w->biases;
+        q.scale_dtype = scale_code(w->scale_dtype);
+        q.group = w->group;
+        q.bits = w->bits;
+        q.y = y;
+        q.ldy = y_stride;
+        q.y_f32 = y_dtype == MR_F32;
+        q.M = tokens;
+        q.N = (int)w->out_features;
+        q.K = (int)w->in_features;
+        if (mr::proj_gemm_ok(q)) {
+            const hipError_t e = mr::launch_proj_gemm(q, mrc::cu_count(), (hipStream_t)stream);
+            return e == hipSuccess ? MR_OK : hip_fail(e, "affine matmul launch");
+        }
+    }
     const hipError_t e = mr::launch_affine_gemv(g, (hipStream_t)stream);
     return e == hipSuccess ? MR_OK : hip_fail(e, "affine matmul launch");
 }
@@ -394,6 +416,24 @@ mr_status mr_linear(const void* x, mr_dtype x_dtype, int32_t tokens, int64_t x_s
     if (w->in_features * (x_dtype == MR_F32 ? 4 : 2) < 16)
         return fail(MR_INVALID_SHAPE, "linear: an activation row of %lld %s values is under 16 bytes",
                     (long long)w->in_features, dtype_name(x_dtype));
+    if (tokens >= mr::PROJ_GEMM_MIN_TOKENS && x_dtype == MR_BF16 && w->dtype == MR_BF16) {
+        // many tokens: MFMA tiles
+        mr::ProjGemmParams q{};
+        q.x = (const uint16_t*)x;
+        q.ldx = x_stride;
+        q.w = (const uint16_t*)w->weight;
+        q.ldw = w->row_stride;
+        q.y = y;
+        q.ldy = y_stride;
+        q.y_f32 = y_dtype == MR_F32;
+        q.M = tokens;
+        q.N = (int)w->out_features;
+        q.K = (int)w->in_features;
+        if (mr::proj_gemm_ok(q)) {
+            const hipError_t e = mr::launch_proj_gemm(q, mrc::cu_count(), (hipStream_t)stream);
+            return e == hipSuccess ? MR_OK : hip_fail(e, "linear launch");
+        }
+    }
     mr::DenseGemvParams g = dense_params(w);
     g.x = x;
     g.x_f32 = x_dtype == MR_F32;

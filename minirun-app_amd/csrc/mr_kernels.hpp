@@ -124,6 +124,29 @@ struct PrefillAttnParams {
 };
 
 hipError_t launch_upproj(const UpProjParams& p, hipStream_t st);
+
+// ---------------------------------------------------------------- token-tiled projections
+// y[M][N] = x[M][K] . W[N][K]^T on MFMA (gemm.hip): x bf16 rows of stride
+// ldx; W dense bf16 rows of stride ldw (packed null), or 4-bit affine rows
+// (packed [N][K/8] uint32, scales / biases [N][K/group] of scale_dtype 0
+// bf16, 1 f16, 2 f32); y bf16 or f32 rows of stride ldy.
+struct ProjGemmParams {
+    const uint16_t* x;
+    int64_t ldx;
+    const uint16_t* w;
+    int64_t ldw;
+    const void* packed;
+    const void* scales;
+    const void* biases;
+    int32_t scale_dtype, group, bits;
+    void* y;
+    int64_t ldy;
+    int32_t y_f32;
+    int32_t M, N, K;
+};
+constexpr int PROJ_GEMM_MIN_TOKENS = 64;  // fewer tokens take the token-tile GEMV kernels
+bool proj_gemm_ok(const ProjGemmParams& p);  // shapes, alignment and formats the kernel takes
+hipError_t launch_proj_gemm(const ProjGemmParams& p, int cu_count, hipStream_t st);
 hipError_t launch_prefill_attn(const PrefillAttnParams& p, hipStream_t st);
 
 // ---------------------------------------------------------------- top-k
