@@ -54,7 +54,9 @@ struct Geo {
 // (8 rows of one parity, one chunk pair) on distinct banks.  The rope chunks
 // (c >= 64) swizzle inside their own 8-chunk group.  The map is an involution.
 __device__ __forceinline__ int swz(int c, int r) {
-    return c < 64 ? (c ^ (r & 15)) : (64 + ((c - 64) ^ (r & 7)));
+    // c < 64: c ^ (r & 15); the rope chunks 64 + j (j < 8): 64 + (j ^ (r & 7)),
+    // which is c ^ (r & 7) -- one select, no branch
+    return c ^ (r & (c < 64 ? 15 : 7));
 }
 
 constexpr float TAU = 8.f;  // log2 headroom before the running max is raised
@@ -193,6 +195,24 @@ __device__ __forceinline__ int ksig(int p) {
     return (p & ~7) | (j < 4 ? 2 * j : 2 * (j - 4) + 1);
 }
 
+// A kernel's parameter block read in one batch: each dword passes through
+// an empty asm that the compiler must treat as changing it, so every load
+// is issued (and waited for once) before any field is used.
+template <typename P>
+__device__ __forceinline__ P load_params(const P& arg) {
+    static_assert(sizeof(P) % 4 == 0, "parameter block of whole dwords");
+    constexpr int NW = sizeof(P) / 4;
+    uint32_t w[NW];
+    const uint32_t* src = reinterpret_cast<const uint32_t*>(&arg);
+#pragma unroll
+    for (int i = 0; i < NW; ++i) w[i] = src[i];
+#pragma unroll
+    for (int i = 0; i < NW; ++i) asm volatile("" : "+s"(w[i]));
+    P q;
+    __builtin_memcpy(&q, w, sizeof(P));
+    return q;
+}
+
 // QK waves of 32 heads (32x32x16 MFMA) or, with QK16, of 16 heads (16x16x32
 // MFMA): a 64-head group then has one QK wave per SIMD beside each PV wave.
 template <int HGS, bool QK16>
@@ -202,7 +222,11 @@ struct WsShape {
 };
 
 template <int DR, bool GATHER, bool PACKED, int HGS, bool QK16>
-__global__ void __launch_bounds__((WsShape<HGS, QK16>::THREADS), 1) mla_decode_ws(DecodeParams p) {
+__global__ void __launch_bounds__((WsShape<HGS, QK16>::THREADS), 1) mla_decode_ws(DecodeParams p_arg) {
+    // every launch parameter in one batch of scalar loads: loaded where each
+    // is first used, they would be several dependent memory round trips
+    // before the first row load
+    const DecodeParams p = load_params(p_arg);
     using G = Geo<DR>;
     constexpr int QKW = WsShape<HGS, QK16>::QKW;
     constexpr int NT = WsShape<HGS, QK16>::THREADS;
@@ -230,11 +254,14 @@ __global__ void __launch_bounds__((WsShape<HGS, QK16>::THREADS), 1) mla_decode_w
     const int bid = blockIdx.x - (GATHER ? p.check_blocks : 0);
     const int xcd = bid & 7;
     const int qb = bid >> 3;
-    const int hg = qb % p.head_groups;
-    const int unit = (qb / p.head_groups) * 8 + xcd;
+    // the divisions by multiply-high: the code before the first loads is
+    // fetched cold by every CU at each launch, so it is kept short
+    const int qg = p.hg_magic ? (int)__umulhi((uint32_t)qb, p.hg_magic) : qb / p.head_groups;
+    const int hg = qb - qg * p.head_groups;
+    const int unit = qg * 8 + xcd;
     if (unit >= p.batch * p.splits) return;
-    const int b = unit / p.splits;
-    const int split = unit % p.splits;
+    const int b = p.split_magic ? (int)__umulhi((uint32_t)unit, p.split_magic) : unit / p.splits;
+    const int split = unit - b * p.splits;
     const int row_begin = split * p.rows_per_split;
     const int row_end = min(row_begin + p.rows_per_split, p.n_rows);
     const int nrows = max(row_end - row_begin, 0);
@@ -547,7 +574,7 @@ __global__ void __launch_bounds__((WsShape<HGS, QK16>::THREADS), 1) mla_decode_w
                     const int v = (rbase + rr < row_end) ? idx_s[rbase + rr - row_begin] : -1;
                     src_row = v >= 0 ? v : 0;
                 } else {
-                    if (rbase + ROWS > row_end) rr = min(rr, row_end - 1 - rbase);
+                    rr = min(rr, row_end - 1 - rbase);  // rows past the split repeat its last row
                     src_row = rbase + rr;
                 }
                 char* dst = base + 1024 * (pw + 4 * k);
@@ -565,6 +592,10 @@ __global__ void __launch_bounds__((WsShape<HGS, QK16>::THREADS), 1) mla_decode_w
                 }
             }
         };
+        // prologue: sub-chunks 0 .. NBUF-2 at once (the QK waves load Q
+        // themselves), issued before the rest of the set-up
+        const int pro0 = min(nsub, NBUF - 1);
+        for (int s = 0; s < pro0; ++s) issue(s, cbuf + s * G::BUF);
         // B operand of PV: k position p holds key row ksig(p), so lane group
         // lg takes rows 8lg + {0,2,4,6} (tr0) and 8lg + {1,3,5,7} (tr1) of
         // column block 16J by transposed reads; lane lc addresses row
@@ -586,10 +617,7 @@ __global__ void __launch_bounds__((WsShape<HGS, QK16>::THREADS), 1) mla_decode_w
         for (int T = 0; T < HT; ++T)
 #pragma unroll
             for (int J = 0; J < 8; ++J) oacc[T][J] = f32x4{0.f, 0.f, 0.f, 0.f};
-        // prologue: sub-chunks 0 .. NBUF-2 at once (the QK waves load Q
-        // themselves), wait for 0
-        const int pro0 = min(nsub, NBUF - 1);
-        for (int s = 0; s < pro0; ++s) issue(s, cbuf + s * G::BUF);
+        // wait for sub-chunk 0
         const int pro = min(nsub, NBUF - 1);
         if (pro >= 3)
             wait_vmcnt<2 * G::NLD>();
@@ -1096,10 +1124,20 @@ hipError_t launch_combine_unabsorb(const CombineUnabsorbParams& p, hipStream_t s
               [&] { hipLaunchKernelGGL((mla_combine_unabsorb<false, false>), grid, block, lds, st, p); });
 }
 
-hipError_t launch_mla_decode(const DecodeParams& p, const CombineParams& cp, bool split_only,
+// floor(2^32 / d) + 1: x / d == __umulhi(x, magic) for every x <= x_max
+// when x_max * d < 2^32; 0 (divide) otherwise
+static uint32_t div_magic(uint32_t d, uint32_t x_max) {
+    if (d <= 1 || (uint64_t)x_max * d >= (1ull << 32)) return 0;
+    return (uint32_t)((1ull << 32) / d + 1);
+}
+
+hipError_t launch_mla_decode(const DecodeParams& p_in, const CombineParams& cp, bool split_only,
                              hipEvent_t const* events, hipStream_t st) {
+    DecodeParams p = p_in;
     const int units = p.batch * p.splits;
     const int grid = p.check_blocks + 8 * p.head_groups * ((units + 7) / 8);
+    p.hg_magic = div_magic((uint32_t)p.head_groups, (uint32_t)grid >> 3);
+    p.split_magic = div_magic((uint32_t)p.splits, (uint32_t)units + 8);
     hipError_t e;
     if (events && (e = hipEventRecord(events[0], st)) != hipSuccess) return e;
     const bool g = p.indices != nullptr;

@@ -40,6 +40,9 @@ struct DecodeParams {
     // the check workgroups' hash tables (2 * slots int32 per token) for lists
     // too long for LDS; null: in LDS
     int32_t* check_table;
+    // x / head_groups and x / splits as __umulhi(x, magic) (floor(2^32 / d)
+    // + 1, exact while x * d < 2^32; 0: divide), set by launch_mla_decode
+    uint32_t hg_magic, split_magic;
 };
 
 struct CombineParams {
