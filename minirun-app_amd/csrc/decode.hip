@@ -195,24 +195,6 @@ __device__ __forceinline__ int ksig(int p) {
     return (p & ~7) | (j < 4 ? 2 * j : 2 * (j - 4) + 1);
 }
 
-// A kernel's parameter block read in one batch: each dword passes through
-// an empty asm that the compiler must treat as changing it, so every load
-// is issued (and waited for once) before any field is used.
-template <typename P>
-__device__ __forceinline__ P load_params(const P& arg) {
-    static_assert(sizeof(P) % 4 == 0, "parameter block of whole dwords");
-    constexpr int NW = sizeof(P) / 4;
-    uint32_t w[NW];
-    const uint32_t* src = reinterpret_cast<const uint32_t*>(&arg);
-#pragma unroll
-    for (int i = 0; i < NW; ++i) w[i] = src[i];
-#pragma unroll
-    for (int i = 0; i < NW; ++i) asm volatile("" : "+s"(w[i]));
-    P q;
-    __builtin_memcpy(&q, w, sizeof(P));
-    return q;
-}
-
 // QK waves of 32 heads (32x32x16 MFMA) or, with QK16, of 16 heads (16x16x32
 // MFMA): a 64-head group then has one QK wave per SIMD beside each PV wave.
 template <int HGS, bool QK16>

@@ -181,6 +181,26 @@ __device__ __forceinline__ void wait_vmcnt() {
     asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
 
+// A kernel's parameter block read in one batch: each dword passes through
+// an empty asm that the compiler must treat as changing it, so every load
+// is issued (and waited for once) before any field is used.  Loaded where
+// each field is first used, the block costs several dependent scalar-memory
+// round trips, which latency-bound kernels pay on their critical path.
+template <typename P>
+__device__ __forceinline__ P load_params(const P& arg) {
+    static_assert(sizeof(P) % 4 == 0, "parameter block of whole dwords");
+    constexpr int NW = sizeof(P) / 4;
+    uint32_t w[NW];
+    const uint32_t* src = reinterpret_cast<const uint32_t*>(&arg);
+#pragma unroll
+    for (int i = 0; i < NW; ++i) w[i] = src[i];
+#pragma unroll
+    for (int i = 0; i < NW; ++i) asm volatile("" : "+s"(w[i]));
+    P q;
+    __builtin_memcpy(&q, w, sizeof(P));
+    return q;
+}
+
 // Full-wave max and sum: the group_sum butterfly over all 64 lanes (DPP and
 // permlane swaps, no LDS round trips); every lane ends with the result.
 __device__ __forceinline__ float wave_max(float v) {
