@@ -91,9 +91,14 @@ const char *mr_get_last_error(void);
  * Layout: the cache is one bf16 row per position; the latent part and the
  * shared rope key are given as two (pointer, row stride) pairs so that both
  * the packed [P, 576] row and the reference's two arrays [P,512] + [P,64]
- * (MLA.swift:28-36) are expressible.  kv_rank must be 512; rope_dim 64 or 0
- * (0 = the V4 form, K = V = row).  Strides are in elements, multiples of 8;
- * base pointers 16-byte aligned.
+ * (MLA.swift:28-36) are expressible.  kv_rank 512 with rope_dim 64 or 0 (0 =
+ * the V4 form, K = V = row) runs the split kernel: strides in elements,
+ * multiples of 8; base pointers 16-byte aligned.  Other widths (kv_rank 1 ..
+ * 2048, rope_dim 0 .. 512, e.g. the reference's synthetic K3 artifact,
+ * kv_lora 16 / rope 4) run an any-width kernel in fp32 (no bf16 rounding of
+ * P), one workgroup per (batch, head), elements read one by one: pointers
+ * element-aligned, strides covering the rows; its workspace only holds the
+ * index checks' words and tables.
  * ------------------------------------------------------------------------ */
 typedef struct mr_mla_decode_args {
     int32_t batch, heads, n_ctx, kv_rank, rope_dim;
@@ -409,8 +414,12 @@ mr_status mr_mla_decode_block(const mr_mla_block_args *args, void *stream);
  * Query i of `tokens` sits at cache position n_ctx - tokens + i and sees
  * keys 0 .. n_ctx - tokens + i (the reference adds -FLT_MAX to the rest);
  * fp32 softmax.  out[i][h] = softmax(q . K^T * scale) . V.
- * Fixed widths: qk_nope 128, qk_rope 64, v_head 128, kv_rank 512.
- * Workspace: the up-projected keys/values, n_ctx * heads * 512 bytes.
+ * Widths qk_nope 128, qk_rope 64, v_head 128, kv_rank 512 run on MFMA
+ * (workspace: the up-projected keys/values in bf16, n_ctx * heads * 512
+ * bytes; 16-byte aligned pointers, strides multiples of 8).  Other widths
+ * (kv_rank and v_head 1 .. 2048, qk_nope 0 .. 1024, qk_rope 0 .. 512) run
+ * any-width kernels in fp32 (workspace n_ctx * heads * (nope + v) * 4 bytes;
+ * element-aligned pointers, strides covering the rows).
  * phase_events: NULL or 3 hipEvents recorded before the up-projection,
  * between the two kernels and after the attention.
  * ------------------------------------------------------------------------ */

@@ -32,7 +32,7 @@ FLAGS = [
 ]
 
 LIB_SOURCES = ["capi.cpp", "capi_adopt.cpp", "capi_block.cpp", "capi_prefill.cpp", "capi_topk.cpp", "decode.hip", "affine.hip",
-               "mla_block.hip", "prefill.hip", "topk.hip", "indexer.hip", "linear.hip", "gemm.hip"]
+               "mla_block.hip", "prefill.hip", "topk.hip", "indexer.hip", "linear.hip", "gemm.hip", "generic.hip"]
 # Per-source flags.  The decode kernel keeps its MFMA accumulators in VGPRs
 # (VGPR-form MFMA): with the AGPR form the compiler shuttles all 64 of them
 # through v_accvgpr moves on every 32-row step.

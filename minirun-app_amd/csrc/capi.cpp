@@ -88,9 +88,20 @@ size_t validate_ws_bytes(int32_t batch, int32_t n_idx) {
            align256(mr::validate_table_bytes(std::max(batch, 0), std::max(n_idx, 0)));
 }
 
+// the widths the split kernel takes; others run the any-width kernel
+bool decode_fast_dims(const mr_mla_decode_args* a) { return a->kv_rank == 512 && (a->rope_dim == 64 || a->rope_dim == 0); }
+
 DecodePlan plan_decode(const mr_mla_decode_args* a) {
     DecodePlan pl{};
     pl.n_rows = a->indices ? a->n_idx : a->n_ctx;
+    pl.checked = a->indices && !(a->flags & MR_DECODE_UNCHECKED);
+    pl.sync_check = pl.checked && (!a->index_status || (a->flags & MR_DECODE_VALIDATE_INDICES));
+    if (!decode_fast_dims(a)) {
+        // any-width kernel: no partials; the index checks' result words and
+        // long lists' tables (laid out as mr_validate_indices lays them out)
+        pl.total = pl.checked ? validate_ws_bytes(a->batch, a->n_idx) : 0;
+        return pl;
+    }
     pl.hg_size = mr::decode_head_group_size(a->heads);
     pl.head_groups = (a->heads + pl.hg_size - 1) / pl.hg_size;
     pl.h_pad = pl.head_groups * pl.hg_size;
@@ -129,8 +140,6 @@ DecodePlan plan_decode(const mr_mla_decode_args* a) {
     pl.ml_bytes = align256(recs * 2 * sizeof(float));
     // index checks in the split launch keep long lists' tables after the
     // partials; a check before the launch uses the workspace first
-    pl.checked = a->indices && !(a->flags & MR_DECODE_UNCHECKED);
-    pl.sync_check = pl.checked && (!a->index_status || (a->flags & MR_DECODE_VALIDATE_INDICES));
     pl.table_bytes = (pl.checked && !pl.sync_check) ? align256(mr::validate_table_bytes(a->batch, a->n_idx)) : 0;
     pl.total = pl.o_bytes + pl.ml_bytes + pl.table_bytes;
     if (pl.sync_check) pl.total = std::max(pl.total, validate_ws_bytes(a->batch, a->n_idx));
@@ -146,14 +155,51 @@ mrc::DecodePartials mrc::decode_partials(const mr_mla_decode_args* a) {
 
 namespace {
 
+// Widths the split kernel does not take (kv_rank other than 512, rope_dim
+// other than 64 or 0): the any-width kernel reads elements one by one, so
+// only element alignment and strides that cover the rows are required.
+mr_status check_decode_any(const mr_mla_decode_args* a) {
+    if (!(std::isfinite(a->scale) && a->scale > 0))
+        return fail(MR_INVALID_SHAPE, "sparse attention queries, shared KV, sinks, indices, or scale are invalid: "
+                                      "scale %g must be finite and positive", double(a->scale));
+    if (a->indices) {
+        if (a->n_idx < 0) return fail(MR_INVALID_SHAPE, "mla decode: n_idx %d is negative", a->n_idx);
+        if (a->n_ctx <= 0) return fail(MR_INVALID_SHAPE, "mla decode: the cache has no rows (n_ctx %d)", a->n_ctx);
+        if (!(a->flags & MR_DECODE_UNCHECKED) && a->n_idx > mr::validate_max_indices())
+            return fail(MR_INVALID_SHAPE, "mla decode: index checks take at most %d entries per token, got %d "
+                        "(MR_DECODE_UNCHECKED skips them)", mr::validate_max_indices(), a->n_idx);
+    } else if (a->n_ctx <= 0) {
+        return fail(MR_INVALID_SHAPE, "mla decode: n_ctx %d must be positive", a->n_ctx);
+    }
+    if (!a->q_lat || !a->latent || !a->out)
+        return fail(MR_INVALID_ARGUMENT, "mla decode: q_lat, latent and out must be non-NULL");
+    if (a->rope_dim && (!a->q_rope || !a->rope_keys))
+        return fail(MR_INVALID_ARGUMENT, "mla decode: rope_dim %d needs q_rope and rope_keys", a->rope_dim);
+    auto al2 = [](const void* q) { return ((uintptr_t)q & 1) == 0; };
+    if (!al2(a->q_lat) || !al2(a->latent) || !al2(a->out) || (a->rope_dim && (!al2(a->q_rope) || !al2(a->rope_keys))))
+        return fail(MR_INVALID_ARGUMENT, "mla decode: q, cache and out pointers must be element-aligned");
+    if (a->q_lat_batch_stride < 0 || a->latent_batch_stride < 0 || a->out_batch_stride < 0 ||
+        a->q_lat_head_stride < a->kv_rank || a->latent_row_stride < a->kv_rank || a->out_head_stride < a->kv_rank)
+        return fail(MR_INVALID_ARGUMENT, "mla decode: strides must be non-negative and cover kv_rank %d", a->kv_rank);
+    if (a->rope_dim && (a->q_rope_batch_stride < 0 || a->rope_batch_stride < 0 || a->q_rope_head_stride < a->rope_dim ||
+                        a->rope_row_stride < a->rope_dim))
+        return fail(MR_INVALID_ARGUMENT, "mla decode: rope strides must be non-negative and cover rope_dim %d",
+                    a->rope_dim);
+    if (a->out_dtype != MR_BF16 && a->out_dtype != MR_F32)
+        return fail(MR_INVALID_DTYPE, "mla decode: out_dtype must be MR_BF16 or MR_F32");
+    if (a->num_splits < 0) return fail(MR_INVALID_ARGUMENT, "mla decode: num_splits must be >= 0");
+    if (int64_t(a->batch) * a->heads > INT32_MAX) return fail(MR_INVALID_SHAPE, "mla decode: batch * heads too large");
+    return MR_OK;
+}
+
 mr_status check_decode(const mr_mla_decode_args* a) {
     if (!a) return fail(MR_INVALID_ARGUMENT, "mr_mla_decode: args is NULL");
     if (a->batch <= 0 || a->heads <= 0)
         return fail(MR_INVALID_SHAPE, "mla decode: batch %d and heads %d must be positive", a->batch, a->heads);
-    if (a->kv_rank != 512)
-        return fail(MR_INVALID_SHAPE, "mla decode: kv_rank must be 512, got %d", a->kv_rank);
-    if (a->rope_dim != 64 && a->rope_dim != 0)
-        return fail(MR_INVALID_SHAPE, "mla decode: rope_dim must be 64 or 0, got %d", a->rope_dim);
+    if (a->kv_rank <= 0 || a->kv_rank > mr::ANY_MAX_RANK || a->rope_dim < 0 || a->rope_dim > mr::ANY_MAX_ROPE)
+        return fail(MR_INVALID_SHAPE, "mla decode: kv_rank %d must be in [1, %d] and rope_dim %d in [0, %d]", a->kv_rank,
+                    mr::ANY_MAX_RANK, a->rope_dim, mr::ANY_MAX_ROPE);
+    if (!decode_fast_dims(a)) return check_decode_any(a);
     if (!(std::isfinite(a->scale) && a->scale > 0))
         return fail(MR_INVALID_SHAPE, "sparse attention queries, shared KV, sinks, indices, or scale are invalid: "
                                       "scale %g must be finite and positive", double(a->scale));
@@ -205,6 +251,50 @@ mr_status check_decode(const mr_mla_decode_args* a) {
 }
 
 }  // namespace
+
+// The any-width decode: the device-status index check as a launch of its
+// own (long lists' tables where mr_validate_indices keeps them), then one
+// workgroup per (batch, head).
+static mr_status decode_any(const mr_mla_decode_args* a, bool device_check, void* stream) {
+    hipStream_t s = (hipStream_t)stream;
+    hipEvent_t const* ev = (hipEvent_t const*)a->phase_events;
+    hipError_t e = hipSuccess;
+    if (ev) e = hipEventRecord(ev[0], s);
+    if (e == hipSuccess && device_check && a->n_idx > 0) {
+        int32_t* tables = (int32_t*)((char*)a->workspace + align256(size_t(a->batch) * 3 * sizeof(int32_t)));
+        e = mr::launch_validate_indices(a->indices, a->batch, a->n_idx, a->n_ctx, tables, a->index_status, s);
+    }
+    mr::AnyDecodeParams q{};
+    q.q_lat = (const uint16_t*)a->q_lat;
+    q.q_lat_bs = a->q_lat_batch_stride;
+    q.q_lat_hs = a->q_lat_head_stride;
+    q.q_rope = (const uint16_t*)a->q_rope;
+    q.q_rope_bs = a->q_rope_batch_stride;
+    q.q_rope_hs = a->q_rope_head_stride;
+    q.latent = (const uint16_t*)a->latent;
+    q.lat_rs = a->latent_row_stride;
+    q.lat_bs = a->latent_batch_stride;
+    q.rope = (const uint16_t*)a->rope_keys;
+    q.rope_rs = a->rope_row_stride;
+    q.rope_bs = a->rope_batch_stride;
+    q.indices = a->indices;
+    q.n_idx = a->n_idx;
+    q.sinks = a->sinks;
+    q.out = a->out;
+    q.out_bs = a->out_batch_stride;
+    q.out_hs = a->out_head_stride;
+    q.out_f32 = a->out_dtype == MR_F32;
+    q.batch = a->batch;
+    q.heads = a->heads;
+    q.n_ctx = a->n_ctx;
+    q.R = a->kv_rank;
+    q.DR = a->rope_dim;
+    q.scale_log2 = float(double(a->scale) * 1.4426950408889634);
+    if (e == hipSuccess) e = mr::launch_mla_decode_any(q, s);
+    if (e == hipSuccess && ev) e = hipEventRecord(ev[1], s);
+    if (e == hipSuccess && ev) e = hipEventRecord(ev[2], s);
+    return e == hipSuccess ? MR_OK : hip_fail(e, "mla decode (any width) launch");
+}
 
 extern "C" {
 
@@ -259,7 +349,7 @@ mr_status mr_mla_decode(const mr_mla_decode_args* a, void* stream) {
     mr_status st = check_decode(a);
     if (st != MR_OK) return st;
     const DecodePlan pl = plan_decode(a);
-    if (!a->workspace || a->workspace_bytes < pl.total)
+    if (pl.total && (!a->workspace || a->workspace_bytes < pl.total))
         return fail(MR_WORKSPACE_TOO_SMALL, "mla decode: workspace %zu bytes < %zu required", a->workspace_bytes, pl.total);
     if (!aligned16(a->workspace)) return fail(MR_INVALID_ARGUMENT, "mla decode: workspace must be 16-byte aligned");
     // index checks: on the device in the split launch when the caller gives
@@ -273,6 +363,7 @@ mr_status mr_mla_decode(const mr_mla_decode_args* a, void* stream) {
     }
     if (checked && !sync_check && !aligned4(a->index_status))
         return fail(MR_INVALID_ARGUMENT, "mla decode: index_status must be 4-byte aligned");
+    if (!decode_fast_dims(a)) return decode_any(a, checked && !sync_check, stream);
     mr::DecodeParams p{};
     p.q_lat = (const uint16_t*)a->q_lat;
     p.q_lat_bs = a->q_lat_batch_stride;

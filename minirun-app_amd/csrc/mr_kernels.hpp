@@ -128,6 +128,51 @@ struct PrefillAttnParams {
 
 hipError_t launch_upproj(const UpProjParams& p, hipStream_t st);
 
+// ---------------------------------------------------------------- any-width MLA (generic.hip)
+// The decode and the prefill at widths the fixed-width kernels do not take,
+// in fp32; elements are read one by one (no alignment beyond 2 bytes).
+constexpr int ANY_MAX_RANK = 2048;  // kv_rank (decode), kv_rank and v_head (prefill)
+constexpr int ANY_MAX_ROPE = 512;   // rope width
+constexpr int ANY_MAX_NOPE = 1024;  // qk_nope width (prefill)
+
+struct AnyDecodeParams {
+    const uint16_t* q_lat;
+    int64_t q_lat_bs, q_lat_hs;
+    const uint16_t* q_rope;
+    int64_t q_rope_bs, q_rope_hs;
+    const uint16_t* latent;
+    int64_t lat_rs, lat_bs;
+    const uint16_t* rope;
+    int64_t rope_rs, rope_bs;
+    const int32_t* indices;  // null: rows 0 .. n_ctx-1
+    int32_t n_idx;
+    const float* sinks;      // [heads] or null
+    void* out;               // [batch][heads][R] with strides out_bs, out_hs
+    int64_t out_bs, out_hs;
+    int32_t out_f32;
+    int32_t batch, heads, n_ctx, R, DR;
+    float scale_log2;
+};
+hipError_t launch_mla_decode_any(const AnyDecodeParams& p, hipStream_t st);
+
+struct AnyPrefillParams {
+    const uint16_t* q;  // [T][H][NOPE + DR]
+    int64_t q_ts, q_hs;
+    const uint16_t* latent;  // [P][R]
+    int64_t lat_rs;
+    const uint16_t* rope;  // [P][DR]
+    int64_t rope_rs;
+    const uint16_t* kv_b;  // [H * (NOPE + V)][R]
+    int64_t kvb_rs;
+    float* kv;  // workspace [H][P][NOPE + V]
+    void* out;  // [T][H][V]
+    int64_t out_ts, out_hs;
+    int32_t out_f32;
+    int32_t T, P, H, R, DR, NOPE, V;
+    float scale_log2;
+};
+hipError_t launch_mla_prefill_any(const AnyPrefillParams& p, hipEvent_t const* events, hipStream_t st);
+
 // ---------------------------------------------------------------- token-tiled projections
 // y[M][N] = x[M][K] . W[N][K]^T on MFMA (gemm.hip): x bf16 rows of stride
 // ldx; W dense bf16 rows of stride ldw (packed null), or 4-bit affine rows

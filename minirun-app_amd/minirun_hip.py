@@ -253,8 +253,9 @@ def decode_args(q_lat, q_rope, latent, rope_keys, *, scale, indices=None, sinks=
                 out_dtype=None, num_splits=0, flags=0, workspace=None, index_status=None):
     """Fill a DecodeArgs from torch tensors.
 
-    q_lat [B,H,512] bf16; q_rope [B,H,64] bf16 or None; latent [B,N,*] or [N,*]
-    bf16 rows (first 512 columns used); rope_keys likewise (64 columns) or
+    q_lat [B,H,R] bf16 (R = kv_rank, 512 for the split kernel, else up to 2048
+    on the any-width kernel); q_rope [B,H,dr] bf16 or None; latent [B,N,*] or
+    [N,*] bf16 rows (first R columns used); rope_keys likewise (dr columns) or
     None; indices [B,K] int32 or None; sinks [H] f32 or None; index_status
     int32 [B,3] device tensor or None (the device-side index check).
     """
@@ -677,24 +678,28 @@ def mla_decode_block(x, weights, cache, position, rope_cos, rope_sin, stream=Non
 
 
 def prefill_args(q, latent, rope_keys, kv_b, *, scale=None, out=None, out_dtype=None, workspace=None):
-    """Fill PrefillArgs: q [T,H,192] bf16; latent [P,>=512] and rope_keys
-    [P,>=64] bf16 row views (both may be views of one [P,576] cache);
-    kv_b [H*256, 512] bf16 (kv_b_proj, output-major)."""
+    """Fill PrefillArgs: q [T,H,nope+rope] bf16; latent [P,>=kv_rank] and
+    rope_keys [P,>=rope] bf16 row views (both may be views of one cache);
+    kv_b [H*(nope+v), kv_rank] bf16 (kv_b_proj, output-major), which fixes
+    kv_rank and v_head.  The widths 128 / 64 / 128 / 512 run on MFMA, others
+    on the any-width kernels."""
     torch = _torch()
     for t, n in ((q, "q"), (latent, "latent"), (rope_keys, "rope_keys"), (kv_b, "kv_b")):
         _need(t, n, torch.bfloat16)
     T, H, D = q.shape
     P = latent.shape[0]
+    nope = D - rope_keys.shape[1]
     a = PrefillArgs()
     a.tokens, a.n_ctx, a.heads = T, P, H
-    a.qk_nope_dim, a.qk_rope_dim, a.v_head_dim, a.kv_rank = D - rope_keys.shape[1], rope_keys.shape[1], 128, 512
+    a.qk_nope_dim, a.qk_rope_dim = nope, rope_keys.shape[1]
+    a.v_head_dim, a.kv_rank = kv_b.shape[0] // H - nope, kv_b.shape[1]
     a.scale = scale if scale is not None else D ** -0.5
     a.q, a.q_token_stride, a.q_head_stride = q.data_ptr(), q.stride(0), q.stride(1)
     a.latent, a.latent_row_stride = latent.data_ptr(), latent.stride(0)
     a.rope_keys, a.rope_row_stride = rope_keys.data_ptr(), rope_keys.stride(0)
     a.kv_b, a.kv_b_row_stride = kv_b.data_ptr(), kv_b.stride(0)
     if out is None:
-        out = torch.empty(T, H, 128, dtype=out_dtype or torch.bfloat16, device=q.device)
+        out = torch.empty(T, H, a.v_head_dim, dtype=out_dtype or torch.bfloat16, device=q.device)
     a.out, a.out_dtype = out.data_ptr(), _dtype_code(out.dtype)
     a.out_token_stride, a.out_head_stride = out.stride(0), out.stride(1)
     need = load().mr_mla_prefill_workspace_size(C.byref(a))

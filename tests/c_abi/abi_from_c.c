@@ -54,10 +54,12 @@ int main(void) {
     a.batch = 1;
     a.heads = 16;
     a.n_ctx = 512;
-    a.kv_rank = 256;
+    a.kv_rank = 4096; /* beyond every kernel's widths */
     a.rope_dim = 64;
     a.scale = 0.07f;
     EXPECT(mr_mla_decode(&a, NULL) == MR_INVALID_SHAPE);
+    a.kv_rank = 256; /* the any-width kernel's: on to the pointer checks */
+    EXPECT(mr_mla_decode(&a, NULL) == MR_INVALID_ARGUMENT);
     EXPECT(mr_mla_decode(NULL, NULL) == MR_INVALID_ARGUMENT);
 
     if (failures) return 1;

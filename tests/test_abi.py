@@ -39,9 +39,13 @@ def test_version_and_error_string():
 def test_decode_rejects_bad_arguments_before_any_gpu_call():
     lib = M.load()
     a = M.DecodeArgs()
-    a.batch, a.heads, a.n_ctx, a.kv_rank, a.rope_dim, a.scale = 1, 16, 512, 256, 64, 0.07
-    assert lib.mr_mla_decode(C.byref(a), None) == M.INVALID_SHAPE
+    a.batch, a.heads, a.n_ctx, a.kv_rank, a.rope_dim, a.scale = 1, 16, 512, 4096, 64, 0.07
+    assert lib.mr_mla_decode(C.byref(a), None) == M.INVALID_SHAPE  # widths beyond the any-width kernel
     assert "kv_rank" in M.last_error()
+    a.kv_rank, a.rope_dim = 256, 600
+    assert lib.mr_mla_decode(C.byref(a), None) == M.INVALID_SHAPE and "rope_dim" in M.last_error()
+    a.rope_dim = 64
+    assert lib.mr_mla_decode(C.byref(a), None) == M.INVALID_ARGUMENT  # other widths: on to the pointer checks
     a.kv_rank = 512
     a.scale = -1.0
     assert lib.mr_mla_decode(C.byref(a), None) == M.INVALID_SHAPE
@@ -59,6 +63,37 @@ def test_workspace_size_is_deterministic_and_covers_partials():
     # per (split, head): O / l as 512 bf16 plus (m, l) as two fp32
     assert n >= 64 * 128 * (512 * 2 + 2 * 4)
     assert n == lib.mr_mla_decode_workspace_size(C.byref(a))
+
+
+def test_any_width_workspace_sizes():
+    # widths the split kernel does not take have no split partials: the
+    # workspace holds only the index checks' words (and long lists' tables)
+    lib = M.load()
+    a = M.DecodeArgs()
+    a.batch, a.heads, a.n_ctx, a.kv_rank, a.rope_dim, a.scale = 2, 4, 37, 16, 4, 12 ** -0.5
+    assert lib.mr_mla_decode_workspace_size(C.byref(a)) == 0
+    a.indices, a.n_idx = 1, 12  # any non-NULL pointer: sizing reads no memory
+    assert lib.mr_mla_decode_workspace_size(C.byref(a)) == lib.mr_validate_indices_workspace_size(2, 12)
+    a.flags = M.DECODE_UNCHECKED
+    assert lib.mr_mla_decode_workspace_size(C.byref(a)) == 0
+    p = M.PrefillArgs()
+    p.tokens, p.n_ctx, p.heads = 5, 9, 4
+    p.qk_nope_dim, p.qk_rope_dim, p.v_head_dim, p.kv_rank = 8, 4, 8, 16
+    assert lib.mr_mla_prefill_workspace_size(C.byref(p)) == -(-(9 * 4 * (8 + 8) * 4) // 256) * 256
+    p.qk_nope_dim, p.qk_rope_dim, p.v_head_dim, p.kv_rank = 128, 64, 128, 512
+    assert lib.mr_mla_prefill_workspace_size(C.byref(p)) == 9 * 4 * 256 * 2 // 256 * 256 + (256 if 9 * 4 * 512 % 256 else 0)
+
+
+def test_prefill_width_limits():
+    lib = M.load()
+    p = M.PrefillArgs()
+    p.tokens, p.n_ctx, p.heads, p.scale = 5, 9, 4, 0.2
+    p.qk_nope_dim, p.qk_rope_dim, p.v_head_dim, p.kv_rank = 8, 4, 8, 4096
+    assert lib.mr_mla_prefill(C.byref(p), None) == M.INVALID_SHAPE and "kv_rank" in M.last_error()
+    p.kv_rank, p.v_head_dim = 16, 0
+    assert lib.mr_mla_prefill(C.byref(p), None) == M.INVALID_SHAPE
+    p.v_head_dim = 8
+    assert lib.mr_mla_prefill(C.byref(p), None) == M.INVALID_ARGUMENT  # NULL pointers
 
 
 def test_validate_indices_rejects_oversize_without_gpu():
@@ -111,10 +146,10 @@ def test_prefill_rejects_bad_arguments_before_any_gpu_call():
     lib = M.load()
     a = M.PrefillArgs()
     a.tokens, a.n_ctx, a.heads = 4096, 4096, 128
-    a.qk_nope_dim, a.qk_rope_dim, a.v_head_dim, a.kv_rank = 128, 64, 128, 256
+    a.qk_nope_dim, a.qk_rope_dim, a.v_head_dim, a.kv_rank = 128, 64, 128, 4096
     a.scale = 192 ** -0.5
-    assert lib.mr_mla_prefill(C.byref(a), None) == M.INVALID_SHAPE
-    assert "kv_rank 512" in M.last_error()
+    assert lib.mr_mla_prefill(C.byref(a), None) == M.INVALID_SHAPE  # beyond the any-width kernels
+    assert "kv_rank" in M.last_error()
     a.kv_rank = 512
     a.n_ctx = 100
     assert lib.mr_mla_prefill(C.byref(a), None) == M.INVALID_SHAPE
