@@ -449,6 +449,51 @@ size_t mr_mla_prefill_workspace_size(const mr_mla_prefill_args *args);
 mr_status mr_mla_prefill(const mr_mla_prefill_args *args, void *stream);
 
 /* ------------------------------------------------------------------------
+ * A whole prompt through the MLA block in one call: K3MLA.forward
+ * (MLA.swift:124-229; state == nil is position 0, a cached prefix of
+ * `position` rows is the state's latents and shared keys):
+ *   h = RMSNorm(x) per token (skipped when input_norm_w is NULL)
+ *   q = q_b(RMSNorm(q_a(h)))            [T][heads][nope + rope]   (:131-139)
+ *   kv = kv_a(h) -> cache rows position .. position+T-1, latent RMSNormed,
+ *        shared key rotated at its position or carried (NoPE)   (:141-157)
+ *   attn = causal attention of the T queries over rows 0 .. position+T-1,
+ *          keys/values up-projected through kv_b (mr_mla_prefill)  (:159-206)
+ *   out = o_proj(attn * sigmoid(g_proj(h)))  (gate when g_proj is given,
+ *                                             :207-211)
+ * Projections run over all T tokens (MFMA tiles from 64 tokens).  kv_b is
+ * dense bf16 (K3's) or affine, dequantized to bf16 in the workspace.  Widths
+ * as mr_mla_prefill takes them; qk_rope_dim even.  rope_cos / rope_sin:
+ * device [T][qk_rope_dim/2], the angles at positions position .. position+T-1
+ * (the query's rope slice and the cached keys rotate), or both NULL (NoPE).
+ * All activations between stages are bf16; every stage is enqueued on
+ * `stream`, in order.  Checks that can fail run before any cache write.
+ * ------------------------------------------------------------------------ */
+typedef struct mr_mla_prefill_block_args {
+    int32_t tokens; /* T >= 1 prompt tokens */
+    int32_t hidden, q_lora_rank, heads, qk_nope_dim, qk_rope_dim, v_head_dim, kv_rank;
+    float eps, scale;
+    const void *x; /* bf16 [T][hidden] */
+    int64_t x_token_stride;
+    const void *input_norm_w, *q_a_norm_w, *kv_a_norm_w;
+    mr_dtype norm_w_dtype; /* bf16 or f32, all three */
+    mr_projection q_a, q_b, kv_a, kv_b, o_proj;
+    mr_projection g_proj; /* MR_PROJ_NONE: no output gate */
+    void *cache_latent; /* bf16 rows, kv_rank wide */
+    int64_t latent_row_stride;
+    void *cache_rope; /* bf16 rows, qk_rope_dim wide (unused when 0) */
+    int64_t rope_row_stride;
+    int32_t position, capacity; /* rows cached before the first token; rows available */
+    const float *rope_cos, *rope_sin; /* device [T][qk_rope_dim/2], or both NULL (NoPE) */
+    void *out; /* bf16 [T][hidden] */
+    int64_t out_token_stride;
+    void *workspace;
+    size_t workspace_bytes;
+} mr_mla_prefill_block_args;
+
+size_t mr_mla_prefill_block_workspace_size(const mr_mla_prefill_block_args *args);
+mr_status mr_mla_prefill_block(const mr_mla_prefill_block_args *args, void *stream);
+
+/* ------------------------------------------------------------------------
  * Index tables of DeepSeek V4 attention (DeepSeekV4Attention.swift:169-237),
  * host side, -1 = invalid entry.  `out` must hold rows*cols entries:
  * window: seq_len*min(seq_len, window) (or window when start_pos > 0);

@@ -982,6 +982,228 @@ mr_status mr_mla_decode_block(const mr_mla_block_args* a, void* stream) {
     return block_proj(attn, hv, &a->o_proj, a->out, nullptr, nd, a->eps, gated ? gate : nullptr, stage, stream);
 }
 
+// ---------------------------------------------------------------- prefill block
+namespace {
+
+// y[t] = W . x[t] for `tokens` bf16 rows into bf16 rows: MFMA tiles from
+// 64 tokens, the token-tiled GEMV below that
+mr_status proj_rows(const void* x, int32_t tokens, int64_t x_stride, const mr_projection* w, void* y, int64_t y_stride,
+                    void* stream) {
+    return w->kind == MR_PROJ_AFFINE
+               ? mr_affine_matmul(x, MR_BF16, tokens, x_stride, &w->affine, y, MR_BF16, y_stride, stream)
+               : mr_linear(x, MR_BF16, tokens, x_stride, &w->dense, y, MR_BF16, y_stride, stream);
+}
+
+// Workspace regions, 256-byte aligned, each [T][width] bf16 unless noted:
+// the normed input (with an input norm), q_lora and its norm, q, the kv_a
+// rows, the gate (gated), the attention output, the dequantized kv_b
+// (affine kv_b, [H*(nope+v)][kv_rank]) and mr_mla_prefill's own workspace.
+struct PrefillBlockLayout {
+    size_t h, q_lora, q_lora_n, q, kv, gate, attn, kv_b, pre, total;
+    mr_mla_prefill_args pre_args;
+};
+
+void prefill_block_layout(const mr_mla_prefill_block_args* a, PrefillBlockLayout* L) {
+    size_t off = 0;
+    auto take = [&](size_t bytes) {
+        const size_t at = off;
+        off += align256(bytes);
+        return at;
+    };
+    const size_t T = size_t(a->tokens);
+    const int dq = a->qk_nope_dim + a->qk_rope_dim;
+    const size_t hv = size_t(a->heads) * a->v_head_dim;
+    L->h = take(a->input_norm_w ? T * a->hidden * 2 : 0);
+    L->q_lora = take(T * a->q_lora_rank * 2);
+    L->q_lora_n = take(T * a->q_lora_rank * 2);
+    L->q = take(T * a->heads * dq * 2);
+    L->kv = take(T * (a->kv_rank + a->qk_rope_dim) * 2);
+    L->gate = take(a->g_proj.kind != MR_PROJ_NONE ? T * hv * 2 : 0);
+    L->attn = take(T * hv * 2);
+    L->kv_b = take(a->kv_b.kind == MR_PROJ_AFFINE ? size_t(a->heads) * (a->qk_nope_dim + a->v_head_dim) * a->kv_rank * 2
+                                                  : 0);
+    mr_mla_prefill_args& p = L->pre_args;
+    p = mr_mla_prefill_args{};
+    p.tokens = a->tokens;
+    p.n_ctx = int32_t(std::min<int64_t>(int64_t(a->position) + a->tokens, INT32_MAX));
+    p.heads = a->heads;
+    p.qk_nope_dim = a->qk_nope_dim;
+    p.qk_rope_dim = a->qk_rope_dim;
+    p.v_head_dim = a->v_head_dim;
+    p.kv_rank = a->kv_rank;
+    p.scale = a->scale;
+    p.q_token_stride = int64_t(a->heads) * dq;
+    p.q_head_stride = dq;
+    p.latent = a->cache_latent;
+    p.latent_row_stride = a->latent_row_stride;
+    p.rope_keys = a->cache_rope;
+    p.rope_row_stride = a->rope_row_stride;
+    if (a->kv_b.kind == MR_PROJ_DENSE) {
+        p.kv_b = a->kv_b.dense.weight;
+        p.kv_b_row_stride = a->kv_b.dense.row_stride;
+    } else {
+        p.kv_b_row_stride = a->kv_rank;
+    }
+    p.out_dtype = MR_BF16;
+    p.out_token_stride = int64_t(hv);
+    p.out_head_stride = a->v_head_dim;
+    L->pre = off;
+    take(mr_mla_prefill_workspace_size(&p));
+    L->total = off;
+}
+
+// Every check the stages would make, before the first launch: a call that
+// fails leaves the cache as it was.
+mr_status check_prefill_block(const mr_mla_prefill_block_args* a) {
+    if (!a) return fail(MR_INVALID_ARGUMENT, "mla prefill block: args is NULL");
+    if (a->tokens <= 0 || a->hidden <= 0 || a->q_lora_rank <= 0 || a->heads <= 0 || a->qk_nope_dim < 0 ||
+        a->qk_rope_dim < 0 || a->qk_rope_dim % 2 || a->v_head_dim <= 0 || a->kv_rank <= 0)
+        return fail(MR_INVALID_SHAPE, "mla prefill block: positive tokens and dims required, an even rope width");
+    if (a->position < 0 || int64_t(a->position) + a->tokens > a->capacity)
+        return fail(MR_INVALID_SHAPE, "mla prefill block: rows %d .. %lld outside the cache capacity %d", a->position,
+                    (long long)a->position + a->tokens - 1, a->capacity);
+    if (!a->x || !a->q_a_norm_w || !a->kv_a_norm_w || !a->cache_latent || (a->qk_rope_dim && !a->cache_rope) ||
+        !a->out || !a->workspace)
+        return fail(MR_INVALID_ARGUMENT, "mla prefill block: NULL pointer");
+    if (!a->rope_cos != !a->rope_sin)
+        return fail(MR_INVALID_ARGUMENT, "mla prefill block: give both rotary tables (rotated MLA) or neither (NoPE)");
+    if (a->x_token_stride < a->hidden || a->out_token_stride < a->hidden)
+        return fail(MR_INVALID_SHAPE, "mla prefill block: x / out token strides %lld / %lld are below hidden %d",
+                    (long long)a->x_token_stride, (long long)a->out_token_stride, a->hidden);
+    if (a->latent_row_stride < a->kv_rank || (a->qk_rope_dim && a->rope_row_stride < a->qk_rope_dim))
+        return fail(MR_INVALID_SHAPE, "mla prefill block: cache row strides %lld / %lld are below %d / %d",
+                    (long long)a->latent_row_stride, (long long)a->rope_row_stride, a->kv_rank, a->qk_rope_dim);
+    if (!act_dtype_ok(a->norm_w_dtype))
+        return fail(MR_INVALID_DTYPE, "mla prefill block: norm weights must be bf16 or f32");
+    if (!(a->eps >= 0) || !std::isfinite(a->eps))
+        return fail(MR_INVALID_ARGUMENT, "mla prefill block: eps must be finite, >= 0");
+    const int dq = a->qk_nope_dim + a->qk_rope_dim;
+    const int64_t hv = int64_t(a->heads) * a->v_head_dim;
+    const bool gated = a->g_proj.kind != MR_PROJ_NONE;
+    struct {
+        const mr_projection* w;
+        int64_t out, in;
+        const char* name;
+    } ws[] = {{&a->q_a, a->q_lora_rank, a->hidden, "q_a_proj"},
+              {&a->q_b, int64_t(a->heads) * dq, a->q_lora_rank, "q_b_proj"},
+              {&a->kv_a, a->kv_rank + a->qk_rope_dim, a->hidden, "kv_a_proj_with_mqa"},
+              {&a->kv_b, int64_t(a->heads) * (a->qk_nope_dim + a->v_head_dim), a->kv_rank, "kv_b_proj"},
+              {&a->o_proj, a->hidden, hv, "o_proj"},
+              {&a->g_proj, hv, a->hidden, "g_proj"}};
+    for (auto& e : ws) {
+        if (e.w == &a->g_proj && !gated) continue;
+        mr_status st = check_projection(e.w, e.name);
+        if (st != MR_OK) return st;
+        if (proj_out(e.w) != e.out || proj_in(e.w) != e.in)
+            return fail(MR_INVALID_SHAPE, "mla prefill block: %s is [%lld, %lld], expected [%lld, %lld]", e.name,
+                        (long long)proj_out(e.w), (long long)proj_in(e.w), (long long)e.out, (long long)e.in);
+    }
+    if (a->kv_b.kind == MR_PROJ_DENSE && a->kv_b.dense.dtype != MR_BF16)
+        return fail(MR_INVALID_DTYPE, "mla prefill block: a dense kv_b_proj must be bf16");
+    PrefillBlockLayout L;
+    prefill_block_layout(a, &L);
+    mr_mla_prefill_args p = L.pre_args;
+    char* W = (char*)a->workspace;
+    p.q = W + L.q;
+    p.out = W + L.attn;
+    if (a->kv_b.kind == MR_PROJ_AFFINE) p.kv_b = W + L.kv_b;
+    if (int64_t(a->position) + a->tokens > INT32_MAX)
+        return fail(MR_INVALID_SHAPE, "mla prefill block: position + tokens exceeds int32");
+    mr_status st = mrc::check_prefill(&p);
+    if (st != MR_OK) return st;
+    if (a->workspace_bytes < L.total)
+        return fail(MR_WORKSPACE_TOO_SMALL, "mla prefill block: workspace %zu bytes < %zu", a->workspace_bytes, L.total);
+    if (!aligned16(a->workspace))
+        return fail(MR_INVALID_ARGUMENT, "mla prefill block: workspace must be 16-byte aligned");
+    return MR_OK;
+}
+
+}  // namespace
+
+size_t mr_mla_prefill_block_workspace_size(const mr_mla_prefill_block_args* a) {
+    if (!a || a->tokens <= 0 || a->heads <= 0 || a->position < 0) return 0;
+    PrefillBlockLayout L;
+    prefill_block_layout(a, &L);
+    return L.total;
+}
+
+mr_status mr_mla_prefill_block(const mr_mla_prefill_block_args* a, void* stream) {
+    mr_status st = check_prefill_block(a);
+    if (st != MR_OK) return st;
+    PrefillBlockLayout L;
+    prefill_block_layout(a, &L);
+    char* W = (char*)a->workspace;
+    const int32_t T = a->tokens;
+    const int dq = a->qk_nope_dim + a->qk_rope_dim;
+    const int64_t hv = int64_t(a->heads) * a->v_head_dim;
+    const int kv_w = a->kv_rank + a->qk_rope_dim;
+    const mr_dtype nd = a->norm_w_dtype;
+    const bool gated = a->g_proj.kind != MR_PROJ_NONE;
+    void* q_lora = W + L.q_lora;
+    void* q_lora_n = W + L.q_lora_n;
+    void* q = W + L.q;
+    void* kv = W + L.kv;
+    void* gate = W + L.gate;
+    void* attn = W + L.attn;
+
+    // the block input, through the input norm when one is given
+    const void* h = a->x;
+    int64_t h_stride = a->x_token_stride;
+    if (a->input_norm_w) {
+        if ((st = mr_rmsnorm(a->x, MR_BF16, T, a->hidden, a->x_token_stride, a->input_norm_w, nd, a->eps, W + L.h,
+                             MR_BF16, a->hidden, stream)) != MR_OK)
+            return st;
+        h = W + L.h;
+        h_stride = a->hidden;
+    }
+    // the projections of h over all T tokens (MLA.swift:131,141,207)
+    if ((st = proj_rows(h, T, h_stride, &a->q_a, q_lora, a->q_lora_rank, stream)) != MR_OK) return st;
+    if ((st = proj_rows(h, T, h_stride, &a->kv_a, kv, kv_w, stream)) != MR_OK) return st;
+    if (gated && (st = proj_rows(h, T, h_stride, &a->g_proj, gate, hv, stream)) != MR_OK) return st;
+    // q = q_b(RMSNorm(q_lora)), its rope slice rotated at each token's position
+    if ((st = mr_rmsnorm(q_lora, MR_BF16, T, a->q_lora_rank, a->q_lora_rank, a->q_a_norm_w, nd, a->eps, q_lora_n,
+                         MR_BF16, a->q_lora_rank, stream)) != MR_OK)
+        return st;
+    if ((st = proj_rows(q_lora_n, T, a->q_lora_rank, &a->q_b, q, int64_t(a->heads) * dq, stream)) != MR_OK) return st;
+    if (a->rope_cos && a->qk_rope_dim &&
+        (st = mr_rope_apply(q, MR_BF16, T, a->heads, dq, a->qk_nope_dim, a->qk_rope_dim, a->rope_cos, a->rope_sin,
+                            stream)) != MR_OK)
+        return st;
+    // the T new cache rows: RMSNorm(latent) and the shared key (:142-157)
+    const mr::CacheAppendParams app{kv,
+                                    0,
+                                    kv_w,
+                                    a->kv_a_norm_w,
+                                    nd == MR_F32,
+                                    a->eps,
+                                    a->kv_rank,
+                                    a->qk_rope_dim,
+                                    a->rope_cos,
+                                    a->rope_sin,
+                                    (uint16_t*)a->cache_latent,
+                                    a->latent_row_stride,
+                                    (uint16_t*)a->cache_rope,
+                                    a->rope_row_stride,
+                                    a->position,
+                                    T};
+    hipError_t e = mr::launch_cache_append(app, (hipStream_t)stream);
+    if (e != hipSuccess) return hip_fail(e, "mla prefill block: cache append launch");
+    // causal attention over rows 0 .. position + T - 1 (:159-206)
+    mr_mla_prefill_args p = L.pre_args;
+    p.q = q;
+    p.out = attn;
+    if (a->kv_b.kind == MR_PROJ_AFFINE) {
+        if ((st = mr_affine_dequantize(&a->kv_b.affine, W + L.kv_b, MR_BF16, stream)) != MR_OK) return st;
+        p.kv_b = W + L.kv_b;
+    }
+    p.workspace = W + L.pre;
+    p.workspace_bytes = L.total - L.pre;
+    if ((st = mr_mla_prefill(&p, stream)) != MR_OK) return st;
+    // out = o_proj(attn * sigmoid(gate)) (:207-211)
+    if (gated && (st = gate_stage(attn, gate, int64_t(T) * hv, attn, stream)) != MR_OK) return st;
+    return proj_rows(attn, T, hv, &a->o_proj, a->out, a->out_token_stride, stream);
+}
+
 // ---------------------------------------------------------------- V4 index tables (host)
 mr_status mr_attention_indices_window(int32_t window, int32_t seq_len, int32_t start_pos, int32_t* out, int32_t* rows,
                                       int32_t* cols) {

@@ -57,7 +57,9 @@ mr_status check_prefill_any(const mr_mla_prefill_args* a) {
     return MR_OK;
 }
 
-mr_status check_prefill(const mr_mla_prefill_args* a) {
+}  // namespace
+
+mr_status mrc::check_prefill(const mr_mla_prefill_args* a) {
     if (!a) return fail(MR_INVALID_ARGUMENT, "mr_mla_prefill: args is NULL");
     if (!prefill_fast_dims(a)) return check_prefill_any(a);
     if (a->tokens <= 0 || a->heads <= 0)
@@ -92,8 +94,6 @@ mr_status check_prefill(const mr_mla_prefill_args* a) {
     return MR_OK;
 }
 
-}  // namespace
-
 extern "C" {
 
 size_t mr_mla_prefill_workspace_size(const mr_mla_prefill_args* a) {
@@ -102,7 +102,7 @@ size_t mr_mla_prefill_workspace_size(const mr_mla_prefill_args* a) {
 }
 
 mr_status mr_mla_prefill(const mr_mla_prefill_args* a, void* stream) {
-    mr_status st = check_prefill(a);
+    mr_status st = mrc::check_prefill(a);
     if (st != MR_OK) return st;
     const size_t need = kv_bytes(a);
     if (!a->workspace || a->workspace_bytes < need)

@@ -27,4 +27,7 @@ struct DecodePartials {
 };
 DecodePartials decode_partials(const mr_mla_decode_args* a);
 
+// Every check mr_mla_prefill makes before its launches, workspace aside.
+mr_status check_prefill(const mr_mla_prefill_args* a);
+
 }  // namespace mrc

@@ -110,6 +110,26 @@ class PrefillArgs(C.Structure):
     ]
 
 
+class PrefillBlockArgs(C.Structure):
+    _fields_ = [
+        ("tokens", C.c_int32),
+        ("hidden", C.c_int32), ("q_lora_rank", C.c_int32), ("heads", C.c_int32), ("qk_nope_dim", C.c_int32),
+        ("qk_rope_dim", C.c_int32), ("v_head_dim", C.c_int32), ("kv_rank", C.c_int32),
+        ("eps", C.c_float), ("scale", C.c_float),
+        ("x", C.c_void_p), ("x_token_stride", C.c_int64),
+        ("input_norm_w", C.c_void_p), ("q_a_norm_w", C.c_void_p), ("kv_a_norm_w", C.c_void_p),
+        ("norm_w_dtype", C.c_int),
+        ("q_a", ProjectionDesc), ("q_b", ProjectionDesc), ("kv_a", ProjectionDesc), ("kv_b", ProjectionDesc),
+        ("o_proj", ProjectionDesc), ("g_proj", ProjectionDesc),
+        ("cache_latent", C.c_void_p), ("latent_row_stride", C.c_int64),
+        ("cache_rope", C.c_void_p), ("rope_row_stride", C.c_int64),
+        ("position", C.c_int32), ("capacity", C.c_int32),
+        ("rope_cos", C.c_void_p), ("rope_sin", C.c_void_p),
+        ("out", C.c_void_p), ("out_token_stride", C.c_int64),
+        ("workspace", C.c_void_p), ("workspace_bytes", C.c_size_t),
+    ]
+
+
 class TopkArgs(C.Structure):
     _fields_ = [
         ("scores", C.c_void_p), ("score_row_stride", C.c_int64), ("rows", C.c_int32), ("cols", C.c_int32),
@@ -169,6 +189,8 @@ SIGNATURES = {
     "mr_mla_decode_block": (C.c_int, [C.POINTER(BlockArgs), _P]),
     "mr_mla_prefill_workspace_size": (C.c_size_t, [C.POINTER(PrefillArgs)]),
     "mr_mla_prefill": (C.c_int, [C.POINTER(PrefillArgs), _P]),
+    "mr_mla_prefill_block_workspace_size": (C.c_size_t, [C.POINTER(PrefillBlockArgs)]),
+    "mr_mla_prefill_block": (C.c_int, [C.POINTER(PrefillBlockArgs), _P]),
     "mr_topk_geometry": (C.c_int, [C.c_int32, C.c_int32, C.c_int32, C.c_int32, C.c_int32, C.c_int32, _I32P]),
     "mr_topk_workspace_size": (C.c_size_t, [C.c_int32, C.c_int32, C.c_int32]),
     "mr_topk_select": (C.c_int, [C.POINTER(TopkArgs), _P]),
@@ -717,6 +739,50 @@ def mla_prefill(q, latent, rope_keys, kv_b, *, scale=None, out=None, out_dtype=N
     a, out, _ = prefill_args(q, latent, rope_keys, kv_b, scale=scale, out=out, out_dtype=out_dtype,
                              workspace=workspace)
     _check(load().mr_mla_prefill(C.byref(a), _stream(stream)))
+    return out
+
+
+def prefill_block_args(x, weights, cache, position, rope_cos, rope_sin, out, *, q_lora_rank=1536, heads=128,
+                       nope=128, rope=64, v=128, kv_rank=512, eps=1e-6, scale=None, workspace=None):
+    """Fill PrefillBlockArgs for the T prompt rows of x [T, hidden] (bf16);
+    `weights` as for block_args; cache [capacity, kv_rank + rope] bf16, rows
+    0 .. position-1 already written; rope_cos / rope_sin [T, rope/2] f32
+    tensors (the angles at position .. position+T-1) or None (NoPE)."""
+    torch = _torch()
+    a = PrefillBlockArgs()
+    a.tokens = x.shape[0]
+    a.hidden, a.q_lora_rank, a.heads, a.qk_nope_dim, a.qk_rope_dim, a.v_head_dim, a.kv_rank = \
+        x.shape[1], q_lora_rank, heads, nope, rope, v, kv_rank
+    a.eps = eps
+    a.scale = scale if scale is not None else (nope + rope) ** -0.5
+    a.x, a.x_token_stride = x.data_ptr(), x.stride(0)
+    a.input_norm_w = weights["input_norm"].data_ptr() if weights.get("input_norm") is not None else None
+    a.q_a_norm_w = weights["q_a_norm"].data_ptr()
+    a.kv_a_norm_w = weights["kv_a_norm"].data_ptr()
+    a.norm_w_dtype = _dtype_code(weights["q_a_norm"].dtype)
+    for n in ("q_a", "q_b", "kv_a", "kv_b", "o_proj", "g_proj"):
+        setattr(a, n, projection(weights.get(n)))
+    a.cache_latent, a.latent_row_stride = cache.data_ptr(), cache.stride(0)
+    a.cache_rope, a.rope_row_stride = (cache[:, kv_rank:].data_ptr() if rope else None), cache.stride(0)
+    a.position, a.capacity = position, cache.shape[0]
+    a.rope_cos = rope_cos.data_ptr() if rope_cos is not None else None
+    a.rope_sin = rope_sin.data_ptr() if rope_sin is not None else None
+    a.out, a.out_token_stride = out.data_ptr(), out.stride(0)
+    need = load().mr_mla_prefill_block_workspace_size(C.byref(a))
+    if workspace is None:
+        workspace = torch.empty(need, dtype=torch.uint8, device=x.device)
+    a.workspace, a.workspace_bytes = workspace.data_ptr(), workspace.numel()
+    return a, workspace
+
+
+def mla_prefill_block(x, weights, cache, position, rope_cos, rope_sin, stream=None, **kw):
+    """K3MLA.forward over a prompt (MLA.swift:124-229): the T rows of x
+    through the block, appending cache rows position .. position+T-1;
+    returns out [T, hidden] bf16."""
+    torch = _torch()
+    out = torch.empty(x.shape[0], x.shape[1], dtype=torch.bfloat16, device=x.device)
+    a, ws = prefill_block_args(x, weights, cache, position, rope_cos, rope_sin, out, **kw)
+    _check(load().mr_mla_prefill_block(C.byref(a), _stream(stream)))
     return out
 
 

@@ -1,5 +1,6 @@
 // K3MLA (ModelAdapters/Operators/MLA.swift): the latent cache, the absorbed
-// decode attention, the whole decode block and the eager prefill.
+// decode attention, the whole decode block, the eager prefill and the whole
+// prefill block.
 import CMinirunHIP
 
 /// The latent cache of K3MLA.State (MLA.swift:28-36): normalized latents
@@ -140,4 +141,55 @@ public func hipMLAPrefill(q: HIPTensor, cache: HIPLatentCache, kvB: HIPTensor, s
         throw HIPError(status: MR_WORKSPACE_TOO_SMALL, description: "prefill workspace too small")
     }
     try HIPError.check(mr_mla_prefill(&a, stream))
+}
+
+/// K3MLA.forward over a whole prompt in one call (MLA.swift:124-229): the T
+/// rows of x [T, hidden] through the projections, the cache append at rows
+/// cache.count ..< cache.count + T (state == nil is an empty cache), the
+/// eager causal attention, the gate and o_proj; out [T, hidden] bf16.
+/// cos/sin: device [T, 32] tables at those positions, nil = NoPE (K3).
+/// `workspace` comes from hipMLAPrefillBlockWorkspaceSize.
+public func hipMLAPrefillBlock(_ x: HIPTensor, weights w: HIPMLABlockWeights, qLoraRank: Int, heads: Int, eps: Float,
+                               cache: inout HIPLatentCache, capacity: Int, cos: UnsafePointer<Float>?,
+                               sin: UnsafePointer<Float>?, into out: HIPTensor, workspace: HIPTensor,
+                               stream: HIPStream = nil) throws {
+    var a = prefillBlockArgs(x, weights: w, qLoraRank: qLoraRank, heads: heads, eps: eps, cache: cache,
+                             capacity: capacity, cos: cos, sin: sin, out: out)
+    a.workspace = workspace.pointer; a.workspace_bytes = workspace.shape[0]
+    guard a.workspace_bytes >= mr_mla_prefill_block_workspace_size(&a) else {
+        throw HIPError(status: MR_WORKSPACE_TOO_SMALL, description: "prefill block workspace too small")
+    }
+    try HIPError.check(mr_mla_prefill_block(&a, stream))
+    cache.count += x.shape[0]
+}
+
+/// Bytes of device scratch hipMLAPrefillBlock needs for this prompt.
+public func hipMLAPrefillBlockWorkspaceSize(_ x: HIPTensor, weights w: HIPMLABlockWeights, qLoraRank: Int, heads: Int,
+                                            cache: HIPLatentCache, out: HIPTensor) -> Int {
+    var a = prefillBlockArgs(x, weights: w, qLoraRank: qLoraRank, heads: heads, eps: 0, cache: cache,
+                             capacity: cache.count + x.shape[0], cos: nil, sin: nil, out: out)
+    return mr_mla_prefill_block_workspace_size(&a)
+}
+
+func prefillBlockArgs(_ x: HIPTensor, weights w: HIPMLABlockWeights, qLoraRank: Int, heads: Int, eps: Float,
+                      cache: HIPLatentCache, capacity: Int, cos: UnsafePointer<Float>?, sin: UnsafePointer<Float>?,
+                      out: HIPTensor) -> mr_mla_prefill_block_args {
+    var a = mr_mla_prefill_block_args()
+    a.tokens = Int32(x.shape[0]); a.hidden = Int32(x.shape[1])
+    a.q_lora_rank = Int32(qLoraRank); a.heads = Int32(heads)
+    a.qk_nope_dim = 128; a.qk_rope_dim = 64; a.v_head_dim = 128; a.kv_rank = 512
+    a.eps = eps; a.scale = Float(1.0 / (192.0).squareRoot())  // over the full query (MLA.swift:170)
+    a.x = x.raw; a.x_token_stride = Int64(x.strides[0])
+    a.input_norm_w = w.inputNorm.map { $0.raw }
+    a.q_a_norm_w = w.qALayerNorm.raw; a.kv_a_norm_w = w.kvALayerNorm.raw
+    a.norm_w_dtype = w.qALayerNorm.dtype
+    a.q_a = w.qAProj.desc; a.q_b = w.qBProj.desc; a.kv_a = w.kvAProjWithMQA.desc
+    a.kv_b = w.kvBProj.desc; a.o_proj = w.oProj.desc
+    a.g_proj = w.gProj?.desc ?? HIPProjection.absent()
+    a.cache_latent = cache.latents.pointer; a.latent_row_stride = Int64(cache.latents.strides[0])
+    a.cache_rope = cache.sharedKeys.pointer; a.rope_row_stride = Int64(cache.sharedKeys.strides[0])
+    a.position = Int32(cache.count); a.capacity = Int32(capacity)
+    a.rope_cos = cos; a.rope_sin = sin
+    a.out = out.pointer; a.out_token_stride = Int64(out.strides[0])
+    return a
 }

@@ -223,3 +223,91 @@ def block_reference(d, hidden=7168, q_lora_rank=1536, heads=128, nope=128, rope=
         attn = _bf(O.sigmoid_gate(attn, g))
     out = _bf(_proj(attn, d["o_proj"]))
     return out, row
+
+
+# ---------------------------------------------------------------- the prefill block
+SYNTH_K3_DIMS = dict(hidden=128, q_lora_rank=32, heads=4, nope=8, rope=4, v=8, kv_rank=16)
+
+
+def prefill_block_inputs(T, position, tag, hidden, q_lora_rank, heads, nope, rope, v, kv_rank, affine=False,
+                         input_norm=False, gated=True, rotary=False, centred=True):
+    """T prompt tokens after `position` cached rows.  Dense weights ~N(0, 1/in)
+    (K3's attention weights are dense bf16) or 4-bit affine ones; the cache
+    holds rows 0..position-1 (~N(0,0.5), roped at their positions when
+    rotary) and zeros after them."""
+    norm = lambda name, n: O.f32_to_bf16(1 + 0.02 * O.bf16_to_f32(O.normal_bf16(f"{tag}.{name}", (n,))))
+    if affine:
+        mk = lambda name, out, inp: affine_weight(f"{tag}.{name}", out, inp, centred=centred)
+    else:
+        mk = lambda name, out, inp: O.normal_bf16(f"{tag}.{name}", (out, inp), std=inp ** -0.5, threads=16)
+    d = {
+        "x": O.normal_bf16(f"{tag}.x", (T, hidden)),
+        "input_norm": norm("input_norm", hidden) if input_norm else None,
+        "q_a_norm": norm("q_a_norm", q_lora_rank),
+        "kv_a_norm": norm("kv_a_norm", kv_rank),
+        "q_a": mk("q_a", q_lora_rank, hidden),
+        "q_b": mk("q_b", heads * (nope + rope), q_lora_rank),
+        "kv_a": mk("kv_a", kv_rank + rope, hidden),
+        "kv_b": mk("kv_b", heads * (nope + v), kv_rank),
+        "o_proj": mk("o_proj", hidden, heads * v),
+    }
+    if gated:
+        d["g_proj"] = mk("g_proj", heads * v, hidden)
+    cache = np.zeros((position + T, kv_rank + rope), np.uint16)
+    if position:
+        rows = O.normal_bf16(f"{tag}.cache", (position, kv_rank + rope), std=0.5)
+        if rotary and rope:
+            rows = rope_rows(rows.reshape(position, 1, -1), np.arange(position), col0=kv_rank,
+                             dim=rope).reshape(position, -1)
+        cache[:position] = rows
+    d["cache"] = cache
+    d["position"] = position
+    return d
+
+
+def _proj_rows(x, w, acc=1):
+    if isinstance(w, tuple):
+        return O.affine_matmul(np.asarray(x, np.float32), *w, acc=acc, threads=16)
+    return O.linear(np.asarray(x, np.float32), w, acc=acc, threads=16)
+
+
+def prefill_block_reference(d, hidden, q_lora_rank, heads, nope, rope, v, kv_rank, eps=1e-6, rotary=False, acc=1):
+    """K3MLA.forward over the prompt (MLA.swift:124-229) on the oracle,
+    rounding to bf16 where the reference's bf16 arrays round (every
+    projection output, the normed activations, the cache rows, the
+    up-projected keys and values of expand, the attention output and the
+    gated product).  Returns (out [T, hidden] f32 of bf16 values, the T new
+    cache rows).  acc=0 accumulates the projections in fp32."""
+    f = O.bf16_to_f32
+    pos = d["position"]
+    x = f(d["x"])
+    T = x.shape[0]
+    h = x if d.get("input_norm") is None else _bf(O.rmsnorm(x, f(d["input_norm"]), eps))
+    q_lora = _bf(_proj_rows(h, d["q_a"], acc))
+    q_lora_n = _bf(O.rmsnorm(q_lora, f(d["q_a_norm"]), eps))
+    q = O.f32_to_bf16(_proj_rows(q_lora_n, d["q_b"], acc)).reshape(T, heads, nope + rope)
+    kv = O.f32_to_bf16(_proj_rows(h, d["kv_a"], acc))
+    rows = np.empty((T, kv_rank + rope), np.uint16)
+    rows[:, :kv_rank] = O.f32_to_bf16(O.rmsnorm(f(kv[:, :kv_rank]), f(d["kv_a_norm"]), eps))
+    rows[:, kv_rank:] = kv[:, kv_rank:]
+    if rotary and rope:
+        cos, sin = O.rope_table(np.arange(pos, pos + T), O.rope_frequencies(rope))
+        q = O.rope_apply_bf16(q, cos, sin, nope, rope)
+        rows[:, kv_rank:] = O.rope_apply_bf16(kv[:, kv_rank:].reshape(T, 1, rope), cos, sin, 0, rope).reshape(T, rope)
+    cache = d["cache"][: pos + T].copy()
+    cache[pos:] = rows
+    kvb = d["kv_b"]
+    if isinstance(kvb, tuple):  # the block reads an affine kv_b dequantized to bf16
+        kvb = O.f32_to_bf16(O.affine_dequantize(*kvb))
+    kvb = kvb.reshape(heads, nope + v, kv_rank)
+    w_uk = np.ascontiguousarray(kvb[:, :nope, :].transpose(2, 0, 1).reshape(kv_rank, heads * nope))
+    w_uv = np.ascontiguousarray(kvb[:, nope:, :].transpose(2, 0, 1).reshape(kv_rank, heads * v))
+    sel_t = np.repeat(np.arange(T, dtype=np.int32), heads)
+    sel_h = np.tile(np.arange(heads, dtype=np.int32), T)
+    attn = O.mla_prefill_rows(q, cache, w_uk, w_uv, sel_t, sel_h, kv_rank=kv_rank, rope_dim=rope, nope_dim=nope,
+                              v_dim=v, scale=(nope + rope) ** -0.5, round_kv=True, threads=16)
+    attn = _bf(attn).reshape(T, heads * v)
+    if d.get("g_proj") is not None:
+        g = _bf(_proj_rows(h, d["g_proj"], acc))
+        attn = _bf(O.sigmoid_gate(attn, g))
+    return _bf(_proj_rows(attn, d["o_proj"], acc)), rows

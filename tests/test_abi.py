@@ -160,6 +160,82 @@ def test_prefill_rejects_bad_arguments_before_any_gpu_call():
     assert lib.mr_mla_prefill_workspace_size(C.byref(a)) == 4096 * 128 * 512
 
 
+def _dense_desc(addr, out_f, in_f, dtype=M.BF16):
+    p = M.ProjectionDesc()
+    p.kind = M.PROJ_DENSE
+    p.dense.weight, p.dense.dtype, p.dense.out_features, p.dense.in_features, p.dense.row_stride = \
+        addr, dtype, out_f, in_f, in_f
+    return p
+
+
+def _k3_prefill_block_args(T=64, position=0):
+    """K3 widths with placeholder device addresses: the checks read no memory."""
+    a = M.PrefillBlockArgs()
+    a.tokens, a.hidden, a.q_lora_rank, a.heads = T, 7168, 1536, 96
+    a.qk_nope_dim, a.qk_rope_dim, a.v_head_dim, a.kv_rank = 128, 64, 128, 512
+    a.eps, a.scale = 1e-6, 192 ** -0.5
+    base = 1 << 32
+    a.x, a.x_token_stride = base, 7168
+    a.q_a_norm_w, a.kv_a_norm_w, a.norm_w_dtype = base + 0x100000, base + 0x200000, M.BF16
+    a.q_a = _dense_desc(base + 0x1000000, 1536, 7168)
+    a.q_b = _dense_desc(base + 0x2000000, 96 * 192, 1536)
+    a.kv_a = _dense_desc(base + 0x3000000, 576, 7168)
+    a.kv_b = _dense_desc(base + 0x4000000, 96 * 256, 512)
+    a.o_proj = _dense_desc(base + 0x5000000, 7168, 96 * 128)
+    a.g_proj = _dense_desc(base + 0x6000000, 96 * 128, 7168)
+    a.cache_latent, a.latent_row_stride = base + 0x10000000, 576
+    a.cache_rope, a.rope_row_stride = base + 0x10000000 + 1024, 576
+    a.position, a.capacity = position, position + T
+    a.out, a.out_token_stride = base + 0x20000000, 7168
+    a.workspace = base + 0x40000000
+    a.workspace_bytes = M.load().mr_mla_prefill_block_workspace_size(C.byref(a))
+    return a
+
+
+def test_prefill_block_workspace_layout():
+    lib = M.load()
+    a = _k3_prefill_block_args(T=64, position=30)
+    al = lambda n: -(-n // 256) * 256
+    T, P = 64, 94
+    want = (al(T * 1536 * 2) * 2 + al(T * 96 * 192 * 2) + al(T * 576 * 2) + al(T * 96 * 128 * 2) * 2
+            + al(P * 96 * 256 * 2))
+    assert a.workspace_bytes == want
+    a.input_norm_w = 1 << 40  # an input norm stages the normed rows
+    assert lib.mr_mla_prefill_block_workspace_size(C.byref(a)) == want + al(T * 7168 * 2)
+    assert lib.mr_mla_prefill_block_workspace_size(None) == 0
+
+
+def test_prefill_block_rejects_bad_arguments_before_any_gpu_call():
+    lib = M.load()
+    call = lambda a: lib.mr_mla_prefill_block(C.byref(a), None)
+    assert lib.mr_mla_prefill_block(None, None) == M.INVALID_ARGUMENT
+    a = _k3_prefill_block_args()
+    a.capacity = 63
+    assert call(a) == M.INVALID_SHAPE and "capacity" in M.last_error()
+    a = _k3_prefill_block_args()
+    a.qk_rope_dim = 63
+    assert call(a) == M.INVALID_SHAPE and "even" in M.last_error()
+    a = _k3_prefill_block_args()
+    a.q_b = _dense_desc(1 << 33, 96 * 192 + 8, 1536)
+    assert call(a) == M.INVALID_SHAPE and "q_b_proj" in M.last_error()
+    a = _k3_prefill_block_args()
+    a.kv_b = _dense_desc(1 << 33, 96 * 256, 512, M.F32)
+    assert call(a) == M.INVALID_DTYPE and "kv_b_proj" in M.last_error()
+    a = _k3_prefill_block_args()
+    a.workspace_bytes -= 256
+    assert call(a) == M.WORKSPACE_TOO_SMALL
+    a = _k3_prefill_block_args()
+    a.rope_cos = 1 << 34  # one rotary table without the other
+    assert call(a) == M.INVALID_ARGUMENT
+    a = _k3_prefill_block_args()
+    a.latent_row_stride = 580  # the attention's fixed-width kernels step 16-byte rows
+    assert call(a) == M.INVALID_ARGUMENT and "multiples of 8" in M.last_error()
+    a = _k3_prefill_block_args()
+    a.kv_rank, a.kv_a, a.kv_b = 4096, _dense_desc(1 << 33, 4160, 7168), _dense_desc(1 << 34, 96 * 256, 4096)
+    a.latent_row_stride = a.rope_row_stride = 4160
+    assert call(a) == M.INVALID_SHAPE and "kv_rank" in M.last_error()
+
+
 def test_header_compiles_as_c_and_host_entry_points_work_from_c(tmp_path):
     """include/minirun_hip.h as a C11 translation unit (what a Swift module
     map imports): a C program links the library and checks the host-side

@@ -46,3 +46,39 @@ def test_workload_weights_hide_common_mode():
     lit, _ = MI.block_reference(MI.block_inputs(ctx=8, tag="cm"))
     cen, _ = MI.block_reference(MI.block_inputs(ctx=8, tag="cm", centred=True))
     assert np.abs(lit).mean() > 100 * np.abs(cen).mean()
+
+
+# ---------------------------------------------------------------- the prefill block's composition
+PB_DIMS = dict(hidden=256, q_lora_rank=64, heads=4, nope=32, rope=16, v=32, kv_rank=64)
+
+
+@pytest.mark.parametrize("affine,rotary,position", [(False, False, 0), (False, False, 9), (True, True, 13)])
+def test_prefill_block_one_token_equals_decode_block(affine, rotary, position):
+    # one prompt token through the eager (expanded) composition equals the
+    # absorbed decode block's composition at the same position
+    # (MLA.swift:174-197 against :198-206): keys and values up-projected
+    # per head against W_UK absorbed into the query and W_UV applied after
+    d = MI.prefill_block_inputs(1, position, f"pb1.{affine}.{position}", affine=affine, input_norm=affine,
+                                rotary=rotary, **PB_DIMS)
+    got, rows = MI.prefill_block_reference(d, rotary=rotary, **PB_DIMS)
+    dd = dict(d, x=d["x"][0])
+    ref, row = MI.block_reference(dd, rotary=rotary, **PB_DIMS)
+    assert np.abs(rows[0].astype(np.int32) - row.astype(np.int32)).max() <= 1
+    ok, maxerr, scale_err = MI.within_block_tolerance(got[0], ref)
+    assert ok, (maxerr, scale_err)
+
+
+def test_prefill_block_reference_is_causal():
+    # token t's output and cache row depend on tokens 0..t only: the first 9
+    # tokens alone give the first 9 rows of the 23-token prompt, bit for bit
+    d = MI.prefill_block_inputs(23, 0, "pbcz", rotary=True, **PB_DIMS)
+    full, rows = MI.prefill_block_reference(d, rotary=True, **PB_DIMS)
+    d9 = dict(d, x=d["x"][:9])
+    part, rows9 = MI.prefill_block_reference(d9, rotary=True, **PB_DIMS)
+    np.testing.assert_array_equal(part, full[:9])
+    np.testing.assert_array_equal(rows9, rows[:9])
+    # and a later token does see the earlier ones
+    d_alt = dict(d, x=d["x"].copy())
+    d_alt["x"][3] = d["x"][4]
+    alt, _ = MI.prefill_block_reference(d_alt, rotary=True, **PB_DIMS)
+    assert np.array_equal(alt[:3], full[:3]) and not np.array_equal(alt[5:], full[5:])
