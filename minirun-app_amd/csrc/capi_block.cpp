@@ -994,6 +994,48 @@ mr_status proj_rows(const void* x, int32_t tokens, int64_t x_stride, const mr_pr
                : mr_linear(x, MR_BF16, tokens, x_stride, &w->dense, y, MR_BF16, y_stride, stream);
 }
 
+// Projections of the same bf16 rows into bf16 rows (n of them, up to 3):
+// one stacked MFMA launch when every weight takes the MFMA path and all are
+// dense bf16 or all affine, else one call each.
+mr_status proj_rows_stacked(const void* x, int32_t tokens, int64_t x_stride, const mr_projection* const* w,
+                            void* const* y, const int64_t* y_stride, int n, void* stream) {
+    mr::ProjGemmParams q[3];
+    bool stack = n > 1 && tokens >= mr::PROJ_GEMM_MIN_TOKENS;
+    for (int i = 0; stack && i < n; ++i) {
+        q[i] = mr::ProjGemmParams{};
+        q[i].x = (const uint16_t*)x;
+        q[i].ldx = x_stride;
+        q[i].y = y[i];
+        q[i].ldy = y_stride[i];
+        q[i].M = tokens;
+        q[i].N = (int)proj_out(w[i]);
+        q[i].K = (int)proj_in(w[i]);
+        if (w[i]->kind == MR_PROJ_AFFINE) {
+            const mr_affine_weight* a = &w[i]->affine;
+            q[i].packed = a->packed;
+            q[i].scales = a->scales;
+            q[i].biases = a->biases;
+            q[i].scale_dtype = scale_code(a->scale_dtype);
+            q[i].group = a->group;
+            q[i].bits = a->bits;
+        } else {
+            if (w[i]->dense.dtype != MR_BF16) stack = false;
+            q[i].w = (const uint16_t*)w[i]->dense.weight;
+            q[i].ldw = w[i]->dense.row_stride;
+        }
+        stack = stack && w[i]->kind == w[0]->kind && mr::proj_gemm_ok(q[i]);
+    }
+    if (stack) {
+        const hipError_t e = mr::launch_proj_gemm_stack(q, n, mrc::cu_count(), (hipStream_t)stream);
+        return e == hipSuccess ? MR_OK : hip_fail(e, "stacked projection launch");
+    }
+    for (int i = 0; i < n; ++i) {
+        mr_status st = proj_rows(x, tokens, x_stride, w[i], y[i], y_stride[i], stream);
+        if (st != MR_OK) return st;
+    }
+    return MR_OK;
+}
+
 // Workspace regions, 256-byte aligned, each [T][width] bf16 unless noted:
 // the normed input (with an input norm), q_lora and its norm, q, the kv_a
 // rows, the gate (gated), the attention output, the dequantized kv_b
@@ -1156,10 +1198,14 @@ mr_status mr_mla_prefill_block(const mr_mla_prefill_block_args* a, void* stream)
         h = W + L.h;
         h_stride = a->hidden;
     }
-    // the projections of h over all T tokens (MLA.swift:131,141,207)
-    if ((st = proj_rows(h, T, h_stride, &a->q_a, q_lora, a->q_lora_rank, stream)) != MR_OK) return st;
-    if ((st = proj_rows(h, T, h_stride, &a->kv_a, kv, kv_w, stream)) != MR_OK) return st;
-    if (gated && (st = proj_rows(h, T, h_stride, &a->g_proj, gate, hv, stream)) != MR_OK) return st;
+    // the projections of h over all T tokens (MLA.swift:131,141,207), one
+    // stacked launch where they allow it
+    {
+        const mr_projection* xw[3] = {&a->q_a, &a->kv_a, &a->g_proj};
+        void* xy[3] = {q_lora, kv, gate};
+        const int64_t ys[3] = {a->q_lora_rank, kv_w, hv};
+        if ((st = proj_rows_stacked(h, T, h_stride, xw, xy, ys, gated ? 3 : 2, stream)) != MR_OK) return st;
+    }
     // q = q_b(RMSNorm(q_lora)), its rope slice rotated at each token's position
     if ((st = mr_rmsnorm(q_lora, MR_BF16, T, a->q_lora_rank, a->q_lora_rank, a->q_a_norm_w, nd, a->eps, q_lora_n,
                          MR_BF16, a->q_lora_rank, stream)) != MR_OK)
@@ -1198,9 +1244,8 @@ mr_status mr_mla_prefill_block(const mr_mla_prefill_block_args* a, void* stream)
     }
     p.workspace = W + L.pre;
     p.workspace_bytes = L.total - L.pre;
-    if ((st = mr_mla_prefill(&p, stream)) != MR_OK) return st;
-    // out = o_proj(attn * sigmoid(gate)) (:207-211)
-    if (gated && (st = gate_stage(attn, gate, int64_t(T) * hv, attn, stream)) != MR_OK) return st;
+    // the output gate (:207-211) rides in the attention's row stores
+    if ((st = mrc::mla_prefill_gated(&p, gated ? gate : nullptr, hv, stream)) != MR_OK) return st;
     return proj_rows(attn, T, hv, &a->o_proj, a->out, a->out_token_stride, stream);
 }
 

@@ -101,9 +101,17 @@ size_t mr_mla_prefill_workspace_size(const mr_mla_prefill_args* a) {
     return kv_bytes(a);
 }
 
-mr_status mr_mla_prefill(const mr_mla_prefill_args* a, void* stream) {
+mr_status mr_mla_prefill(const mr_mla_prefill_args* a, void* stream) { return mrc::mla_prefill_gated(a, nullptr, 0, stream); }
+
+}  // extern "C"
+
+mr_status mrc::mla_prefill_gated(const mr_mla_prefill_args* a, const void* gate, int64_t gate_ts, void* stream) {
     mr_status st = mrc::check_prefill(a);
     if (st != MR_OK) return st;
+    if (gate && (a->out_dtype != MR_BF16 || a->out_head_stride != a->v_head_dim ||
+                 a->out_token_stride != int64_t(a->heads) * a->v_head_dim || gate_ts != a->out_token_stride ||
+                 !aligned16(gate)))
+        return fail(MR_INVALID_ARGUMENT, "mla prefill: a gated prefill writes contiguous bf16 rows");
     const size_t need = kv_bytes(a);
     if (!a->workspace || a->workspace_bytes < need)
         return fail(MR_WORKSPACE_TOO_SMALL, "mla prefill: workspace %zu bytes < %zu required", a->workspace_bytes, need);
@@ -134,7 +142,10 @@ mr_status mr_mla_prefill(const mr_mla_prefill_args* a, void* stream) {
         q.NOPE = a->qk_nope_dim;
         q.V = a->v_head_dim;
         q.scale_log2 = float(double(a->scale) * 1.4426950408889634);
-        const hipError_t e = mr::launch_mla_prefill_any(q, ev, s);
+        hipError_t e = mr::launch_mla_prefill_any(q, ev, s);
+        if (e == hipSuccess && gate)
+            e = mr::launch_gate_mul((const uint16_t*)a->out, (const uint16_t*)gate, int64_t(a->tokens) * gate_ts,
+                                    (uint16_t*)a->out, s);
         return e == hipSuccess ? MR_OK : hip_fail(e, "mla prefill (any width) launch");
     }
     uint16_t* kv = (uint16_t*)a->workspace;
@@ -170,6 +181,8 @@ mr_status mr_mla_prefill(const mr_mla_prefill_args* a, void* stream) {
     p.P = a->n_ctx;
     p.H = a->heads;
     p.scale_log2 = float(double(a->scale) * 1.4426950408889634);
+    p.gate = (const uint16_t*)gate;
+    p.gate_ts = gate_ts;
 
     hipError_t e = hipSuccess;
     if (ev) e = hipEventRecord(ev[0], s);
@@ -179,5 +192,3 @@ mr_status mr_mla_prefill(const mr_mla_prefill_args* a, void* stream) {
     if (e == hipSuccess && ev) e = hipEventRecord(ev[2], s);
     return e == hipSuccess ? MR_OK : hip_fail(e, "mla prefill launch");
 }
-
-}  // extern "C"

@@ -29,5 +29,9 @@ DecodePartials decode_partials(const mr_mla_decode_args* a);
 
 // Every check mr_mla_prefill makes before its launches, workspace aside.
 mr_status check_prefill(const mr_mla_prefill_args* a);
+// mr_mla_prefill with the output gate of MLA.swift:207-211 applied to its
+// bf16 output (contiguous [T][H * v] rows, gate rows of the same stride);
+// gate null: mr_mla_prefill itself.
+mr_status mla_prefill_gated(const mr_mla_prefill_args* a, const void* gate, int64_t gate_ts, void* stream);
 
 }  // namespace mrc

@@ -38,6 +38,11 @@
 // output stores.
 //
 // Rows past T (x) or N (W) repeat the last row; their outputs are not stored.
+//
+// One launch can stack up to three projections of the same tokens (e.g.
+// q_a, kv_a and g_proj of one activation): their N tiles follow each other
+// in the grid, and a workgroup takes its projection's weight, output and
+// shape from the stack entry its tile falls in.
 #include <algorithm>
 
 #include "mr_kernels.hpp"
@@ -83,7 +88,7 @@ struct PgShape {
 };
 
 template <int TM, bool AFFINE, bool YF32>
-__global__ void __launch_bounds__(PG_THREADS, 1) proj_gemm_kernel(ProjGemmParams p) {
+__global__ void __launch_bounds__(PG_THREADS, 1) proj_gemm_kernel(ProjGemmStack ps) {
     using S = PgShape<TM, AFFINE>;
     constexpr int BK = S::BK, CPR = S::CPR, KS = S::KS, A_EL = S::A_EL, B_EL = S::B_EL, STAGE = S::STAGE;
     constexpr int WM = TM / 2;                 // rows per wave
@@ -95,7 +100,8 @@ __global__ void __launch_bounds__(PG_THREADS, 1) proj_gemm_kernel(ProjGemmParams
     extern __shared__ __attribute__((aligned(16))) uint16_t lds[];
     const int tid = threadIdx.x, w = tid >> 6, l = tid & 63;
 
-    const int m_tiles = (p.M + TM - 1) / TM, n_tiles = (p.N + PG_TN - 1) / PG_TN;
+    // the stacked projections share x and M; their N tiles follow each other
+    const int m_tiles = (ps.seg[0].M + TM - 1) / TM, n_tiles = ps.tile_end[ps.nseg - 1];
     const int total = m_tiles * n_tiles;
     // XCD-aware order: consecutive workgroups go to the 8 XCDs in turn, so
     // XCD x gets tile ids x * total / 8 ..; ids run over groups of 4 M
@@ -107,7 +113,10 @@ __global__ void __launch_bounds__(PG_THREADS, 1) proj_gemm_kernel(ProjGemmParams
     const int group = bid / (GM * n_tiles), first_m = group * GM;
     const int gsize = min(m_tiles - first_m, GM);
     const int mt = first_m + (bid % (GM * n_tiles)) % gsize;
-    const int nt = (bid % (GM * n_tiles)) / gsize;
+    const int nt_all = (bid % (GM * n_tiles)) / gsize;
+    const int seg = (nt_all >= ps.tile_end[0]) + (nt_all >= ps.tile_end[1]);
+    const ProjGemmParams p = ps.seg[seg];
+    const int nt = nt_all - (seg ? ps.tile_end[seg - 1] : 0);
     const int m0 = mt * TM, n0 = nt * PG_TN;
     const int KT = p.K / BK;
 
@@ -325,20 +334,20 @@ __global__ void __launch_bounds__(PG_THREADS, 1) proj_gemm_kernel(ProjGemmParams
 }
 
 template <int TM, bool AFFINE, bool YF32>
-hipError_t launch_tm(const ProjGemmParams& p, hipStream_t st) {
+hipError_t launch_tm(const ProjGemmStack& ps, hipStream_t st) {
     using S = PgShape<TM, AFFINE>;
-    const int m_tiles = (p.M + TM - 1) / TM, n_tiles = (p.N + PG_TN - 1) / PG_TN;
+    const int m_tiles = (ps.seg[0].M + TM - 1) / TM, n_tiles = ps.tile_end[ps.nseg - 1];
     const size_t lds = YF32 ? S::LDS_F32 : S::LDS_BF16;
     const auto kern = proj_gemm_kernel<TM, AFFINE, YF32>;
     const hipError_t attr = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     if (attr != hipSuccess) return attr;
-    hipLaunchKernelGGL(kern, dim3((unsigned)(m_tiles * n_tiles)), dim3(PG_THREADS), lds, st, p);
+    hipLaunchKernelGGL(kern, dim3((unsigned)(m_tiles * n_tiles)), dim3(PG_THREADS), lds, st, ps);
     return hipGetLastError();
 }
 
 template <int TM, bool AFFINE>
-hipError_t launch_y(const ProjGemmParams& p, hipStream_t st) {
-    return p.y_f32 ? launch_tm<TM, AFFINE, true>(p, st) : launch_tm<TM, AFFINE, false>(p, st);
+hipError_t launch_y(const ProjGemmStack& ps, hipStream_t st) {
+    return ps.seg[0].y_f32 ? launch_tm<TM, AFFINE, true>(ps, st) : launch_tm<TM, AFFINE, false>(ps, st);
 }
 
 }  // namespace
@@ -367,12 +376,31 @@ bool proj_gemm_ok(const ProjGemmParams& p) {
     return true;
 }
 
-hipError_t launch_proj_gemm(const ProjGemmParams& p, int cu_count, hipStream_t st) {
-    if (!proj_gemm_ok(p)) return hipErrorInvalidValue;
+hipError_t launch_proj_gemm_stack(const ProjGemmParams* segs, int n, int cu_count, hipStream_t st) {
+    if (n < 1 || n > 3) return hipErrorInvalidValue;
+    ProjGemmStack ps{};
+    ps.nseg = n;
+    int tiles = 0;
+    for (int i = 0; i < 3; ++i) {
+        if (i < n) {
+            const ProjGemmParams& q = segs[i];
+            if (!proj_gemm_ok(q) || q.M != segs[0].M || !q.packed != !segs[0].packed || q.y_f32 != segs[0].y_f32)
+                return hipErrorInvalidValue;
+            ps.seg[i] = q;
+            tiles += (q.N + PG_TN - 1) / PG_TN;
+            ps.tile_end[i] = tiles;
+        } else {
+            ps.tile_end[i] = INT32_MAX;
+        }
+    }
     // 256-row tiles when they alone fill the GPU, else 128
-    const bool big = (int64_t)((p.M + 255) / 256) * ((p.N + PG_TN - 1) / PG_TN) >= cu_count;
-    if (p.packed) return big ? launch_y<256, true>(p, st) : launch_y<128, true>(p, st);
-    return big ? launch_y<256, false>(p, st) : launch_y<128, false>(p, st);
+    const bool big = (int64_t)((segs[0].M + 255) / 256) * tiles >= cu_count;
+    if (segs[0].packed) return big ? launch_y<256, true>(ps, st) : launch_y<128, true>(ps, st);
+    return big ? launch_y<256, false>(ps, st) : launch_y<128, false>(ps, st);
+}
+
+hipError_t launch_proj_gemm(const ProjGemmParams& p, int cu_count, hipStream_t st) {
+    return launch_proj_gemm_stack(&p, 1, cu_count, st);
 }
 
 }  // namespace mr

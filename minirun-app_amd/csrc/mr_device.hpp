@@ -71,6 +71,20 @@ __device__ __forceinline__ uint32_t pack_bf16x2_hw(float lo, float hi) {
     return __builtin_bit_cast(uint32_t, v);
 }
 
+// sigmoid(g) = 1 / (1 + 2^(-g log2 e)) on the hardware exp2 and reciprocal
+// (each within 1 ulp); 0 and 1 at the extremes.
+__device__ __forceinline__ float sigmoid_f32(float g) {
+    return __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(-g * 1.4426950408889634f));
+}
+
+// The output gate of MLA.swift:207-211 on two bf16 elements packed in a
+// word: bf16(x * sigmoid(g)) per half.
+__device__ __forceinline__ uint32_t gated_bf16x2(uint32_t x, uint32_t g) {
+    const float lo = __uint_as_float(x << 16) * sigmoid_f32(__uint_as_float(g << 16));
+    const float hi = __uint_as_float(x & 0xffff0000u) * sigmoid_f32(__uint_as_float(g & 0xffff0000u));
+    return pack_bf16x2_hw(lo, hi);
+}
+
 // One correctly rounded fp32 operation each, never fused into an FMA with a
 // neighbour (hipcc contracts a*b+c by default; these carry no contract flag).
 __device__ __forceinline__ float mul_rn(float a, float b) {

@@ -124,6 +124,11 @@ struct PrefillAttnParams {
     int32_t out_f32;
     int32_t T, P, H;
     float scale_log2;  // softmax scale * log2(e)
+    // bf16 out only: null, or the output gate (MLA.swift:207-211) applied
+    // as the rows are stored, out = bf16(bf16(attn) * sigmoid(gate)) with
+    // gate[i][h * 128 + d] at gate + i * gate_ts
+    const uint16_t* gate;
+    int64_t gate_ts;
 };
 
 hipError_t launch_upproj(const UpProjParams& p, hipStream_t st);
@@ -192,9 +197,18 @@ struct ProjGemmParams {
     int32_t y_f32;
     int32_t M, N, K;
 };
+// Up to three projections of the same M tokens in one launch: entry s owns
+// the N tiles tile_end[s-1] .. tile_end[s] - 1 (tile_end past nseg: INT32_MAX).
+struct ProjGemmStack {
+    ProjGemmParams seg[3];
+    int32_t nseg;
+    int32_t tile_end[3];
+};
 constexpr int PROJ_GEMM_MIN_TOKENS = 64;  // fewer tokens take the token-tile GEMV kernels
 bool proj_gemm_ok(const ProjGemmParams& p);  // shapes, alignment and formats the kernel takes
 hipError_t launch_proj_gemm(const ProjGemmParams& p, int cu_count, hipStream_t st);
+// n entries with one M, all dense or all affine, one output dtype; each proj_gemm_ok
+hipError_t launch_proj_gemm_stack(const ProjGemmParams* segs, int n, int cu_count, hipStream_t st);
 hipError_t launch_prefill_attn(const PrefillAttnParams& p, hipStream_t st);
 
 // ---------------------------------------------------------------- top-k

@@ -453,6 +453,21 @@ __global__ void __launch_bounds__(256, 2) prefill_attn_kernel(PrefillAttnParams 
         if (kt + 1 < ntiles) step(kt + 1, std::integral_constant<int, 1>{});
     }
 
+    // the gate chunks this lane stores below, requested before the
+    // normalisation and the LDS staging so that their latency overlaps them;
+    // the gate and the output stream past L2 (nontemporal), which keeps the
+    // keys and values that later query tiles of this head read
+    u32x4 gv[8];
+    const bool gated = p.gate != nullptr && !p.out_f32;
+    if (gated) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const int q = l + 64 * i, qq = min(q0 + 32 * w + (q >> 4), p.T - 1);
+            gv[i] = __builtin_nontemporal_load((const u32x4*)(p.gate + (int64_t)qq * p.gate_ts + head * AT_DV +
+                                                              (q & 15) * 8));
+        }
+    }
+
     // normalise: the two halves of the wave hold partial sums of one query
     const float l_tot = xor32_sum(l_part);
     const float inv = 1.f / l_tot;
@@ -494,7 +509,13 @@ __global__ void __launch_bounds__(256, 2) prefill_attn_kernel(PrefillAttnParams 
         const int qq = q0 + 32 * w + row;
         u32x4 v = *(const u32x4*)(st + row * AT_DV + ((ch ^ (row & 15)) << 3));
         if (row >> 4) v = u32x4{v[2], v[3], v[0], v[1]};
-        if (qq < p.T) *(u32x4*)((uint16_t*)p.out + (int64_t)qq * p.out_ts + (int64_t)head * p.out_hs + ch * 8) = v;
+        if (qq >= p.T) continue;
+        if (gated) {
+#pragma unroll
+            for (int k = 0; k < 4; ++k) v[k] = gated_bf16x2(v[k], gv[i][k]);
+        }
+        __builtin_nontemporal_store(v, (u32x4*)((uint16_t*)p.out + (int64_t)qq * p.out_ts + (int64_t)head * p.out_hs +
+                                                ch * 8));
     }
 }
 
