@@ -14,25 +14,29 @@
 //
 // One workgroup of 4 waves computes a TM x 256 tile of y (TM = 256 or 128),
 // each wave a (TM/2) x 128 block of 32x32x16 bf16 MFMA tiles.  K streams in
-// k-tiles of BK (64 dense, 32 affine) through two LDS stages; a stage holds
-// the x tile [TM][BK] and the W tile(s) [256][BK] in rows of CPR = BK / 8
-// 16-byte chunks, chunk c of row r in slot c ^ f(r) (f = (r >> 1) & 7 for
-// CPR 8, (r >> 2) & 3 for CPR 4), so the 16 lanes of a ds_read_b128 phase
-// (16 consecutive rows, one chunk) hit 16 distinct bank groups.
+// k-tiles of BK = 32 through NS LDS stages (4 dense, 2 affine); a stage holds
+// the x tile [TM][32] and the W tile(s) [256][32] in rows of 4 16-byte
+// chunks, chunk c of row r in slot c ^ ((r >> 2) & 3), so the 16 lanes of a
+// ds_read_b128 phase (16 consecutive rows, one chunk) hit 16 distinct bank
+// groups.
 //
-// Pipeline, iteration kt (stage kt % 2 is complete when it starts):
-//   - x (and dense W) k-tile kt + 1 goes to the other stage by global -> LDS
-//     DMA (issued by every wave, 1 KB per instruction);
+// Pipeline, iteration kt (stage kt % NS is complete when it starts):
+//   - x (and dense W) k-tile kt + NS - 1 goes to the stage read in the
+//     previous iteration by global -> LDS DMA (issued by every wave, 1 KB
+//     per instruction): dense tiles keep up to NS - 1 k-tiles (96 KB per
+//     workgroup) in flight and issue each k-tile's DMA a k-step's share at
+//     a time between that k-step's MFMAs; affine ones issue k-tile kt + 1
+//     at the top of the iteration;
 //   - affine W: the packed words, scales and biases of k-tile kt + 2 go to
 //     an LDS slot by DMA too, and those of k-tile kt + 1 (fetched one
 //     iteration earlier) are dequantized into the other stage.  Thread t
 //     owns W row t of the tile, and the 64 rows of a wave are fetched by
 //     that wave's own DMA, so its vmcnt wait alone makes them visible to it;
-//   - the k-steps' MFMAs on stage kt % 2, fragments read one step ahead;
+//   - the k-steps' MFMAs on stage kt % NS, fragments read one step ahead;
 //   - one barrier, after this wave's DMA of kt + 1 has landed.
-// Past the last k-tile the issues repeat the last one (into the stage or
-// slot that is never read again), so every iteration issues the same loads
-// and the vmcnt waits are constants.  Every global load is a DMA issued from
+// Past the last k-tile the issues repeat the last one (into a stage or slot
+// that is never read again), so every iteration issues the same loads and
+// the vmcnt waits are constants.  Every global load is a DMA issued from
 // inline asm and waited for explicitly (the compiler neither sees them nor
 // adds waits of its own); the only compiler-visible global accesses are the
 // output stores.
@@ -55,7 +59,8 @@ constexpr int PG_TN = 256, PG_THREADS = 256;
 
 template <int CPR>
 __device__ __forceinline__ int pg_slot(int r, int c) {
-    return CPR == 4 ? r * 4 + (c ^ ((r >> 2) & 3)) : r * 8 + (c ^ ((r >> 1) & 7));
+    static_assert(CPR == 4, "rows of four 16-byte chunks");
+    return r * 4 + (c ^ ((r >> 2) & 3));
 }
 
 // DMA of 4 bytes per lane (lane i lands at lds_dst_wave_base + 4 i); the
@@ -76,13 +81,14 @@ constexpr int PG_PSLOT = 256 * 16 + 2 * 256 * 4;  // bytes
 
 template <int TM, bool AFFINE>
 struct PgShape {
-    static constexpr int BK = AFFINE ? 32 : 64;
+    static constexpr int BK = 32;
+    static constexpr int NS = AFFINE ? 2 : 4;             // LDS stages (k-tiles)
     static constexpr int CPR = BK / 8;                    // 16-byte chunks per row
     static constexpr int KS = BK / 16;                    // 16-deep MFMA steps per k-tile
     static constexpr int A_EL = TM * BK;                  // x tile elements
     static constexpr int B_EL = PG_TN * BK;               // one W tile's elements
     static constexpr int STAGE = A_EL + (AFFINE ? 2 : 1) * B_EL;
-    static constexpr int RING = 2 * STAGE * 2;            // bytes of the two stages
+    static constexpr int RING = NS * STAGE * 2;           // bytes of the stages
     static constexpr size_t LDS_BF16 = std::max<size_t>(RING + (AFFINE ? 2 * PG_PSLOT : 0), (size_t)TM * PG_TN * 2);
     static constexpr size_t LDS_F32 = std::max<size_t>(RING + (AFFINE ? 2 * PG_PSLOT : 0), (size_t)TM / 2 * PG_TN * 4);
 };
@@ -90,7 +96,7 @@ struct PgShape {
 template <int TM, bool AFFINE, bool YF32>
 __global__ void __launch_bounds__(PG_THREADS, 1) proj_gemm_kernel(ProjGemmStack ps) {
     using S = PgShape<TM, AFFINE>;
-    constexpr int BK = S::BK, CPR = S::CPR, KS = S::KS, A_EL = S::A_EL, B_EL = S::B_EL, STAGE = S::STAGE;
+    constexpr int BK = S::BK, NS = S::NS, CPR = S::CPR, KS = S::KS, A_EL = S::A_EL, B_EL = S::B_EL, STAGE = S::STAGE;
     constexpr int WM = TM / 2;                 // rows per wave
     constexpr int MI = WM / 32;                // 32-row MFMA tiles per wave
     constexpr int RPI = 64 / CPR;              // rows per DMA instruction
@@ -125,7 +131,7 @@ __global__ void __launch_bounds__(PG_THREADS, 1) proj_gemm_kernel(ProjGemmStack 
     // (l % CPR) ^ f(row).  Byte offsets from the tile's first row.
     const uint16_t* abase = p.x + (int64_t)m0 * p.ldx;
     const uint16_t* bbase = AFFINE ? nullptr : p.w + (int64_t)n0 * p.ldw;
-    auto chunk_of = [](int row, int sc) { return CPR == 4 ? sc ^ ((row >> 2) & 3) : sc ^ ((row >> 1) & 7); };
+    auto chunk_of = [](int row, int sc) { return sc ^ ((row >> 2) & 3); };
     uint32_t aoff[DA], boff[DB > 0 ? DB : 1];
 #pragma unroll
     for (int q = 0; q < DA; ++q) {
@@ -140,8 +146,8 @@ __global__ void __launch_bounds__(PG_THREADS, 1) proj_gemm_kernel(ProjGemmStack 
         }
     }
     const int wu = __builtin_amdgcn_readfirstlane(w);
-    auto issue_dma = [&](int kt) {  // k-tile min(kt, KT - 1) into stage kt % 2
-        uint16_t* st = lds + (kt & 1) * STAGE;
+    auto issue_dma = [&](int kt) {  // k-tile min(kt, KT - 1) into stage kt % NS
+        uint16_t* st = lds + (kt & (NS - 1)) * STAGE;
         const uint32_t ko = (uint32_t)min(kt, KT - 1) * BK * 2;
 #pragma unroll
         for (int q = 0; q < DA; ++q) dma16_off(abase, aoff[q] + ko, st + 512 * (DA * wu + q));
@@ -176,7 +182,7 @@ __global__ void __launch_bounds__(PG_THREADS, 1) proj_gemm_kernel(ProjGemmStack 
     // slot kt % 2 (landed) -> hi and lo bf16 rows of stage kt % 2
     auto dequant_w = [&](int kt) {
         const char* slot = pslots + (kt & 1) * PG_PSLOT;
-        uint16_t* sh = lds + (kt & 1) * STAGE + A_EL;
+        uint16_t* sh = lds + (kt & (NS - 1)) * STAGE + A_EL;
         uint16_t* sl = sh + B_EL;
         kt = min(kt, KT - 1);
         const u32x4 q = *(const u32x4*)(slot + 16 * tid);
@@ -213,7 +219,7 @@ __global__ void __launch_bounds__(PG_THREADS, 1) proj_gemm_kernel(ProjGemmStack 
 #pragma unroll
         for (int j = 0; j < 4; ++j) acc[i][j] = f32x16{};
     auto read = [&](int kt, int ks, bf16x8(&a)[MI], bf16x8(&b)[NB][4]) {
-        const uint16_t* sa = lds + (kt & 1) * STAGE;
+        const uint16_t* sa = lds + (kt & (NS - 1)) * STAGE;
         const int ch = 2 * ks + (l >> 5);
 #pragma unroll
         for (int i = 0; i < MI; ++i) a[i] = *(const bf16x8*)(sa + 8 * pg_slot<CPR>(wm * WM + i * 32 + (l & 31), ch));
@@ -231,23 +237,74 @@ __global__ void __launch_bounds__(PG_THREADS, 1) proj_gemm_kernel(ProjGemmStack 
 #pragma unroll
                 for (int j = 0; j < 4; ++j) acc[i][j] = mfma32(b[u][j], a[i], acc[i][j]);
     };
+    // dense: DMA instruction q (of DA + DB) of k-tile kt, and one k-step's
+    // MFMAs with the k-step's share of a k-tile's DMA spread among them, so
+    // the MFMA pipe stays busy while the address unit takes the loads
+    constexpr int NQ = DA + DB, QS = NQ / KS;
+    static_assert(AFFINE || NQ % KS == 0, "DMA instructions split evenly over the k-steps");
+    auto dma_one = [&](int kt, int q) {
+        uint16_t* st = lds + (kt & (NS - 1)) * STAGE;
+        const uint32_t ko = (uint32_t)min(kt, KT - 1) * BK * 2;
+        if (q < DA)
+            dma16_off(abase, aoff[q] + ko, st + 512 * (DA * wu + q));
+        else
+            dma16_off(bbase, boff[q - DA] + ko, st + A_EL + 512 * (DB * wu + q - DA));
+    };
+    auto mma_dma = [&](const bf16x8(&a)[MI], const bf16x8(&b)[NB][4], int kt_dma, int ks) {
+        constexpr int NM = MI * 4;
+#pragma unroll
+        for (int m = 0; m < NM; ++m) {
+            acc[m / 4][m % 4] = mfma32(b[0][m % 4], a[m / 4], acc[m / 4][m % 4]);
+#pragma unroll
+            for (int r = 0; r < QS; ++r)
+                if (m == (r + 1) * NM / QS - 1) {
+                    dma_one(kt_dma, ks * QS + r);
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+        }
+    };
 
-    // prologue: stage 0 complete; the affine slot of k-tile 1 in flight
-    issue_dma(0);
+    // prologue: stage 0 complete, k-tiles 1 .. NS - 2 (and the affine slot
+    // of k-tile 1) in flight
+#pragma unroll
+    for (int k = 0; k < NS - 1; ++k) issue_dma(k);
+    constexpr int LATER = (NS - 2) * (DA + DB);  // DMA of the k-tiles after the next one
     if constexpr (AFFINE) {
         issue_w(0);
         issue_w(1);
-        wait_vmcnt<DP>();
+        wait_vmcnt<LATER + DP>();
         dequant_w(0);
     } else {
-        wait_vmcnt<0>();
+        wait_vmcnt<LATER>();
     }
     lds_barrier();
     bf16x8 fa[2][MI], fb[2][NB][4];
     read(0, 0, fa[0], fb[0]);
+    if constexpr (!AFFINE) {
+        // k-tile kt + NS - 1 is issued a k-step's share at a time; the wait
+        // before the last k-step's MFMAs leaves k-tiles kt + 2 .. kt + NS - 2
+        // and the shares of kt + NS - 1 issued so far in flight
+        static_assert(NS >= 3, "the interleaved DMA needs a stage beyond the next");
+        constexpr int WAIT = (NS - 3) * NQ + (NQ - QS);
 #pragma unroll 1
-    for (int kt = 0; kt < KT; ++kt) {
-        issue_dma(kt + 1);
+        for (int kt = 0; kt < KT; ++kt) {
+#pragma unroll
+            for (int ks = 0; ks < KS; ++ks) {
+                const int nx = (ks + 1) & 1;
+                if (ks + 1 < KS) {
+                    read(kt, ks + 1, fa[nx], fb[nx]);
+                } else {
+                    wait_vmcnt<WAIT>();  // this wave's DMA of k-tile kt + 1 landed
+                    lds_barrier();       // every wave's; every wave done with stage kt
+                    read(kt + 1, 0, fa[nx], fb[nx]);  // past the last k-tile: a stage never used, in bounds
+                }
+                mma_dma(fa[ks & 1], fb[ks & 1], kt + NS - 1, ks);
+            }
+        }
+    }
+#pragma unroll 1
+    for (int kt = 0; AFFINE && kt < KT; ++kt) {
+        issue_dma(kt + NS - 1);
         if constexpr (AFFINE) {
             issue_w(kt + 2);
             wait_vmcnt<DA + DP>();  // this wave's slot of k-tile kt + 1
@@ -259,7 +316,7 @@ __global__ void __launch_bounds__(PG_THREADS, 1) proj_gemm_kernel(ProjGemmStack 
             if (ks + 1 < KS) {
                 read(kt, ks + 1, fa[nx], fb[nx]);
             } else {
-                wait_vmcnt<DP>();  // this wave's DMA of k-tile kt + 1 landed
+                wait_vmcnt<LATER + DP>();  // this wave's DMA of k-tile kt + 1 landed
                 lds_barrier();     // every wave's; every wave done with stage kt
                 read(kt + 1, 0, fa[nx], fb[nx]);  // past the last k-tile: a stage never used, in bounds
             }
@@ -353,7 +410,7 @@ hipError_t launch_y(const ProjGemmStack& ps, hipStream_t st) {
 }  // namespace
 
 bool proj_gemm_ok(const ProjGemmParams& p) {
-    const int bk = p.packed ? 32 : 64;
+    const int bk = 32;
     if (p.M <= 0 || p.N <= 0 || p.N % 8 || p.K % bk || p.K < bk) return false;
     if (((uintptr_t)p.x & 15) || p.ldx % 8 || p.ldx < p.K || ((uintptr_t)p.y & 15) || p.ldy % (p.y_f32 ? 4 : 8) ||
         p.ldy < p.N)
