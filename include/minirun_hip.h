@@ -537,11 +537,13 @@ mr_status mr_indexer_scores(const void *queries, mr_dtype q_dtype, int32_t seq, 
  * (device int32: 0 or MR_NONFINITE), with no host synchronisation; without
  * a status buffer (or with MR_TOPK_CHECK) the call reads the flags back and
  * returns MR_NONFINITE, as the reference throws; MR_TOPK_UNCHECKED skips
- * that read.  Limits: top_k selected
- * <= 4096, offset + available - 1 <= INT32_MAX.  Rows of more than 32768
- * keys are ranked in slices of 32768 on as many workgroups and merged.
- * Workspace: mr_topk_workspace_size(rows, cols, top_k) bytes (per-row NaN
- * flags; for rows of more than 32768 columns also the slices' candidates).
+ * that read.  Any top_k; offset + available - 1 <= INT32_MAX.  Rows of
+ * more than 32768 keys are ranked in slices of 32768 on as many workgroups
+ * and merged; more than 4096 selected keys are ranked in slices of 4096
+ * (each sorted whole) and merged.  Workspace: mr_topk_workspace_size(rows,
+ * cols, top_k) bytes (per-row NaN flags; for sliced rows also the slices'
+ * sorted lists, two buffers of rows x slices x min(top_k, slice) 8-byte
+ * composites at the first merge round).
  * ------------------------------------------------------------------------ */
 enum { MR_TOPK_CHECK = 1, MR_TOPK_UNCHECKED = 2 };
 

@@ -66,8 +66,6 @@ mr_status mr_topk_geometry(int32_t rows, int32_t cols, int32_t top_k, int32_t ra
     if (available > cols)
         return fail(MR_INVALID_SHAPE, "score matrix has fewer compressed keys than the sequence position requires");
     const int32_t sel = top_k < available ? top_k : available;
-    if (sel > mr::TOPK_MAX)
-        return fail(MR_INVALID_SHAPE, "top-k selection: %d keys per row exceed the limit of %d", sel, mr::TOPK_MAX);
     if (available > 0 && int64_t(offset) + available - 1 > INT32_MAX)
         return fail(MR_INVALID_SHAPE, "lightning cache index overflows Int");
     if (selected) *selected = sel;
@@ -76,7 +74,9 @@ mr_status mr_topk_geometry(int32_t rows, int32_t cols, int32_t top_k, int32_t ra
 
 size_t mr_topk_workspace_size(int32_t rows, int32_t cols, int32_t top_k) {
     if (rows <= 0 || cols < 0 || top_k <= 0) return 0;
-    return mr::topk_workspace_bytes(rows, cols, top_k < mr::TOPK_MAX ? top_k : mr::TOPK_MAX);
+    // a row selects at most min(top_k, cols) keys (cols bounds the keys any
+    // start position makes available); the size grows with that count
+    return mr::topk_workspace_bytes(rows, cols, top_k < cols ? top_k : cols);
 }
 
 mr_status mr_topk_select(const mr_topk_args* a, void* stream) {

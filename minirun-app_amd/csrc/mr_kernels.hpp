@@ -224,12 +224,13 @@ struct TopkParams {
     int32_t* out;  // [rows][selected], row stride out_stride
     int64_t out_stride;
     int32_t* nan_flags;  // [rows]: 1 when the row holds a NaN
-    // rows of more than TOPK_SLICE keys: `slices` workgroups per row each
-    // rank TOPK_SLICE keys and write their first `selected` composites
-    // (score image << 32 | key, ascending; ~0 past the slice's keys) to
-    // cand[row][slice][selected], and their NaN flag to slice_nan[row][slice];
-    // merge rounds then reduce the sorted lists pairwise (set by the launcher)
-    int32_t slices;
+    // rows of more than TOPK_SLICE keys (or more than TOPK_MAX selected):
+    // `slices` workgroups per row each rank a slice of the keys and write
+    // their first min(selected, list_len) composites (score image << 32 |
+    // key, ascending; ~0 past them) to cand[row][slice][list_len], and their
+    // NaN flag to slice_nan[row][slice]; merge rounds then reduce the sorted
+    // lists pairwise (set by the launcher)
+    int32_t slices, list_len;
     unsigned long long* cand;
     int32_t* slice_nan;
     // one row: the kernel that writes the row's NaN flag also writes the

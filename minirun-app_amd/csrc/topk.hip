@@ -479,13 +479,15 @@ __global__ void __launch_bounds__(NT) topk_select_kernel(TopkParams p) {
         unsigned long long x[EPT];
         sort_lds<NT, EPT>(comp, npow, x);
         if (p.slices > 1) {  // this slice's sorted composites, ~0 past its keys
-            unsigned long long* crow = p.cand + ((int64_t)row * p.slices + slice) * p.selected;
+            unsigned long long* crow = p.cand + ((int64_t)row * p.slices + slice) * p.list_len;
 #pragma unroll
             for (int e = 0; e < EPT; ++e) {
                 const int i = EPT * tid + e;
-                if (i < p.selected)
+                if (i < p.list_len)
                     crow[i] = i < k ? ((x[e] >> 16) << 32) | (uint32_t)(key0 + (int)(uint32_t)(x[e] & 0xffffull)) : TK_NONE;
             }
+            // the list past what the sort held
+            for (int i = EPT * NT + tid; i < p.list_len; i += NT) crow[i] = TK_NONE;
             return;
         }
         int32_t* orow = p.out + (int64_t)row * p.out_stride;
@@ -578,8 +580,8 @@ __global__ void __launch_bounds__(NT) topk_select_kernel(TopkParams p) {
     }
     if (bucketed || k <= 1) {
         if (p.slices > 1) {  // this slice's sorted composites, ~0 past its keys
-            unsigned long long* crow = p.cand + ((int64_t)row * p.slices + slice) * p.selected;
-            for (int i = tid; i < p.selected; i += NT)
+            unsigned long long* crow = p.cand + ((int64_t)row * p.slices + slice) * p.list_len;
+            for (int i = tid; i < p.list_len; i += NT)
                 crow[i] = i < k ? ((comp[i] >> 16) << 32) | (uint32_t)(key0 + (int)(uint32_t)(comp[i] & 0xffffull)) : TK_NONE;
         } else {
             int32_t* orow = p.out + (int64_t)row * p.out_stride;
@@ -1317,22 +1319,23 @@ __global__ void __launch_bounds__(1024) topk_spread_finish(TopkParams p) {
 
 // One merge round over rows of sorted composite lists: list pair q of a row
 // (lists 2q and 2q+1 of `lists`, each `len` long; an odd last list passes
-// through) -> the first `len` of their merge.  Output position i takes its
-// split from a merge-path binary search over global memory (the lists are
-// short and cached).  The last round (one pair left) writes the keys
-// instead, offset + key or -1 past `visible`, and the row's NaN flag.
-__global__ void __launch_bounds__(256) topk_merge_kernel(TopkParams p, const unsigned long long* in, int lists,
+// through) -> the first len_out = min(2 len, selected) of their merge (~0
+// past an odd list's end).  Output position i takes its split from a
+// merge-path binary search over global memory (the lists are short and
+// cached).  The last round (one pair left) writes the keys instead, offset
+// + key or -1 past `visible`, and the row's NaN flag.
+__global__ void __launch_bounds__(256) topk_merge_kernel(TopkParams p, const unsigned long long* in, int lists, int len,
                                                           unsigned long long* outc) {
     const int row = blockIdx.y;
     const int q = blockIdx.x;
-    const int len = p.selected;
+    const int len_out = (int)min((int64_t)2 * len, (int64_t)p.selected);
     const unsigned long long* A = in + ((int64_t)row * lists + 2 * q) * len;
     const bool pair = 2 * q + 1 < lists;
     const unsigned long long* B = A + len;
     const int nout = (lists + 1) / 2;
     const bool last = nout == 1;
     const int visible = p.start_pos == 0 ? (row + 1) / p.ratio : p.available;
-    for (int i = threadIdx.x; i < len; i += 256) {
+    for (int i = threadIdx.x; i < len_out; i += 256) {
         unsigned long long v;
         if (pair) {
             // a = number of the first i + 1 outputs taken from A
@@ -1349,13 +1352,13 @@ __global__ void __launch_bounds__(256) topk_merge_kernel(TopkParams p, const uns
             const unsigned long long b = i - lo >= 0 ? B[i - lo] : 0ull;
             v = lo == 0 ? b : (i - lo < 0 ? a : (a > b ? a : b));
         } else {
-            v = A[i];
+            v = i < len ? A[i] : TK_NONE;
         }
         if (last) {
             const int key = (int)(uint32_t)(v & 0xffffffffull);
             p.out[(int64_t)row * p.out_stride + i] = key >= visible ? -1 : p.offset + key;
         } else {
-            outc[((int64_t)row * nout + q) * len + i] = v;
+            outc[((int64_t)row * nout + q) * len_out + i] = v;
         }
     }
     if (last && threadIdx.x == 0) {
@@ -1406,15 +1409,28 @@ SpreadLayout spread_layout(int32_t rows, int slices) {
     return L;
 }
 
-}  // namespace
+// Keys per slice workgroup when more than TOPK_MAX keys are selected: a
+// slice sorts all of its keys (at most TOPK_MAX), and the merge rounds
+// double the lists' length up to `selected`.
+constexpr int TOPK_LARGE_SLICE = TOPK_MAX;
 
-size_t topk_workspace_bytes(int32_t rows, int32_t cols, int32_t selected) {
-    size_t bytes = a256(size_t(rows) * 4);
+// Bytes of one of the two composite buffers of the merge rounds: the largest
+// rows x lists x length over the rounds.
+size_t merge_buffer_bytes(int32_t rows, int64_t slices, int64_t len, int64_t selected) {
+    size_t most = 0;
+    for (int64_t lists = slices;; lists = (lists + 1) / 2, len = std::min(2 * len, selected)) {
+        most = std::max(most, size_t(rows) * size_t(lists) * size_t(len) * 8);
+        if (lists <= 1) break;
+    }
+    return a256(most);
+}
+
+size_t small_k_bytes(int32_t rows, int32_t cols, int32_t selected) {
     size_t extra = 0;
     if (cols > TOPK_SLICE) {
         const size_t slices = (size_t(cols) + TOPK_SLICE - 1) / TOPK_SLICE;
         extra = a256(size_t(rows) * slices * 4);
-        extra += 2 * a256(size_t(rows) * slices * size_t(selected) * 8);
+        extra += 2 * merge_buffer_bytes(rows, (int64_t)slices, selected, selected);
     }
     if (rows <= TOPK_SPREAD_MAX_ROWS && cols > TOPK_SPREAD_MIN_KEYS) {
         // the ranked keys never exceed the columns
@@ -1422,16 +1438,71 @@ size_t topk_workspace_bytes(int32_t rows, int32_t cols, int32_t selected) {
                                                   TOPK_SPREAD_MAX_SLICES);
         extra = std::max(extra, spread_layout(rows, slices).end);
     }
-    return bytes + extra;
+    return extra;
 }
+
+}  // namespace
+
+size_t topk_workspace_bytes(int32_t rows, int32_t cols, int32_t selected) {
+    size_t bytes = a256(size_t(rows) * 4);
+    if (selected <= TOPK_MAX) return bytes + small_k_bytes(rows, cols, selected);
+    // more than TOPK_MAX keys: slices of TOPK_LARGE_SLICE and merge rounds;
+    // a call whose rows turn out to select fewer takes the paths above
+    const int64_t slices = (int64_t(cols) + TOPK_LARGE_SLICE - 1) / TOPK_LARGE_SLICE;
+    const size_t large = a256(size_t(rows) * size_t(slices) * 4) +
+                         2 * merge_buffer_bytes(rows, slices, TOPK_LARGE_SLICE, selected);
+    return bytes + std::max(large, small_k_bytes(rows, cols, TOPK_MAX));
+}
+
+namespace {
+
+// The pairwise merge rounds over `slices` sorted lists of `len` composites
+// per row in buf[0], down to the keys.
+hipError_t merge_rounds(const TopkParams& p, unsigned long long* const* buf, int slices, int len, hipStream_t st) {
+    int lists = slices, cur = 0;
+    while (lists > 1) {
+        const int nout = (lists + 1) / 2;
+        hipLaunchKernelGGL(topk_merge_kernel, dim3((unsigned)nout, (unsigned)p.rows), dim3(256), 0, st, p,
+                           (const unsigned long long*)buf[cur], lists, len, buf[cur ^ 1]);
+        const hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+        lists = nout;
+        len = (int)std::min<int64_t>(2 * (int64_t)len, p.selected);
+        cur ^= 1;
+    }
+    return hipSuccess;
+}
+
+}  // namespace
 
 hipError_t launch_topk_select(const TopkParams& p0, void* workspace, int32_t* status, hipStream_t st) {
     TopkParams p = p0;
     p.slices = 1;
+    p.list_len = p.selected;
     // a single row's status comes from the kernel that flags its NaN (the
     // selection, or the last merge round), not from a launch of its own
     p.status_direct = p.rows == 1 ? status : nullptr;
-    if (spread_applies(p.rows, p.available)) {
+    if (p.selected > TOPK_MAX) {
+        // more keys than one workgroup orders: every slice of
+        // TOPK_LARGE_SLICE keys sorts all of its keys, and the merge rounds
+        // keep the first `selected` of each merge
+        char* ws = (char*)workspace + a256(size_t(p.rows) * 4);
+        const int slices = (p.available + TOPK_LARGE_SLICE - 1) / TOPK_LARGE_SLICE;
+        const int64_t max_slices = (int64_t(p.cols) + TOPK_LARGE_SLICE - 1) / TOPK_LARGE_SLICE;
+        p.slices = slices;
+        p.list_len = TOPK_LARGE_SLICE;
+        p.slice_nan = (int32_t*)ws;
+        ws += a256(size_t(p.rows) * size_t(max_slices) * 4);
+        unsigned long long* buf[2] = {
+            (unsigned long long*)ws,
+            (unsigned long long*)(ws + merge_buffer_bytes(p.rows, max_slices, TOPK_LARGE_SLICE, p.selected))};
+        p.cand = buf[0];
+        static_assert(1024 * 4 == TOPK_LARGE_SLICE, "one key per register of a 1024 x 4 slice");
+        hipLaunchKernelGGL((topk_select_kernel<1024, 4>), dim3((unsigned)p.rows, (unsigned)slices), dim3(1024), 0, st, p);
+        hipError_t e = hipGetLastError();
+        if (e == hipSuccess) e = merge_rounds(p, buf, slices, TOPK_LARGE_SLICE, st);
+        if (e != hipSuccess) return e;
+    } else if (spread_applies(p.rows, p.available)) {
         // a few rows of many keys: each row over many workgroups
         const int slices = (p.available + TOPK_SPREAD_SLICE - 1) / TOPK_SPREAD_SLICE;
         char* ws = (char*)workspace + a256(size_t(p.rows) * 4);
@@ -1459,21 +1530,14 @@ hipError_t launch_topk_select(const TopkParams& p0, void* workspace, int32_t* st
         p.slices = slices;
         p.slice_nan = (int32_t*)ws;
         ws += a256(size_t(p.rows) * max_slices * 4);
-        unsigned long long* buf[2] = {(unsigned long long*)ws,
-                                      (unsigned long long*)(ws + a256(size_t(p.rows) * max_slices * size_t(p.selected) * 8))};
+        unsigned long long* buf[2] = {
+            (unsigned long long*)ws,
+            (unsigned long long*)(ws + merge_buffer_bytes(p.rows, max_slices, p.selected, p.selected))};
         p.cand = buf[0];
         hipLaunchKernelGGL((topk_select_kernel<1024, 32>), dim3((unsigned)p.rows, (unsigned)slices), dim3(1024), 0, st, p);
         hipError_t e = hipGetLastError();
+        if (e == hipSuccess) e = merge_rounds(p, buf, slices, p.selected, st);
         if (e != hipSuccess) return e;
-        int lists = slices, cur = 0;
-        while (lists > 1) {
-            const int nout = (lists + 1) / 2;
-            hipLaunchKernelGGL(topk_merge_kernel, dim3((unsigned)nout, (unsigned)p.rows), dim3(256), 0, st, p,
-                               (const unsigned long long*)buf[cur], lists, buf[cur ^ 1]);
-            if ((e = hipGetLastError()) != hipSuccess) return e;
-            lists = nout;
-            cur ^= 1;
-        }
     }
     hipError_t e = hipGetLastError();
     if (e == hipSuccess && status && !p.status_direct) {

@@ -93,6 +93,23 @@ def test_slices_ties_odd_counts_and_masking(M):
     compare(M, z, 4096, 1, 98303, 0, "all-equal-3-slices")
 
 
+def test_more_than_4096_selected(M):
+    # `selecting` takes any topK (DeepSeekV4Attention.swift:582-645): more
+    # than 4096 keys run as slices of 4096 that each sort all their keys,
+    # then merge rounds whose lists double up to top_k
+    compare(M, normal("tk.big1", (1, 70000)), 10000, 1, 69999, 3, "k10000-of-70000")
+    compare(M, normal("tk.big2", (1, 262144)), 16384, 4, 1048575, 0, "k16384-of-262144")
+    s = np.floor(normal("tk.big3", (1, 20000)) * 2).astype(np.float32)   # ~10 distinct values
+    compare(M, s, 8000, 1, 19999, 0, "k8000-ties")
+    compare(M, np.zeros((1, 9000), np.float32), 9000, 1, 8999, 0, "all-equal-every-key")
+    compare(M, normal("tk.big4", (1, 12000)), 5000, 1, 9000, 0, "k5000-cols-past-available")
+
+
+def test_more_than_4096_selected_prefill_rows(M):
+    # prefill rows (start position 0): row r sees keys 0 .. r, the rest -1
+    compare(M, normal("tk.bigpf", (4200, 4200)), 4150, 1, 0, 0, "prefill-k4150")
+
+
 def test_nan_in_a_late_slice_is_reported(M):
     import torch
 
@@ -106,6 +123,14 @@ def test_nan_in_a_late_slice_is_reported(M):
     status = torch.full((1,), -1, dtype=torch.int32, device="cuda")
     M.lightning_select(dev(normal("tk.nanok", (1, 140000))), 256, 1, 131071, 0, check=False, status=status)
     assert int(status.item()) == 0
+    # the same with more than 4096 selected keys (slices of 4096): a NaN in a
+    # middle slice, and one past the ranked keys, through the device status
+    for col in (50000, 139999):
+        s = normal("tk.nanb", (1, 140000))
+        s[0, col] = np.nan
+        status = torch.full((1,), -1, dtype=torch.int32, device="cuda")
+        M.lightning_select(dev(s), 6000, 1, 131071, 0, check=False, status=status)
+        assert int(status.item()) == MH.NONFINITE, col
 
 
 def test_nan_is_reported(M):

@@ -115,7 +115,6 @@ def test_index_table_errors():
     (2, 4, 2, 0, 0, 0, "invalid lightning-index selection geometry"),
     (2, 4, 2, 1, 3, 0, "exactly one token"),
     (1, 2, 2, 1, 3, 0, "fewer compressed keys"),
-    (1, 8192, 5000, 1, 8191, 0, "exceed the limit"),
     (1, 8, 5000, 1, 7, 0, None),
     (1, 8, 4, 1, 7, 2147483645, "overflows"),
 ])
@@ -127,7 +126,7 @@ def test_topk_geometry_errors(rows, cols, top_k, ratio, start, offset, needle):
         M.topk_geometry(rows, cols, top_k, ratio, start, offset)
     assert needle in e.value.message, e.value.message
     # the oracle rejects the reference's own geometry errors alike
-    if rows > 0 and "limit" not in needle and "overflows" not in needle:
+    if rows > 0 and "overflows" not in needle:
         st, _ = O.topk_select(np.zeros((rows, cols), np.float32), top_k, ratio, start, offset)
         assert st == O.INVALID_SHAPE
 
@@ -137,6 +136,23 @@ def test_topk_geometry_counts():
     assert M.topk_geometry(1, 262144, 2048, 4, 1048575, 0) == 2048   # V4 at 1M positions: no key limit
     assert M.topk_geometry(300, 75, 16, 4, 0, 128) == 16
     assert M.topk_geometry(3, 4, 16, 4, 0, 0) == 0   # fewer than ratio tokens: empty rows
+    # any top_k, as `selecting` takes any (DeepSeekV4Attention.swift:582-645)
+    assert M.topk_geometry(1, 8192, 5000, 1, 8191, 0) == 5000
+    assert M.topk_geometry(1, 262144, 100000, 4, 1048575, 0) == 100000
+
+
+def test_topk_workspace_covers_large_selections():
+    # more than 4096 selected keys: slices of 4096 and merge rounds whose
+    # lists double up to top_k; the size grows with top_k and covers what
+    # the small-k paths need for the same rows and columns
+    L = M.load()
+    small = L.mr_topk_workspace_size(1, 262144, 4096)
+    big = L.mr_topk_workspace_size(1, 262144, 16384)
+    assert big > small > 0
+    assert L.mr_topk_workspace_size(1, 262144, 16384) <= L.mr_topk_workspace_size(1, 262144, 262144)
+    # 64 slices of 4096: the first round holds 64 lists of 4096 composites
+    assert big >= 2 * 64 * 4096 * 8
+    assert L.mr_topk_workspace_size(5000, 5000, 4500) >= 2 * 5000 * 2 * 4096 * 8
 
 
 # ---------------------------------------------------------------- lightning-index scores
