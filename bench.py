@@ -595,6 +595,48 @@ def time_projections(torch, M, reps=20):
     return out
 
 
+def time_prefill_block(torch, M, reps=10):
+    """The K3 attention block over a 4096-token prompt in one call
+    (mr_mla_prefill_block, K3MLA.forward with state == nil): hidden 7168, 96
+    heads, q_lora 1536, dense bf16 weights ~N(0, 1/in), gate, NoPE.  The
+    average of `reps` back-to-back calls between two events, and the
+    projections' share of the flops."""
+    import ctypes as C
+
+    g = torch.Generator(device="cuda")
+    g.manual_seed(0x4B33504246)
+    T, Hk, hid, ql = PROJ_T, 96, 7168, 1536
+
+    def dw(o, i):
+        return M.DenseWeights((torch.randn(o, i, generator=g, device="cuda") * i ** -0.5).to(torch.bfloat16))
+
+    w = {"input_norm": None,
+         "q_a_norm": (1 + 0.02 * torch.randn(ql, generator=g, device="cuda")).to(torch.bfloat16),
+         "kv_a_norm": (1 + 0.02 * torch.randn(R, generator=g, device="cuda")).to(torch.bfloat16),
+         "q_a": dw(ql, hid), "q_b": dw(Hk * 192, ql), "kv_a": dw(R + DR, hid), "kv_b": dw(Hk * 256, R),
+         "o_proj": dw(hid, Hk * 128), "g_proj": dw(Hk * 128, hid)}
+    x = torch.randn(T, hid, generator=g, device="cuda").to(torch.bfloat16)
+    cache = torch.zeros(T, R + DR, device="cuda", dtype=torch.bfloat16)
+    out = torch.empty(T, hid, device="cuda", dtype=torch.bfloat16)
+    a, ws = M.prefill_block_args(x, w, cache, 0, None, None, out, q_lora_rank=ql, heads=Hk, nope=128, rope=DR,
+                                 v=128, kv_rank=R)
+    lib = M.load()
+    sp = M._stream(torch.cuda.current_stream())
+    for _ in range(3):
+        M._check(lib.mr_mla_prefill_block(C.byref(a), sp))
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        M._check(lib.mr_mla_prefill_block(C.byref(a), sp))
+    e1.record()
+    torch.cuda.synchronize()
+    us = e0.elapsed_time(e1) / reps * 1e3
+    proj = 2.0 * T * (ql * hid + (R + DR) * hid + Hk * 128 * hid + Hk * 192 * ql + hid * Hk * 128)
+    attn = ATTN_FLOP * Hk / H + UPPROJ_FLOP * Hk / H
+    return {"us": round(us, 1), "projection_tflop": round(proj / 1e12, 3), "attention_tflop": round(attn / 1e12, 3),
+            "tflops": round((proj + attn) / (us * 1e-6) / 1e12, 1), "workspace_mb": round(ws.numel() / 1e6, 1)}
+
+
 def cpu_baseline(torch, budget_s=4.0):
     """The decode layer (H=128, N=32768) on this host's cores.  The value is
     the layer as torch-CPU fp32 BLAS products (the fastest CPU form of the
@@ -690,6 +732,9 @@ def main():
     log(f"bench: projections at T={PROJ_T} (4-bit affine and dense bf16, MFMA)")
     pj = time_projections(torch, M)
     log(f"bench: projections {pj}")
+    log(f"bench: K3 prefill block, {PROJ_T} tokens in one call")
+    pb = time_prefill_block(torch, M)
+    log(f"bench: prefill block {pb}")
     mp = mfma_probe(torch, M)
     log(f"bench: mfma probe {mp}")
 
@@ -737,6 +782,7 @@ def main():
         "gather_8x768x2048_us": round(gx_ms * 1e3, 2),
         "gather_hbm_fraction": round(8 * 768 * (2048 // 2 + 4 * 2048 // 64) / (gx_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
         "projections_t4096": pj,
+        "k3_prefill_block_t4096": pb,
         "mfma_probe_tflops": mp["tflops"],
         "mfma_probe_clock_ghz": mp["clock_ghz"],
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
