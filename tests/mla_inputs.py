@@ -311,3 +311,43 @@ def prefill_block_reference(d, hidden, q_lora_rank, heads, nope, rope, v, kv_ran
         g = _bf(_proj_rows(h, d["g_proj"], acc))
         attn = _bf(O.sigmoid_gate(attn, g))
     return _bf(_proj_rows(attn, d["o_proj"], acc)), rows
+
+
+def prefill_block_reference_rows(d, sel, hidden, q_lora_rank, heads, nope, rope, v, kv_rank, eps=1e-6):
+    """prefill_block_reference (NoPE) for the token rows `sel` only: every
+    token's kv_a row goes into the cache (all of them are keys), but the
+    queries, the attention, the gate and o_proj are formed for `sel`.
+    Returns (out [len(sel), hidden], the T new cache rows)."""
+    f = O.bf16_to_f32
+    pos = d["position"]
+    x = f(d["x"])
+    T = x.shape[0]
+    sel = np.asarray(sel)
+    h = x if d.get("input_norm") is None else _bf(O.rmsnorm(x, f(d["input_norm"]), eps))
+    kv = O.f32_to_bf16(_proj_rows(h, d["kv_a"]))
+    rows = np.empty((T, kv_rank + rope), np.uint16)
+    rows[:, :kv_rank] = O.f32_to_bf16(O.rmsnorm(f(kv[:, :kv_rank]), f(d["kv_a_norm"]), eps))
+    rows[:, kv_rank:] = kv[:, kv_rank:]
+    cache = d["cache"][: pos + T].copy()
+    cache[pos:] = rows
+    hs = h[sel]
+    q_lora = _bf(_proj_rows(hs, d["q_a"]))
+    q_lora_n = _bf(O.rmsnorm(q_lora, f(d["q_a_norm"]), eps))
+    q_sel = O.f32_to_bf16(_proj_rows(q_lora_n, d["q_b"])).reshape(len(sel), heads, nope + rope)
+    q = np.zeros((T, heads, nope + rope), np.uint16)  # only the sampled rows are read
+    q[sel] = q_sel
+    kvb = d["kv_b"]
+    if isinstance(kvb, tuple):
+        kvb = O.f32_to_bf16(O.affine_dequantize(*kvb))
+    kvb = kvb.reshape(heads, nope + v, kv_rank)
+    w_uk = np.ascontiguousarray(kvb[:, :nope, :].transpose(2, 0, 1).reshape(kv_rank, heads * nope))
+    w_uv = np.ascontiguousarray(kvb[:, nope:, :].transpose(2, 0, 1).reshape(kv_rank, heads * v))
+    sel_t = np.repeat(sel.astype(np.int32), heads)
+    sel_h = np.tile(np.arange(heads, dtype=np.int32), len(sel))
+    attn = O.mla_prefill_rows(q, cache, w_uk, w_uv, sel_t, sel_h, kv_rank=kv_rank, rope_dim=rope, nope_dim=nope,
+                              v_dim=v, scale=(nope + rope) ** -0.5, round_kv=True, threads=16)
+    attn = _bf(attn).reshape(len(sel), heads * v)
+    if d.get("g_proj") is not None:
+        g = _bf(_proj_rows(hs, d["g_proj"]))
+        attn = _bf(O.sigmoid_gate(attn, g))
+    return _bf(_proj_rows(attn, d["o_proj"])), rows

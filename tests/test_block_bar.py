@@ -82,3 +82,14 @@ def test_prefill_block_reference_is_causal():
     d_alt["x"][3] = d["x"][4]
     alt, _ = MI.prefill_block_reference(d_alt, rotary=True, **PB_DIMS)
     assert np.array_equal(alt[:3], full[:3]) and not np.array_equal(alt[5:], full[5:])
+
+
+def test_prefill_block_sampled_rows_equal_full_reference():
+    # the sampled-row form used at 4096 tokens gives the full composition's
+    # rows bit for bit
+    d = MI.prefill_block_inputs(30, 0, "pbsr", **PB_DIMS)
+    full, rows = MI.prefill_block_reference(d, **PB_DIMS)
+    sel = [0, 7, 29]
+    part, rows2 = MI.prefill_block_reference_rows(d, sel, **PB_DIMS)
+    np.testing.assert_array_equal(rows2, rows)
+    np.testing.assert_array_equal(part, full[sel])

@@ -107,6 +107,30 @@ def test_k3_dense_gated_nope(M, T, position):
     check_prefill_block(M, d, K3, False, f"prefill-block-k3-{T}-{position}")
 
 
+def test_k3_4096_tokens_sampled_rows(M):
+    # the K3 block over a whole 4096-token prompt (the prefill workload's
+    # length): every cache row, and the outputs of sampled token rows (both
+    # ends, tile boundaries, a few seeded ones) over all 7168 columns
+    T = 4096
+    print(f"prefill block K3 T={T} sampled rows", flush=True)
+    d = MI.prefill_block_inputs(T, 0, "pbk3full", **K3)
+    out, cache = run_prefill_block(M, d, K3, False)
+    rng = np.random.default_rng(4096)
+    sel = np.array(sorted({0, 1, 63, 64, 127, 128, 255, 256, 2047, 4095} | set(int(r) for r in rng.integers(0, T, 4))))
+    ref, rows = MI.prefill_block_reference_rows(d, sel, **K3)
+    R = K3["kv_rank"]
+    for cols in (slice(0, R), slice(R, None)):  # latents; the shared keys (NoPE: kv_a's outputs as they are)
+        g, r = O.bf16_to_f32(bits16(cache)[:, cols]), O.bf16_to_f32(rows[:, cols])
+        assert np.all(np.abs(g - r) <= 2 ** -7 * np.abs(r) + 2 ** -9 * np.abs(r).max(axis=1, keepdims=True))
+    got = f32(out)[sel]
+    ok, maxerr, scale_err = MI.within_block_tolerance(got, ref)
+    n_hip = misses(got, ref)
+    print(f"prefill-block-k3-4096: max|ref|={np.abs(ref).max():.3e} max|d|={maxerr:.3e} scale_err={scale_err:.3e}; "
+          f"outside the workload bar: {n_hip} of {ref.size}", flush=True)
+    assert ok, (maxerr, scale_err)
+    assert n_hip == 0, n_hip
+
+
 def test_affine_rotary_input_norm(M):
     # 4-bit affine projections (128 heads), an input norm, rotary query and
     # keys at positions 37..100, no gate
