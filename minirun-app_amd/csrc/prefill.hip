@@ -396,33 +396,44 @@ __global__ void __launch_bounds__(256, 2) prefill_attn_kernel(PrefillAttnParams 
 #pragma unroll
             for (int d = 0; d < 4; ++d) o[d] *= alpha;
         }
-        float ls = 0.f;
+        // four partial sums, so the additions are not one serial chain
+        float ls[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
             for (int i = 0; i < 16; ++i) {
                 const float e = __builtin_amdgcn_exp2f(fmaf(s[kb][i], p.scale_log2, -m_run));
                 s[kb][i] = e;
-                ls += e;
+                ls[i & 3] += e;
             }
-        l_part += ls;
+        l_part += (ls[0] + ls[1]) + (ls[2] + ls[3]);
 
-        // O^T += V^T . P^T: k-step t covers tile keys 16t .. 16t+15
+        // O^T += V^T . P^T: k-step t covers tile keys 16t .. 16t+15.  The
+        // transposed V reads of step t + 1 go out before step t's products
+        // (two fragment sets), so no product waits for its own reads.
         __builtin_amdgcn_s_setprio(1);
-#pragma unroll
-        for (int t = 0; t < 4; ++t) {
-            const int kb = t >> 1, base = 8 * (t & 1);
-            bf16x8 pb;
-#pragma unroll
-            for (int e = 0; e < 8; ++e) pb[e] = (__bf16)s[kb][base + e];
+        bf16x8 va[2][4];
+        auto vread = [&](int t, bf16x8(&a)[4]) {
 #pragma unroll
             for (int db = 0; db < 4; ++db) {
                 const int d = 32 * db + tr_d;
                 const bf16x4 lo = ds_read_tr16(vt + v_off(16 * t + tr_key, d));
                 const bf16x4 hi = ds_read_tr16(vt + v_off(16 * t + 8 + tr_key, d));
-                const bf16x8 a = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-                o[db] = mfma32(a, pb, o[db]);
+                a[db] = bf16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
             }
+        };
+        vread(0, va[0]);
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            if (t + 1 < 4) vread(t + 1, va[(t + 1) & 1]);
+            __builtin_amdgcn_sched_barrier(0);
+            const int kb = t >> 1, base = 8 * (t & 1);
+            bf16x8 pb;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) pb[e] = (__bf16)s[kb][base + e];
+#pragma unroll
+            for (int db = 0; db < 4; ++db) o[db] = mfma32(va[t & 1][db], pb, o[db]);
+            __builtin_amdgcn_sched_barrier(0);
         }
         __builtin_amdgcn_s_setprio(0);
     };
