@@ -62,6 +62,30 @@ int main(void) {
     EXPECT(mr_mla_decode(&a, NULL) == MR_INVALID_ARGUMENT);
     EXPECT(mr_mla_decode(NULL, NULL) == MR_INVALID_ARGUMENT);
 
+    /* the prefill block: workspace geometry, then shape and pointer checks */
+    mr_mla_prefill_block_args pb;
+    memset(&pb, 0, sizeof pb);
+    EXPECT(mr_mla_prefill_block_workspace_size(NULL) == 0);
+    EXPECT(mr_mla_prefill_block_workspace_size(&pb) == 0); /* no tokens */
+    pb.tokens = 64;
+    pb.hidden = 256;
+    pb.q_lora_rank = 64;
+    pb.heads = 4;
+    pb.qk_nope_dim = 32;
+    pb.qk_rope_dim = 16;
+    pb.v_head_dim = 32;
+    pb.kv_rank = 64;
+    pb.capacity = 64;
+    EXPECT(mr_mla_prefill_block_workspace_size(&pb) > 0);
+    EXPECT(mr_mla_prefill_block(&pb, NULL) == MR_INVALID_ARGUMENT); /* no pointers */
+    EXPECT(strstr(mr_get_last_error(), "NULL") != NULL);
+    pb.capacity = 63; /* rows 0 .. 63 do not fit */
+    EXPECT(mr_mla_prefill_block(&pb, NULL) == MR_INVALID_SHAPE);
+    pb.capacity = 64;
+    pb.qk_rope_dim = 15;
+    EXPECT(mr_mla_prefill_block(&pb, NULL) == MR_INVALID_SHAPE);
+    EXPECT(mr_mla_prefill_block(NULL, NULL) == MR_INVALID_ARGUMENT);
+
     if (failures) return 1;
     printf("abi_from_c: ok\n");
     return 0;
