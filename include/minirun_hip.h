@@ -16,7 +16,8 @@
  *  - Functions return mr_status and never abort.  mr_get_last_error() gives a
  *    message for the last non-OK status on the calling thread.
  *  - No entry point allocates device memory: scratch comes in as a
- *    caller-provided workspace whose size a *_workspace_size function states.
+ *    caller-provided workspace whose size a *_workspace_size function states
+ *    (0 for arguments whose widths or counts the entry point rejects).
  */
 #ifndef MINIRUN_HIP_H
 #define MINIRUN_HIP_H

@@ -825,7 +825,9 @@ bool block_layout(const mr_mla_block_args* a, BlockLayout* L) {
 }  // namespace
 
 size_t mr_mla_decode_block_workspace_size(const mr_mla_block_args* a) {
-    if (!a || a->heads <= 0 || a->position < 0) return 0;
+    if (!a || a->hidden <= 0 || a->q_lora_rank <= 0 || a->heads <= 0 || a->qk_nope_dim < 0 || a->qk_rope_dim < 0 ||
+        a->v_head_dim <= 0 || a->kv_rank <= 0 || a->position < 0)
+        return 0;
     BlockLayout L;
     block_layout(a, &L);
     return L.total;
@@ -1163,7 +1165,9 @@ mr_status check_prefill_block(const mr_mla_prefill_block_args* a) {
 }  // namespace
 
 size_t mr_mla_prefill_block_workspace_size(const mr_mla_prefill_block_args* a) {
-    if (!a || a->tokens <= 0 || a->heads <= 0 || a->position < 0) return 0;
+    if (!a || a->tokens <= 0 || a->hidden <= 0 || a->q_lora_rank <= 0 || a->heads <= 0 || a->qk_nope_dim < 0 ||
+        a->qk_rope_dim < 0 || a->v_head_dim <= 0 || a->kv_rank <= 0 || a->position < 0)
+        return 0;
     PrefillBlockLayout L;
     prefill_block_layout(a, &L);
     return L.total;

@@ -97,7 +97,7 @@ mr_status mrc::check_prefill(const mr_mla_prefill_args* a) {
 extern "C" {
 
 size_t mr_mla_prefill_workspace_size(const mr_mla_prefill_args* a) {
-    if (!a || a->n_ctx <= 0 || a->heads <= 0) return 0;
+    if (!a || a->n_ctx <= 0 || a->heads <= 0 || a->qk_nope_dim < 0 || a->v_head_dim <= 0) return 0;
     return kv_bytes(a);
 }
 

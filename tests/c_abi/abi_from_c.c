@@ -77,6 +77,9 @@ int main(void) {
     pb.kv_rank = 64;
     pb.capacity = 64;
     EXPECT(mr_mla_prefill_block_workspace_size(&pb) > 0);
+    pb.kv_rank = -64; /* a width the call rejects: no size */
+    EXPECT(mr_mla_prefill_block_workspace_size(&pb) == 0);
+    pb.kv_rank = 64;
     EXPECT(mr_mla_prefill_block(&pb, NULL) == MR_INVALID_ARGUMENT); /* no pointers */
     EXPECT(strstr(mr_get_last_error(), "NULL") != NULL);
     pb.capacity = 63; /* rows 0 .. 63 do not fit */
