@@ -167,6 +167,36 @@ def test_prompt_in_one_call_equals_two_chunks(M):
     np.testing.assert_array_equal(np.concatenate([bits16(out1), bits16(out2)]), bits16(out_all))
 
 
+def test_one_token_prompt_equals_decode_block(M):
+    """A one-token prompt after 4095 cached rows (K3's block: dense, gated,
+    NoPE, 96 heads) through the prefill block (expanded keys and values,
+    the fixed-width prefill kernels) and through the decode block (absorbed
+    queries, the split decode): the two HIP paths of the same K3MLA.forward
+    step write the same cache row (within one bf16 ulp: the projections'
+    GEMV launches differ) and outputs within the block bar of each other."""
+    import torch
+
+    position = 4095
+    print(f"one-token prompt vs decode block, K3, position {position}", flush=True)
+    d = MI.prefill_block_inputs(1, position, "pb1tok", **K3)
+    out_p, cache_p = run_prefill_block(M, d, K3, False)
+    w = {k: (dev(d[k]) if d.get(k) is not None else None) for k in ("input_norm", "q_a_norm", "kv_a_norm")}
+    for k in ("q_a", "q_b", "kv_a", "kv_b", "o_proj", "g_proj"):
+        w[k] = projection(M, d.get(k))
+    cache_d = dev(d["cache"])
+    kw = {k: K3[k] for k in ("hidden", "q_lora_rank", "heads", "nope", "rope", "v", "kv_rank")}
+    out_d = M.mla_decode_block(dev(d["x"][0]), w, cache_d, position, None, None, **kw)
+    sync()
+    rp, rd = bits16(cache_p)[position].astype(np.int32), bits16(cache_d)[position].astype(np.int32)
+    print(f"cache row: largest difference {np.abs(rp - rd).max()} bf16 ulps", flush=True)
+    assert np.abs(rp - rd).max() <= 1
+    np.testing.assert_array_equal(bits16(cache_p)[:position], bits16(cache_d)[:position])
+    got, ref = f32(out_p)[0], f32(out_d)
+    ok, maxerr, scale_err = MI.within_block_tolerance(got, ref)
+    print(f"prefill vs decode block: max|d|={maxerr:.3e} scale_err={scale_err:.3e}", flush=True)
+    assert ok, (maxerr, scale_err)
+
+
 def test_failed_checks_leave_the_cache(M):
     # a call that fails its checks writes nothing
     import torch
