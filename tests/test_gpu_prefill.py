@@ -122,3 +122,20 @@ def test_prefill_4096_tokens_128_heads_sampled(M):
     st, sh = t.ravel().astype(np.int32), h.ravel().astype(np.int32)
     ref = O.mla_prefill_rows(q, cache, w_uk, w_uv, st, sh, round_kv=True)
     check_rows(got[st, sh], ref, "prefill-4096x128")
+
+
+def test_prefill_long_prefix_ragged_heads_sampled(M):
+    # 2048 queries after a 5000-row cached prefix (query i at position
+    # 5000 + i: key tiles and query tiles out of step), 100 heads (not a
+    # multiple of the 8 XCDs: the plain work order)
+    T, P, H = 2048, 7048, 100
+    print(f"prefill T={T} P={P} H={H}", flush=True)
+    q, cache, w_uk, w_uv, kv_b = prefill_inputs(T, P, H, "c3p")
+    got = run(M, q, cache, kv_b)
+    assert np.isfinite(got).all()
+    rows = np.array([0, 1, 23, 24, 63, 64, 127, 128, 255, 256, 1111, 2046, 2047])
+    heads = np.array([0, 3, 50, 99])
+    t, h = np.meshgrid(rows, heads, indexing="ij")
+    st, sh = t.ravel().astype(np.int32), h.ravel().astype(np.int32)
+    ref = O.mla_prefill_rows(q, cache, w_uk, w_uv, st, sh, round_kv=True)
+    check_rows(got[st, sh], ref, "prefill-2048+5000x100")
