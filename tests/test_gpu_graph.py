@@ -1,5 +1,5 @@
-"""The decode path inside a captured HIP graph (torch.cuda.CUDAGraph), as a
-serving loop captures one decode step and replays it.  The entry points
+"""The decode and prefill entry points inside a captured HIP graph (torch.cuda.CUDAGraph), as a
+serving loop captures one step and replays it.  The entry points
 below enqueue only kernels on the caller's stream (no memset, no host sync,
 no allocation), so they can be captured; every replay must equal the eager
 call bit for bit, with eager work of the program's own and synchronisations
@@ -7,7 +7,8 @@ between the replays.  Cases: the dense decode (H=128, N=32768) on a caller
 workspace; the same through mr_mla_decode_noalloc (the library's static
 scratch, the form for callers that cannot allocate); the gathered decode
 with the device-side index status (B=4, K=2048 of 131072 rows); the K3
-decode block (dense projections, output gate, 96 heads)."""
+decode block (dense projections, output gate, 96 heads); the K3 prefill
+block over a 64-token chunk."""
 import ctypes as C
 
 import numpy as np
@@ -157,3 +158,35 @@ def test_k3_block_replays(M):
     g = capture(call)
     replay_and_compare(M, g, out, eager, "K3 decode block")
     assert torch.equal(cache[d["position"]].view(torch.int16), row.view(torch.int16))
+
+
+def test_k3_prefill_block_replays(M):
+    # a 64-token chunk after 100 cached rows (projections on MFMA tiles,
+    # attention with the gate in its stores); the cache rows it appends are
+    # the same on every replay
+    import torch
+
+    dims = dict(MI.K3_DIMS)
+    T, position = 64, 100
+    print(f"graph: K3 prefill block, {T} tokens after {position} rows", flush=True)
+    d = MI.prefill_block_inputs(T, position, "graph.pb", **dims)
+    w = {k: (dev(d[k]) if d.get(k) is not None else None) for k in ("input_norm", "q_a_norm", "kv_a_norm")}
+    for k in ("q_a", "q_b", "kv_a", "kv_b", "o_proj", "g_proj"):
+        w[k] = projection(M, d.get(k))
+    cache = dev(d["cache"])
+    x = dev(d["x"])
+    out = torch.empty(T, dims["hidden"], dtype=torch.bfloat16, device="cuda")
+    kw = {k: dims[k] for k in ("q_lora_rank", "heads", "nope", "rope", "v", "kv_rank")}
+    a, ws = M.prefill_block_args(x, w, cache, position, None, None, out, **kw)
+    lib = M.load()
+
+    def call():
+        assert lib.mr_mla_prefill_block(C.byref(a), M._stream(None)) == M.OK, M.last_error()
+
+    call()
+    torch.cuda.synchronize()
+    eager = out.clone()
+    rows = cache[position:].clone()
+    g = capture(call)
+    replay_and_compare(M, g, out, eager, "K3 prefill block")
+    assert torch.equal(cache[position:].view(torch.int16), rows.view(torch.int16))
