@@ -83,13 +83,31 @@ struct DecodePlan {
     size_t o_bytes, ml_bytes, table_bytes, total;
 };
 
+// 0 for counts the checks refuse, and for tables of WS_LIMIT bytes or more
 size_t validate_ws_bytes(int32_t batch, int32_t n_idx) {
-    return align256(size_t(std::max(batch, 0)) * 3 * sizeof(int32_t)) +
-           align256(mr::validate_table_bytes(std::max(batch, 0), std::max(n_idx, 0)));
+    if (batch <= 0 || n_idx < 0 || n_idx > mr::validate_max_indices()) return 0;
+    const size_t total = align256(size_t(batch) * 3 * sizeof(int32_t)) + align256(mr::validate_table_bytes(batch, n_idx));
+    return total < mrc::WS_LIMIT ? total : 0;
 }
 
 // the widths the split kernel takes; others run the any-width kernel
 bool decode_fast_dims(const mr_mla_decode_args* a) { return a->kv_rank == 512 && (a->rope_dim == 64 || a->rope_dim == 0); }
+
+// the counts and widths both kernels accept (the checks below refuse the
+// rest): the workspace sizes are reported for these only, and stay far
+// below 2^56 for them
+bool decode_counts_ok(const mr_mla_decode_args* a) {
+    if (a->batch <= 0 || a->heads <= 0 || int64_t(a->batch) * (int64_t(a->heads) + 63) > INT32_MAX) return false;
+    if (a->kv_rank <= 0 || a->kv_rank > mr::ANY_MAX_RANK || a->rope_dim < 0 || a->rope_dim > mr::ANY_MAX_ROPE)
+        return false;
+    if (a->n_ctx <= 0) return false;
+    if (!a->indices) return true;
+    if (a->n_idx < 0) return false;
+    if (!(a->flags & MR_DECODE_UNCHECKED) &&
+        (a->n_idx > mr::validate_max_indices() || validate_ws_bytes(a->batch, a->n_idx) == 0))
+        return false;
+    return !decode_fast_dims(a) || int64_t(a->n_idx) <= int64_t(mr::MAX_GATHER_ROWS) * mr::MAX_COMBINE_SPLITS;
+}
 
 DecodePlan plan_decode(const mr_mla_decode_args* a) {
     DecodePlan pl{};
@@ -199,6 +217,13 @@ mr_status check_decode(const mr_mla_decode_args* a) {
     if (a->kv_rank <= 0 || a->kv_rank > mr::ANY_MAX_RANK || a->rope_dim < 0 || a->rope_dim > mr::ANY_MAX_ROPE)
         return fail(MR_INVALID_SHAPE, "mla decode: kv_rank %d must be in [1, %d] and rope_dim %d in [0, %d]", a->kv_rank,
                     mr::ANY_MAX_RANK, a->rope_dim, mr::ANY_MAX_ROPE);
+    // head counts padded to whole head groups (64) stay in 32 bits
+    if (int64_t(a->batch) * (int64_t(a->heads) + 63) > INT32_MAX)
+        return fail(MR_INVALID_SHAPE, "mla decode: batch %d * heads %d too large", a->batch, a->heads);
+    if (a->indices && !(a->flags & MR_DECODE_UNCHECKED) && a->n_idx >= 0 && a->n_idx <= mr::validate_max_indices() &&
+        validate_ws_bytes(a->batch, a->n_idx) == 0)
+        return fail(MR_INVALID_SHAPE, "mla decode: index check tables for batch %d x %d entries overflow a workspace",
+                    a->batch, a->n_idx);
     if (!decode_fast_dims(a)) return check_decode_any(a);
     if (!(std::isfinite(a->scale) && a->scale > 0))
         return fail(MR_INVALID_SHAPE, "sparse attention queries, shared KV, sinks, indices, or scale are invalid: "
@@ -303,7 +328,7 @@ const char* mr_version(void) { return "minirun-hip 0.1.0 gfx950"; }
 const char* mr_get_last_error(void) { return g_last_error.c_str(); }
 
 size_t mr_mla_decode_workspace_size(const mr_mla_decode_args* args) {
-    if (!args) return 0;
+    if (!args || !decode_counts_ok(args)) return 0;
     return plan_decode(args).total;
 }
 
@@ -319,6 +344,8 @@ mr_status mr_validate_indices(const int32_t* indices, int32_t batch, int32_t n_i
     if (n_idx == 0) return MR_OK;
     if (n_idx > mr::validate_max_indices())
         return fail(MR_INVALID_SHAPE, "index validation: n_idx %d exceeds %d", n_idx, mr::validate_max_indices());
+    if (mr_validate_indices_workspace_size(batch, n_idx) == 0)
+        return fail(MR_INVALID_SHAPE, "index validation: the tables of %d x %d entries overflow a workspace", batch, n_idx);
     if (!indices || !workspace) return fail(MR_INVALID_ARGUMENT, "index validation: NULL indices or workspace");
     if (workspace_bytes < mr_validate_indices_workspace_size(batch, n_idx))
         return fail(MR_WORKSPACE_TOO_SMALL, "index validation: workspace %zu bytes < %zu", workspace_bytes,

@@ -17,6 +17,9 @@ using mrc::align256;
 using mrc::dtype_name;
 using mrc::fail;
 using mrc::hip_fail;
+using mrc::WS_LIMIT;
+using mrc::ws_add;
+using mrc::ws_mul;
 
 namespace {
 
@@ -785,22 +788,25 @@ bool block_layout(const mr_mla_block_args* a, BlockLayout* L) {
     size_t off = 0;
     auto take = [&](size_t bytes) {
         const size_t at = off;
-        off += align256(bytes);
+        off = ws_add(off, align256(bytes));
         return at;
     };
-    const int dq = a->qk_nope_dim + a->qk_rope_dim;
-    const size_t hv = size_t(a->heads) * a->v_head_dim;
-    L->h = take(size_t(a->hidden) * 2);
-    L->h_kv = take(size_t(a->hidden) * 2);  // the key path's (and the gate's) normed x
-    L->q_lora = take(size_t(a->q_lora_rank) * 2);
-    L->q_lora_n = take(size_t(a->q_lora_rank) * 2);
-    L->q = take(size_t(a->heads) * dq * 2);
-    L->q_lat = take(size_t(a->heads) * a->kv_rank * 2);
-    L->kv = take(size_t(a->kv_rank + a->qk_rope_dim) * 2);
-    L->ctx = take(size_t(a->heads) * a->kv_rank * 2);
-    L->attn = take(hv * 2);
-    L->gate = take(hv * 2);
-    L->stage = take(hv * 2);  // the gated o_proj input when the gate is its own stage
+    auto dim = [](int64_t v) { return size_t(std::max<int64_t>(v, 0)); };
+    const size_t dq = dim(int64_t(a->qk_nope_dim) + a->qk_rope_dim);
+    const size_t H = dim(a->heads);
+    const size_t hv = ws_mul(H, dim(a->v_head_dim));
+    L->h = take(ws_mul(dim(a->hidden), 2));
+    L->h_kv = take(ws_mul(dim(a->hidden), 2));  // the key path's (and the gate's) normed x
+    L->q_lora = take(ws_mul(dim(a->q_lora_rank), 2));
+    L->q_lora_n = take(ws_mul(dim(a->q_lora_rank), 2));
+    L->q = take(ws_mul(ws_mul(H, dq), 2));
+    L->q_lat = take(ws_mul(ws_mul(H, dim(a->kv_rank)), 2));
+    L->kv = take(ws_mul(dim(int64_t(a->kv_rank) + a->qk_rope_dim), 2));
+    L->ctx = take(ws_mul(ws_mul(H, dim(a->kv_rank)), 2));
+    L->attn = take(ws_mul(hv, 2));
+    L->gate = take(ws_mul(hv, 2));
+    L->stage = take(ws_mul(hv, 2));  // the gated o_proj input when the gate is its own stage
+    const int dqi = int(std::min<size_t>(dq, INT32_MAX));
     mr_mla_decode_args& d = L->dec_args;
     d = mr_mla_decode_args{};
     d.batch = 1;
@@ -810,7 +816,7 @@ bool block_layout(const mr_mla_block_args* a, BlockLayout* L) {
     d.rope_dim = a->qk_rope_dim;
     d.scale = a->scale;
     d.q_lat_head_stride = a->kv_rank;
-    d.q_rope_head_stride = dq;
+    d.q_rope_head_stride = dqi;
     d.latent_row_stride = a->latent_row_stride;
     d.rope_row_stride = a->rope_row_stride;
     d.out_dtype = MR_BF16;
@@ -830,7 +836,7 @@ size_t mr_mla_decode_block_workspace_size(const mr_mla_block_args* a) {
         return 0;
     BlockLayout L;
     block_layout(a, &L);
-    return L.total;
+    return L.total < WS_LIMIT ? L.total : 0;
 }
 
 mr_status mr_mla_decode_block(const mr_mla_block_args* a, void* stream) {
@@ -874,6 +880,7 @@ mr_status mr_mla_decode_block(const mr_mla_block_args* a, void* stream) {
         return fail(MR_INVALID_SHAPE, "mla block: nope dim %d exceeds 1024", a->qk_nope_dim);
     BlockLayout L;
     block_layout(a, &L);
+    if (L.total >= WS_LIMIT) return fail(MR_INVALID_SHAPE, "mla block: the workspace these widths need overflows");
     if (a->workspace_bytes < L.total)
         return fail(MR_WORKSPACE_TOO_SMALL, "mla block: workspace %zu bytes < %zu", a->workspace_bytes, L.total);
     if (!aligned16(a->workspace)) return fail(MR_INVALID_ARGUMENT, "mla block: workspace must be 16-byte aligned");
@@ -1051,21 +1058,23 @@ void prefill_block_layout(const mr_mla_prefill_block_args* a, PrefillBlockLayout
     size_t off = 0;
     auto take = [&](size_t bytes) {
         const size_t at = off;
-        off += align256(bytes);
+        off = ws_add(off, align256(bytes));
         return at;
     };
-    const size_t T = size_t(a->tokens);
-    const int dq = a->qk_nope_dim + a->qk_rope_dim;
-    const size_t hv = size_t(a->heads) * a->v_head_dim;
-    L->h = take(a->input_norm_w ? T * a->hidden * 2 : 0);
-    L->q_lora = take(T * a->q_lora_rank * 2);
-    L->q_lora_n = take(T * a->q_lora_rank * 2);
-    L->q = take(T * a->heads * dq * 2);
-    L->kv = take(T * (a->kv_rank + a->qk_rope_dim) * 2);
-    L->gate = take(a->g_proj.kind != MR_PROJ_NONE ? T * hv * 2 : 0);
-    L->attn = take(T * hv * 2);
-    L->kv_b = take(a->kv_b.kind == MR_PROJ_AFFINE ? size_t(a->heads) * (a->qk_nope_dim + a->v_head_dim) * a->kv_rank * 2
-                                                  : 0);
+    auto dim = [](int64_t v) { return size_t(std::max<int64_t>(v, 0)); };
+    const size_t T = dim(a->tokens), H = dim(a->heads);
+    const int dq = int(std::min<int64_t>(std::max<int64_t>(int64_t(a->qk_nope_dim) + a->qk_rope_dim, 0), INT32_MAX));
+    const size_t hv = ws_mul(H, dim(a->v_head_dim));
+    L->h = take(a->input_norm_w ? ws_mul(ws_mul(T, dim(a->hidden)), 2) : 0);
+    L->q_lora = take(ws_mul(ws_mul(T, dim(a->q_lora_rank)), 2));
+    L->q_lora_n = take(ws_mul(ws_mul(T, dim(a->q_lora_rank)), 2));
+    L->q = take(ws_mul(ws_mul(ws_mul(T, H), size_t(dq)), 2));
+    L->kv = take(ws_mul(ws_mul(T, dim(int64_t(a->kv_rank) + a->qk_rope_dim)), 2));
+    L->gate = take(a->g_proj.kind != MR_PROJ_NONE ? ws_mul(ws_mul(T, hv), 2) : 0);
+    L->attn = take(ws_mul(ws_mul(T, hv), 2));
+    L->kv_b = take(a->kv_b.kind == MR_PROJ_AFFINE
+                       ? ws_mul(ws_mul(ws_mul(H, dim(int64_t(a->qk_nope_dim) + a->v_head_dim)), dim(a->kv_rank)), 2)
+                       : 0);
     mr_mla_prefill_args& p = L->pre_args;
     p = mr_mla_prefill_args{};
     p.tokens = a->tokens;
@@ -1155,6 +1164,8 @@ mr_status check_prefill_block(const mr_mla_prefill_block_args* a) {
         return fail(MR_INVALID_SHAPE, "mla prefill block: position + tokens exceeds int32");
     mr_status st = mrc::check_prefill(&p);
     if (st != MR_OK) return st;
+    if (L.total >= WS_LIMIT)
+        return fail(MR_INVALID_SHAPE, "mla prefill block: the workspace these widths need overflows");
     if (a->workspace_bytes < L.total)
         return fail(MR_WORKSPACE_TOO_SMALL, "mla prefill block: workspace %zu bytes < %zu", a->workspace_bytes, L.total);
     if (!aligned16(a->workspace))
@@ -1170,7 +1181,7 @@ size_t mr_mla_prefill_block_workspace_size(const mr_mla_prefill_block_args* a) {
         return 0;
     PrefillBlockLayout L;
     prefill_block_layout(a, &L);
-    return L.total;
+    return L.total < WS_LIMIT ? L.total : 0;
 }
 
 mr_status mr_mla_prefill_block(const mr_mla_prefill_block_args* a, void* stream) {

@@ -21,7 +21,8 @@ bool prefill_fast_dims(const mr_mla_prefill_args* a) {
 
 size_t kv_bytes(const mr_mla_prefill_args* a) {
     if (!prefill_fast_dims(a))  // fp32 keys and values, [heads][n_ctx][nope + v]
-        return align256(size_t(a->n_ctx) * size_t(a->heads) * size_t(std::max(a->qk_nope_dim + a->v_head_dim, 0)) * 4);
+        return align256(size_t(a->n_ctx) * size_t(a->heads) *
+                        size_t(std::max<int64_t>(int64_t(a->qk_nope_dim) + a->v_head_dim, 0)) * 4);
     return align256(size_t(a->n_ctx) * size_t(a->heads) * 256 * 2);
 }
 
@@ -97,7 +98,13 @@ mr_status mrc::check_prefill(const mr_mla_prefill_args* a) {
 extern "C" {
 
 size_t mr_mla_prefill_workspace_size(const mr_mla_prefill_args* a) {
-    if (!a || a->n_ctx <= 0 || a->heads <= 0 || a->qk_nope_dim < 0 || a->v_head_dim <= 0) return 0;
+    // 0 for the widths and counts the call refuses (check_prefill_any's
+    // limits; the fixed widths are inside them)
+    if (!a || a->n_ctx <= 0 || a->heads <= 0 || a->kv_rank <= 0 || a->kv_rank > mr::ANY_MAX_RANK ||
+        a->qk_nope_dim < 0 || a->qk_nope_dim > mr::ANY_MAX_NOPE || a->qk_rope_dim < 0 ||
+        a->qk_rope_dim > mr::ANY_MAX_ROPE || a->v_head_dim <= 0 || a->v_head_dim > mr::ANY_MAX_RANK ||
+        int64_t(a->n_ctx) * a->heads > INT32_MAX)
+        return 0;
     return kv_bytes(a);
 }
 

@@ -3,6 +3,7 @@
 
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cstdint>
 
 #include "../../include/minirun_hip.h"
@@ -14,6 +15,15 @@ mr_status hip_fail(hipError_t e, const char* what);
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 inline bool aligned4(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 3u) == 0; }
 inline size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
+
+// Workspace arithmetic that cannot wrap: products and sums saturate at
+// WS_LIMIT, a size no workspace reaches (64 PiB); a layout that reaches it
+// is refused, and its *_workspace_size reports 0.
+constexpr size_t WS_LIMIT = size_t(1) << 56;
+inline size_t ws_mul(size_t a, size_t b) { return (b && a > WS_LIMIT / b) ? WS_LIMIT : std::min(a * b, WS_LIMIT); }
+inline size_t ws_add(size_t a, size_t b) {
+    return std::min(a, WS_LIMIT) + std::min(b, WS_LIMIT) >= WS_LIMIT ? WS_LIMIT : a + b;
+}
 const char* dtype_name(mr_dtype d);
 int cu_count();  // compute units of the current device (cached per device)
 

@@ -1,0 +1,137 @@
+"""Argument checks of the C-ABI under random arguments (hypothesis), on the
+host: with every device pointer NULL no call reaches a GPU call, so each
+must come back with a status (never a crash, never MR_OK with work left
+undone) and, when refused, with a message; the workspace-size functions
+never wrap (0 for widths a call rejects, else a size below 2^56).  Shapes
+range over zero, negative and very large values, scales over non-finite
+ones."""
+import ctypes as C
+import math
+
+import pytest
+from hypothesis import HealthCheck, given, settings
+from hypothesis import strategies as st
+
+import minirun_hip as M
+
+REFUSED = {M.INVALID_SHAPE, M.INVALID_ARGUMENT, M.INVALID_DTYPE, M.WORKSPACE_TOO_SMALL}
+SETTINGS = settings(max_examples=300, deadline=None, suppress_health_check=[HealthCheck.too_slow])
+
+dim = st.one_of(st.integers(-5, 4200), st.sampled_from([0, 1, 16, 64, 96, 128, 512, 576, 2 ** 31 - 1, -2 ** 31]))
+big = st.one_of(st.integers(-3, 300000), st.sampled_from([0, 1, 32768, 131072, 2 ** 31 - 1, -2 ** 31]))
+stride = st.one_of(st.integers(-10, 5000), st.sampled_from([0, 576, 2 ** 40, -(2 ** 40)]))
+scale = st.one_of(st.floats(allow_nan=True, allow_infinity=True, width=32), st.sampled_from([0.0722, -1.0, 0.0]))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    return M.load()
+
+
+def refused(status):
+    assert status in REFUSED, status
+    assert M.last_error(), "a refused call leaves a message"
+
+
+@SETTINGS
+@given(batch=dim, heads=dim, n_ctx=big, kv_rank=dim, rope=dim, sc=scale, ls=stride, out_dtype=st.integers(-1, 6),
+       n_idx=big, flags=st.integers(0, 15), gathered=st.booleans(), splits=big)
+def test_decode_checks(lib, batch, heads, n_ctx, kv_rank, rope, sc, ls, out_dtype, n_idx, flags, gathered, splits):
+    a = M.DecodeArgs()
+    a.batch, a.heads, a.n_ctx, a.kv_rank, a.rope_dim, a.scale = batch, heads, n_ctx, kv_rank, rope, sc
+    a.latent_row_stride = a.rope_row_stride = ls
+    a.q_lat_head_stride = a.q_rope_head_stride = a.out_head_stride = ls
+    a.out_dtype, a.n_idx, a.flags, a.num_splits = out_dtype, n_idx, flags, splits
+    if gathered:
+        # a placeholder address: the NULL queries are refused before any
+        # pointer is read, and the size functions read none
+        a.indices = C.c_void_p(256)
+    size = lib.mr_mla_decode_workspace_size(C.byref(a))
+    assert 0 <= size < 2 ** 56
+    if batch <= 0 or heads <= 0 or n_ctx <= 0 or (gathered and n_idx < 0):
+        assert size == 0
+    for entry in (lib.mr_mla_decode, lib.mr_mla_decode_noalloc):
+        refused(entry(C.byref(a), None))
+
+
+@SETTINGS
+@given(tokens=dim, n_ctx=big, heads=dim, nope=dim, rope=dim, v=dim, kv_rank=dim, sc=scale, qs=stride,
+       out_dtype=st.integers(-1, 6))
+def test_prefill_checks(lib, tokens, n_ctx, heads, nope, rope, v, kv_rank, sc, qs, out_dtype):
+    a = M.PrefillArgs()
+    a.tokens, a.n_ctx, a.heads = tokens, n_ctx, heads
+    a.qk_nope_dim, a.qk_rope_dim, a.v_head_dim, a.kv_rank = nope, rope, v, kv_rank
+    a.scale = sc
+    a.q_token_stride = a.q_head_stride = a.latent_row_stride = a.rope_row_stride = qs
+    a.kv_b_row_stride = a.out_token_stride = a.out_head_stride = qs
+    a.out_dtype = out_dtype
+    size = lib.mr_mla_prefill_workspace_size(C.byref(a))
+    assert 0 <= size < 2 ** 56
+    refused(lib.mr_mla_prefill(C.byref(a), None))
+
+
+def _block_dims(a, hidden, q_lora, heads, nope, rope, v, kv_rank):
+    a.hidden, a.q_lora_rank, a.heads = hidden, q_lora, heads
+    a.qk_nope_dim, a.qk_rope_dim, a.v_head_dim, a.kv_rank = nope, rope, v, kv_rank
+
+
+@SETTINGS
+@given(hidden=dim, q_lora=dim, heads=dim, nope=dim, rope=dim, v=dim, kv_rank=dim, position=big, capacity=big,
+       eps=scale, nd=st.integers(-1, 6))
+def test_decode_block_checks(lib, hidden, q_lora, heads, nope, rope, v, kv_rank, position, capacity, eps, nd):
+    a = M.BlockArgs()
+    _block_dims(a, hidden, q_lora, heads, nope, rope, v, kv_rank)
+    a.eps = eps
+    a.position, a.capacity = position, capacity
+    a.norm_w_dtype = nd
+    size = lib.mr_mla_decode_block_workspace_size(C.byref(a))
+    assert 0 <= size < 2 ** 56
+    if min(hidden, q_lora, heads, v, kv_rank) <= 0 or min(nope, rope) < 0 or position < 0:
+        assert size == 0
+    refused(lib.mr_mla_decode_block(C.byref(a), None))
+
+
+@SETTINGS
+@given(tokens=dim, hidden=dim, q_lora=dim, heads=dim, nope=dim, rope=dim, v=dim, kv_rank=dim, position=big,
+       capacity=big, eps=scale, xs=stride)
+def test_prefill_block_checks(lib, tokens, hidden, q_lora, heads, nope, rope, v, kv_rank, position, capacity, eps, xs):
+    a = M.PrefillBlockArgs()
+    a.tokens = tokens
+    _block_dims(a, hidden, q_lora, heads, nope, rope, v, kv_rank)
+    a.eps = eps
+    a.position, a.capacity = position, capacity
+    a.x_token_stride = a.out_token_stride = a.latent_row_stride = a.rope_row_stride = xs
+    size = lib.mr_mla_prefill_block_workspace_size(C.byref(a))
+    assert 0 <= size < 2 ** 56
+    if min(tokens, hidden, q_lora, heads, v, kv_rank) <= 0 or min(nope, rope) < 0 or position < 0:
+        assert size == 0
+    refused(lib.mr_mla_prefill_block(C.byref(a), None))
+
+
+@SETTINGS
+@given(batch=dim, n_idx=big, n_rows=big)
+def test_validate_indices_checks(lib, batch, n_idx, n_rows):
+    size = lib.mr_validate_indices_workspace_size(batch, n_idx)
+    assert 0 <= size < 2 ** 56
+    if batch <= 0 or n_idx < 0:
+        assert size == 0
+    tok, pos = C.c_int32(7), C.c_int32(7)
+    status = lib.mr_validate_indices(None, batch, n_idx, n_rows, None, 0, C.byref(tok), C.byref(pos), None)
+    assert tok.value == -1 and pos.value == -1
+    if status != M.OK:  # no entries is the one case with nothing to check
+        refused(status)
+    else:
+        assert n_idx == 0 and batch > 0 and n_rows >= 0
+
+
+@SETTINGS
+@given(rows=dim, cols=big, top_k=big, ratio=st.integers(-2, 300), start=big, offset=big)
+def test_topk_geometry(lib, rows, cols, top_k, ratio, start, offset):
+    sel = C.c_int32(-7)
+    status = lib.mr_topk_geometry(rows, cols, top_k, ratio, start, offset, C.byref(sel))
+    if status == M.OK:
+        assert 0 <= sel.value <= max(cols, 0)
+    else:
+        refused(status)
+    size = lib.mr_topk_workspace_size(rows, cols, top_k)
+    assert 0 <= size < 2 ** 56
