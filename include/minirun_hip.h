@@ -17,7 +17,9 @@
  *    message for the last non-OK status on the calling thread.
  *  - No entry point allocates device memory: scratch comes in as a
  *    caller-provided workspace whose size a *_workspace_size function states
- *    (0 for arguments whose widths or counts the entry point rejects).
+ *    (0 for arguments whose widths or counts the entry point rejects, and
+ *    for layouts of 2^56 bytes or more, which the entry point refuses with
+ *    MR_INVALID_SHAPE).
  */
 #ifndef MINIRUN_HIP_H
 #define MINIRUN_HIP_H
