@@ -72,8 +72,15 @@ mr_status mr_topk_geometry(int32_t rows, int32_t cols, int32_t top_k, int32_t ra
     return MR_OK;
 }
 
+// Score matrices whose workspace could reach 2^56 bytes (every buffer is at
+// most 64 bytes per score plus a slice's worth per row) have no size; the
+// selection refuses them.
+static bool topk_ws_fits(int32_t rows, int32_t cols) {
+    return double(rows) * (double(cols) + 8192.0) * 64.0 < double(mrc::WS_LIMIT);
+}
+
 size_t mr_topk_workspace_size(int32_t rows, int32_t cols, int32_t top_k) {
-    if (rows <= 0 || cols < 0 || top_k <= 0) return 0;
+    if (rows <= 0 || cols < 0 || top_k <= 0 || !topk_ws_fits(rows, cols)) return 0;
     // a row selects at most min(top_k, cols) keys (cols bounds the keys any
     // start position makes available); the size grows with that count
     return mr::topk_workspace_bytes(rows, cols, top_k < cols ? top_k : cols);
@@ -84,6 +91,8 @@ mr_status mr_topk_select(const mr_topk_args* a, void* stream) {
     int32_t selected = 0;
     mr_status st = mr_topk_geometry(a->rows, a->cols, a->top_k, a->ratio, a->start_pos, a->offset, &selected);
     if (st != MR_OK) return st;
+    if (!topk_ws_fits(a->rows, a->cols))
+        return fail(MR_INVALID_SHAPE, "top-k selection: %d rows of %d scores overflow a workspace", a->rows, a->cols);
     if (!a->scores || (selected > 0 && !a->out))
         return fail(MR_INVALID_ARGUMENT, "top-k selection: scores and out must be non-NULL");
     if (a->score_row_stride < a->cols || (selected > 0 && a->out_row_stride < selected))

@@ -6,7 +6,7 @@ never wrap (0 for widths a call rejects, else a size below 2^56).  Shapes
 range over zero, negative and very large values, scales over non-finite
 ones."""
 import ctypes as C
-import math
+import os
 
 import pytest
 from hypothesis import HealthCheck, given, settings
@@ -15,7 +15,11 @@ from hypothesis import strategies as st
 import minirun_hip as M
 
 REFUSED = {M.INVALID_SHAPE, M.INVALID_ARGUMENT, M.INVALID_DTYPE, M.WORKSPACE_TOO_SMALL}
-SETTINGS = settings(max_examples=300, deadline=None, suppress_health_check=[HealthCheck.too_slow])
+# derandomized: the same examples on every run (a longer search:
+# MR_FUZZ_EXAMPLES=5000 MR_FUZZ_RANDOM=1)
+SETTINGS = settings(max_examples=int(os.environ.get("MR_FUZZ_EXAMPLES", "300")), deadline=None,
+                    derandomize=not os.environ.get("MR_FUZZ_RANDOM"),
+                    suppress_health_check=[HealthCheck.too_slow])
 
 dim = st.one_of(st.integers(-5, 4200), st.sampled_from([0, 1, 16, 64, 96, 128, 512, 576, 2 ** 31 - 1, -2 ** 31]))
 big = st.one_of(st.integers(-3, 300000), st.sampled_from([0, 1, 32768, 131072, 2 ** 31 - 1, -2 ** 31]))
