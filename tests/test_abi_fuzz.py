@@ -4,7 +4,12 @@ must come back with a status (never a crash, never MR_OK with work left
 undone) and, when refused, with a message; the workspace-size functions
 never wrap (0 for widths a call rejects, else a size below 2^56).  Shapes
 range over zero, negative and very large values, scales over non-finite
-ones."""
+ones.
+
+The host-side tables (window and compressed attention indices, the top-k
+selection geometry) are compared with the oracle's restatement of the
+reference over random arguments: the same status, and on success the same
+table (bit for bit) or the same selected-key count."""
 import ctypes as C
 import os
 
@@ -13,6 +18,8 @@ from hypothesis import HealthCheck, given, settings
 from hypothesis import strategies as st
 
 import minirun_hip as M
+import numpy as np
+import oracle as O
 
 REFUSED = {M.INVALID_SHAPE, M.INVALID_ARGUMENT, M.INVALID_DTYPE, M.WORKSPACE_TOO_SMALL}
 # derandomized: the same examples on every run (a longer search:
@@ -139,3 +146,53 @@ def test_topk_geometry(lib, rows, cols, top_k, ratio, start, offset):
         refused(status)
     size = lib.mr_topk_workspace_size(rows, cols, top_k)
     assert 0 <= size < 2 ** 56
+
+
+def _status_of(call):
+    try:
+        return M.OK, call()
+    except M.MRError as e:
+        assert e.message
+        return e.status, None
+
+
+@SETTINGS
+@given(window=st.integers(-2, 160), seq=st.one_of(st.just(1), st.integers(-2, 160)),
+       start=st.one_of(st.just(0), st.integers(-2, 400), st.integers(2 ** 20, 2 ** 31 - 1)))
+def test_window_indices_match_oracle(window, seq, start):
+    st_o, exp = O.window_indices(window, seq, start)
+    st_m, got = _status_of(lambda: M.attention_indices_window(window, seq, start))
+    assert st_m == st_o
+    if st_o == O.OK:
+        np.testing.assert_array_equal(got, exp)
+
+
+@SETTINGS
+@given(ratio=st.integers(-2, 200), seq=st.one_of(st.just(1), st.integers(-2, 160)),
+       start=st.one_of(st.just(0), st.integers(-2, 3000)),
+       offset=st.one_of(st.integers(-2, 5000), st.integers(2 ** 31 - 3000, 2 ** 31 - 1)))
+def test_compressed_indices_match_oracle(ratio, seq, start, offset):
+    st_o, exp = O.compressed_indices(ratio, seq, start, offset)
+    st_m, got = _status_of(lambda: M.attention_indices_compressed(ratio, seq, start, offset))
+    assert st_m == st_o
+    if st_o == O.OK:
+        np.testing.assert_array_equal(got, exp)
+
+
+@SETTINGS
+@given(rows=st.one_of(st.just(1), st.integers(-1, 6)), cols=st.integers(-1, 40), top_k=st.integers(-1, 50),
+       ratio=st.integers(-1, 9), start=st.one_of(st.just(0), st.integers(-2, 60)), offset=st.integers(-2, 9))
+def test_topk_geometry_matches_oracle(lib, rows, cols, top_k, ratio, start, offset):
+    # the oracle's selection over zero scores reports the same status and,
+    # on success, as many keys per row as the geometry promises; a negative
+    # count has no score matrix, and the geometry refuses it
+    sel = C.c_int32(-7)
+    st_m = lib.mr_topk_geometry(rows, cols, top_k, ratio, start, offset, C.byref(sel))
+    if rows < 0 or cols < 0:
+        assert st_m == M.INVALID_SHAPE
+        return
+    scores = np.zeros((max(rows, 1), max(cols, 1)), np.float32)[:rows, :cols]
+    st_o, out = O.topk_select(np.ascontiguousarray(scores), top_k, ratio, start, offset)
+    assert st_m == st_o
+    if st_o == O.OK:
+        assert out.shape == (rows, sel.value)
