@@ -1,0 +1,88 @@
+"""A seeded random sweep of mr_mla_decode against the oracle: dense and
+gathered (sparse) forms over random batch sizes, head counts (including
+counts that are not multiples of the head groups), context lengths, split
+counts, output dtypes, rope widths (64 and 0, the split kernel's; 32 and 16
+at kv_rank 512, 128 and 256, the any-width kernel's), index lists (sorted or
+not, with -1 sentinels, an all-sentinel token) and attention sinks.  Each
+case names its draw (seed, index) so a failure can be rerun alone.
+
+Bar: |hip - oracle| <= 1e-2 + 2e-2 |oracle| elementwise (mla_inputs.
+within_tolerance), output-scale error below 1e-2 for bf16 outputs and 2e-3
+for f32 outputs (the split kernel's partials are bf16 beyond 4096 records);
+a token whose list holds only sentinels gives exact zeros."""
+import numpy as np
+import pytest
+
+import oracle as O
+from test_gpu_any_width import decode_inputs, run_decode
+from test_gpu_block import check, f32
+
+pytestmark = pytest.mark.gpu
+
+SEED = 20261202
+N_CASES = 24
+WIDTHS = [(512, 64), (512, 64), (512, 0), (512, 32), (256, 16), (128, 0)]
+HEADS = [1, 3, 16, 17, 32, 40, 48, 64, 96, 100, 128, 160]
+
+
+def draw(i):
+    rng = np.random.default_rng([SEED, i])
+    R, DR = WIDTHS[rng.integers(len(WIDTHS))]
+    c = dict(
+        B=int(rng.integers(1, 4)),
+        H=int(HEADS[rng.integers(len(HEADS))]),
+        N=int(rng.integers(1, 5000)),
+        R=R,
+        DR=DR,
+        splits=int(rng.integers(1, 80)) if rng.random() < 0.4 else 0,
+        f32=bool(rng.random() < 0.35),
+        sparse=bool(rng.random() < 0.5),
+        sinks=bool(rng.random() < 0.4),
+        sorted=bool(rng.random() < 0.5),
+    )
+    if c["sparse"]:
+        c["K"] = int(rng.integers(1, min(c["N"], 2500) + 1))
+    return c
+
+
+def indices(rng, c):
+    B, N, K = c["B"], c["N"], c["K"]
+    idx = np.stack([rng.choice(N, K, replace=False) for _ in range(B)]).astype(np.int32)
+    if c["sorted"]:
+        idx.sort(axis=1)
+    holes = rng.random(idx.shape) < 0.1
+    idx[holes] = -1
+    if B > 1:
+        idx[B - 1, :] = -1  # one token with no valid row
+    return idx
+
+
+@pytest.mark.parametrize("i", range(N_CASES))
+def test_decode_sweep(i):
+    import torch
+
+    import minirun_hip as M
+
+    M.load()
+    c = draw(i)
+    print(f"sweep case ({SEED}, {i}): {c}", flush=True)
+    B, H, N, R, DR = c["B"], c["H"], c["N"], c["R"], c["DR"]
+    scale = (128 + DR) ** -0.5 if DR else R ** -0.5
+    q_lat, q_rope, cache = decode_inputs(f"sw.{i}", B, H, N, R, DR)
+    rng = np.random.default_rng([SEED, i, 1])
+    idx = indices(rng, c) if c["sparse"] else None
+    sinks = O.bf16_to_f32(O.normal_bf16(f"sw.{i}.sinks", (H,))) if c["sinks"] and c["sparse"] else None
+    ydt = torch.float32 if c["f32"] else torch.bfloat16
+    st, out = run_decode(M, q_lat, q_rope, cache, R, DR, scale, ydt, indices=idx, sinks=sinks,
+                         num_splits=c["splits"])
+    assert st == M.OK, M.last_error()
+    if idx is None:
+        ref = np.stack([O.mla_decode(q_lat[b], None if q_rope is None else q_rope[b], cache[b], kv_rank=R,
+                                     rope_dim=DR, scale=scale, acc=1)[0] for b in range(B)])
+    else:
+        ost, ref = O.sparse_attention(q_lat, q_rope, cache, idx, sinks, kv_rank=R, rope_dim=DR, scale=scale, acc=1)
+        assert ost == O.OK
+    got = f32(out)
+    if idx is not None and B > 1:
+        assert np.all(got[B - 1] == 0.0), "a token with only sentinels gives zeros"
+    check(got, ref, f"sweep-{i}", scale_bar=2e-3 if c["f32"] else 1e-2)
