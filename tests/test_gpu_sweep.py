@@ -1,15 +1,19 @@
-"""A seeded random sweep of mr_mla_decode against the oracle: dense and
-gathered (sparse) forms over random batch sizes, head counts (including
-counts that are not multiples of the head groups), context lengths, split
-counts, output dtypes, rope widths (64 and 0, the split kernel's; 32 and 16
-at kv_rank 512, 128 and 256, the any-width kernel's), index lists (sorted or
-not, with -1 sentinels, an all-sentinel token) and attention sinks.  Each
-case names its draw (seed, index) so a failure can be rerun alone.
+"""Seeded random sweeps of mr_mla_decode and mr_mla_prefill against the
+oracle.  Decode: dense and gathered (sparse) forms over random batch sizes,
+head counts (including counts that are not multiples of the head groups),
+context lengths, split counts, output dtypes, rope widths (64 and 0, the
+split kernel's; 32 and 16 at kv_rank 512, 128 and 256, the any-width
+kernel's), index lists (sorted or not, with -1 sentinels, an all-sentinel
+token) and attention sinks.  Each case names its draw (seed, index) so a
+failure can be rerun alone.
 
 Bar: |hip - oracle| <= 1e-2 + 2e-2 |oracle| elementwise (mla_inputs.
 within_tolerance), output-scale error below 1e-2 for bf16 outputs and 2e-3
 for f32 outputs (the split kernel's partials are bf16 beyond 4096 records);
-a token whose list holds only sentinels gives exact zeros."""
+a token whose list holds only sentinels gives exact zeros.  Prefill: random
+prompt lengths, cached prefixes, head counts, query scales and output dtypes,
+sampled (token, head) rows at the prefill bars (elementwise, and a per-row
+relative L2 error of at most 1e-2)."""
 import numpy as np
 import pytest
 
@@ -86,3 +90,39 @@ def test_decode_sweep(i):
     if idx is not None and B > 1:
         assert np.all(got[B - 1] == 0.0), "a token with only sentinels gives zeros"
     check(got, ref, f"sweep-{i}", scale_bar=2e-3 if c["f32"] else 1e-2)
+
+
+N_PREFILL = 12
+
+
+def draw_prefill(i):
+    rng = np.random.default_rng([SEED, 1000 + i])
+    T = int(rng.integers(1, 700))
+    return dict(T=T, P=T + (int(rng.integers(0, 900)) if rng.random() < 0.6 else 0), H=int(rng.integers(1, 13)),
+                q_std=float(rng.choice([1.0, 4.0])), f32=bool(rng.random() < 0.35),
+                rows=int(rng.integers(24, 64)))
+
+
+@pytest.mark.parametrize("i", range(N_PREFILL))
+def test_prefill_sweep(i):
+    # causal prefill over a cached prefix of P - T rows (the last T rows are
+    # the prompt's own): random sampled (token, head) rows against the oracle
+    # with keys and values rounded to bf16 as the HIP path stores them
+    import torch
+
+    import minirun_hip as M
+    from test_gpu_prefill import check_rows, prefill_inputs, run
+
+    M.load()
+    c = draw_prefill(i)
+    print(f"prefill sweep case ({SEED}, {1000 + i}): {c}", flush=True)
+    T, P, H = c["T"], c["P"], c["H"]
+    q, cache, w_uk, w_uv, kv_b = prefill_inputs(T, P, H, f"swp.{i}", c["q_std"])
+    got = run(M, q, cache, kv_b, out_dtype=torch.float32 if c["f32"] else None)
+    rng = np.random.default_rng([SEED, 1000 + i, 1])
+    n = min(c["rows"], T * H)
+    flat = rng.choice(T * H, n, replace=False)
+    st, sh = (flat // H).astype(np.int32), (flat % H).astype(np.int32)
+    st[0], sh[0] = T - 1, H - 1  # the last query sees every row
+    ref = O.mla_prefill_rows(q, cache, w_uk, w_uv, st, sh, round_kv=True).reshape(n, 128)
+    check_rows(got[st, sh], ref, f"prefill-sweep-{i}")
