@@ -13,7 +13,9 @@ for f32 outputs (the split kernel's partials are bf16 beyond 4096 records);
 a token whose list holds only sentinels gives exact zeros.  Prefill: random
 prompt lengths, cached prefixes, head counts, query scales and output dtypes,
 sampled (token, head) rows at the prefill bars (elementwise, and a per-row
-relative L2 error of at most 1e-2)."""
+relative L2 error of at most 1e-2).  Top-k selection: random geometry
+(decode tokens at later positions, prompts from position 0, compression
+ratios, offsets), scores with ties and -inf masks; indices bit for bit."""
 import numpy as np
 import pytest
 
@@ -126,3 +128,40 @@ def test_prefill_sweep(i):
     st[0], sh[0] = T - 1, H - 1  # the last query sees every row
     ref = O.mla_prefill_rows(q, cache, w_uk, w_uv, st, sh, round_kv=True).reshape(n, 128)
     check_rows(got[st, sh], ref, f"prefill-sweep-{i}")
+
+
+N_TOPK = 20
+
+
+def draw_topk(i):
+    rng = np.random.default_rng([SEED, 2000 + i])
+    ratio = int(rng.integers(1, 9))
+    if rng.random() < 0.5:  # one decode token at a later position
+        cols = int(rng.integers(1, 40000))
+        rows, start = 1, int(rng.integers(0, cols * ratio))
+    else:  # a prompt from position 0
+        rows = int(rng.integers(1, 65))
+        cols = int(rng.integers(max(rows // ratio, 1), 3000))
+        start = 0
+    return dict(rows=rows, cols=cols, ratio=ratio, start=start, top_k=int(rng.integers(1, 9000)),
+                offset=int(rng.integers(0, 1 << 20)), ties=bool(rng.random() < 0.4),
+                masked=bool(rng.random() < 0.3))
+
+
+@pytest.mark.parametrize("i", range(N_TOPK))
+def test_topk_sweep(i):
+    # bit-exact indices: random geometry, scores with many ties (a few
+    # distinct values: ascending key id breaks them) and -inf masked keys
+    import minirun_hip as M
+    from test_gpu_topk import compare
+
+    M.load()
+    c = draw_topk(i)
+    print(f"top-k sweep case ({SEED}, {2000 + i}): {c}", flush=True)
+    rng = np.random.default_rng([SEED, 2000 + i, 1])
+    s = rng.standard_normal((c["rows"], c["cols"])).astype(np.float32)
+    if c["ties"]:
+        s = np.round(s * 2).astype(np.float32) * np.float32(0.5)
+    if c["masked"]:
+        s[rng.random(s.shape) < 0.2] = -np.inf
+    compare(M, s, c["top_k"], c["ratio"], c["start"], c["offset"], f"sweep-{i}")
