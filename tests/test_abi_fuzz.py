@@ -1,10 +1,12 @@
 """Argument checks of the C-ABI under random arguments (hypothesis), on the
-host: with every device pointer NULL no call reaches a GPU call, so each
-must come back with a status (never a crash, never MR_OK with work left
-undone) and, when refused, with a message; the workspace-size functions
-never wrap (0 for widths a call rejects, else a size below 2^56).  Shapes
-range over zero, negative and very large values, scales over non-finite
-ones.
+host: the attention entry points, the projections (affine, gathered, dense),
+RMSNorm, rotary, cache append, absorption, un-absorption, index checks and
+the top-k selection.  With every device buffer NULL no call reaches a GPU
+call, so each must come back with a status (never a crash, never MR_OK
+with work left undone) and, when refused, with a message; the
+workspace-size functions never wrap (0 for widths a call rejects, else a
+size below 2^56).  Shapes range over zero, negative and very large values,
+scales over non-finite ones.
 
 The host-side tables (window and compressed attention indices, the top-k
 selection geometry) are compared with the oracle's restatement of the
@@ -196,3 +198,76 @@ def test_topk_geometry_matches_oracle(lib, rows, cols, top_k, ratio, start, offs
     assert st_m == st_o
     if st_o == O.OK:
         assert out.shape == (rows, sel.value)
+
+
+dtype = st.integers(-1, 6)
+
+
+def _affine(packed_null, out_f, in_f, group, bits, sdt):
+    w = M.AffineWeightDesc()
+    w.packed = None if packed_null else C.c_void_p(256)
+    w.scales = w.biases = None
+    w.out_features, w.in_features, w.group, w.bits, w.scale_dtype = out_f, in_f, group, bits, sdt
+    return w
+
+
+def refused_or_empty(status, *counts):
+    # a call with nothing to do may return MR_OK; any other call here has a
+    # NULL buffer and must be refused
+    if status == M.OK:
+        assert min(counts) <= 0, counts
+    else:
+        refused(status)
+
+
+@SETTINGS
+@given(tokens=dim, out_f=big, in_f=big, group=st.sampled_from([0, 16, 32, 64, 128, -64]),
+       bits=st.sampled_from([0, 2, 3, 4, 8, 16]), sdt=dtype, xdt=dtype, ydt=dtype, xs=stride, ys=stride,
+       experts=st.integers(-2, 300), k=st.integers(-2, 10), pn=st.booleans())
+def test_affine_entry_checks(lib, tokens, out_f, in_f, group, bits, sdt, xdt, ydt, xs, ys, experts, k, pn):
+    w = _affine(pn, out_f, in_f, group, bits, sdt)
+    refused(lib.mr_affine_dequantize(C.byref(w), None, ydt, None))
+    refused_or_empty(lib.mr_affine_matmul(None, xdt, tokens, xs, C.byref(w), None, ydt, ys, None), tokens)
+    refused_or_empty(lib.mr_affine_gather_matmul(None, xdt, tokens, xs, C.byref(w), experts, None, k, None, ydt,
+                                                 None), tokens, k)
+    refused(lib.mr_affine_dequantize(None, None, ydt, None))
+
+
+@SETTINGS
+@given(tokens=dim, out_f=big, in_f=big, wdt=dtype, xdt=dtype, ydt=dtype, xs=stride, ys=stride, rs=stride,
+       wn=st.booleans())
+def test_linear_checks(lib, tokens, out_f, in_f, wdt, xdt, ydt, xs, ys, rs, wn):
+    w = M.DenseWeightDesc()
+    w.weight = None if wn else C.c_void_p(256)
+    w.dtype, w.out_features, w.in_features, w.row_stride = wdt, out_f, in_f, rs
+    refused_or_empty(lib.mr_linear(None, xdt, tokens, xs, C.byref(w), None, ydt, ys, None), tokens)
+    refused(lib.mr_linear(None, xdt, tokens, xs, None, None, ydt, ys, None))
+
+
+@SETTINGS
+@given(rows=big, d=dim, xdt=dtype, wdt=dtype, odt=dtype, xs=stride, os_=stride, eps=scale, n_pos=big,
+       inner=dim, col0=st.integers(-3, 600), kv_rank=dim, rope=dim, tokens=big, heads=dim, nope=dim, v=dim,
+       kind=st.integers(-1, 3))
+def test_norm_rope_cache_absorb_checks(lib, rows, d, xdt, wdt, odt, xs, os_, eps, n_pos, inner, col0, kv_rank, rope,
+                                       tokens, heads, nope, v, kind):
+    refused_or_empty(lib.mr_rmsnorm(None, xdt, rows, d, xs, None, wdt, eps, None, odt, os_, None), rows)
+    refused_or_empty(lib.mr_rope_apply(None, xdt, n_pos, inner, xs, col0, d, None, None, None), n_pos, inner)
+    refused_or_empty(lib.mr_mla_cache_append(None, xdt, xs, tokens, None, wdt, eps, kv_rank, rope, None, None, None,
+                                             os_, None, os_, col0, None), tokens)
+    p = M.ProjectionDesc()
+    p.kind = kind
+    p.affine = _affine(False, heads * (nope + v) if heads > 0 and nope + v > 0 else 0, kv_rank, 64, 4, M.BF16)
+    refused_or_empty(lib.mr_mla_absorb_query(None, xs, heads, nope, v, C.byref(p), None, os_, None), heads)
+    refused_or_empty(lib.mr_mla_unabsorb_values(None, xs, heads, nope, v, C.byref(p), None, odt, None), heads)
+    refused(lib.mr_mla_absorb_query(None, xs, heads, nope, v, None, None, os_, None))
+
+
+@SETTINGS
+@given(rows=dim, cols=big, top_k=big, ratio=st.integers(-2, 9), start=big, offset=big, flags=st.integers(0, 15),
+       os_=stride, ss=stride, ws=st.sampled_from([0, 1 << 20]))
+def test_topk_select_checks(lib, rows, cols, top_k, ratio, start, offset, flags, os_, ss, ws):
+    a = M.TopkArgs()
+    a.rows, a.cols, a.top_k, a.ratio, a.start_pos, a.offset, a.flags = rows, cols, top_k, ratio, start, offset, flags
+    a.score_row_stride, a.out_row_stride, a.workspace_bytes = ss, os_, ws
+    refused(lib.mr_topk_select(C.byref(a), None))
+    refused(lib.mr_topk_select(None, None))
